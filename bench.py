@@ -1,0 +1,245 @@
+"""Benchmark of the NF4 QLoRA linear path on one MI355X.
+
+    python bench.py [--steps K] [--warmup W] [--gpus 1] [--no-cpu] [--layers 28]
+
+Workload: the 28-layer NF4 linear stack of Qwen2.5-1.5B, forward + backward,
+M = 2048 packed tokens, LoRA r = 16 (alpha 32) with dropout 0.05 on q_proj and v_proj, random-init
+weights W ~ N(0, 0.02) quantised to NF4 with double quantisation on the GPU, synthetic fp16
+activations ~ N(0, 1) and upstream gradients ~ N(0, 1e-2), all resident in HBM before timing.
+One step = every layer's forward then every layer's backward (dX of all seven projections plus
+the LoRA gradients).  value = algorithmic TFLOP/s of the step (2 M N K per GEMM; dequant counts
+no FLOPs).
+
+Also measured live with HIP events on the launch stream: each kernel of the step in isolation
+(average launch duration -> TFLOP/s or GB/s), and the NF4 dequant of all 28 layers (3.30 GB of
+algorithmic traffic, far above the 256 MB Infinity Cache) -> GB/s against the 8 TB/s HBM peak.
+The CPU baseline times the CPU oracle (numpy dequant + fp32 torch GEMMs) on one layer's
+forward + backward, on this host's cores.
+"""
+
+import argparse
+import json
+import os
+import sys
+import time
+
+HBM_PEAK_GBS = 8000.0
+FP16_PEAK_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense fp16 MFMA)
+
+
+def _events(torch):
+    return torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+
+
+def time_op(torch, fn, reps):
+    """Average duration (ms) of fn over `reps` back-to-back launches, HIP events on the current
+    stream (the stream every operator launches on)."""
+    fn()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        fn()
+    e1.record()
+    torch.cuda.synchronize()
+    return e0.elapsed_time(e1) / reps
+
+
+def kernel_table(torch, st, reps):
+    """Each operator of one layer's step in isolation (layer 0), with its algorithmic work."""
+    from decentrik_prime_amd import w4linear as W
+    m, D, I, KV, r = st.m, 1536, 8960, 256, 16
+    L, lo, z, x, dy, o = st.layers[0], st.lora[0], st.z[0], st.x, st.dy, st.out
+    ks, s = st.keep_scale, st.s
+    gu = st.gu[0]
+    gu_save = gu.clone()
+    g = lambda mm, n, k: 2.0 * mm * n * k  # noqa: E731
+    rows = [
+        # name, fn, flops, bytes, launches per step (per layer)
+        ("w4_gateup_swiglu_fwd", lambda: W.gateup_swiglu_forward(x, L["gu"], act=st.act, gu=gu),
+         g(m, 2 * I, D), None, 1),
+        ("w4_linear_fwd down", lambda: W.linear_forward(st.act, L["d"], out=o["y"]), g(m, D, I), None, 1),
+        ("w4_linear_fwd q+lora", lambda: W.linear_forward(x, L["q"], None, z["q"], lo["Bq"], s, out=o["q"]),
+         g(m, D, D) + g(m, D, r), None, 1),
+        ("w4_linear_fwd o", lambda: W.linear_forward(x, L["o"], out=o["o"]), g(m, D, D), None, 1),
+        ("w4_linear_fwd k", lambda: W.linear_forward(x, L["k"], out=o["k"]), g(m, KV, D), None, 1),
+        ("w4_linear_fwd v+lora", lambda: W.linear_forward(x, L["v"], None, z["v"], lo["Bv"], s, out=o["v"]),
+         g(m, KV, D) + g(m, KV, r), None, 1),
+        ("w4_down_swiglu_bwd", lambda: W.down_swiglu_backward(dy["d"], L["d"], gu), g(m, I, D), None, 1),
+        ("w4_linear_bwd_dx gate|up", lambda: W.linear_backward_dx(gu, L["gu"], out=st.dx_mlp),
+         g(m, D, 2 * I), None, 1),
+        ("w4_linear_bwd_dx o", lambda: W.linear_backward_dx(dy["o"], L["o"], out=st.dx_o), g(m, D, D), None, 1),
+        ("w4_linear_bwd_dx q+lora", lambda: W.linear_backward_dx(dy["q"], L["q"], z["q"], lo["Aq"], lo["mq"], ks,
+                                                                  out=st.dx_qkv), g(m, D, D) + g(m, D, r), None, 1),
+        ("w4_linear_bwd_dx k", lambda: W.linear_backward_dx(dy["k"], L["k"], out=st.dx_qkv, accumulate=True),
+         g(m, D, KV), None, 1),
+        ("lora_down", lambda: W.lora_down(x, lo["Aq"], lo["mq"], ks, out=z["q"]), g(m, r, D),
+         m * D * 3 + r * D * 2 + m * r * 2, 2),
+        ("lora_grads q", lambda: W.lora_grads(dy["q"], z["q"], x, lo["Bq"], s, lo["mq"], ks),
+         g(m, r, D) * 3, None, 1),
+    ]
+    out = []
+    for name, fn, flops, nbytes, per_layer in rows:
+        ms = time_op(torch, fn, reps)
+        row = {"kernel": name, "avg_us": round(ms * 1e3, 2), "launches_per_layer": per_layer,
+               "gflop": round(flops / 1e9, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
+               "frac_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+        if nbytes:
+            row["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+        out.append(row)
+    gu.copy_(gu_save)
+    return out
+
+
+def dequant_bandwidth(torch, st, reps):
+    """NF4 dequant of every layer into its own fp16 output (the working set, 3.30 GB of
+    algorithmic traffic for 28 layers, does not fit the 256 MB Infinity Cache)."""
+    from decentrik_prime_amd import k_nf4
+    outs = [torch.empty(L["packed"].numel, dtype=torch.float16, device=st.device) for L in st.layers]
+
+    def run():
+        for L, out in zip(st.layers, outs):
+            k_nf4.dequant_layer(L["packed"], st.code2, st.nf4, out)
+    ms = time_op(torch, run, reps)
+    n_weights = st.layers[0]["packed"].numel
+    bytes_per_weight = 0.5 + 1 / 64 + 8 / 16384 + 2
+    per_launch_bytes = n_weights * bytes_per_weight
+    avg_launch_ms = ms / len(st.layers)
+    gbps = per_launch_bytes / (avg_launch_ms * 1e-3) / 1e9
+    del outs
+    torch.cuda.empty_cache()
+    return {"kernel": "nf4_dequant_kernel (dequant_layer)", "weights_per_launch": n_weights,
+            "bytes_per_weight": bytes_per_weight, "bytes_per_launch": int(per_launch_bytes),
+            "avg_us": round(avg_launch_ms * 1e3, 2), "gbps": round(gbps, 1),
+            "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)}
+
+
+def cpu_baseline(layers=1, m=2048):
+    """The CPU oracle on `layers` layer(s) of the same workload: numpy NF4 dequant of the seven
+    weights + fp32 torch GEMMs of the forward and backward with the LoRA terms."""
+    import numpy as np
+    import torch
+    from oracle import linear, mlp, nf4
+    torch.set_num_threads(os.cpu_count())
+    rng = np.random.default_rng(0)
+    D, I, KV, r = 1536, 8960, 256, 16
+    shapes = {"q": (D, D), "k": (KV, D), "v": (KV, D), "o": (D, D), "g": (2 * I, D), "d": (D, I)}
+    qs = {}
+    for name, shp in shapes.items():
+        w = (rng.standard_normal(shp, dtype=np.float32) * 0.02).astype(np.float16)
+        qs[name] = nf4.quantize(w)
+    x = rng.standard_normal((m, D), dtype=np.float32).astype(np.float16)
+    a = (rng.uniform(-1, 1, (r, D)) / np.sqrt(D)).astype(np.float16)
+    bq = (rng.standard_normal((D, r)) * 0.02).astype(np.float16)
+    bv = (rng.standard_normal((KV, r)) * 0.02).astype(np.float16)
+    mask = (rng.random((m, D)) >= 0.05).astype(np.uint8)
+    dys = {k: (rng.standard_normal((m, n), dtype=np.float32) * 1e-2).astype(np.float16)
+           for k, n in (("q", D), ("k", KV), ("v", KV), ("o", D), ("d", D))}
+    ks = linear.keep_scale(0.05)
+    t0 = time.perf_counter()
+    for _ in range(layers):
+        wd = {k: nf4.dequant(q["packed"], q["qabs"], q["scale2"], q["offset2"], q["code2"]).reshape(shapes[k])
+              for k, q in qs.items()}
+        _, zq = linear.linear_fwd(x, wd["q"], None, mask, ks, a, bq, 2.0)
+        linear.linear_fwd(x, wd["k"])
+        _, zv = linear.linear_fwd(x, wd["v"], None, mask, ks, a, bv, 2.0)
+        linear.linear_fwd(x, wd["o"])
+        gu, h, _ = mlp.mlp_fwd(x, wd["g"], wd["d"])
+        mlp.mlp_bwd(dys["d"], gu, wd["g"], wd["d"])
+        linear.linear_bwd(dys["o"], wd["o"])
+        linear.linear_bwd(dys["q"], wd["q"], zq, x, mask, ks, a, bq, 2.0)
+        linear.linear_bwd(dys["k"], wd["k"])
+        linear.linear_bwd(dys["v"], wd["v"], zv, x, mask, ks, a, bv, 2.0)
+    dt = time.perf_counter() - t0
+    from decentrik_prime_amd.stack import layer_flops
+    flops = layers * layer_flops(m)
+    return {"value": round(flops / dt / 1e12, 4), "unit": "TFLOP/s", "cores": torch.get_num_threads(),
+            "kind": "port",
+            "sample": f"{layers} layer(s) of config 4 fwd+bwd at M={m} (NF4 dequant + fp32 GEMMs), "
+                      f"{dt:.2f} s; full 28-layer step extrapolated = {dt * 28 / layers:.1f} s",
+            "cpu_model": _cpu_model(), "os_cpu_count": os.cpu_count()}
+
+
+def _cpu_model():
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=10)
+    ap.add_argument("--warmup", type=int, default=2)
+    ap.add_argument("--layers", type=int, default=28)
+    ap.add_argument("--m", type=int, default=2048)
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--reps", type=int, default=20)
+    args = ap.parse_args()
+    if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
+        print("bench.py measures one GPU: the NF4 linear path has no multi-GPU leg in this build "
+              "(it would shard data-parallel over packed tokens with one LoRA-gradient all-reduce)",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import torch
+    from decentrik_prime_amd.stack import NF4LinearStack
+    torch.cuda.set_device(0)
+    print(f"[bench] building {args.layers}-layer NF4 stack, M={args.m}", file=sys.stderr, flush=True)
+    st = NF4LinearStack(args.layers, args.m, seed=0, device="cuda")
+    torch.cuda.synchronize()
+    for _ in range(args.warmup):
+        st.step()
+    torch.cuda.synchronize()
+    print("[bench] warmup done", file=sys.stderr, flush=True)
+    e0, e1 = _events(torch)
+    t0 = time.perf_counter()
+    e0.record()
+    for _ in range(args.steps):
+        st.step()
+    e1.record()
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    ms_per_step = e0.elapsed_time(e1) / args.steps
+    value = st.flops_per_step / (ms_per_step * 1e-3) / 1e12
+    print(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} TFLOP/s (wall {wall:.2f} s)",
+          file=sys.stderr, flush=True)
+
+    result = {
+        "metric": "NF4 QLoRA linear fwd+bwd TFLOP/s (M=2048, Qwen2.5-1.5B); dequant GB/s",
+        "value": round(value, 2), "unit": "TFLOP/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms_per_step, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp16", "data": "synthetic",
+        "config": {"workload": "config 4: Qwen2.5-1.5B NF4 linear stack fwd+bwd",
+                   "layers": args.layers, "m_tokens": args.m, "lora_rank": 16, "lora_alpha": 32,
+                   "lora_dropout": 0.05, "lora_on": ["q_proj", "v_proj"],
+                   "flop_per_step": st.flops_per_step},
+    }
+    if not args.no_kernels:
+        kernels = kernel_table(torch, st, args.reps)
+        print("[bench] kernel table done", file=sys.stderr, flush=True)
+        dq = dequant_bandwidth(torch, st, max(3, args.reps // 4))
+        print(f"[bench] dequant {dq['gbps']} GB/s", file=sys.stderr, flush=True)
+        dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
+        result["roofline"] = {
+            "kernel": dom["kernel"], "bound": "mfma", "achieved": dom["tflops"],
+            "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac_fp16_peak"],
+            "traffic": None,
+            "per_launch": f"{dom['gflop']} GFLOP algorithmic / {dom['avg_us']} us average launch"}
+        result["dequant"] = {**dq, "roofline": {"bound": "hbm", "achieved": dq["gbps"],
+                                                "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                                                "frac": dq["frac_hbm_peak"]}}
+        result["kernels"] = kernels
+    if not args.no_cpu:
+        print("[bench] CPU baseline (oracle, 1 layer)", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(1, args.m)
+    print(json.dumps(result), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,485 @@
+// Fused NF4 (W4) GEMMs on gfx950: dequant in LDS, v_mfma_f32_32x32x16_f16, fp32 accumulate.
+//
+//   forward  "NT":  C[m][n] = sum_k A[m][k] * W[n][k]      W stored [N][K], K contiguous
+//   backward "NN":  C[m][n] = sum_k A[m][k] * W[k][n]      W stored [K][N], N contiguous
+//
+// A is fp16 row-major [M][K] (X or dY).  A 256-thread workgroup (4 waves, 2 x 2) owns a
+// BM x BN tile of C and walks K in steps of 64 with two LDS buffers: while the MFMAs consume one
+// buffer, the next A tile and the next packed W tile are already in registers and are written
+// into the other buffer, the W tile being dequantised on the way (NF4 table and second-level code
+// table resident in LDS).  Both LDS tiles are K-contiguous rows padded to 72 halves, so every
+// MFMA operand is one conflict-free ds_read_b128; the NN producer transposes a 4 x 8 block of
+// weights in registers before writing it.  One first-level block covers 64 consecutive weights of
+// a stored row, so each 16-byte packed chunk (NT) or 4-byte chunk (NN) has a single absmax.
+//
+// Epilogues (fused, per output element, rounding like the reference's separate ops):
+//   LINEAR      y = fp16(acc + bias); + LoRA: fp16(fp32(y) + s * fp32(fp16(z B^T)))     (forward)
+//               dX = fp32(fp16(acc)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0)        (backward)
+//               the rank-16 LoRA product is one extra MFMA per 32 x 32 tile and rank slice.
+//   SWIGLU_FWD  the B rows of each wave's 64 columns are 32 gate rows and the matching 32 up
+//               rows, so g and u of one output sit in the same lane and register:
+//               act = fp16(silu(fp16(g)) * fp16(u)), optional [g | u] store.
+//   SWIGLU_BWD  dact = fp16(acc), then the gated-SiLU backward in place on gu.
+#include "dk_common.h"
+
+namespace {
+
+constexpr int kBK = 64;
+constexpr int kStride = kBK + 8;  // halves per LDS row (144 bytes)
+constexpr int kThreads = 256;
+
+enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
+
+struct GemmParams {
+  const f16* a;
+  int64_t lda;
+  int64_t M, N, K;
+  const uint8_t* packed;
+  const uint8_t* qabs;
+  const float* scale2;
+  const float* offset2;
+  const float* code2;
+  const float* nf4;
+  int64_t inter;        // SwiGLU: gate/up width I
+  const f16* bias;      // [N] or null
+  const f16* lz;        // LoRA left factor [M][rank] (z forward, dz backward) or null
+  const f16* lr;        // LoRA right factor: forward B [N][rank]; backward A [rank][N]
+  int64_t rank;
+  float lora_scale;
+  const uint8_t* mask;  // backward dropout keep-mask [M][N] or null
+  float keep_scale;
+  void* out;
+  int64_t ldo;
+  int out_mode;
+  f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
+  int tiles_m;
+};
+
+__device__ __forceinline__ uint32_t dq_pair(const float* lut, uint32_t byte, float amax) {
+  const f16 even = dk_h(__fmul_rn(lut[(byte >> 4) & 15u], amax));
+  const f16 odd = dk_h(__fmul_rn(lut[byte & 15u], amax));
+  return dk_pack2(even, odd);
+}
+
+template <int BM, int BN, bool TRANS, int EPI>
+__global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
+  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int A_CHUNKS = BM * kBK / 8 / kThreads;
+  constexpr int B_UNITS = BN / 128 > 0 ? BN / 128 : 1;
+  constexpr int B_ACTIVE = BN * 2;  // NT: 16-byte chunks; NN: 4 x 8 units (both 2 * BN)
+  static_assert(TM >= 1 && TN >= 1, "tile too small");
+  static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
+
+  __shared__ __attribute__((aligned(16))) f16 As[2][BM * kStride];
+  __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * kStride];
+  __shared__ float lut[16];
+  __shared__ float c2t[256];
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int wm = wave & 1, wn = wave >> 1;
+
+  // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin, so give each XCD a
+  // contiguous run of tiles (M fastest: consecutive tiles share the same W tile in that L2).
+  int b = blockIdx.x;
+  const int nb = gridDim.x;
+  if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
+  const int64_t m0 = (int64_t)(b % p.tiles_m) * BM;
+  const int64_t n0 = (int64_t)(b / p.tiles_m) * BN;
+
+  if (tid < 16) lut[tid] = p.nf4[tid];
+  c2t[tid] = p.code2[tid];
+
+  const int64_t M = p.M, N = p.N, K = p.K;
+  const int nk = (int)(K / kBK);
+
+  // ---- global -> register staging
+  u32x4 a_reg[A_CHUNKS];
+  uint32_t b_word[B_UNITS][TRANS ? 4 : 4];
+  uint32_t b_code[B_UNITS][TRANS ? 4 : 1];
+  float b_s2[B_UNITS][TRANS ? 4 : 1];
+  float b_o2[B_UNITS][TRANS ? 4 : 1];
+
+  auto load_tiles = [&](int kt) {
+    const int64_t k0 = (int64_t)kt * kBK;
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c >> 3, col8 = c & 7;
+      const int64_t gm = m0 + row;
+      if (gm < M) {
+        a_reg[i] = *reinterpret_cast<const u32x4*>(p.a + gm * p.lda + k0 + col8 * 8);
+      } else {
+        a_reg[i] = u32x4{0u, 0u, 0u, 0u};
+      }
+    }
+#pragma unroll
+    for (int i = 0; i < B_UNITS; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < B_ACTIVE) {
+        if (!TRANS) {
+          const int row = c >> 1, half = c & 1;
+          int64_t n = n0 + row;
+          if (EPI == EPI_SWIGLU_FWD) {
+            const int64_t g = n >> 6, w = n & 63;
+            n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
+          }
+          const int64_t elem = n * K + k0 + half * 32;
+          const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
+          b_word[i][0] = v[0];
+          b_word[i][1] = v[1];
+          b_word[i][2] = v[2];
+          b_word[i][3] = v[3];
+          const int64_t q = elem >> 6;
+          b_code[i][0] = p.qabs[q];
+          b_s2[i][0] = p.scale2[q >> 8];
+          b_o2[i][0] = p.offset2[q >> 8];
+        } else {
+          const int ng = c % (BN / 8), kg = c / (BN / 8);
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const int64_t elem = (k0 + 4 * kg + r) * N + n0 + 8 * ng;
+            b_word[i][r] = *reinterpret_cast<const uint32_t*>(p.packed + (elem >> 1));
+            const int64_t q = elem >> 6;
+            b_code[i][r] = p.qabs[q];
+            b_s2[i][r] = p.scale2[q >> 8];
+            b_o2[i][r] = p.offset2[q >> 8];
+          }
+        }
+      }
+    }
+  };
+
+  auto store_tiles = [&](int buf) {
+    f16* as = As[buf];
+    f16* bs = Bs[buf];
+#pragma unroll
+    for (int i = 0; i < A_CHUNKS; ++i) {
+      const int c = tid + kThreads * i;
+      const int row = c >> 3, col8 = c & 7;
+      *reinterpret_cast<u32x4*>(as + row * kStride + col8 * 8) = a_reg[i];
+    }
+#pragma unroll
+    for (int i = 0; i < B_UNITS; ++i) {
+      const int c = tid + kThreads * i;
+      if (c < B_ACTIVE) {
+        if (!TRANS) {
+          const int row = c >> 1, half = c & 1;
+          const float amax = dk_absmax(c2t[b_code[i][0]], b_s2[i][0], b_o2[i][0]);
+          f16* dst = bs + row * kStride + half * 32;
+#pragma unroll
+          for (int d = 0; d < 4; ++d) {
+            const uint32_t w = b_word[i][d];
+            u32x4 o;
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) o[bb] = dq_pair(lut, (w >> (8 * bb)) & 0xffu, amax);
+            *reinterpret_cast<u32x4*>(dst + d * 8) = o;
+          }
+        } else {
+          const int ng = c % (BN / 8), kg = c / (BN / 8);
+          f16 v[4][8];
+#pragma unroll
+          for (int r = 0; r < 4; ++r) {
+            const float amax = dk_absmax(c2t[b_code[i][r]], b_s2[i][r], b_o2[i][r]);
+            const uint32_t w = b_word[i][r];
+#pragma unroll
+            for (int bb = 0; bb < 4; ++bb) {
+              const uint32_t byte = (w >> (8 * bb)) & 0xffu;
+              v[r][2 * bb] = dk_h(__fmul_rn(lut[byte >> 4], amax));
+              v[r][2 * bb + 1] = dk_h(__fmul_rn(lut[byte & 15u], amax));
+            }
+          }
+#pragma unroll
+          for (int col = 0; col < 8; ++col) {
+            u32x2 o;
+            o[0] = dk_pack2(v[0][col], v[1][col]);
+            o[1] = dk_pack2(v[2][col], v[3][col]);
+            *reinterpret_cast<u32x2*>(bs + (8 * ng + col) * kStride + 4 * kg) = o;
+          }
+        }
+      }
+    }
+  };
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  const int lrow = lane & 31;
+  const int lk = 8 * (lane >> 5);
+
+  load_tiles(0);
+  __syncthreads();  // lut / c2t visible
+  store_tiles(0);
+  __syncthreads();
+
+  for (int kt = 0; kt < nk; ++kt) {
+    const int cur = kt & 1;
+    if (kt + 1 < nk) load_tiles(kt + 1);
+    const f16* as = As[cur];
+    const f16* bs = Bs[cur];
+#pragma unroll
+    for (int s = 0; s < kBK / 16; ++s) {
+      f16x8 af[TM], bf[TN];
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+        af[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk);
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+    }
+    if (kt + 1 < nk) store_tiles(cur ^ 1);
+    __syncthreads();
+  }
+
+  // ---- epilogue.  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
+  // 8 * (v / 4) + 4 * (lane / 32) + v % 4 for register v.
+  const int rsub = 4 * (lane >> 5);
+  if (EPI == EPI_LINEAR) {
+    const bool has_lora = p.lz != nullptr;
+    f16* out16 = reinterpret_cast<f16*>(p.out);
+    float* out32 = reinterpret_cast<float*>(p.out);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t mrow0 = m0 + wm * WM + 32 * i;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + wn * WN + 32 * j + lrow;
+        f32x16 lo;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
+        if (has_lora) {
+          const int64_t zm = mrow0 + lrow;
+          for (int rc = 0; rc < p.rank; rc += 16) {
+            f16x8 zf, rf;
+            if (zm < M) {
+              zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
+            }
+            if (!TRANS) {
+              rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk + e) * N + n];
+            }
+            lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
+          }
+        }
+        const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+          if (m >= M) continue;
+          const f16 y16 = dk_h(__fadd_rn(acc[i][j][v], bias));
+          float r = (float)y16;
+          if (has_lora) {
+            float lf = (float)dk_h(lo[v]);
+            if (TRANS) {
+              if (p.mask) lf = p.mask[m * N + n] ? __fmul_rn(lf, p.keep_scale) : 0.0f;
+            } else {
+              lf = __fmul_rn(p.lora_scale, lf);
+            }
+            r = __fadd_rn(r, lf);
+          }
+          const int64_t o = m * p.ldo + n;
+          if (p.out_mode == DK_OUT_F16) {
+            out16[o] = dk_h(r);
+          } else if (p.out_mode == DK_OUT_F32) {
+            out32[o] = r;
+          } else {
+            out32[o] = __fadd_rn(out32[o], r);
+          }
+        }
+      }
+    }
+  } else if (EPI == EPI_SWIGLU_FWD) {
+    f16* act = reinterpret_cast<f16*>(p.out);
+    const int64_t hcol = (n0 + wn * WN) / 2 + lrow;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t mrow0 = m0 + wm * WM + 32 * i;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+        if (m >= M) continue;
+        const f16 g16 = dk_h(acc[i][0][v]);
+        const f16 u16 = dk_h(acc[i][1][v]);
+        const float g = (float)g16;
+        const float silu = g / (1.0f + __expf(-g));
+        act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
+        if (p.gu) {
+          p.gu[m * 2 * p.inter + hcol] = g16;
+          p.gu[m * 2 * p.inter + p.inter + hcol] = u16;
+        }
+      }
+    }
+  } else {  // EPI_SWIGLU_BWD: N == inter
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t mrow0 = m0 + wm * WM + 32 * i;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = n0 + wn * WN + 32 * j + lrow;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+          if (m >= M) continue;
+          const float da = (float)dk_h(acc[i][j][v]);
+          f16* gp = p.gu + m * 2 * p.inter + n;
+          const float g = (float)gp[0];
+          const float u = (float)gp[p.inter];
+          const float e = 1.0f + __expf(-g);
+          const float sig = 1.0f / e;
+          const float silu = g / e;
+          gp[p.inter] = dk_h(da * silu);
+          gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
+        }
+      }
+    }
+  }
+}
+
+template <int BM, int BN, bool TRANS, int EPI>
+int launch(GemmParams p, hipStream_t stream) {
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  const int64_t tiles = (int64_t)p.tiles_m * (p.N / BN);
+  if (tiles <= 0 || tiles > 0x7fffffff) return DK_ERR_INVALID;
+  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)tiles), dim3(kThreads),
+                     0, stream, p);
+  DK_CHECK_LAUNCH();
+  return 0;
+}
+
+bool weight_ok(const dk_nf4_weight* w) {
+  return w && w->packed && w->qabs && w->scale2 && w->offset2 && w->code2 && w->nf4 &&
+         w->rows > 0 && w->cols > 0 && (w->rows * w->cols) % DK_ELEMS_PER_SB == 0;
+}
+
+void set_weight(GemmParams& p, const dk_nf4_weight* w) {
+  p.packed = w->packed;
+  p.qabs = w->qabs;
+  p.scale2 = w->scale2;
+  p.offset2 = w->offset2;
+  p.code2 = w->code2;
+  p.nf4 = w->nf4;
+}
+
+int check_lora(const void* left, const void* right, int64_t rank) {
+  if ((left == nullptr) != (right == nullptr)) return DK_ERR_INVALID;
+  if (left && (rank < 16 || rank > 64 || rank % 16)) return DK_ERR_INVALID;
+  if (left && !dk_aligned(left, 16)) return DK_ERR_ALIGN;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
+                                const void* bias, const void* z, const void* lora_b,
+                                int64_t rank, float lora_scale, void* y, int64_t ldy,
+                                hipStream_t stream) {
+  if (m < 0 || !weight_ok(w) || !x || !y) return DK_ERR_INVALID;
+  if (w->rows % 64 || w->cols % kBK || ldx < w->cols || ldy < w->rows) return DK_ERR_INVALID;
+  if (int e = check_lora(z, lora_b, rank)) return e;
+  if (z && !dk_aligned(lora_b, 16)) return DK_ERR_ALIGN;
+  if (!dk_aligned(x, 16) || ldx % 8 || !dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
+  if (m == 0) return 0;
+  GemmParams p = {};
+  p.a = (const f16*)x;
+  p.lda = ldx;
+  p.M = m;
+  p.N = w->rows;
+  p.K = w->cols;
+  set_weight(p, w);
+  p.bias = (const f16*)bias;
+  p.lz = (const f16*)z;
+  p.lr = (const f16*)lora_b;
+  p.rank = rank;
+  p.lora_scale = lora_scale;
+  p.out = y;
+  p.ldo = ldy;
+  p.out_mode = DK_OUT_F16;
+  if (p.N % 128 == 0) return launch<128, 128, false, EPI_LINEAR>(p, stream);
+  return launch<128, 64, false, EPI_LINEAR>(p, stream);
+}
+
+extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
+                                   const dk_nf4_weight* w, const void* dz, const void* lora_a,
+                                   int64_t rank, const uint8_t* mask, float keep_scale, void* dx,
+                                   int64_t lddx, int out_mode, hipStream_t stream) {
+  if (m < 0 || !weight_ok(w) || !dy || !dx) return DK_ERR_INVALID;
+  if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
+  if (w->cols % 64 || w->rows % kBK || lddy < w->rows || lddx < w->cols) return DK_ERR_INVALID;
+  if (int e = check_lora(dz, lora_a, rank)) return e;
+  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(w->packed, 4)) return DK_ERR_ALIGN;
+  if (m == 0) return 0;
+  GemmParams p = {};
+  p.a = (const f16*)dy;
+  p.lda = lddy;
+  p.M = m;
+  p.N = w->cols;
+  p.K = w->rows;
+  set_weight(p, w);
+  p.lz = (const f16*)dz;
+  p.lr = (const f16*)lora_a;
+  p.rank = rank;
+  p.mask = mask;
+  p.keep_scale = mask ? keep_scale : 1.0f;
+  p.out = dx;
+  p.ldo = lddx;
+  p.out_mode = out_mode;
+  if (p.N % 128 == 0) return launch<128, 128, true, EPI_LINEAR>(p, stream);
+  return launch<128, 64, true, EPI_LINEAR>(p, stream);
+}
+
+extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
+                                       const dk_nf4_weight* w_gu, void* act, void* gu_out,
+                                       hipStream_t stream) {
+  if (m < 0 || !weight_ok(w_gu) || !x || !act) return DK_ERR_INVALID;
+  if (w_gu->rows % 128 || w_gu->cols % kBK || ldx < w_gu->cols) return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16) || ldx % 8 || !dk_aligned(w_gu->packed, 16)) return DK_ERR_ALIGN;
+  if (m == 0) return 0;
+  GemmParams p = {};
+  p.a = (const f16*)x;
+  p.lda = ldx;
+  p.M = m;
+  p.N = w_gu->rows;  // logical columns: 2 * inter, interleaved in groups of 32
+  p.K = w_gu->cols;
+  p.inter = w_gu->rows / 2;
+  set_weight(p, w_gu);
+  p.out = act;
+  p.ldo = p.inter;
+  p.gu = (f16*)gu_out;
+  return launch<128, 128, false, EPI_SWIGLU_FWD>(p, stream);
+}
+
+extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
+                                     const dk_nf4_weight* w_down, void* gu, hipStream_t stream) {
+  if (m < 0 || !weight_ok(w_down) || !dh || !gu) return DK_ERR_INVALID;
+  if (w_down->cols % 64 || w_down->rows % kBK || lddh < w_down->rows) return DK_ERR_INVALID;
+  if (!dk_aligned(dh, 16) || lddh % 8 || !dk_aligned(w_down->packed, 4)) return DK_ERR_ALIGN;
+  if (m == 0) return 0;
+  GemmParams p = {};
+  p.a = (const f16*)dh;
+  p.lda = lddh;
+  p.M = m;
+  p.N = w_down->cols;  // inter
+  p.K = w_down->rows;  // d_model
+  p.inter = w_down->cols;
+  set_weight(p, w_down);
+  p.gu = (f16*)gu;
+  if (p.N % 128 == 0) return launch<128, 128, true, EPI_SWIGLU_BWD>(p, stream);
+  return launch<128, 64, true, EPI_SWIGLU_BWD>(p, stream);
+}

@@ -1,0 +1,131 @@
+"""The NF4 linear stack of Qwen2.5-1.5B (28 layers), forward + backward, on the fused kernels.
+
+Per layer (shapes of solution/fast_qwen.py:53 QWEN15: D = 1536, I = 8960, KV = 256, r = 16),
+with M packed tokens:
+
+  forward   z_q = lora_down(X, A_q, mask_q)            z_v likewise        (rank-16 LoRA inputs)
+            q = X W_q^T + s z_q B_q^T,  k = X W_k^T,  v = X W_v^T + s z_v B_v^T
+            o = X W_o^T                                 (X stands in for the attention output)
+            act, gu = SwiGLU(X W_gu^T)                  gate|up as one GEMM, gu kept
+            y = act W_d^T
+  backward  gu <- SwiGLU'(dY_d W_d, gu)                 down^T GEMM + SwiGLU backward fused
+            dX_mlp = gu W_gu                            [M, 2I] x [2I, D]
+            dX_o = dY_o W_o
+            dA_q, dB_q, dz_q = lora_grads(dY_q, ...)    and the same for v
+            dX_qkv = dY_q W_q + mask_q ks dz_q A_q + dY_k W_k + dY_v W_v + mask_v ks dz_v A_v
+
+The upstream gradients dY_* are fixed random tensors (the attention and norm backward that would
+produce them are not part of the linear stack).  The step's algorithmic work is
+``FLOP_PER_LAYER`` per layer (dequant counted as no FLOPs).
+"""
+
+import torch
+
+from . import k_nf4, quant
+from .w4linear import (down_swiglu_backward, gateup_swiglu_forward, linear_backward_dx,
+                       linear_forward, lora_down, lora_grads)
+
+D, I, KV, R = 1536, 8960, 256, 16
+SHAPES = {"q_proj": (D, D), "k_proj": (KV, D), "v_proj": (KV, D), "o_proj": (D, D),
+          "gate_proj": (I, D), "up_proj": (I, D), "down_proj": (D, I)}
+
+
+def layer_flops(m, d=D, inter=I, kv=KV, r=R):
+    """Algorithmic FLOPs of one layer's forward + backward at M = m tokens (2 M N K per GEMM)."""
+    fwd = 2 * m * d * (d + 2 * kv + d + 2 * inter) + 2 * m * inter * d
+    lora_fwd = 2 * m * d * r * 2 + 2 * m * r * (d + kv)           # two downs, two ups
+    bwd = fwd                                                        # dX of every projection
+    lora_bwd = 4 * 2 * m * d * r + 2 * (2 * m * r * (d + kv))      # dA, dX_lora (x2); dB, dz
+    return fwd + lora_fwd + bwd + lora_bwd
+
+
+FLOP_PER_LAYER_M2048 = layer_flops(2048)
+
+
+class NF4LinearStack:
+    """Random-init NF4 weights (W ~ N(0, 0.02), quantised on the GPU), rank-16 LoRA on q and v,
+    and synthetic activations, all resident on `device`."""
+
+    def __init__(self, n_layers=28, m=2048, seed=0, device="cuda", p_drop=0.05, lora_scale=2.0,
+                 save_gu=True):
+        self.n_layers, self.m, self.device = n_layers, m, torch.device(device)
+        self.s = float(lora_scale)
+        self.keep_scale = 1.0 / float(torch.tensor(1.0 - p_drop, dtype=torch.float32))
+        gen = torch.Generator(device=self.device)
+        gen.manual_seed(seed)
+        dev = self.device
+        self.code2 = quant.code2_on(dev)
+        self.nf4 = quant.nf4_table(dev)
+        self.layers, self.lora = [], []
+        for _ in range(n_layers):
+            linears = {}
+            for name in k_nf4.LAYER_WEIGHTS:
+                w = (torch.randn(SHAPES[name], generator=gen, device=dev) * 0.02).half()
+                linears[name] = quant.Linear4bit(quant.quantize_4bit(w, self.code2))
+                del w
+            packed, _ = k_nf4.repack_layer(linears, dev)
+            self.layers.append(dict(
+                packed=packed,
+                q=packed.weight("q_proj", self.code2, self.nf4),
+                k=packed.weight("k_proj", self.code2, self.nf4),
+                v=packed.weight("v_proj", self.code2, self.nf4),
+                o=packed.weight("o_proj", self.code2, self.nf4),
+                gu=packed.weights(("gate_proj", "up_proj"), self.code2, self.nf4),
+                d=packed.weight("down_proj", self.code2, self.nf4)))
+            bound = 1.0 / D ** 0.5
+            lo = {}
+            for t, out in (("q", D), ("v", KV)):
+                lo["A" + t] = ((torch.rand(R, D, generator=gen, device=dev) * 2 - 1) * bound).half()
+                lo["B" + t] = (torch.randn(out, R, generator=gen, device=dev) * 0.02).half()
+                lo["m" + t] = (torch.rand(m, D, generator=gen, device=dev) >= p_drop).to(torch.uint8)
+            self.lora.append(lo)
+        self.x = torch.randn(m, D, generator=gen, device=dev).half()
+        self.dy = {k: (torch.randn(m, n, generator=gen, device=dev) * 1e-2).half()
+                   for k, n in (("q", D), ("k", KV), ("v", KV), ("o", D), ("d", D))}
+        self.save_gu = save_gu
+        f16 = torch.float16
+        self.out = {k: torch.empty(m, n, dtype=f16, device=dev)
+                    for k, n in (("q", D), ("k", KV), ("v", KV), ("o", D), ("y", D))}
+        self.act = torch.empty(m, I, dtype=f16, device=dev)
+        self.gu = [torch.empty(m, 2 * I, dtype=f16, device=dev) for _ in range(n_layers)]
+        self.z = [{t: torch.empty(m, R, dtype=f16, device=dev) for t in ("q", "v")}
+                  for _ in range(n_layers)]
+        self.dx_qkv = torch.empty(m, D, dtype=torch.float32, device=dev)
+        self.dx_o = torch.empty(m, D, dtype=f16, device=dev)
+        self.dx_mlp = torch.empty(m, D, dtype=f16, device=dev)
+        self.grads = [None] * n_layers
+
+    @property
+    def flops_per_step(self):
+        return self.n_layers * layer_flops(self.m)
+
+    def forward_layer(self, i):
+        L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
+        lora_down(x, lo["Aq"], lo["mq"], self.keep_scale, out=z["q"])
+        lora_down(x, lo["Av"], lo["mv"], self.keep_scale, out=z["v"])
+        linear_forward(x, L["q"], None, z["q"], lo["Bq"], self.s, out=o["q"])
+        linear_forward(x, L["k"], out=o["k"])
+        linear_forward(x, L["v"], None, z["v"], lo["Bv"], self.s, out=o["v"])
+        linear_forward(x, L["o"], out=o["o"])
+        gateup_swiglu_forward(x, L["gu"], act=self.act, gu=self.gu[i])
+        linear_forward(self.act, L["d"], out=o["y"])
+
+    def backward_layer(self, i):
+        L, lo, z, x, dy = self.layers[i], self.lora[i], self.z[i], self.x, self.dy
+        gu = self.gu[i]
+        down_swiglu_backward(dy["d"], L["d"], gu)
+        linear_backward_dx(gu, L["gu"], out=self.dx_mlp)
+        linear_backward_dx(dy["o"], L["o"], out=self.dx_o)
+        daq, dbq, dzq = lora_grads(dy["q"], z["q"], x, lo["Bq"], self.s, lo["mq"], self.keep_scale)
+        dav, dbv, dzv = lora_grads(dy["v"], z["v"], x, lo["Bv"], self.s, lo["mv"], self.keep_scale)
+        linear_backward_dx(dy["q"], L["q"], dzq, lo["Aq"], lo["mq"], self.keep_scale, out=self.dx_qkv)
+        linear_backward_dx(dy["k"], L["k"], out=self.dx_qkv, accumulate=True)
+        linear_backward_dx(dy["v"], L["v"], dzv, lo["Av"], lo["mv"], self.keep_scale,
+                           out=self.dx_qkv, accumulate=True)
+        self.grads[i] = (daq, dbq, dav, dbv)
+
+    def step(self):
+        for i in range(self.n_layers):
+            self.forward_layer(i)
+        for i in reversed(range(self.n_layers)):
+            self.backward_layer(i)

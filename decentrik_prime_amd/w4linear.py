@@ -1,0 +1,297 @@
+"""Fused NF4 QLoRA linear operators (forward, dX backward, LoRA gradients, gate|up SwiGLU).
+
+These replace the reference's dequant-to-workspace + ``torch.mm``/``addmm`` call sites and the
+LoRA lines around them (solution/fast_qwen.py:943-947, 1037, 1080-1112, 1310-1383;
+solution/k_norm.py:49-53, 65-71; solution/k_rope.py:39-43, 54-58).  The NF4 weight is never
+materialised in fp16: each GEMM workgroup dequantises its W tile into LDS (``dk_w4_*`` in
+libdk.so).  Every op runs on ``torch.cuda.current_stream()`` and allocates only its outputs
+(and, for the LoRA gradients, a small fp32 partial-sum workspace) through torch.
+"""
+
+import torch
+
+from . import _lib
+from .quant import code2_on, nf4_table
+
+
+class W4:
+    """An NF4 weight [rows, cols] on the GPU: views of the four sections plus the two tables."""
+
+    def __init__(self, packed, qabs, scale2, offset2, code2, nf4, rows, cols):
+        self.packed, self.qabs, self.scale2, self.offset2 = packed, qabs, scale2, offset2
+        self.code2, self.nf4 = code2, nf4
+        self.rows, self.cols = int(rows), int(cols)
+        n = self.rows * self.cols
+        if n % 16384:
+            raise ValueError("an NF4 weight must fill whole second-level blocks (16384 weights)")
+        if (packed.numel() != n // 2 or qabs.numel() != n // 64 or scale2.numel() != n // 16384
+                or offset2.numel() != n // 16384):
+            raise ValueError("NF4 section sizes do not match the weight shape")
+        self._c = _lib.NF4WeightC(packed.data_ptr(), qabs.data_ptr(), scale2.data_ptr(),
+                                  offset2.data_ptr(), code2.data_ptr(), nf4.data_ptr(),
+                                  self.rows, self.cols)
+
+    @property
+    def shape(self):
+        return (self.rows, self.cols)
+
+    @property
+    def device(self):
+        return self.packed.device
+
+    def c_ref(self):
+        import ctypes
+        return ctypes.byref(self._c)
+
+    @classmethod
+    def from_sections(cls, packed, qabs, scale2, offset2, start, rows, cols, code2, nf4):
+        n = rows * cols
+        if start % 16384:
+            raise ValueError("weight does not start on a second-level block")
+        return cls(packed[start // 2:(start + n) // 2], qabs[start // 64:(start + n) // 64],
+                   scale2[start // 16384:(start + n) // 16384],
+                   offset2[start // 16384:(start + n) // 16384], code2, nf4, rows, cols)
+
+    @classmethod
+    def from_params(cls, param, nf4=None):
+        """From a Params4bit-like weight (``.data`` packed, ``.quant_state`` nested NF4)."""
+        qs = param.quant_state
+        rows, cols = int(qs.shape[0]), int(qs.shape[1])
+        dev = param.data.device
+        n = rows * cols
+        offset2 = qs.offset.float().reshape(1).expand(n // 16384).contiguous().to(dev)
+        return cls(param.data.reshape(-1), qs.absmax.reshape(-1), qs.state2.absmax.reshape(-1).float(),
+                   offset2, qs.state2.code.float().to(dev),
+                   nf4 if nf4 is not None else nf4_table(dev), rows, cols)
+
+    def dequantize(self, out=None):
+        """fp16 [rows, cols] (the reference's workspace view of this weight)."""
+        from .k_nf4 import dequant_tensors
+        if out is None:
+            out = torch.empty(self.rows, self.cols, dtype=torch.float16, device=self.device)
+        dequant_tensors(self.packed, self.qabs, self.scale2, self.offset2,
+                        self.rows * self.cols // 64, self.code2, self.nf4, out.view(-1))
+        return out
+
+
+def _check16(t, name, shape=None):
+    if t.dtype != torch.float16 or not t.is_cuda:
+        raise ValueError(f"{name} must be a CUDA fp16 tensor, got {t.dtype} on {t.device}")
+    if t.dim() != 2 or t.stride(1) != 1:
+        raise ValueError(f"{name} must be 2-D with unit column stride")
+    if shape is not None and tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
+def _mask_ok(mask, shape):
+    if mask is None:
+        return None
+    if mask.dtype == torch.bool:
+        mask = mask.view(torch.uint8)
+    if mask.dtype != torch.uint8 or tuple(mask.shape) != tuple(shape) or not mask.is_contiguous():
+        raise ValueError(f"mask must be a contiguous uint8/bool tensor of shape {tuple(shape)}")
+    return mask
+
+
+def lora_down(x, lora_A, mask=None, keep_scale=1.0, out=None):
+    """z = fp16(drop(x) A^T), drop(x) = fp16(mask ? x * keep_scale : 0).  x [M, K], A [r, K]."""
+    _check16(x, "x")
+    m, k = x.shape
+    _check16(lora_A, "lora_A")
+    r = lora_A.shape[0]
+    if lora_A.shape[1] != k or not x.is_contiguous() or not lora_A.is_contiguous():
+        raise ValueError("lora_down: x [M, K] and A [r, K] must be contiguous and agree on K")
+    mask = _mask_ok(mask, (m, k))
+    if out is None:
+        out = torch.empty(m, r, dtype=torch.float16, device=x.device)
+    rc = _lib.lib().dk_lora_down(_lib.ptr(x), _lib.ptr(mask), float(keep_scale), _lib.ptr(lora_A),
+                                 _lib.ptr(out), m, k, r, _lib.stream_handle(x.device))
+    _lib.check(rc, "dk_lora_down")
+    return out
+
+
+def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None):
+    """y = fp16(fp32(fp16(x W^T + bias)) + s * fp32(fp16(z B^T)))  (LoRA part optional).
+    x [M, in] fp16, w a W4 [out, in], z [M, r], lora_B [out, r]."""
+    _check16(x, "x")
+    m = x.shape[0]
+    if x.shape[1] != w.cols:
+        raise ValueError(f"x has {x.shape[1]} features, weight expects {w.cols}")
+    if bias is not None:
+        _check16(bias.view(1, -1), "bias", (1, w.rows))
+    if (z is None) != (lora_B is None):
+        raise ValueError("z and lora_B go together")
+    r = 0
+    if z is not None:
+        r = z.shape[1]
+        _check16(z, "z", (m, r))
+        _check16(lora_B, "lora_B", (w.rows, r))
+        if not z.is_contiguous() or not lora_B.is_contiguous():
+            raise ValueError("z and lora_B must be contiguous")
+    if out is None:
+        out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
+    _check16(out, "out", (m, w.rows))
+    rc = _lib.lib().dk_w4_linear_fwd(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
+                                     _lib.ptr(z), _lib.ptr(lora_B), r, float(lora_scale),
+                                     _lib.ptr(out), out.stride(0), _lib.stream_handle(x.device))
+    _lib.check(rc, "dk_w4_linear_fwd")
+    return out
+
+
+def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, out=None,
+                       out_dtype=torch.float32, accumulate=False):
+    """dX = fp32(fp16(dy W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0).
+    dy [M, out] fp16, w a W4 [out, in], dz [M, r], lora_A [r, in], mask [M, in].
+    out_dtype float16 rounds dX to fp16; accumulate=True adds into an fp32 `out`."""
+    _check16(dy, "dy")
+    m = dy.shape[0]
+    if dy.shape[1] != w.rows:
+        raise ValueError(f"dy has {dy.shape[1]} columns, weight has {w.rows} rows")
+    if (dz is None) != (lora_A is None):
+        raise ValueError("dz and lora_A go together")
+    r = 0
+    if dz is not None:
+        r = dz.shape[1]
+        _check16(dz, "dz", (m, r))
+        _check16(lora_A, "lora_A", (r, w.cols))
+        if not dz.is_contiguous() or not lora_A.is_contiguous():
+            raise ValueError("dz and lora_A must be contiguous")
+    mask = _mask_ok(mask, (m, w.cols))
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs an output tensor")
+        out = torch.empty(m, w.cols, dtype=out_dtype, device=dy.device)
+    if out.dtype == torch.float16:
+        mode = _lib.DK_OUT_F16
+        if accumulate:
+            raise ValueError("accumulation is into fp32 only")
+    elif out.dtype == torch.float32:
+        mode = _lib.DK_OUT_F32_ACCUM if accumulate else _lib.DK_OUT_F32
+    else:
+        raise ValueError("dX is fp16 or fp32")
+    if tuple(out.shape) != (m, w.cols) or out.stride(1) != 1:
+        raise ValueError("dX output has the wrong shape or layout")
+    rc = _lib.lib().dk_w4_linear_bwd_dx(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), _lib.ptr(dz),
+                                        _lib.ptr(lora_A), r, _lib.ptr(mask), float(keep_scale),
+                                        _lib.ptr(out), out.stride(0), mode,
+                                        _lib.stream_handle(dy.device))
+    _lib.check(rc, "dk_w4_linear_bwd_dx")
+    return out
+
+
+def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
+    """(dA fp32 [r, in], dB fp32 [out, r], dz fp16 [M, r]) with
+    dB = fp32(fp16(dy^T z)) s, dz = fp16(fp16(dy B) s), dA = fp32(fp16(dz^T drop(x)))."""
+    for t, nm in ((dy, "dy"), (z, "z"), (x, "x"), (lora_B, "lora_B")):
+        _check16(t, nm)
+        if not t.is_contiguous():
+            raise ValueError(f"{nm} must be contiguous")
+    m, n_out = dy.shape
+    r = z.shape[1]
+    k = x.shape[1]
+    if z.shape[0] != m or x.shape[0] != m or tuple(lora_B.shape) != (n_out, r):
+        raise ValueError("lora_grads: inconsistent shapes")
+    mask = _mask_ok(mask, (m, k))
+    L = _lib.lib()
+    dev = dy.device
+    da = torch.empty(r, k, dtype=torch.float32, device=dev)
+    db = torch.empty(n_out, r, dtype=torch.float32, device=dev)
+    dz = torch.empty(m, r, dtype=torch.float16, device=dev)
+    nbytes = int(L.dk_lora_grads_workspace(m, n_out, k, r))
+    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev)
+    rc = L.dk_lora_grads(_lib.ptr(dy), _lib.ptr(z), _lib.ptr(x), _lib.ptr(mask), float(keep_scale),
+                         _lib.ptr(lora_B), float(lora_scale), m, n_out, k, r, _lib.ptr(da),
+                         _lib.ptr(db), _lib.ptr(dz), _lib.ptr(ws), nbytes, _lib.stream_handle(dev))
+    _lib.check(rc, "dk_lora_grads")
+    return da, db, dz
+
+
+def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True):
+    """gate|up as one NF4 GEMM with the gated-SiLU epilogue.  w_gu is [2I, in] (gate rows then up
+    rows).  Returns (act [M, I], gu [M, 2I] or None)."""
+    _check16(x, "x")
+    m = x.shape[0]
+    inter = w_gu.rows // 2
+    if x.shape[1] != w_gu.cols or w_gu.rows % 2:
+        raise ValueError("gate|up weight does not match x")
+    dev = x.device
+    if act is None:
+        act = torch.empty(m, inter, dtype=torch.float16, device=dev)
+    _check16(act, "act", (m, inter))
+    if not act.is_contiguous():
+        raise ValueError("act must be contiguous")
+    if save_gu and gu is None:
+        gu = torch.empty(m, 2 * inter, dtype=torch.float16, device=dev)
+    if gu is not None:
+        _check16(gu, "gu", (m, 2 * inter))
+        if not gu.is_contiguous():
+            raise ValueError("gu must be contiguous")
+    rc = _lib.lib().dk_w4_gateup_swiglu_fwd(_lib.ptr(x), x.stride(0), m, w_gu.c_ref(), _lib.ptr(act),
+                                            _lib.ptr(gu), _lib.stream_handle(dev))
+    _lib.check(rc, "dk_w4_gateup_swiglu_fwd")
+    return act, gu
+
+
+def down_swiglu_backward(dh, w_down, gu):
+    """dact = fp16(dh W_down), then gu <- [dgate | dup] in place.  Returns gu."""
+    _check16(dh, "dh")
+    _check16(gu, "gu", (dh.shape[0], 2 * w_down.cols))
+    if dh.shape[1] != w_down.rows or not gu.is_contiguous():
+        raise ValueError("down backward: shapes do not match")
+    rc = _lib.lib().dk_w4_down_swiglu_bwd(_lib.ptr(dh), dh.stride(0), dh.shape[0], w_down.c_ref(),
+                                          _lib.ptr(gu), _lib.stream_handle(dh.device))
+    _lib.check(rc, "dk_w4_down_swiglu_bwd")
+    return gu
+
+
+class QLoRALinearFunction(torch.autograd.Function):
+    """y = x W^T (+ bias) + s * (drop(x) A^T) B^T with a frozen NF4 W; gradients for x, A, B.
+    The dropout keep-mask is an input (uint8 [M, in]), as in the reference's norm kernel."""
+
+    @staticmethod
+    def forward(ctx, x, lora_A, lora_B, w, bias, mask, keep_scale, lora_scale):
+        a16 = lora_A.detach().half().contiguous()
+        b16 = lora_B.detach().half().contiguous()
+        z = lora_down(x, a16, mask, keep_scale)
+        y = linear_forward(x, w, bias, z, b16, lora_scale)
+        ctx.save_for_backward(x, z, a16, b16, mask if mask is not None else torch.empty(0))
+        ctx.w, ctx.ks, ctx.s, ctx.has_mask = w, keep_scale, lora_scale, mask is not None
+        ctx.dtypes = (lora_A.dtype, lora_B.dtype)
+        return y
+
+    @staticmethod
+    def backward(ctx, dy):
+        x, z, a16, b16, mask = ctx.saved_tensors
+        mask = mask if ctx.has_mask else None
+        dy = dy.contiguous().half()
+        da, db, dz = lora_grads(dy, z, x, b16, ctx.s, mask, ctx.ks)
+        dx = linear_backward_dx(dy, ctx.w, dz, a16, mask, ctx.ks, out_dtype=torch.float32)
+        return (dx.to(x.dtype), da.to(ctx.dtypes[0]), db.to(ctx.dtypes[1]),
+                None, None, None, None, None)
+
+
+class QLoRALinear(torch.nn.Module):
+    """A frozen NF4 linear with a trainable rank-r LoRA (A kaiming-uniform, B given or zero)."""
+
+    def __init__(self, w, rank=16, alpha=32, dropout=0.05, bias=None):
+        super().__init__()
+        self.w = w
+        self.bias = bias
+        self.lora_A = torch.nn.Parameter(torch.empty(rank, w.cols, dtype=torch.float32, device=w.device))
+        self.lora_B = torch.nn.Parameter(torch.zeros(w.rows, rank, dtype=torch.float32, device=w.device))
+        torch.nn.init.kaiming_uniform_(self.lora_A, a=5 ** 0.5)
+        self.scale = alpha / rank
+        self.p = dropout
+        self.keep_scale = 1.0 / float(torch.tensor(1.0 - dropout, dtype=torch.float32))
+
+    def forward(self, x, mask=None):
+        if mask is None and self.training and self.p > 0:
+            mask = (torch.rand(x.shape, device=x.device) >= self.p).to(torch.uint8)
+        ks = self.keep_scale if mask is not None else 1.0
+        return QLoRALinearFunction.apply(x, self.lora_A, self.lora_B, self.w, self.bias, mask, ks,
+                                         self.scale)
+
+
+def default_tables(device):
+    """(code2, nf4) fp32 tables on `device`."""
+    return code2_on(device), nf4_table(device)

@@ -1,0 +1,150 @@
+/* C ABI of libdk.so: the gfx950 kernels of the NF4 QLoRA linear path.
+ *
+ * Conventions (the reference's operator conventions, solution/k_nf4.py:176-205,
+ * solution/k_mlp.py:50-63):
+ *   - every pointer is a device pointer into caller-allocated memory; nothing is allocated here;
+ *   - every launch is asynchronous on `stream` (a hipStream_t; 0 = the null stream);
+ *   - fp16 tensors are passed as void* (IEEE binary16), row-major and contiguous unless a leading
+ *     dimension is given;
+ *   - return 0 on success, a negative DK_ERR_* for an argument error detected before any launch,
+ *     or a positive hipError_t from the launch;
+ *   - no mutable global state: entry points may be called from any host thread.
+ */
+#ifndef DK_H
+#define DK_H
+
+#include <stdint.h>
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define DK_ERR_INVALID (-1)   /* a size or a null pointer that the operation cannot accept */
+#define DK_ERR_ALIGN (-2)     /* a pointer or an offset breaks the alignment the kernel needs */
+#define DK_ERR_WORKSPACE (-3) /* the workspace is missing or too small */
+
+/* An NF4 double-quantised weight [rows, cols] (out_features x in_features), element
+ * e = row * cols + col.  The four sections are those of the reference's repacked layer
+ * (solution/k_nf4.py:64-95): packed nibbles (even element in the high nibble), one uint8 code
+ * per 64 weights, one fp32 scale and one fp32 offset per 16384 weights.  code2 is the 256-entry
+ * second-level code table and nf4 the 16-entry NF4 table, both fp32. */
+typedef struct dk_nf4_weight {
+  const uint8_t* packed;  /* [rows * cols / 2]     */
+  const uint8_t* qabs;    /* [rows * cols / 64]    */
+  const float* scale2;    /* [rows * cols / 16384] */
+  const float* offset2;   /* [rows * cols / 16384] */
+  const float* code2;     /* [256] */
+  const float* nf4;       /* [16]  */
+  int64_t rows;
+  int64_t cols;
+} dk_nf4_weight;
+
+/* Human-readable text for a return code (static storage). */
+const char* dk_error_string(int code);
+
+/* ------------------------------------------------------------------------------------------
+ * NF4 dequant.  Replaces k_nf4.dequant_tensors / nf4_layer_dequant_kernel
+ * (solution/k_nf4.py:40-57, 176-181): out[e] = fp16(NF4[nib(e)] * absmax[e / 64]) for every
+ * element of n_qblocks * 64, bit-exact.  packed must be 4-byte aligned, out 16-byte aligned. */
+int dk_nf4_dequant(const uint8_t* packed, const uint8_t* qabs, const float* scale2,
+                   const float* offset2, const float* code2, const float* nf4, void* out_f16,
+                   int64_t n_qblocks, hipStream_t stream);
+
+/* NF4 quantisation with double quantisation (blocksize 64, second level 256) of an fp16 weight.
+ * Replaces the bitsandbytes quantisation the reference's weights come from (Params4bit with
+ * quant_type="nf4", compress_statistics=True, blocksize=64; solution/test_kernels.py:46-56,
+ * format checks solution/k_nf4.py:98-114).  numel % 16384 == 0.  absmax_ws: fp32
+ * [numel / 64] scratch; sum_ws: one uint64 of scratch.  offset2 receives the weight's mean
+ * offset, broadcast per second-level block (solution/k_nf4.py:168). */
+int dk_nf4_quantize(const void* w_f16, int64_t numel, const float* code2, const float* nf4,
+                    uint8_t* packed, uint8_t* qabs, float* scale2, float* offset2,
+                    float* absmax_ws, uint64_t* sum_ws, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * Gated SiLU on the fused [gate | up] rows.  Replace k_mlp.gated_silu_forward /
+ * gated_silu_backward (solution/k_mlp.py:20-63): gu is [n_rows, 2 * inter] fp16.
+ * forward:  act = fp16(silu(g) * u), act [n_rows, inter].
+ * backward: gu <- [dact * u * sig * (1 + g * (1 - sig)) | dact * silu(g)], in place. */
+int dk_gated_silu_fwd(const void* gu, void* act, int64_t n_rows, int64_t inter,
+                      hipStream_t stream);
+int dk_gated_silu_bwd(void* gu, const void* dact, int64_t n_rows, int64_t inter,
+                      hipStream_t stream);
+
+/* Example SwiGLU of the stock path (solution/swiglu.py:15-37), flat fp16 tensors of n elements:
+ * out = gate * sigmoid(gate) * up; dgate, dup from grad. */
+int dk_swiglu_fwd(const void* gate, const void* up, void* out, int64_t n, hipStream_t stream);
+int dk_swiglu_bwd(const void* grad, const void* gate, const void* up, void* dgate, void* dup,
+                  int64_t n, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
+ * LoRA down projection with the dropout of its input.  Replaces the norm kernel's dropout lines
+ * and the lora_A GEMM (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944):
+ *   Xd = fp16(mask ? fp32(x) * keep_scale : 0),   z = fp16(Xd A^T)
+ * x [m, k] fp16, mask [m, k] uint8 (nonzero = keep; NULL = no dropout), a [rank, k] fp16,
+ * z [m, rank] fp16.  rank % 16 == 0, rank <= 64, k % 8 == 0. */
+int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const void* a, void* z,
+                 int64_t m, int64_t k, int64_t rank, hipStream_t stream);
+
+/* Fused NF4 linear forward: y = X W^T (+ bias) (+ lora_scale * (z B^T)), dequant in LDS.
+ * Replaces torch.addmm on the dequantised workspace plus the LoRA-B GEMM and the epilogue's
+ * LoRA add (solution/fast_qwen.py:945-947; solution/k_rope.py:39-43, 54-58), rounding like them:
+ *   y = fp16(fp32(fp16(X W^T + bias)) + s * fp32(fp16(z B^T))).
+ * x [m, w.cols] fp16 (row stride ldx elements), y [m, w.rows] fp16 (row stride ldy),
+ * bias [w.rows] fp16 or NULL, z [m, rank] fp16 and lora_b [w.rows, rank] fp16, or both NULL.
+ * w.rows % 64 == 0, w.cols % 64 == 0. */
+int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
+                     const void* bias, const void* z, const void* lora_b, int64_t rank,
+                     float lora_scale, void* y, int64_t ldy, hipStream_t stream);
+
+/* Output modes of the backward dX GEMM. */
+#define DK_OUT_F16 0         /* dx is fp16, overwritten */
+#define DK_OUT_F32 1         /* dx is fp32, overwritten */
+#define DK_OUT_F32_ACCUM 2   /* dx is fp32, dx += result */
+
+/* Fused NF4 linear backward to the input: dX = dY W with the transposed dequant done in LDS,
+ * plus the LoRA input-gradient term through the dropout mask.  Replaces the dX GEMMs and the
+ * LoRA dX lines (solution/fast_qwen.py:1310, 1320-1327, 1350, 1364, 1376-1377;
+ * solution/k_norm.py:65-71):
+ *   dX = fp32(fp16(dY W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0)
+ * dy [m, w.rows] fp16 (row stride lddy), dx [m, w.cols] (row stride lddx) in out_mode,
+ * dz [m, rank] fp16, lora_a [rank, w.cols] fp16 and mask [m, w.cols] uint8, or all NULL. */
+int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m, const dk_nf4_weight* w,
+                        const void* dz, const void* lora_a, int64_t rank, const uint8_t* mask,
+                        float keep_scale, void* dx, int64_t lddx, int out_mode,
+                        hipStream_t stream);
+
+/* LoRA parameter gradients and the LoRA-down gradient.  Replaces
+ * solution/fast_qwen.py:1369-1374:
+ *   dB = fp32(fp16(dY^T z)) * s              [w_rows, rank] fp32
+ *   dz = fp16(fp16(dY B) * s)                [m, rank] fp16
+ *   dA = fp32(fp16(dz^T Xd)), Xd as in dk_lora_down   [rank, k] fp32
+ * dy [m, n_out] fp16, z [m, rank], x [m, k], mask [m, k] (NULL = no dropout), lora_b
+ * [n_out, rank].  ws: fp32 scratch of dk_lora_grads_workspace(m, n_out, k, rank) bytes. */
+int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank);
+int dk_lora_grads(const void* dy, const void* z, const void* x, const uint8_t* mask,
+                  float keep_scale, const void* lora_b, float lora_scale, int64_t m,
+                  int64_t n_out, int64_t k, int64_t rank, float* da, float* db, void* dz,
+                  void* ws, int64_t ws_bytes, hipStream_t stream);
+
+/* gate|up as one NF4 GEMM with the gated-SiLU epilogue.  Replaces the gate and up GEMMs and
+ * gated_silu_forward (solution/fast_qwen.py:1080-1108; solution/k_mlp.py:20-29):
+ *   g = fp16(X Wg^T), u = fp16(X Wu^T), act = fp16(silu(g) * u)
+ * w_gu is [2 * inter, k]: the gate rows then the up rows (the repacked layer's gate|up order,
+ * solution/k_nf4.py:7-9).  act [m, inter]; gu_out [m, 2 * inter] receives [g | u] when not NULL
+ * (the saved gate|up of the backward).  inter % 32 == 0, k % 64 == 0. */
+int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w_gu,
+                            void* act, void* gu_out, hipStream_t stream);
+
+/* Down-projection backward fused with the gated-SiLU backward.  Replaces dact = dh W_d and
+ * gated_silu_backward (solution/fast_qwen.py:1310-1312; solution/k_mlp.py:32-47):
+ *   dact = fp16(dh W_d);  gu <- [dact * u * sig * (1 + g * (1 - sig)) | dact * silu(g)]
+ * dh [m, w_down.rows] fp16, w_down [d_model, inter], gu [m, 2 * inter] in/out. */
+int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const dk_nf4_weight* w_down,
+                          void* gu, hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* DK_H */

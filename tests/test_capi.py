@@ -1,0 +1,105 @@
+"""CPU checks of the boundary: libdk.so loads, exports every entry point include/dk.h declares,
+rejects bad arguments before any launch, and the Python mirror keeps the reference's rules."""
+
+import ctypes
+import os
+
+import pytest
+import torch
+
+from decentrik_prime_amd import _lib, k_nf4, stack
+
+
+def test_library_exports_every_declared_symbol():
+    names = _lib.header_symbols()
+    assert len(names) >= 14
+    lib = _lib.lib()
+    for name in names:
+        assert hasattr(lib, name), name
+    assert set(names) == set(_lib.SIGNATURES), "ctypes signatures and header disagree"
+
+
+def test_built_for_gfx950():
+    blob = open(_lib.LIB_PATH, "rb").read()
+    assert b"gfx950" in blob
+
+
+def test_argument_errors_come_back_before_launch():
+    lib = _lib.lib()
+    # null pointers / negative sizes -> DK_ERR_INVALID, without touching a device
+    assert lib.dk_nf4_dequant(None, None, None, None, None, None, None, 4, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_nf4_dequant(None, None, None, None, None, None, None, -1, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_lora_down(None, None, 1.0, None, None, 8, 64, 16, None) == _lib.DK_ERR_INVALID
+    w = _lib.NF4WeightC(1, 1, 1, 1, 1, 1, 100, 100)     # 10000 weights: not whole 16384 blocks
+    assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 100, 8, ctypes.byref(w), None, None, None, 0,
+                                2.0, ctypes.c_void_p(16), 100, None) == _lib.DK_ERR_INVALID
+    # misaligned packed pointer (needs 4 bytes) and fp16 output (needs 16 bytes)
+    assert lib.dk_nf4_dequant(ctypes.c_void_p(2), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * 1536 * 16 * 4
+    assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
+    with pytest.raises(ValueError):
+        _lib.check(_lib.DK_ERR_INVALID, "probe")
+
+
+def test_zero_rows_is_a_no_op():
+    lib = _lib.lib()
+    assert lib.dk_gated_silu_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 64, None) == 0
+    assert lib.dk_nf4_dequant(ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), 0, None) == 0
+
+
+class _Layer:
+    def __init__(self, n_qblocks):
+        self.n_qblocks = n_qblocks
+        self.packed = torch.zeros(n_qblocks * 32, dtype=torch.uint8)
+        self.qabs = torch.zeros(n_qblocks, dtype=torch.uint8)
+        self.scale2 = torch.zeros(-(-n_qblocks // 256))
+        self.offset2 = torch.zeros(-(-n_qblocks // 256))
+
+
+def test_dequant_range_alignment_rules():
+    layer = _Layer(3000)
+    out = torch.empty(3000 * 64, dtype=torch.float16)
+    code2 = torch.zeros(256)
+    nf4 = torch.zeros(16)
+    for q0, q1, dst in ((256, 3000, None), (0, 1500, None), (0, 1024, 64)):
+        with pytest.raises(ValueError):
+            k_nf4.dequant_range(layer, q0, q1, code2, nf4, out, dst)
+    # aligned, but CPU tensors: rejected by the operator's device check, still a ValueError
+    with pytest.raises(ValueError):
+        k_nf4.dequant_range(layer, 1024, 3000, code2, nf4, out)
+
+
+def test_section_layout_matches_reference_sizes():
+    # one Qwen2.5-1.5B layer: 46,792,704 weights = 731,136 first-level blocks, 24,150,400 bytes
+    n_q = sum(r * c for r, c in stack.SHAPES.values()) // 64
+    assert n_q == 731136
+    offs, nbytes = k_nf4.section_layout(n_q)
+    assert nbytes == 24150400
+    assert offs == (0, 23396352, 24127488, 24138944)
+    assert all(o % 64 == 0 for o in offs)
+
+
+def test_layer_flops():
+    # per-GEMM list: forward q, k, v, o, gate|up, down; LoRA downs/ups; dX of each projection;
+    # LoRA backward dA, dz, dB, dX-term for q and v
+    M, D, I, KV, r = 2048, 1536, 8960, 256, 16
+    g = lambda m, n, k: 2 * m * n * k  # noqa: E731
+    fwd = g(M, D, D) + 2 * g(M, KV, D) + g(M, D, D) + g(M, 2 * I, D) + g(M, D, I)
+    lora_f = 2 * g(M, r, D) + g(M, D, r) + g(M, KV, r)
+    lora_b = (g(r, D, M) + g(M, r, D) + g(D, r, M) + g(M, D, r)
+              + g(r, D, M) + g(M, r, KV) + g(KV, r, M) + g(M, D, r))
+    assert stack.FLOP_PER_LAYER_M2048 == 2 * fwd + lora_f + lora_b == 384282132480
+    assert abs(28 * stack.FLOP_PER_LAYER_M2048 / 1e12 - 10.760) < 1e-3
+
+
+def test_package_has_no_oracle_dependency():
+    pkg = os.path.dirname(_lib.__file__)
+    for root, _, files in os.walk(pkg):
+        for f in files:
+            if f.endswith(".py"):
+                text = open(os.path.join(root, f)).read()
+                assert "import oracle" not in text and "from oracle" not in text, f

@@ -1,0 +1,202 @@
+"""GPU parity of the fused NF4 GEMMs, LoRA kernels and gated SiLU against the CPU oracle, at the
+BASELINE configurations' full sizes (M = 2048, Qwen2.5-1.5B shapes) and at small / ragged sizes.
+Tolerance (from the north star): rtol 1e-2, atol 2e-2 on GEMM outputs and LoRA gradients,
+relative to the output scale where the outputs are small (LoRA gradients, dY ~ N(0, 1e-2))."""
+
+import os
+
+import numpy as np
+import pytest
+
+from tests.helpers import assert_close, cuda, cuda16, host, log, lora_inputs, nf4_weight, to_w4
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+RTOL, ATOL = 1e-2, 2e-2
+F16 = np.float16
+
+
+def _h(a):
+    return np.asarray(a).view(F16)
+
+
+def _scaled_close(got, want, what):
+    """rtol 1e-2 / atol 2e-2 relative to the tensor's own scale (for small-valued gradients)."""
+    s = float(np.abs(want).max()) or 1.0
+    assert_close(np.asarray(got, np.float64) / s, np.asarray(want, np.float64) / s, RTOL, ATOL, what)
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    return t
+
+
+def test_gated_silu_kernels(torch):
+    from decentrik_prime_amd import k_mlp
+    from oracle import mlp
+    log("gated silu n=333 inter=8960 (vector path) and golden inter=1100 (scalar path)")
+    rng = np.random.default_rng(4)
+    gu = (rng.standard_normal((333, 2 * 8960)) * 2).astype(F16)
+    act = torch.empty(333, 8960, dtype=torch.float16, device="cuda")
+    k_mlp.gated_silu_forward(cuda16(gu), act)
+    assert_close(host(act), mlp.gated_silu_fwd(gu), 2e-3, 2e-3, "act")
+    da = rng.standard_normal((333, 8960)).astype(F16)
+    buf = cuda16(gu)
+    k_mlp.gated_silu_backward(buf, cuda16(da))
+    assert_close(host(buf), mlp.gated_silu_bwd(gu, da), 3e-3, 3e-3, "dgu")
+    g = np.load(os.path.join(GOLD, "mlp_small.npz"))
+    act = torch.empty(3, 1100, dtype=torch.float16, device="cuda")
+    k_mlp.gated_silu_forward(cuda(g["gu"]).view(torch.float16), act)
+    assert_close(host(act), _h(g["act"]), 2e-3, 2e-3, "act golden")
+    buf = cuda(g["gu"]).view(torch.float16).clone()
+    k_mlp.gated_silu_backward(buf, cuda(g["dact"]).view(torch.float16))
+    assert_close(host(buf), _h(g["dgu"]), 3e-3, 3e-3, "dgu golden")
+
+
+def test_example_swiglu(torch):
+    from decentrik_prime_amd import swiglu
+    from oracle import mlp
+    log("example SwiGLU autograd")
+    rng = np.random.default_rng(5)
+    gate = (rng.standard_normal((77, 300)) * 2).astype(F16)
+    up = rng.standard_normal((77, 300)).astype(F16)
+    g_t = cuda16(gate).requires_grad_(True)
+    u_t = cuda16(up).requires_grad_(True)
+    out = swiglu.swiglu(g_t, u_t)
+    assert_close(host(out), mlp.swiglu_fwd(gate, up), 2e-3, 2e-3, "out")
+    grad = rng.standard_normal((77, 300)).astype(F16)
+    out.backward(cuda16(grad))
+    dg, du = mlp.swiglu_bwd(grad, gate, up)
+    assert_close(host(g_t.grad), dg, 3e-3, 3e-3, "dgate")
+    assert_close(host(u_t.grad), du, 3e-3, 3e-3, "dup")
+
+
+def test_linear_golden_small(torch):
+    from decentrik_prime_amd import w4linear
+    log("linear golden M=64 [128,128] r=16")
+    g = dict(np.load(os.path.join(GOLD, "linear_small.npz")))
+    q = dict(packed=g["packed"], qabs=g["qabs"], scale2=g["scale2"], offset2=g["offset2"],
+             code2=g["code2"], rows=128, cols=128)
+    w = to_w4(q)
+    ks = float(np.float32(1) / np.float32(0.95))
+    x = cuda(g["x"]).view(torch.float16)
+    mask = cuda(g["mask"])
+    z = w4linear.lora_down(x, cuda(g["a"]).view(torch.float16), mask, ks)
+    assert_close(host(z), _h(g["z"]), RTOL, ATOL, "z")
+    y = w4linear.linear_forward(x, w, None, z, cuda(g["b"]).view(torch.float16), 2.0)
+    assert_close(host(y), _h(g["y"]), RTOL, ATOL, "y")
+    dy = cuda(g["dy"]).view(torch.float16)
+    da, db, dz = w4linear.lora_grads(dy, z, x, cuda(g["b"]).view(torch.float16), 2.0, mask, ks)
+    _scaled_close(host(dz), _h(g["dZ"]), "dz")
+    _scaled_close(host(da), g["dA"], "dA")
+    _scaled_close(host(db), g["dB"], "dB")
+    dx = w4linear.linear_backward_dx(dy, w, dz, cuda(g["a"]).view(torch.float16), mask, ks)
+    _scaled_close(host(dx), g["dx"], "dx")
+
+
+@pytest.mark.parametrize("m", [2048, 333])
+def test_qproj_forward_config1(torch, m):
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"config 1: q_proj forward + LoRA, M={m}")
+    q = nf4_weight(1536, 1536, seed=100)
+    x, a, b, mask, _ = lora_inputs(m, 1536, 1536, seed=1)
+    ks = linear.keep_scale(0.05)
+    y_ref, z_ref = linear.linear_fwd(x, q["deq"], None, mask, ks, a, b, 2.0)
+    w = to_w4(q)
+    z = w4linear.lora_down(cuda16(x), cuda16(a), cuda(mask), ks)
+    y = w4linear.linear_forward(cuda16(x), w, None, z, cuda16(b), 2.0)
+    torch.cuda.synchronize()
+    assert_close(host(z), z_ref, RTOL, ATOL, "z")
+    assert_close(host(y), y_ref, RTOL, ATOL, "y")
+
+
+def test_kproj_forward_with_bias(torch):
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log("k_proj forward with bias, no LoRA, M=2048")
+    q = nf4_weight(256, 1536, seed=101)
+    rng = np.random.default_rng(9)
+    x = rng.standard_normal((2048, 1536)).astype(F16)
+    bias = (rng.standard_normal(256) * 0.1).astype(F16)
+    y_ref, _ = linear.linear_fwd(x, q["deq"], bias)
+    y = w4linear.linear_forward(cuda16(x), to_w4(q), cuda16(bias))
+    assert_close(host(y), y_ref, RTOL, ATOL, "y")
+
+
+@pytest.mark.parametrize("name,rows,m", [("q_proj", 1536, 2048), ("v_proj", 256, 2048),
+                                         ("q_proj", 1536, 200)])
+def test_backward_config3(torch, name, rows, m):
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"config 3: {name} backward M={m}")
+    q = nf4_weight(rows, 1536, seed=102 if name == "q_proj" else 103)
+    x, a, b, mask, dy = lora_inputs(m, 1536, rows, seed=2)
+    ks = linear.keep_scale(0.05)
+    _, z = linear.linear_fwd(x, q["deq"], None, mask, ks, a, b, 2.0)
+    ref = linear.linear_bwd(dy, q["deq"], z, x, mask, ks, a, b, 2.0)
+    w = to_w4(q)
+    da, db, dz = w4linear.lora_grads(cuda16(dy), cuda16(z), cuda16(x), cuda16(b), 2.0, cuda(mask), ks)
+    dx = w4linear.linear_backward_dx(cuda16(dy), w, dz, cuda16(a), cuda(mask), ks)
+    torch.cuda.synchronize()
+    _scaled_close(host(dz), ref["dZ"], "dz")
+    _scaled_close(host(da), ref["dA"], "dA")
+    _scaled_close(host(db), ref["dB"], "dB")
+    _scaled_close(host(dx), ref["dx"], "dx")
+    # accumulate and fp16 output modes
+    acc = torch.ones(m, 1536, dtype=torch.float32, device="cuda")
+    w4linear.linear_backward_dx(cuda16(dy), w, out=acc, accumulate=True)
+    _scaled_close(host(acc) - 1.0, ref["dx_base"].astype(np.float32), "dx accumulate")
+    d16 = w4linear.linear_backward_dx(cuda16(dy), w, out_dtype=torch.float16)
+    _scaled_close(host(d16), ref["dx_base"], "dx fp16")
+
+
+def test_mlp_config2(torch):
+    from decentrik_prime_amd import w4linear
+    from oracle import linear, mlp
+    log("config 2: gate|up SwiGLU forward + down, M=2048")
+    I = 8960
+    qg = nf4_weight(2 * I, 1536, seed=104)          # gate rows then up rows
+    qd = nf4_weight(1536, I, seed=105)
+    x = np.random.default_rng(3).standard_normal((2048, 1536)).astype(F16)
+    gu_ref, h_ref, _ = mlp.mlp_fwd(x, qg["deq"], qd["deq"])
+    act, gu = w4linear.gateup_swiglu_forward(cuda16(x), to_w4(qg))
+    torch.cuda.synchronize()
+    assert_close(host(gu), gu_ref, RTOL, ATOL, "gu")
+    assert_close(host(act), h_ref, RTOL, ATOL, "act")
+    # down projection on the GPU's own act (isolates the down GEMM)
+    y = w4linear.linear_forward(act, to_w4(qd))
+    y_ref = linear.mm16(host(act), qd["deq"].T)
+    assert_close(host(y), y_ref, RTOL, ATOL, "down")
+    # backward: down^T fused with the SwiGLU backward, then gate|up^T
+    dh = (np.random.default_rng(4).standard_normal((2048, 1536)) * 1e-2).astype(F16)
+    gu_np = host(gu)
+    dgu_ref, dx_ref = mlp.mlp_bwd(dh, gu_np, qg["deq"], qd["deq"])
+    w4linear.down_swiglu_backward(cuda16(dh), to_w4(qd), gu)
+    torch.cuda.synchronize()
+    _scaled_close(host(gu), dgu_ref, "dgu")
+    dx = w4linear.linear_backward_dx(gu, to_w4(qg), out_dtype=torch.float16)
+    _scaled_close(host(dx), linear.mm16(host(gu), qg["deq"]), "dX mlp")
+    _scaled_close(host(dx), dx_ref, "dX mlp vs oracle chain")
+
+
+def test_autograd_function(torch):
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log("QLoRALinearFunction autograd, M=256")
+    q = nf4_weight(1536, 1536, seed=106)
+    x, a, b, mask, dy = lora_inputs(256, 1536, 1536, seed=6)
+    ks = linear.keep_scale(0.05)
+    w = to_w4(q)
+    xt = cuda16(x).requires_grad_(True)
+    at = cuda(a.astype(np.float32)).requires_grad_(True)
+    bt = cuda(b.astype(np.float32)).requires_grad_(True)
+    y = w4linear.QLoRALinearFunction.apply(xt, at, bt, w, None, cuda(mask), ks, 2.0)
+    y.backward(cuda16(dy))
+    y_ref, z = linear.linear_fwd(x, q["deq"], None, mask, ks, a, b, 2.0)
+    ref = linear.linear_bwd(dy, q["deq"], z, x, mask, ks, a, b, 2.0)
+    assert_close(host(y), y_ref, RTOL, ATOL, "y")
+    _scaled_close(host(at.grad), ref["dA"], "dA")
+    _scaled_close(host(bt.grad), ref["dB"], "dB")
+    _scaled_close(host(xt.grad).astype(np.float32), ref["dx"], "dx")

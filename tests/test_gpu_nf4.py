@@ -1,0 +1,160 @@
+"""GPU parity of the NF4 kernels against the CPU oracle: dequant bit-exact (golden fixtures,
+config 0, prefix / range / untouched-rest cases of dev/test_emu.py:57-70 and
+solution/test_kernels.py:69-84), the repacked layer, and the GPU quantiser bit-exact against the
+oracle quantiser."""
+
+import os
+
+import numpy as np
+import pytest
+
+from tests.helpers import cuda, host, log, nf4_weight
+
+pytestmark = pytest.mark.gpu
+GOLD = os.path.join(os.path.dirname(__file__), "golden")
+
+
+@pytest.fixture(scope="module")
+def torch_dev():
+    import torch
+    return torch
+
+
+def _dequant(torch, g, nq=None):
+    from decentrik_prime_amd import k_nf4, quant
+    nq = g["qabs"].size if nq is None else nq
+    out = torch.full((nq * 64,), float("nan"), dtype=torch.float16, device="cuda")
+    k_nf4.dequant_tensors(cuda(g["packed"][:nq * 32]), cuda(g["qabs"][:nq]),
+                          cuda(g["scale2"][:-(-nq // 256)]), cuda(g["offset2"][:-(-nq // 256)]),
+                          nq, cuda(g["code2"]), quant.nf4_table("cuda"), out)
+    torch.cuda.synchronize()
+    return host(out).view(np.uint16)
+
+
+def test_dequant_golden_blocks(torch_dev):
+    log("dequant golden nf4_blocks")
+    g = dict(np.load(os.path.join(GOLD, "nf4_blocks.npz")))
+    assert np.array_equal(_dequant(torch_dev, g), g["out"])
+    # prefix: two second-level blocks (partial last workgroup)
+    assert np.array_equal(_dequant(torch_dev, g, 512), g["out"][:512 * 64])
+
+
+def test_dequant_golden_vproj(torch_dev):
+    log("dequant golden nf4_vproj")
+    g = dict(np.load(os.path.join(GOLD, "nf4_vproj.npz")))
+    assert np.array_equal(_dequant(torch_dev, g), g["out"])
+
+
+def test_dequant_config0_bit_exact(torch_dev):
+    log("dequant config 0: q_proj [1536, 1536]")
+    q = nf4_weight(1536, 1536, seed=100)
+    got = _dequant(torch_dev, q)
+    assert np.array_equal(got, q["deq"].reshape(-1).view(np.uint16))
+
+
+def test_dequant_range_leaves_the_rest(torch_dev):
+    torch = torch_dev
+    from decentrik_prime_amd import k_nf4, quant
+    log("dequant_range into a zeroed buffer")
+
+    class L:
+        pass
+    q = nf4_weight(1024, 256, seed=5)       # 4096 first-level blocks
+    lay = L()
+    lay.n_qblocks = q["qabs"].size
+    lay.packed, lay.qabs = cuda(q["packed"]), cuda(q["qabs"])
+    lay.scale2, lay.offset2 = cuda(q["scale2"]), cuda(q["offset2"])
+    code2, nf4 = cuda(q["code2"]), quant.nf4_table("cuda")
+    out = torch.zeros(lay.n_qblocks * 64, dtype=torch.float16, device="cuda")
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        k_nf4.dequant_range(lay, 1024, lay.n_qblocks, code2, nf4, out)
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    assert not host(out)[:1024 * 64].any()
+    k_nf4.dequant_range(lay, 0, 1024, code2, nf4, out)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out).view(np.uint16), q["deq"].reshape(-1).view(np.uint16))
+    # into a destination offset of a shared region
+    out2 = torch.zeros(2048 * 64, dtype=torch.float16, device="cuda")
+    k_nf4.dequant_range(lay, 2048, 3072, code2, nf4, out2, dst=1024 * 64)
+    torch.cuda.synchronize()
+    assert np.array_equal(host(out2)[1024 * 64:].view(np.uint16),
+                          q["deq"].reshape(-1)[2048 * 64:3072 * 64].view(np.uint16))
+    with pytest.raises(ValueError):
+        k_nf4.dequant_range(lay, 256, lay.n_qblocks, code2, nf4, out)
+
+
+def test_quantiser_matches_oracle(torch_dev):
+    torch = torch_dev
+    from decentrik_prime_amd import quant
+    from oracle import nf4
+    log("GPU quantiser vs oracle quantiser")
+    assert np.array_equal(host(quant.dynamic_map_signed()), nf4.dynamic_map_signed())
+    for rows, cols, seed in ((256, 1536, 1), (1536, 1536, 100), (64, 256, 7)):
+        w = (np.random.default_rng(seed).standard_normal((rows, cols)) * 0.02).astype(np.float16)
+        want = nf4.quantize(w)
+        p = quant.quantize_4bit(cuda(w))
+        torch.cuda.synchronize()
+        qs = p.quant_state
+        assert np.array_equal(host(p.data).reshape(-1), want["packed"]), (rows, cols)
+        assert np.array_equal(host(qs.absmax), want["qabs"]), (rows, cols)
+        assert np.array_equal(host(qs.state2.absmax), want["scale2"]), (rows, cols)
+        assert host(qs.offset)[0] == want["offset"], (rows, cols)
+
+
+def test_quantiser_edge_blocks(torch_dev):
+    torch = torch_dev
+    from decentrik_prime_amd import quant
+    from oracle import nf4
+    log("GPU quantiser: zero blocks, ties, subnormals")
+    rng = np.random.default_rng(11)
+    w = (rng.standard_normal(16384 * 2) * 0.02).astype(np.float16)
+    w[:64] = 0                                  # an all-zero first-level block
+    w[64:128] = np.float16(6e-8)                # fp16 subnormals
+    t = nf4.nf4_table()
+    w[128:192] = (t[np.arange(64) % 16] * np.float32(0.03125)).astype(np.float16)  # exact codes
+    w[192:256] = np.float16(-1.0)
+    want = nf4.quantize(w)
+    p = quant.quantize_4bit(cuda(w.reshape(2, 16384)))
+    torch.cuda.synchronize()
+    assert np.array_equal(host(p.data).reshape(-1), want["packed"])
+    assert np.array_equal(host(p.quant_state.absmax), want["qabs"])
+
+
+def test_repacked_layer_dequant_and_split(torch_dev):
+    torch = torch_dev
+    from decentrik_prime_amd import k_nf4, quant
+    from oracle import nf4
+    log("repack_layer + dequant_layer + split ranges")
+    shapes = {"q_proj": (256, 128), "k_proj": (128, 128), "v_proj": (128, 128),
+              "o_proj": (256, 128), "gate_proj": (384, 128), "up_proj": (384, 128),
+              "down_proj": (128, 384)}
+    linears, refs = {}, {}
+    for i, name in enumerate(k_nf4.LAYER_WEIGHTS):
+        w = (np.random.default_rng(i).standard_normal(shapes[name]) * 0.05).astype(np.float16)
+        q = nf4.quantize(w)
+        refs[name] = nf4.dequant(q["packed"], q["qabs"], q["scale2"], q["offset2"], q["code2"])
+        linears[name] = quant.Linear4bit(quant.quantize_4bit(cuda(w)))
+    packed, code2 = k_nf4.repack_layer(linears, torch.device("cuda"))
+    nf4t = quant.nf4_table("cuda")
+    out = torch.empty(packed.numel, dtype=torch.float16, device="cuda")
+    k_nf4.dequant_layer(packed, code2, nf4t, out)
+    torch.cuda.synchronize()
+    got = host(out)
+    for name in k_nf4.LAYER_WEIGHTS:
+        start, rows, cols = packed.segments[name]
+        assert np.array_equal(got[start:start + rows * cols].view(np.uint16),
+                              refs[name].view(np.uint16)), name
+        # the re-pointed weight still describes the same bytes
+        wt = linears[name].weight
+        assert wt.data.data_ptr() == packed.packed.data_ptr() + start // 2
+    split = k_nf4.RANGE_ALIGN
+    out3 = torch.zeros_like(out)
+    k_nf4.dequant_range(packed, split, packed.n_qblocks, code2, nf4t, out3)
+    torch.cuda.synchronize()
+    assert not host(out3)[:split * 64].any()
+    k_nf4.dequant_range(packed, 0, split, code2, nf4t, out3)
+    torch.cuda.synchronize()
+    assert torch.equal(out3, out)
