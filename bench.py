@@ -114,6 +114,17 @@ def dequant_bandwidth(torch, st, reps):
             "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+def copy_calibration(torch, reps, nbytes=512 << 20):
+    """A plain device copy of known size (read nbytes + write nbytes per launch): the reference
+    against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled."""
+    a = torch.empty(nbytes, dtype=torch.uint8, device="cuda").fill_(1)
+    b = torch.empty_like(a)
+    ms = time_op(torch, lambda: b.copy_(a), reps)
+    del a, b
+    return {"kernel": "copy (torch)", "bytes_read": nbytes, "bytes_written": nbytes,
+            "avg_us": round(ms * 1e3, 2), "gbps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1)}
+
+
 def cpu_baseline(layers=1, m=2048):
     """The CPU oracle on `layers` layer(s) of the same workload: numpy NF4 dequant of the seven
     weights + fp32 torch GEMMs of the forward and backward with the LoRA terms."""
@@ -178,8 +189,13 @@ def main():
     ap.add_argument("--layers", type=int, default=28)
     ap.add_argument("--m", type=int, default=2048)
     ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-layers", type=int, default=6,
+                    help="layers of the CPU-oracle sample (about 10-30 s of CPU work)")
     ap.add_argument("--no-kernels", action="store_true")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--kernels-only", action="store_true",
+                    help="skip the step timing: per-kernel table, dequant and a copy of known size "
+                         "(the calibration of rocprofv3 FETCH_SIZE / WRITE_SIZE)")
     args = ap.parse_args()
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the NF4 linear path has no multi-GPU leg in this build "
@@ -193,6 +209,11 @@ def main():
     print(f"[bench] building {args.layers}-layer NF4 stack, M={args.m}", file=sys.stderr, flush=True)
     st = NF4LinearStack(args.layers, args.m, seed=0, device="cuda")
     torch.cuda.synchronize()
+    if args.kernels_only:
+        print(json.dumps({"kernels": kernel_table(torch, st, args.reps),
+                          "dequant": dequant_bandwidth(torch, st, args.reps),
+                          "copy": copy_calibration(torch, args.reps)}), flush=True)
+        return
     for _ in range(args.warmup):
         st.step()
     torch.cuda.synchronize()
@@ -236,8 +257,8 @@ def main():
                                                 "frac": dq["frac_hbm_peak"]}}
         result["kernels"] = kernels
     if not args.no_cpu:
-        print("[bench] CPU baseline (oracle, 1 layer)", file=sys.stderr, flush=True)
-        result["cpu_baseline"] = cpu_baseline(1, args.m)
+        print(f"[bench] CPU baseline (oracle, {args.cpu_layers} layers)", file=sys.stderr, flush=True)
+        result["cpu_baseline"] = cpu_baseline(args.cpu_layers, args.m)
     print(json.dumps(result), flush=True)
 
 

@@ -41,9 +41,10 @@ SIGNATURES = {
     "dk_swiglu_bwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_lora_down": (_int, [_c_p, _c_p, _f32, _c_p, _c_p, _i64, _i64, _i64, _c_p]),
     "dk_w4_linear_fwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _c_p, _i64, _f32, _c_p, _i64,
-                                _c_p]),
+                                _c_p, _i64, _c_p]),
     "dk_w4_linear_bwd_dx": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _i64, _c_p, _f32, _c_p,
-                                   _i64, _int, _c_p]),
+                                   _i64, _int, _c_p, _i64, _c_p]),
+    "dk_w4_linear_workspace": (_i64, [_i64, _W, _int]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "dk_lora_grads": (_int, [_c_p, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64, _i64,
                              _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),

@@ -10,6 +10,7 @@ typedef _Float16 f16;
 typedef _Float16 f16x2 __attribute__((ext_vector_type(2)));
 typedef _Float16 f16x4 __attribute__((ext_vector_type(4)));
 typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
 typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
@@ -32,6 +33,15 @@ static inline bool dk_aligned(const void* p, uintptr_t a) {
 
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default round mode).
 __device__ __forceinline__ f16 dk_h(float x) { return (f16)x; }
+
+// Logistic parts of the gated SiLU for the GEMM epilogues: e = 1 + exp(-g), sig = 1/e and
+// silu = g/e through one hardware reciprocal (v_rcp_f32, about 1 ulp) instead of two IEEE
+// divisions; far below the fp16 rounding of the results.
+__device__ __forceinline__ void dk_silu_parts(float g, float* sig, float* silu) {
+  const float r = __builtin_amdgcn_rcpf(1.0f + __expf(-g));
+  *sig = r;
+  *silu = g * r;
+}
 
 // Pack two fp16 into one dword, lower address in the low half.
 __device__ __forceinline__ uint32_t dk_pack2(f16 lo, f16 hi) {

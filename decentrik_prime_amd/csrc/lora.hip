@@ -17,7 +17,7 @@ namespace {
 
 constexpr int kThreads = 256;
 constexpr int kRowsPerBlock = kThreads / 64;
-constexpr int kChunkRows = 128;
+constexpr int kChunkRows = 256;
 
 __device__ __forceinline__ float wave_sum(float v) {
   for (int off = 32; off > 0; off >>= 1) v += __shfl_xor(v, off);
@@ -86,8 +86,9 @@ __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restri
   }
 }
 
-// Partial column sums over one 128-row chunk: part[chunk][n][r] = sum_m P[m][n] Q[m][r], two
-// columns per thread.  DROP: P is the dropout of x (mask may be null).
+// Partial column sums over one 256-row chunk: part[chunk][n][r] = sum_m P[m][n] Q[m][r].  A block
+// owns 64 columns (one per lane); its 4 waves take every 4th row of the chunk and are summed in a
+// fixed order through LDS.  DROP: P is the dropout of x (mask may be null).
 template <int R, bool DROP>
 __global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restrict__ P,
                                                              const uint8_t* __restrict__ mask,
@@ -95,39 +96,55 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restri
                                                              float* __restrict__ part,
                                                              int64_t rows, int64_t cols) {
   __shared__ float qs[kChunkRows][R];
+  __shared__ float red[kRowsPerBlock - 1][64][R + 1];
   const int64_t chunk = blockIdx.y;
   const int64_t r0 = chunk * kChunkRows;
-  const int64_t nrows = rows - r0 < kChunkRows ? rows - r0 : kChunkRows;
+  const int nrows = (int)(rows - r0 < kChunkRows ? rows - r0 : kChunkRows);
   for (int i = threadIdx.x; i < kChunkRows * R; i += kThreads) {
     const int rr = i / R, r = i % R;
     qs[rr][r] = rr < nrows ? (float)Q[(r0 + rr) * R + r] : 0.0f;
   }
   __syncthreads();
-  const int64_t n = ((int64_t)blockIdx.x * kThreads + threadIdx.x) * 2;
-  if (n >= cols) return;
-  float a0[R], a1[R];
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const int64_t n = (int64_t)blockIdx.x * 64 + lane;
+  float acc[R];
 #pragma unroll
-  for (int r = 0; r < R; ++r) a0[r] = a1[r] = 0.0f;
-  for (int rr = 0; rr < nrows; ++rr) {
-    const int64_t m = r0 + rr;
-    const f16x2 pv = *reinterpret_cast<const f16x2*>(P + m * cols + n);
-    float p0 = (float)pv[0], p1 = (float)pv[1];
-    if (DROP && mask) {
-      const uint8_t* mk = mask + m * cols + n;
-      p0 = mk[0] ? (float)dk_h(__fmul_rn(p0, ks)) : 0.0f;
-      p1 = mk[1] ? (float)dk_h(__fmul_rn(p1, ks)) : 0.0f;
-    }
+  for (int r = 0; r < R; ++r) acc[r] = 0.0f;
+  if (n < cols) {
+    // U rows per batch: their loads are all in flight before the first one is used
+    constexpr int U = 8;
+    for (int rr0 = w; rr0 < nrows; rr0 += kRowsPerBlock * U) {
+      float pv[U];
+      int rc[U];
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      a0[r] += p0 * qs[rr][r];
-      a1[r] += p1 * qs[rr][r];
+      for (int u = 0; u < U; ++u) {
+        const int rr = rr0 + u * kRowsPerBlock;
+        rc[u] = rr < nrows ? rr : nrows - 1;
+        const int64_t m = r0 + rc[u];
+        float v = (float)P[m * cols + n];
+        if (DROP && mask) v = mask[m * cols + n] ? (float)dk_h(__fmul_rn(v, ks)) : 0.0f;
+        pv[u] = rr < nrows ? v : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < U; ++u)
+#pragma unroll
+        for (int r = 0; r < R; ++r) acc[r] += pv[u] * qs[rc[u]][r];
     }
   }
-  float* dst = part + (chunk * cols + n) * R;
+  if (w > 0) {
 #pragma unroll
-  for (int r = 0; r < R; ++r) {
-    dst[r] = a0[r];
-    dst[R + r] = a1[r];
+    for (int r = 0; r < R; ++r) red[w - 1][lane][r] = acc[r];
+  }
+  __syncthreads();
+  if (w == 0 && n < cols) {
+    float* dst = part + (chunk * cols + n) * R;
+#pragma unroll
+    for (int r = 0; r < R; ++r) {
+      float s = acc[r];
+#pragma unroll
+      for (int v = 0; v < kRowsPerBlock - 1; ++v) s += red[v][lane][r];
+      dst[r] = s;
+    }
   }
 }
 
@@ -216,14 +233,14 @@ extern "C" int dk_lora_grads(const void* dy, const void* z, const void* x, const
                            (f16*)dz, m, n_out);
   if (e) return e;
   // dB = fp32(fp16(dY^T z)) * s
-  e = cols_dispatch<false>(rank, dim3((unsigned)((n_out + 2 * kThreads - 1) / (2 * kThreads)), (unsigned)chunks),
+  e = cols_dispatch<false>(rank, dim3((unsigned)((n_out + 63) / 64), (unsigned)chunks),
                            stream, (const f16*)dy, nullptr, 1.0f, (const f16*)z, part, m, n_out);
   if (e) return e;
   hipLaunchKernelGGL(lora_finalize_kernel<false>, dim3((unsigned)((n_out * rank + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, stream, part, chunks, n_out, rank, lora_scale, db);
   DK_CHECK_LAUNCH();
   // dA = fp32(fp16(dz^T Xd))
-  e = cols_dispatch<true>(rank, dim3((unsigned)((k + 2 * kThreads - 1) / (2 * kThreads)), (unsigned)chunks),
+  e = cols_dispatch<true>(rank, dim3((unsigned)((k + 63) / 64), (unsigned)chunks),
                           stream, (const f16*)x, mask, ks, (const f16*)dz, part, m, k);
   if (e) return e;
   hipLaunchKernelGGL(lora_finalize_kernel<true>, dim3((unsigned)((k * rank + kThreads - 1) / kThreads)),

@@ -3,30 +3,38 @@
 //   forward  "NT":  C[m][n] = sum_k A[m][k] * W[n][k]      W stored [N][K], K contiguous
 //   backward "NN":  C[m][n] = sum_k A[m][k] * W[k][n]      W stored [K][N], N contiguous
 //
-// A is fp16 row-major [M][K] (X or dY).  A 256-thread workgroup (4 waves, 2 x 2) owns a
-// BM x BN tile of C and walks K in steps of 64 with two LDS buffers: while the MFMAs consume one
-// buffer, the next A tile and the next packed W tile are already in registers and are written
-// into the other buffer, the W tile being dequantised on the way (NF4 table and second-level code
-// table resident in LDS).  Both LDS tiles are K-contiguous rows padded to 72 halves, so every
-// MFMA operand is one conflict-free ds_read_b128; the NN producer transposes a 4 x 8 block of
-// weights in registers before writing it.  One first-level block covers 64 consecutive weights of
-// a stored row, so each 16-byte packed chunk (NT) or 4-byte chunk (NN) has a single absmax.
+// A is fp16 row-major [M][K] (X or dY).  A workgroup owns a BM x BN tile of C and walks K in
+// steps of 64.  It has 8 waves in two roles (warp specialisation):
+//   - 4 consumer waves (2 x 2, each a (BM/2) x (BN/2) sub-tile) only read MFMA fragments from LDS
+//     and issue MFMAs;
+//   - 4 producer waves load the A tile and the packed W tile from global memory three steps
+//     ahead (three register stages), look the NF4 values up in an LDS table one step ahead, and
+//     write the A tile and the dequantised W tile into the LDS buffer of the next step.
+// Each SIMD holds one consumer and one producer wave, so the producer's VALU dequant issues while
+// the consumer's MFMAs run.  Two LDS buffers; one barrier per step.  Both LDS tiles are
+// K-contiguous rows padded to 72 halves, so every MFMA operand is one ds_read_b128.  One
+// first-level block covers 64 consecutive weights of a stored row, so each 16-byte packed chunk
+// (NT) or 4-byte chunk (NN) has a single absmax.  The NN producer transposes a 4 x 8 block of
+// weights in registers before writing it, 16 lanes covering one LDS row segment.
 //
 // Epilogues (fused, per output element, rounding like the reference's separate ops):
 //   LINEAR      y = fp16(acc + bias); + LoRA: fp16(fp32(y) + s * fp32(fp16(z B^T)))     (forward)
 //               dX = fp32(fp16(acc)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0)        (backward)
 //               the rank-16 LoRA product is one extra MFMA per 32 x 32 tile and rank slice.
-//   SWIGLU_FWD  the B rows of each wave's 64 columns are 32 gate rows and the matching 32 up
-//               rows, so g and u of one output sit in the same lane and register:
+//   SWIGLU_FWD  the B rows of each consumer wave's 64 columns are 32 gate rows and the matching
+//               32 up rows, so g and u of one output sit in the same lane and register:
 //               act = fp16(silu(fp16(g)) * fp16(u)), optional [g | u] store.
 //   SWIGLU_BWD  dact = fp16(acc), then the gated-SiLU backward in place on gu.
+// Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
+// of the same kernel sums them in split order and runs the epilogue.
 #include "dk_common.h"
 
 namespace {
 
 constexpr int kBK = 64;
 constexpr int kStride = kBK + 8;  // halves per LDS row (144 bytes)
-constexpr int kThreads = 256;
+constexpr int kThreads = 512;     // 4 consumer + 4 producer waves
+constexpr int kRoleThreads = 256;
 
 enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
 
@@ -52,73 +60,86 @@ struct GemmParams {
   int64_t ldo;
   int out_mode;
   f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
-  int tiles_m;
+  int tiles_n;
+  int splits;           // split-K factor (1: none)
+  float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
+  int reduce;           // split-K second launch: sum the partials, then the epilogue
 };
-
-__device__ __forceinline__ uint32_t dq_pair(const float* lut, uint32_t byte, float amax) {
-  const f16 even = dk_h(__fmul_rn(lut[(byte >> 4) & 15u], amax));
-  const f16 odd = dk_h(__fmul_rn(lut[byte & 15u], amax));
-  return dk_pack2(even, odd);
-}
 
 template <int BM, int BN, bool TRANS, int EPI>
 __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CHUNKS = BM * kBK / 8 / kThreads;
+  constexpr int A_CHUNKS = BM * kBK / 8 / kRoleThreads;
   constexpr int B_UNITS = BN / 128 > 0 ? BN / 128 : 1;
   constexpr int B_ACTIVE = BN * 2;  // NT: 16-byte chunks; NN: 4 x 8 units (both 2 * BN)
+  constexpr int NAM = TRANS ? 4 : 1;  // absmax values per B unit
+  constexpr int TILE = BM * BN;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
 
   __shared__ __attribute__((aligned(16))) f16 As[2][BM * kStride];
   __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * kStride];
-  __shared__ float lut[16];
+  // byte -> (NF4[high nibble], NF4[low nibble]): one 8-byte lookup dequantises two weights
+  __shared__ f32x2 pair_lut[256];
   __shared__ float c2t[256];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int wm = wave & 1, wn = wave >> 1;
+  const bool producer = wave >= 4;
 
   // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin, so give each XCD a
-  // contiguous run of tiles (M fastest: consecutive tiles share the same W tile in that L2).
+  // contiguous run of tiles, N fastest: an XCD keeps one band of A rows in its L2 while the
+  // packed W tiles (a quarter of the bytes per row) stream past it.  With split-K the splits of
+  // one tile are consecutive, so they share an XCD and its L2.
   int b = blockIdx.x;
   const int nb = gridDim.x;
   if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
-  const int64_t m0 = (int64_t)(b % p.tiles_m) * BM;
-  const int64_t n0 = (int64_t)(b / p.tiles_m) * BN;
-
-  if (tid < 16) lut[tid] = p.nf4[tid];
-  c2t[tid] = p.code2[tid];
-
+  const int grid_splits = p.reduce ? 1 : p.splits;
+  const int split = b % grid_splits;
+  const int tile = b / grid_splits;
+  const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
+  const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
   const int64_t M = p.M, N = p.N, K = p.K;
-  const int nk = (int)(K / kBK);
+  const int nk_all = (int)(K / kBK);
+  const int ks0 = (int)((int64_t)nk_all * split / p.splits);
+  const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - ks0;
 
-  // ---- global -> register staging
-  u32x4 a_reg[A_CHUNKS];
-  uint32_t b_word[B_UNITS][TRANS ? 4 : 4];
-  uint32_t b_code[B_UNITS][TRANS ? 4 : 1];
-  float b_s2[B_UNITS][TRANS ? 4 : 1];
-  float b_o2[B_UNITS][TRANS ? 4 : 1];
+  if (!p.reduce && producer) {
+    // =========================== producer waves ===========================
+    const int pt = tid - kRoleThreads;
+    pair_lut[pt] = f32x2{p.nf4[pt >> 4], p.nf4[pt & 15]};
+    c2t[pt] = p.code2[pt];
 
-  auto load_tiles = [&](int kt) {
-    const int64_t k0 = (int64_t)kt * kBK;
+    struct Stage {
+      u32x4 a_reg[A_CHUNKS];
+      uint32_t b_word[B_UNITS][4];
+      uint32_t b_code[B_UNITS][NAM];
+      float b_s2[B_UNITS][NAM];
+      float b_o2[B_UNITS][NAM];
+    };
+    struct Looked {
+      f32x2 v[B_UNITS][16];
+      float c2[B_UNITS][NAM];
+    };
+
+    // Every load is unconditional (rows past M read row M - 1, whose products land only in
+    // output rows that are never stored; steps past the last repeat it; surplus threads of a
+    // narrow B tile repeat a valid chunk), so the compiler counts outstanding loads exactly and
+    // waits only for the stage it consumes.
+    auto load_tiles = [&](Stage& sg, int kt) {
+      const int64_t k0 = (int64_t)(ks0 + (kt < nk ? kt : nk - 1)) * kBK;
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 3, col8 = c & 7;
-      const int64_t gm = m0 + row;
-      if (gm < M) {
-        a_reg[i] = *reinterpret_cast<const u32x4*>(p.a + gm * p.lda + k0 + col8 * 8);
-      } else {
-        a_reg[i] = u32x4{0u, 0u, 0u, 0u};
+      for (int i = 0; i < A_CHUNKS; ++i) {
+        const int c = pt + kRoleThreads * i;
+        const int row = c >> 3, col8 = c & 7;
+        const int64_t gm = m0 + row < M ? m0 + row : M - 1;
+        sg.a_reg[i] = *reinterpret_cast<const u32x4*>(p.a + gm * p.lda + k0 + col8 * 8);
       }
-    }
 #pragma unroll
-    for (int i = 0; i < B_UNITS; ++i) {
-      const int c = tid + kThreads * i;
-      if (c < B_ACTIVE) {
+      for (int i = 0; i < B_UNITS; ++i) {
+        const int c = (pt + kRoleThreads * i) & (B_ACTIVE - 1);
         if (!TRANS) {
           const int row = c >> 1, half = c & 1;
           int64_t n = n0 + row;
@@ -128,81 +149,138 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
           }
           const int64_t elem = n * K + k0 + half * 32;
           const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
-          b_word[i][0] = v[0];
-          b_word[i][1] = v[1];
-          b_word[i][2] = v[2];
-          b_word[i][3] = v[3];
+#pragma unroll
+          for (int d = 0; d < 4; ++d) sg.b_word[i][d] = v[d];
           const int64_t q = elem >> 6;
-          b_code[i][0] = p.qabs[q];
-          b_s2[i][0] = p.scale2[q >> 8];
-          b_o2[i][0] = p.offset2[q >> 8];
+          sg.b_code[i][0] = p.qabs[q];
+          sg.b_s2[i][0] = p.scale2[q >> 8];
+          sg.b_o2[i][0] = p.offset2[q >> 8];
         } else {
-          const int ng = c % (BN / 8), kg = c / (BN / 8);
+          const int kg = c & 15, ng = c >> 4;  // k fastest: 16 lanes fill one LDS row segment
 #pragma unroll
           for (int r = 0; r < 4; ++r) {
             const int64_t elem = (k0 + 4 * kg + r) * N + n0 + 8 * ng;
-            b_word[i][r] = *reinterpret_cast<const uint32_t*>(p.packed + (elem >> 1));
+            sg.b_word[i][r] = *reinterpret_cast<const uint32_t*>(p.packed + (elem >> 1));
             const int64_t q = elem >> 6;
-            b_code[i][r] = p.qabs[q];
-            b_s2[i][r] = p.scale2[q >> 8];
-            b_o2[i][r] = p.offset2[q >> 8];
+            sg.b_code[i][r] = p.qabs[q];
+            sg.b_s2[i][r] = p.scale2[q >> 8];
+            sg.b_o2[i][r] = p.offset2[q >> 8];
           }
         }
       }
-    }
-  };
+    };
 
-  auto store_tiles = [&](int buf) {
-    f16* as = As[buf];
-    f16* bs = Bs[buf];
+    auto look_up = [&](const Stage& sg, Looked& lk) {
 #pragma unroll
-    for (int i = 0; i < A_CHUNKS; ++i) {
-      const int c = tid + kThreads * i;
-      const int row = c >> 3, col8 = c & 7;
-      *reinterpret_cast<u32x4*>(as + row * kStride + col8 * 8) = a_reg[i];
-    }
+      for (int i = 0; i < B_UNITS; ++i) {
 #pragma unroll
-    for (int i = 0; i < B_UNITS; ++i) {
-      const int c = tid + kThreads * i;
-      if (c < B_ACTIVE) {
-        if (!TRANS) {
-          const int row = c >> 1, half = c & 1;
-          const float amax = dk_absmax(c2t[b_code[i][0]], b_s2[i][0], b_o2[i][0]);
-          f16* dst = bs + row * kStride + half * 32;
+        for (int d = 0; d < 4; ++d)
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
-            const uint32_t w = b_word[i][d];
-            u32x4 o;
+          for (int bb = 0; bb < 4; ++bb) lk.v[i][4 * d + bb] = pair_lut[(sg.b_word[i][d] >> (8 * bb)) & 0xffu];
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) o[bb] = dq_pair(lut, (w >> (8 * bb)) & 0xffu, amax);
-            *reinterpret_cast<u32x4*>(dst + d * 8) = o;
-          }
-        } else {
-          const int ng = c % (BN / 8), kg = c / (BN / 8);
-          f16 v[4][8];
+        for (int r = 0; r < NAM; ++r) lk.c2[i][r] = c2t[sg.b_code[i][r]];
+      }
+    };
+
+    auto store_tiles = [&](const Stage& sg, const Looked& lk, int buf) {
+      f16* as = As[buf];
+      f16* bs = Bs[buf];
 #pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const float amax = dk_absmax(c2t[b_code[i][r]], b_s2[i][r], b_o2[i][r]);
-            const uint32_t w = b_word[i][r];
+      for (int i = 0; i < A_CHUNKS; ++i) {
+        const int c = pt + kRoleThreads * i;
+        const int row = c >> 3, col8 = c & 7;
+        *reinterpret_cast<u32x4*>(as + row * kStride + col8 * 8) = sg.a_reg[i];
+      }
 #pragma unroll
-            for (int bb = 0; bb < 4; ++bb) {
-              const uint32_t byte = (w >> (8 * bb)) & 0xffu;
-              v[r][2 * bb] = dk_h(__fmul_rn(lut[byte >> 4], amax));
-              v[r][2 * bb + 1] = dk_h(__fmul_rn(lut[byte & 15u], amax));
+      for (int i = 0; i < B_UNITS; ++i) {
+        const int c = pt + kRoleThreads * i;
+        if (c < B_ACTIVE) {
+          if (!TRANS) {
+            const int row = c >> 1, half = c & 1;
+            const float amax = dk_absmax(lk.c2[i][0], sg.b_s2[i][0], sg.b_o2[i][0]);
+            f16* dst = bs + row * kStride + half * 32;
+#pragma unroll
+            for (int d = 0; d < 4; ++d) {
+              u32x4 o;
+#pragma unroll
+              for (int bb = 0; bb < 4; ++bb) {
+                const f32x2 nv = lk.v[i][4 * d + bb];
+                o[bb] = dk_pack2(dk_h(__fmul_rn(nv[0], amax)), dk_h(__fmul_rn(nv[1], amax)));
+              }
+              *reinterpret_cast<u32x4*>(dst + d * 8) = o;
+            }
+          } else {
+            const int kg = c & 15, ng = c >> 4;
+            f16 v[4][8];
+#pragma unroll
+            for (int r = 0; r < 4; ++r) {
+              const float amax = dk_absmax(lk.c2[i][r], sg.b_s2[i][r], sg.b_o2[i][r]);
+#pragma unroll
+              for (int bb = 0; bb < 4; ++bb) {
+                const f32x2 nv = lk.v[i][4 * r + bb];
+                v[r][2 * bb] = dk_h(__fmul_rn(nv[0], amax));
+                v[r][2 * bb + 1] = dk_h(__fmul_rn(nv[1], amax));
+              }
+            }
+#pragma unroll
+            for (int col = 0; col < 8; ++col) {
+              u32x2 o;
+              o[0] = dk_pack2(v[0][col], v[1][col]);
+              o[1] = dk_pack2(v[2][col], v[3][col]);
+              *reinterpret_cast<u32x2*>(bs + (8 * ng + col) * kStride + 4 * kg) = o;
             }
           }
-#pragma unroll
-          for (int col = 0; col < 8; ++col) {
-            u32x2 o;
-            o[0] = dk_pack2(v[0][col], v[1][col]);
-            o[1] = dk_pack2(v[2][col], v[3][col]);
-            *reinterpret_cast<u32x2*>(bs + (8 * ng + col) * kStride + 4 * kg) = o;
-          }
         }
       }
-    }
-  };
+    };
 
+    // Step j lives in register stage j % 3 and LDS buffer j % 2.  While the consumers run step
+    // j, the producers issue the loads of step j + 3 into the stage step j has vacated and write
+    // step j + 1 into the other buffer; each load has two steps of MFMA time to land.  Steps past
+    // the last repeat it into a buffer that is not read again: no branch around memory
+    // operations inside the loop.
+    Stage s0, s1, s2;
+    Looked lk;
+    load_tiles(s0, 0);
+    load_tiles(s1, 1);
+    load_tiles(s2, 2);
+    __syncthreads();  // lookup tables visible
+    look_up(s0, lk);
+    store_tiles(s0, lk, 0);
+    __syncthreads();  // step 0 in buffer 0
+    int j = 0;
+    for (; j + 3 <= nk; j += 3) {
+      load_tiles(s0, j + 3);
+      look_up(s1, lk);
+      store_tiles(s1, lk, (j + 1) & 1);
+      __syncthreads();
+      load_tiles(s1, j + 4);
+      look_up(s2, lk);
+      store_tiles(s2, lk, j & 1);
+      __syncthreads();
+      load_tiles(s2, j + 5);
+      look_up(s0, lk);
+      store_tiles(s0, lk, (j + 1) & 1);
+      __syncthreads();
+    }
+    if (j < nk) {
+      look_up(s1, lk);
+      store_tiles(s1, lk, (j + 1) & 1);
+      __syncthreads();
+    }
+    if (j + 1 < nk) {
+      look_up(s2, lk);
+      store_tiles(s2, lk, j & 1);
+      __syncthreads();
+    }
+    return;
+  }
+  if (producer) return;  // split-K second launch: the consumers sum the partials
+
+  // =========================== consumer waves ===========================
+  const int wm = wave & 1, wn = wave >> 1;
+  const int lrow = lane & 31;
+  const int lk8 = 8 * (lane >> 5);
   f32x16 acc[TM][TN];
 #pragma unroll
   for (int i = 0; i < TM; ++i)
@@ -211,36 +289,62 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
 #pragma unroll
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-  const int lrow = lane & 31;
-  const int lk = 8 * (lane >> 5);
+  if (!p.reduce) {
+    auto compute = [&](int buf) {
+      const f16* as = As[buf];
+      const f16* bs = Bs[buf];
+#pragma unroll
+      for (int s = 0; s < kBK / 16; ++s) {
+        f16x8 af[TM], bf[TN];
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+          af[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk8);
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk8);
+#pragma unroll
+        for (int i = 0; i < TM; ++i)
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+      }
+    };
+    // the same number of barriers as the producers: 2 before step 0, one per step
+    __syncthreads();
+    __syncthreads();
+    for (int kt = 0; kt < nk; ++kt) {
+      compute(kt & 1);
+      __syncthreads();
+    }
 
-  load_tiles(0);
-  __syncthreads();  // lut / c2t visible
-  store_tiles(0);
-  __syncthreads();
-
-  for (int kt = 0; kt < nk; ++kt) {
-    const int cur = kt & 1;
-    if (kt + 1 < nk) load_tiles(kt + 1);
-    const f16* as = As[cur];
-    const f16* bs = Bs[cur];
-#pragma unroll
-    for (int s = 0; s < kBK / 16; ++s) {
-      f16x8 af[TM], bf[TN];
-#pragma unroll
-      for (int i = 0; i < TM; ++i)
-        af[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk);
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-        bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk);
+    // split-K, first launch: store the fp32 partial tile (lane-major, so each register store is
+    // 256 contiguous bytes) and stop; the epilogue runs in the second launch
+    if (p.splits > 1) {
+      float* mine = p.part + ((int64_t)tile * p.splits + split) * TILE;
 #pragma unroll
       for (int i = 0; i < TM; ++i)
 #pragma unroll
         for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            mine[(((wave * TM + i) * TN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
+      return;
     }
-    if (kt + 1 < nk) store_tiles(cur ^ 1);
-    __syncthreads();
+  } else {
+    // split-K, second launch: sum the partials in split order (a fixed order, so the result is
+    // deterministic); the kernel boundary orders it after every partial store
+    const float* all = p.part + (int64_t)tile * p.splits * TILE;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int idx = (((wave * TM + i) * TN + j) * 16 + v) * 64 + lane;
+          float s = 0.0f;
+          for (int sp = 0; sp < p.splits; ++sp) s += all[(int64_t)sp * TILE + idx];
+          acc[i][j][v] = s;
+        }
   }
 
   // ---- epilogue.  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
@@ -264,16 +368,16 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
           for (int rc = 0; rc < p.rank; rc += 16) {
             f16x8 zf, rf;
             if (zm < M) {
-              zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk);
+              zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk8);
             } else {
 #pragma unroll
               for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
             }
             if (!TRANS) {
-              rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk);
+              rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk8);
             } else {
 #pragma unroll
-              for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk + e) * N + n];
+              for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk8 + e) * N + n];
             }
             lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
           }
@@ -317,8 +421,8 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
         if (m >= M) continue;
         const f16 g16 = dk_h(acc[i][0][v]);
         const f16 u16 = dk_h(acc[i][1][v]);
-        const float g = (float)g16;
-        const float silu = g / (1.0f + __expf(-g));
+        float sig, silu;
+        dk_silu_parts((float)g16, &sig, &silu);
         act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
         if (p.gu) {
           p.gu[m * 2 * p.inter + hcol] = g16;
@@ -341,9 +445,8 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
           f16* gp = p.gu + m * 2 * p.inter + n;
           const float g = (float)gp[0];
           const float u = (float)gp[p.inter];
-          const float e = 1.0f + __expf(-g);
-          const float sig = 1.0f / e;
-          const float silu = g / e;
+          float sig, silu;
+          dk_silu_parts(g, &sig, &silu);
           gp[p.inter] = dk_h(da * silu);
           gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
         }
@@ -352,15 +455,77 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
   }
 }
 
+// Launch plan: tile shape and split-K factor.  256 CUs; a 256 x 128 tile's 114 KB of LDS leaves
+// one workgroup per CU, the 128-row tiles two.  Shapes with too few tiles to fill the chip split
+// K when it is long (at least 16 steps per split, so the partial-tile traffic stays small next
+// to the MFMA work) and otherwise use narrower tiles.
+struct Plan {
+  int bm, bn, splits;
+  int64_t tiles;
+};
+
+Plan plan_for(int64_t M, int64_t N, int64_t K, int epi) {
+  const int64_t nk = K / kBK;
+  const int64_t mt256 = (M + 255) / 256, mt128 = (M + 127) / 128;
+  if (N % 128 == 0 && mt256 * (N / 128) >= 256) return {256, 128, 1, mt256 * (N / 128)};
+  Plan pl{128, 128, 1, mt128 * (N / 128)};
+  if (N % 128 != 0) pl = {128, 64, 1, mt128 * (N / 64)};
+  if (epi != EPI_LINEAR || pl.tiles >= 256) return pl;
+  if (nk >= 64) {
+    int64_t s = (512 + pl.tiles - 1) / pl.tiles;
+    if (s > nk / 16) s = nk / 16;
+    if (s > 8) s = 8;
+    if (s >= 2) pl.splits = (int)s;
+    return pl;
+  }
+  if (pl.bn == 128) pl = {128, 64, 1, mt128 * (N / 64)};
+  return pl;
+}
+
+int64_t plan_workspace(const Plan& pl) {
+  if (pl.splits <= 1) return 0;
+  return pl.tiles * pl.splits * pl.bm * pl.bn * (int64_t)sizeof(float);
+}
+
 template <int BM, int BN, bool TRANS, int EPI>
-int launch(GemmParams p, hipStream_t stream) {
-  p.tiles_m = (int)((p.M + BM - 1) / BM);
-  const int64_t tiles = (int64_t)p.tiles_m * (p.N / BN);
-  if (tiles <= 0 || tiles > 0x7fffffff) return DK_ERR_INVALID;
-  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)tiles), dim3(kThreads),
-                     0, stream, p);
+int launch(GemmParams p, int splits, hipStream_t stream) {
+  p.tiles_n = (int)(p.N / BN);
+  const int64_t tiles = ((p.M + BM - 1) / BM) * (int64_t)p.tiles_n;
+  p.splits = splits;
+  p.reduce = 0;
+  if (tiles <= 0 || tiles * splits > 0x7fffffff) return DK_ERR_INVALID;
+  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)(tiles * splits)),
+                     dim3(kThreads), 0, stream, p);
   DK_CHECK_LAUNCH();
+  if (splits > 1) {
+    p.reduce = 1;
+    hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)tiles),
+                       dim3(kThreads), 0, stream, p);
+    DK_CHECK_LAUNCH();
+  }
   return 0;
+}
+
+// Runs the plan; without a workspace the plan's split-K is dropped (same kernel, one split).
+template <bool TRANS, int EPI>
+int dispatch(GemmParams p, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  Plan pl = plan_for(p.M, p.N, p.K, EPI);
+  if (pl.splits > 1) {
+    if (ws == nullptr) {
+      pl.splits = 1;
+    } else {
+      if (ws_bytes < plan_workspace(pl)) return DK_ERR_WORKSPACE;
+      if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
+      p.part = reinterpret_cast<float*>(ws);
+    }
+  }
+  if (pl.bm == 256) return launch<256, 128, TRANS, EPI>(p, pl.splits, stream);
+  if (pl.bn == 128) return launch<128, 128, TRANS, EPI>(p, pl.splits, stream);
+  if constexpr (EPI == EPI_SWIGLU_FWD) {
+    return DK_ERR_INVALID;
+  } else {
+    return launch<128, 64, TRANS, EPI>(p, pl.splits, stream);
+  }
 }
 
 bool weight_ok(const dk_nf4_weight* w) {
@@ -389,7 +554,7 @@ int check_lora(const void* left, const void* right, int64_t rank) {
 extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
                                 const void* bias, const void* z, const void* lora_b,
                                 int64_t rank, float lora_scale, void* y, int64_t ldy,
-                                hipStream_t stream) {
+                                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || !weight_ok(w) || !x || !y) return DK_ERR_INVALID;
   if (w->rows % 64 || w->cols % kBK || ldx < w->cols || ldy < w->rows) return DK_ERR_INVALID;
   if (int e = check_lora(z, lora_b, rank)) return e;
@@ -411,14 +576,14 @@ extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_
   p.out = y;
   p.ldo = ldy;
   p.out_mode = DK_OUT_F16;
-  if (p.N % 128 == 0) return launch<128, 128, false, EPI_LINEAR>(p, stream);
-  return launch<128, 64, false, EPI_LINEAR>(p, stream);
+  return dispatch<false, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
                                    const dk_nf4_weight* w, const void* dz, const void* lora_a,
                                    int64_t rank, const uint8_t* mask, float keep_scale, void* dx,
-                                   int64_t lddx, int out_mode, hipStream_t stream) {
+                                   int64_t lddx, int out_mode, void* workspace,
+                                   int64_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || !weight_ok(w) || !dy || !dx) return DK_ERR_INVALID;
   if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
   if (w->cols % 64 || w->rows % kBK || lddy < w->rows || lddx < w->cols) return DK_ERR_INVALID;
@@ -440,8 +605,7 @@ extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
   p.out = dx;
   p.ldo = lddx;
   p.out_mode = out_mode;
-  if (p.N % 128 == 0) return launch<128, 128, true, EPI_LINEAR>(p, stream);
-  return launch<128, 64, true, EPI_LINEAR>(p, stream);
+  return dispatch<true, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
@@ -462,7 +626,7 @@ extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
   p.out = act;
   p.ldo = p.inter;
   p.gu = (f16*)gu_out;
-  return launch<128, 128, false, EPI_SWIGLU_FWD>(p, stream);
+  return dispatch<false, EPI_SWIGLU_FWD>(p, nullptr, 0, stream);
 }
 
 extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
@@ -480,6 +644,11 @@ extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
   p.inter = w_down->cols;
   set_weight(p, w_down);
   p.gu = (f16*)gu;
-  if (p.N % 128 == 0) return launch<128, 128, true, EPI_SWIGLU_BWD>(p, stream);
-  return launch<128, 64, true, EPI_SWIGLU_BWD>(p, stream);
+  return dispatch<true, EPI_SWIGLU_BWD>(p, nullptr, 0, stream);
+}
+
+extern "C" int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward) {
+  if (m <= 0 || !weight_ok(w)) return 0;
+  const int64_t n = backward ? w->cols : w->rows, k = backward ? w->rows : w->cols;
+  return plan_workspace(plan_for(m, n, k, EPI_LINEAR));
 }

@@ -8,6 +8,8 @@ libdk.so).  Every op runs on ``torch.cuda.current_stream()`` and allocates only 
 (and, for the LoRA gradients, a small fp32 partial-sum workspace) through torch.
 """
 
+import threading
+
 import torch
 
 from . import _lib
@@ -74,6 +76,24 @@ class W4:
         return out
 
 
+_WS = {}
+_WS_LOCK = threading.Lock()
+
+
+def _workspace(w, m, backward, device):
+    """Split-K scratch for a fused linear (None when the shape needs none): one buffer per
+    (device, stream), grown on demand.  Kernels on one stream run in order, so they share it."""
+    nbytes = int(_lib.lib().dk_w4_linear_workspace(m, w.c_ref(), int(backward)))
+    if nbytes == 0:
+        return None, 0
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        buf = _WS.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = _WS[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return buf, nbytes
+
+
 def _check16(t, name, shape=None):
     if t.dtype != torch.float16 or not t.is_cuda:
         raise ValueError(f"{name} must be a CUDA fp16 tensor, got {t.dtype} on {t.device}")
@@ -131,9 +151,11 @@ def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=Non
     if out is None:
         out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
     _check16(out, "out", (m, w.rows))
+    ws, nbytes = _workspace(w, m, False, x.device)
     rc = _lib.lib().dk_w4_linear_fwd(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
                                      _lib.ptr(z), _lib.ptr(lora_B), r, float(lora_scale),
-                                     _lib.ptr(out), out.stride(0), _lib.stream_handle(x.device))
+                                     _lib.ptr(out), out.stride(0), _lib.ptr(ws), nbytes,
+                                     _lib.stream_handle(x.device))
     _lib.check(rc, "dk_w4_linear_fwd")
     return out
 
@@ -171,9 +193,10 @@ def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, o
         raise ValueError("dX is fp16 or fp32")
     if tuple(out.shape) != (m, w.cols) or out.stride(1) != 1:
         raise ValueError("dX output has the wrong shape or layout")
+    ws, nbytes = _workspace(w, m, True, dy.device)
     rc = _lib.lib().dk_w4_linear_bwd_dx(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), _lib.ptr(dz),
                                         _lib.ptr(lora_A), r, _lib.ptr(mask), float(keep_scale),
-                                        _lib.ptr(out), out.stride(0), mode,
+                                        _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws), nbytes,
                                         _lib.stream_handle(dy.device))
     _lib.check(rc, "dk_w4_linear_bwd_dx")
     return out

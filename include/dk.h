@@ -92,10 +92,19 @@ int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const voi
  *   y = fp16(fp32(fp16(X W^T + bias)) + s * fp32(fp16(z B^T))).
  * x [m, w.cols] fp16 (row stride ldx elements), y [m, w.rows] fp16 (row stride ldy),
  * bias [w.rows] fp16 or NULL, z [m, rank] fp16 and lora_b [w.rows, rank] fp16, or both NULL.
- * w.rows % 64 == 0, w.cols % 64 == 0. */
+ * w.rows % 64 == 0, w.cols % 64 == 0.
+ * workspace: scratch of dk_w4_linear_workspace(m, w, 0) bytes, 256-byte aligned, for the
+ * split-K partial tiles (a second launch on the same stream sums them in a fixed order and runs
+ * the epilogue); NULL runs without split-K.  Launches that overlap in time must not share it. */
 int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
                      const void* bias, const void* z, const void* lora_b, int64_t rank,
-                     float lora_scale, void* y, int64_t ldy, hipStream_t stream);
+                     float lora_scale, void* y, int64_t ldy, void* workspace,
+                     int64_t workspace_bytes, hipStream_t stream);
+
+/* Workspace bytes the fused linear needs at m rows (0: no split-K for this shape);
+ * backward = 0 for dk_w4_linear_fwd, 1 for dk_w4_linear_bwd_dx.  No counterpart in the
+ * reference (cuBLAS manages its own workspace); part of the drop-in for its torch.mm calls. */
+int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward);
 
 /* Output modes of the backward dX GEMM. */
 #define DK_OUT_F16 0         /* dx is fp16, overwritten */
@@ -108,11 +117,12 @@ int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight*
  * solution/k_norm.py:65-71):
  *   dX = fp32(fp16(dY W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0)
  * dy [m, w.rows] fp16 (row stride lddy), dx [m, w.cols] (row stride lddx) in out_mode,
- * dz [m, rank] fp16, lora_a [rank, w.cols] fp16 and mask [m, w.cols] uint8, or all NULL. */
+ * dz [m, rank] fp16, lora_a [rank, w.cols] fp16 and mask [m, w.cols] uint8, or all NULL.
+ * workspace as for dk_w4_linear_fwd, sized by dk_w4_linear_workspace(m, w, 1). */
 int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m, const dk_nf4_weight* w,
                         const void* dz, const void* lora_a, int64_t rank, const uint8_t* mask,
                         float keep_scale, void* dx, int64_t lddx, int out_mode,
-                        hipStream_t stream);
+                        void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 /* LoRA parameter gradients and the LoRA-down gradient.  Replaces
  * solution/fast_qwen.py:1369-1374:

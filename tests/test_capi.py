@@ -32,12 +32,13 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_lora_down(None, None, 1.0, None, None, 8, 64, 16, None) == _lib.DK_ERR_INVALID
     w = _lib.NF4WeightC(1, 1, 1, 1, 1, 1, 100, 100)     # 10000 weights: not whole 16384 blocks
     assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 100, 8, ctypes.byref(w), None, None, None, 0,
-                                2.0, ctypes.c_void_p(16), 100, None) == _lib.DK_ERR_INVALID
+                                2.0, ctypes.c_void_p(16), 100, None, 0, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_w4_linear_workspace(2048, ctypes.byref(w), 0) == 0
     # misaligned packed pointer (needs 4 bytes) and fp16 output (needs 16 bytes)
     assert lib.dk_nf4_dequant(ctypes.c_void_p(2), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
-    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * 1536 * 16 * 4
+    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 8 * 1536 * 16 * 4
     assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
     with pytest.raises(ValueError):
         _lib.check(_lib.DK_ERR_INVALID, "probe")
