@@ -45,8 +45,9 @@ def time_op(torch, fn, reps):
     return e0.elapsed_time(e1) / reps
 
 
-def kernel_table(torch, st, reps):
-    """Each operator of one layer's step in isolation (layer 0), with its algorithmic work."""
+def kernel_table(torch, st, reps, only=None):
+    """Each operator of one layer's step in isolation (layer 0), with its algorithmic work.
+    `only`: a set of operator names to restrict the table to."""
     from decentrik_prime_amd import w4linear as W
     m, D, I, KV, r = st.m, 1536, 8960, 256, 16
     L, lo, z, x, dy, o = st.layers[0], st.lora[0], st.z[0], st.x, st.dy, st.out
@@ -80,6 +81,8 @@ def kernel_table(torch, st, reps):
     ]
     out = []
     for name, fn, flops, nbytes, per_layer in rows:
+        if only is not None and name not in only:
+            continue
         ms = time_op(torch, fn, reps)
         row = {"kernel": name, "avg_us": round(ms * 1e3, 2), "launches_per_layer": per_layer,
                "gflop": round(flops / 1e9, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
@@ -181,6 +184,120 @@ def _cpu_model():
     return "unknown"
 
 
+# ---------------------------------------------------------------------------------------------
+# rocprofv3 summaries (rocpd SQLite databases written by `rocprofv3 -d DIR -o run ...`)
+
+def _short(name):
+    """Kernel name without 'void', anonymous namespaces and the argument list (an Itanium-mangled
+    name of this library's kernels is reduced to its identifier and integer/bool template
+    arguments)."""
+    import re
+    if name.startswith("_Z"):
+        m = re.search(r"(\d+)([A-Za-z_]\w*)", name[name.find("N_1") + 3:] if "N_1" in name else name[2:])
+        if m:
+            ident = m.group(2)[:int(m.group(1))]
+            rest = m.group(2)[int(m.group(1)):]
+            targs = re.findall(r"L([ib])(\d+)E", rest.split("EEv")[0]) if rest.startswith("I") else []
+            vals = [("true" if v == "1" else "false") if t == "b" else v for t, v in targs]
+            return ident + (f"<{', '.join(vals)}>" if vals else "")
+        return name[:100]
+    name = name.replace("(anonymous namespace)::", "")
+    if name.startswith("void "):
+        name = name[5:]
+    depth, cut = 0, len(name)
+    for i, ch in enumerate(name):   # cut at the '(' of the argument list (outside template <>)
+        if ch == "<":
+            depth += 1
+        elif ch == ">":
+            depth -= 1
+        elif ch == "(" and depth == 0:
+            cut = i
+            break
+    return re.sub(r"\s+", " ", name[:cut])[:100]
+
+
+def summarize_trace(db, top=40):
+    """Per-kernel dispatch statistics of a kernel trace: calls, average and total duration,
+    grouped by kernel name and grid (a kernel instance launched at several shapes is split)."""
+    import collections
+    import sqlite3
+    cur = sqlite3.connect(db).cursor()
+    agg = collections.defaultdict(list)
+    for name, dur, gx, gy, gz, wx, wy, wz in cur.execute(
+            "select name, duration, grid_x, grid_y, grid_z, workgroup_x, workgroup_y, workgroup_z "
+            "from kernels"):
+        wgs = (gx // max(wx, 1)) * (gy // max(wy, 1)) * (gz // max(wz, 1))
+        agg[(_short(name), wgs, wx * wy * wz)].append(dur)
+    total = sum(sum(v) for v in agg.values())
+    lines = [f"{'kernel':78s} {'wgs':>7s} {'wg':>4s} {'calls':>6s} {'avg_us':>9s} "
+             f"{'total_ms':>9s} {'pct':>6s}"]
+    for (k, wgs, wx), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
+        lines.append(f"{k:78s} {wgs:7d} {wx:4d} {len(v):6d} {sum(v) / len(v) / 1e3:9.2f} "
+                     f"{sum(v) / 1e6:9.3f} {100 * sum(v) / total:6.2f}")
+    return "\n".join(lines)
+
+
+def _counter_by_dispatch(db, counter):
+    import sqlite3
+    cur = sqlite3.connect(db).cursor()
+    rows = {}
+    for did, name, grid, wg, val in cur.execute(
+            "select dispatch_id, kernel_name, grid_size, workgroup_size, value "
+            "from counters_collection where counter_name = ?", (counter,)):
+        key = (did, _short(name), grid // max(wg, 1), wg)
+        rows[key] = rows.get(key, 0.0) + val
+    return rows
+
+
+def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
+    """HBM traffic per operator call from a FETCH_SIZE run and a WRITE_SIZE run (KiB per
+    dispatch), each scaled by what the same counter reads for the calibration copy of
+    `copy_bytes` read + `copy_bytes` written (the __amd_rocclr_copyBuffer dispatches within a
+    factor of two of the largest one: nothing else in the run copies a quarter as much).
+    groups: [(operator name, kernel-name substring, operator calls in the run)]."""
+    out = []
+    scaled = {}
+    for label, db, counter in (("fetch", fetch_db, "FETCH_SIZE"), ("write", write_db, "WRITE_SIZE")):
+        rows = _counter_by_dispatch(db, counter)
+        copies = [v for k, v in rows.items() if k[1].startswith("__amd_rocclr_copyBuffer")]
+        if not copies:
+            raise SystemExit(f"{db}: no {counter} value of a copy dispatch")
+        kib = [v for v in copies if v >= 0.5 * max(copies)]
+        kib_avg = sum(kib) / len(kib)
+        factor = copy_bytes / (kib_avg * 1024.0)
+        out.append(f"{counter}: calibration copy {copy_bytes} B -> {kib_avg:.0f} KiB per dispatch "
+                   f"(n={len(kib)}), scale factor {factor:.4f}")
+        for op, pattern, calls in groups:
+            sel = {k: v for k, v in rows.items() if pattern in k[1]}
+            per_kernel = {}
+            for k, v in sel.items():
+                per_kernel.setdefault((k[1], k[2]), []).append(v)
+            for (name, wgs), vals in sorted(per_kernel.items()):
+                out.append(f"  {op} | {name} wgs={wgs}: {len(vals)} dispatches, "
+                           f"{sum(vals) / len(vals):.0f} KiB each (raw)")
+            per_call = sum(sel.values()) * 1024.0 * factor / calls
+            scaled[(op, label)] = per_call
+            out.append(f"  {op}: {label} {per_call:.4g} B per operator call (scaled, {calls} calls)")
+    for op, _, _ in groups:
+        f, w = scaled[(op, "fetch")], scaled[(op, "write")]
+        out.append(f"TRAFFIC {op} | fetch {f:.0f} | write {w:.0f} | total {f + w:.0f}")
+    return "\n".join(out)
+
+
+def committed_traffic(op):
+    """HBM bytes per call of `op` from the TRAFFIC lines of the committed profile summaries."""
+    import glob
+    here = os.path.dirname(os.path.abspath(__file__))
+    for path in sorted(glob.glob(os.path.join(here, "profiles", "*.txt"))):
+        for line in open(path):
+            if line.startswith("TRAFFIC ") and line[8:].split(" | ")[0] == op:
+                parts = line.strip().split(" | ")
+                return {"bytes": int(parts[3].split()[1]), "fetch": int(parts[1].split()[1]),
+                        "write": int(parts[2].split()[1]),
+                        "source": os.path.relpath(path, here)}
+    return None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -196,7 +313,27 @@ def main():
     ap.add_argument("--kernels-only", action="store_true",
                     help="skip the step timing: per-kernel table, dequant and a copy of known size "
                          "(the calibration of rocprofv3 FETCH_SIZE / WRITE_SIZE)")
+    ap.add_argument("--op", default=None,
+                    help="with --kernels-only: comma-separated operator names to run "
+                         "('dequant' for the dequant) instead of the whole table")
+    ap.add_argument("--summarize-trace", metavar="DB",
+                    help="print the per-kernel table of a rocprofv3 kernel-trace database")
+    ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
+                    help="print HBM traffic per operator call from FETCH_SIZE / WRITE_SIZE runs")
+    ap.add_argument("--group", action="append", default=[],
+                    help="with --summarize-pmc: 'operator=kernel-name substring@calls'")
     args = ap.parse_args()
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
+        return
+    if args.summarize_pmc:
+        groups = []
+        for g in args.group:
+            op, rest = g.split("=", 1)
+            pattern, calls = rest.rsplit("@", 1)
+            groups.append((op, pattern, int(calls)))
+        print(summarize_pmc(*args.summarize_pmc, groups))
+        return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
         print("bench.py measures one GPU: the NF4 linear path has no multi-GPU leg in this build "
               "(it would shard data-parallel over packed tokens with one LoRA-gradient all-reduce)",
@@ -210,14 +347,28 @@ def main():
     st = NF4LinearStack(args.layers, args.m, seed=0, device="cuda")
     torch.cuda.synchronize()
     if args.kernels_only:
-        print(json.dumps({"kernels": kernel_table(torch, st, args.reps),
-                          "dequant": dequant_bandwidth(torch, st, args.reps),
-                          "copy": copy_calibration(torch, args.reps)}), flush=True)
+        only = set(args.op.split(",")) if args.op else None
+        res = {"kernels": kernel_table(torch, st, args.reps, only)}
+        if only is None or "dequant" in only:
+            res["dequant"] = dequant_bandwidth(torch, st, args.reps)
+        res["copy"] = copy_calibration(torch, args.reps)
+        res["calls_per_operator"] = args.reps + 1
+        print(json.dumps(res), flush=True)
         return
     for _ in range(args.warmup):
         st.step()
     torch.cuda.synchronize()
     print("[bench] warmup done", file=sys.stderr, flush=True)
+    kernels = None
+    if not args.no_kernels:
+        # each operator in isolation first: the one with the largest share of the step is the
+        # dominant kernel, whose launches are then timed inside the timed steps
+        kernels = kernel_table(torch, st, args.reps)
+        dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
+        st.probe = (dom["kernel"], [])
+        print(f"[bench] kernel table done; dominant operator {dom['kernel']}", file=sys.stderr,
+              flush=True)
+    torch.cuda.synchronize()
     e0, e1 = _events(torch)
     t0 = time.perf_counter()
     e0.record()
@@ -241,20 +392,29 @@ def main():
                    "lora_dropout": 0.05, "lora_on": ["q_proj", "v_proj"],
                    "flop_per_step": st.flops_per_step},
     }
-    if not args.no_kernels:
-        kernels = kernel_table(torch, st, args.reps)
-        print("[bench] kernel table done", file=sys.stderr, flush=True)
+    if kernels is not None:
+        name, events = st.probe
+        st.probe = None
+        live_ms = sum(a.elapsed_time(b) for a, b in events) / len(events)
+        achieved = dom["gflop"] * 1e9 / (live_ms * 1e-3) / 1e12
+        traffic = committed_traffic(name)
+        result["roofline"] = {
+            "kernel": name, "bound": "mfma", "achieved": round(achieved, 1),
+            "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
+            "traffic": traffic["bytes"] if traffic else None,
+            "per_launch": f"{dom['gflop']} GFLOP algorithmic / {live_ms * 1e3:.2f} us average over "
+                          f"{len(events)} launches inside the timed steps (HIP events on the launch "
+                          f"stream); {dom['avg_us']} us in isolation",
+            "traffic_source": (f"{traffic['source']}: FETCH_SIZE {traffic['fetch']} B + WRITE_SIZE "
+                               f"{traffic['write']} B per call, scaled by a copy of known size")
+                              if traffic else None}
         dq = dequant_bandwidth(torch, st, max(3, args.reps // 4))
         print(f"[bench] dequant {dq['gbps']} GB/s", file=sys.stderr, flush=True)
-        dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
-        result["roofline"] = {
-            "kernel": dom["kernel"], "bound": "mfma", "achieved": dom["tflops"],
-            "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": dom["frac_fp16_peak"],
-            "traffic": None,
-            "per_launch": f"{dom['gflop']} GFLOP algorithmic / {dom['avg_us']} us average launch"}
+        dq_traffic = committed_traffic("dequant")
         result["dequant"] = {**dq, "roofline": {"bound": "hbm", "achieved": dq["gbps"],
                                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                                                "frac": dq["frac_hbm_peak"]}}
+                                                "frac": dq["frac_hbm_peak"],
+                                                "traffic": dq_traffic["bytes"] if dq_traffic else None}}
         result["kernels"] = kernels
     if not args.no_cpu:
         print(f"[bench] CPU baseline (oracle, {args.cpu_layers} layers)", file=sys.stderr, flush=True)

@@ -1,55 +1,60 @@
 // NF4 double-quantised weights on gfx950: the HBM-rate dequant and the blockwise quantiser.
 //
-// Dequant (replaces solution/k_nf4.py:40-57).  One thread handles four 8-weight chunks
-// (4 packed bytes -> 16 bytes of fp16 each).  Chunk c of a block is c = block*1024 + j*256 + tid,
-// so every load instruction of a wave reads 256 contiguous bytes and every store instruction
-// writes 1 KiB contiguous: the kernel is a pure coalesced stream, 2.516 bytes of HBM traffic per
-// weight (0.5 packed + 1/64 code + 8/16384 scale/offset in, 2 out).
+// Dequant (replaces solution/k_nf4.py:40-57).  One thread handles a "quad" of 32 weights: one
+// 16-byte load of packed nibbles (half a first-level block, so one absmax), 64 bytes of fp16 out.
+// A workgroup's 256 quads are 8192 weights, half a second-level block, so scale2/offset2 are
+// uniform (scalar loads).  The 64 output bytes of a lane are staged in LDS and written back
+// lane-contiguous, so every store instruction of a wave writes 1 KiB contiguous.  HBM traffic:
+// 2.516 bytes per weight (0.5 packed + 1/64 code + 8/16384 scale/offset in, 2 out).
 #include "dk_common.h"
 
 namespace {
 
 constexpr int kDqThreads = 256;
-constexpr int kDqChunksPerThread = 4;
-constexpr int kDqChunksPerBlock = kDqThreads * kDqChunksPerThread;  // 1024 chunks = 128 qblocks
+constexpr int kDqQuadsPerBlock = kDqThreads;   // 8192 weights = half a second-level block
+
+__device__ __forceinline__ u32x4 dequant_word(uint32_t w, float a, const float* lut) {
+  u32x4 o;
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    const uint32_t byte = (w >> (8 * b)) & 0xffu;
+    const f16 even = dk_h(__fmul_rn(lut[byte >> 4], a));   // element 2j: high nibble
+    const f16 odd = dk_h(__fmul_rn(lut[byte & 15u], a));
+    o[b] = dk_pack2(even, odd);
+  }
+  return o;
+}
 
 __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
-    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
+    const u32x4* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ scale2, const float* __restrict__ offset2,
     const float* __restrict__ code2, const float* __restrict__ nf4, u32x4* __restrict__ out,
-    int64_t n_chunks) {
+    int64_t n_quads) {
   __shared__ float lut[16];
+  // per wave: 64 lanes x 4 chunks of 16 bytes, one pad chunk per 64 against bank conflicts
+  __shared__ u32x4 stage[kDqThreads / 64][64 * 4 + 4];
   if (threadIdx.x < 16) lut[threadIdx.x] = nf4[threadIdx.x];
-  __syncthreads();
-  const int64_t base = (int64_t)blockIdx.x * kDqChunksPerBlock + threadIdx.x;
-  uint32_t word[kDqChunksPerThread];
-  float amax[kDqChunksPerThread];
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int64_t first = (int64_t)blockIdx.x * kDqQuadsPerBlock;
+  const int64_t sb = first >> 9;                    // 512 quads per second-level block
+  const float s2 = scale2[sb], o2 = offset2[sb];
+  const int64_t t = first + threadIdx.x;
+  const int64_t tc = t < n_quads ? t : n_quads - 1;   // clamped: its result is not stored
+  const u32x4 w = __builtin_nontemporal_load(packed + tc);
+  const float amax = dk_absmax(code2[qabs[tc >> 1]], s2, o2);
+  __syncthreads();   // lut
 #pragma unroll
-  for (int j = 0; j < kDqChunksPerThread; ++j) {
-    const int64_t c = base + j * kDqThreads;
-    if (c < n_chunks) {
-      word[j] = __builtin_nontemporal_load(packed + c);
-      const int64_t q = c >> 3;             // 8 chunks per first-level block
-      const int64_t sb = c >> 11;           // 2048 chunks per second-level block
-      amax[j] = dk_absmax(code2[qabs[q]], scale2[sb], offset2[sb]);
-    }
+  for (int j = 0; j < 4; ++j) {
+    const int idx = lane * 4 + j;
+    stage[wave][idx + (idx >> 6)] = dequant_word(w[j], amax, lut);
   }
+  __syncthreads();
+  const int64_t chunk0 = (first + wave * 64) * 4;     // first 8-weight chunk of this wave
+  const int64_t n_chunks = n_quads * 4;
 #pragma unroll
-  for (int j = 0; j < kDqChunksPerThread; ++j) {
-    const int64_t c = base + j * kDqThreads;
-    if (c < n_chunks) {
-      const uint32_t w = word[j];
-      const float a = amax[j];
-      u32x4 o;
-#pragma unroll
-      for (int b = 0; b < 4; ++b) {
-        const uint32_t byte = (w >> (8 * b)) & 0xffu;
-        const f16 even = dk_h(__fmul_rn(lut[byte >> 4], a));
-        const f16 odd = dk_h(__fmul_rn(lut[byte & 15u], a));
-        o[b] = dk_pack2(even, odd);
-      }
-      out[c] = o;
-    }
+  for (int j = 0; j < 4; ++j) {
+    const int idx = j * 64 + lane;
+    if (chunk0 + idx < n_chunks) out[chunk0 + idx] = stage[wave][idx + (idx >> 6)];
   }
 }
 
@@ -163,12 +168,12 @@ extern "C" int dk_nf4_dequant(const uint8_t* packed, const uint8_t* qabs, const 
   if (n_qblocks < 0) return DK_ERR_INVALID;
   if (n_qblocks == 0) return 0;
   if (!packed || !qabs || !scale2 || !offset2 || !code2 || !nf4 || !out_f16) return DK_ERR_INVALID;
-  if (!dk_aligned(packed, 4) || !dk_aligned(out_f16, 16)) return DK_ERR_ALIGN;
-  const int64_t n_chunks = n_qblocks * 8;
-  const int64_t grid = (n_chunks + kDqChunksPerBlock - 1) / kDqChunksPerBlock;
+  if (!dk_aligned(packed, 16) || !dk_aligned(out_f16, 16)) return DK_ERR_ALIGN;
+  const int64_t n_quads = n_qblocks * 2;
+  const int64_t grid = (n_quads + kDqQuadsPerBlock - 1) / kDqQuadsPerBlock;
   hipLaunchKernelGGL(nf4_dequant_kernel, dim3((unsigned)grid), dim3(kDqThreads), 0, stream,
-                     reinterpret_cast<const uint32_t*>(packed), qabs, scale2, offset2, code2, nf4,
-                     reinterpret_cast<u32x4*>(out_f16), n_chunks);
+                     reinterpret_cast<const u32x4*>(packed), qabs, scale2, offset2, code2, nf4,
+                     reinterpret_cast<u32x4*>(out_f16), n_quads);
   DK_CHECK_LAUNCH();
   return 0;
 }

@@ -11,11 +11,13 @@
 //     ahead (three register stages), look the NF4 values up in an LDS table one step ahead, and
 //     write the A tile and the dequantised W tile into the LDS buffer of the next step.
 // Each SIMD holds one consumer and one producer wave, so the producer's VALU dequant issues while
-// the consumer's MFMAs run.  Two LDS buffers; one barrier per step.  Both LDS tiles are
-// K-contiguous rows padded to 72 halves, so every MFMA operand is one ds_read_b128.  One
-// first-level block covers 64 consecutive weights of a stored row, so each 16-byte packed chunk
-// (NT) or 4-byte chunk (NN) has a single absmax.  The NN producer transposes a 4 x 8 block of
-// weights in registers before writing it, 16 lanes covering one LDS row segment.
+// the consumer's MFMAs run.  Two LDS buffers; one barrier per step.  The producers read W as
+// 16-byte chunks of packed nibbles (32 consecutive weights of a stored row, inside one
+// first-level block, so one absmax each) and write the dequantised chunk in its stored order:
+//   NT  the W tile is K-contiguous rows padded to 72 halves, like the A tile, so every MFMA
+//       operand is one ds_read_b128;
+//   NN  the W tile is N-contiguous rows (stored order) padded by 16 halves; the consumers build
+//       each K-contiguous operand from two ds_read_b64_tr_b16 (gfx950 transposing LDS reads).
 //
 // Epilogues (fused, per output element, rounding like the reference's separate ops):
 //   LINEAR      y = fp16(acc + bias); + LoRA: fp16(fp32(y) + s * fp32(fp16(z B^T)))     (forward)
@@ -26,13 +28,15 @@
 //               act = fp16(silu(fp16(g)) * fp16(u)), optional [g | u] store.
 //   SWIGLU_BWD  dact = fp16(acc), then the gated-SiLU backward in place on gu.
 // Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
-// of the same kernel sums them in split order and runs the epilogue.
+// (the REDUCE instance: consumer waves only, no LDS) sums them in split order and runs the
+// epilogue.
 #include "dk_common.h"
 
 namespace {
 
 constexpr int kBK = 64;
-constexpr int kStride = kBK + 8;  // halves per LDS row (144 bytes)
+constexpr int kStride = kBK + 8;  // halves per K-contiguous LDS row (144 bytes)
+constexpr int kPadT = 16;         // NN: halves of padding per N-contiguous LDS row of the W tile
 constexpr int kThreads = 512;     // 4 consumer + 4 producer waves
 constexpr int kRoleThreads = 256;
 
@@ -63,23 +67,26 @@ struct GemmParams {
   int tiles_n;
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
-  int reduce;           // split-K second launch: sum the partials, then the epilogue
 };
 
-template <int BM, int BN, bool TRANS, int EPI>
-__global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
+// REDUCE: the split-K second launch (consumer waves only): sum the partials, then the epilogue.
+// 128-row tiles are held to 128 VGPRs (4 waves per SIMD: two workgroups per CU).
+template <int BM, int BN, bool TRANS, int EPI, bool REDUCE>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 ? 4 : 2)))
+void w4_gemm_kernel(GemmParams p) {
   constexpr int WM = BM / 2, WN = BN / 2;
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int A_CHUNKS = BM * kBK / 8 / kRoleThreads;
   constexpr int B_UNITS = BN / 128 > 0 ? BN / 128 : 1;
-  constexpr int B_ACTIVE = BN * 2;  // NT: 16-byte chunks; NN: 4 x 8 units (both 2 * BN)
-  constexpr int NAM = TRANS ? 4 : 1;  // absmax values per B unit
+  constexpr int B_ACTIVE = BN * 2;  // 16-byte packed chunks (32 weights) per W tile
+  constexpr int B_LD = TRANS ? BN + kPadT : kStride;   // halves per LDS row of the W tile
+  constexpr int B_HALVES = TRANS ? kBK * B_LD : BN * kStride;
   constexpr int TILE = BM * BN;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
 
   __shared__ __attribute__((aligned(16))) f16 As[2][BM * kStride];
-  __shared__ __attribute__((aligned(16))) f16 Bs[2][BN * kStride];
+  __shared__ __attribute__((aligned(16))) f16 Bs[2][B_HALVES];
   // byte -> (NF4[high nibble], NF4[low nibble]): one 8-byte lookup dequantises two weights
   __shared__ f32x2 pair_lut[256];
   __shared__ float c2t[256];
@@ -96,9 +103,11 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
   int b = blockIdx.x;
   const int nb = gridDim.x;
   if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
-  const int grid_splits = p.reduce ? 1 : p.splits;
-  const int split = b % grid_splits;
-  const int tile = b / grid_splits;
+  // first launch: the splits of a tile are consecutive; REDUCE: one workgroup per 32 x 32 block
+  // index of the consumer sub-tiles, so the partial sums are read by TM * TN times more waves
+  const int per_tile = REDUCE ? TM * TN : p.splits;
+  const int split = REDUCE ? 0 : b % per_tile;
+  const int tile = b / per_tile;
   const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
   const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
   const int64_t M = p.M, N = p.N, K = p.K;
@@ -106,7 +115,7 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
   const int ks0 = (int)((int64_t)nk_all * split / p.splits);
   const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - ks0;
 
-  if (!p.reduce && producer) {
+  if (!REDUCE && producer) {
     // =========================== producer waves ===========================
     const int pt = tid - kRoleThreads;
     pair_lut[pt] = f32x2{p.nf4[pt >> 4], p.nf4[pt & 15]};
@@ -115,13 +124,13 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
     struct Stage {
       u32x4 a_reg[A_CHUNKS];
       uint32_t b_word[B_UNITS][4];
-      uint32_t b_code[B_UNITS][NAM];
-      float b_s2[B_UNITS][NAM];
-      float b_o2[B_UNITS][NAM];
+      uint32_t b_code[B_UNITS];
+      float b_s2[B_UNITS];
+      float b_o2[B_UNITS];
     };
     struct Looked {
       f32x2 v[B_UNITS][16];
-      float c2[B_UNITS][NAM];
+      float c2[B_UNITS];
     };
 
     // Every load is unconditional (rows past M read row M - 1, whose products land only in
@@ -139,7 +148,11 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
       }
 #pragma unroll
       for (int i = 0; i < B_UNITS; ++i) {
+        // one 16-byte chunk of packed nibbles = 32 consecutive weights of a stored row, inside
+        // one first-level block.  NT: row n of W, k half `half`; NN: row k of W, columns
+        // 32 * chunk of the tile.
         const int c = (pt + kRoleThreads * i) & (B_ACTIVE - 1);
+        int64_t elem;
         if (!TRANS) {
           const int row = c >> 1, half = c & 1;
           int64_t n = n0 + row;
@@ -147,26 +160,18 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
             const int64_t g = n >> 6, w = n & 63;
             n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
           }
-          const int64_t elem = n * K + k0 + half * 32;
-          const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
-#pragma unroll
-          for (int d = 0; d < 4; ++d) sg.b_word[i][d] = v[d];
-          const int64_t q = elem >> 6;
-          sg.b_code[i][0] = p.qabs[q];
-          sg.b_s2[i][0] = p.scale2[q >> 8];
-          sg.b_o2[i][0] = p.offset2[q >> 8];
+          elem = n * K + k0 + half * 32;
         } else {
-          const int kg = c & 15, ng = c >> 4;  // k fastest: 16 lanes fill one LDS row segment
-#pragma unroll
-          for (int r = 0; r < 4; ++r) {
-            const int64_t elem = (k0 + 4 * kg + r) * N + n0 + 8 * ng;
-            sg.b_word[i][r] = *reinterpret_cast<const uint32_t*>(p.packed + (elem >> 1));
-            const int64_t q = elem >> 6;
-            sg.b_code[i][r] = p.qabs[q];
-            sg.b_s2[i][r] = p.scale2[q >> 8];
-            sg.b_o2[i][r] = p.offset2[q >> 8];
-          }
+          constexpr int CPR = BN / 32;   // chunks per W-tile row
+          elem = (k0 + c / CPR) * N + n0 + 32 * (c % CPR);
         }
+        const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
+#pragma unroll
+        for (int d = 0; d < 4; ++d) sg.b_word[i][d] = v[d];
+        const int64_t q = elem >> 6;
+        sg.b_code[i] = p.qabs[q];
+        sg.b_s2[i] = p.scale2[q >> 8];
+        sg.b_o2[i] = p.offset2[q >> 8];
       }
     };
 
@@ -177,8 +182,7 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
         for (int d = 0; d < 4; ++d)
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) lk.v[i][4 * d + bb] = pair_lut[(sg.b_word[i][d] >> (8 * bb)) & 0xffu];
-#pragma unroll
-        for (int r = 0; r < NAM; ++r) lk.c2[i][r] = c2t[sg.b_code[i][r]];
+        lk.c2[i] = c2t[sg.b_code[i]];
       }
     };
 
@@ -195,40 +199,25 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
       for (int i = 0; i < B_UNITS; ++i) {
         const int c = pt + kRoleThreads * i;
         if (c < B_ACTIVE) {
+          // NT: W-tile row n holds k contiguous (the MFMA operand layout); NN: W-tile row k
+          // holds n contiguous (the consumers read it with transposing LDS loads)
+          f16* dst;
           if (!TRANS) {
-            const int row = c >> 1, half = c & 1;
-            const float amax = dk_absmax(lk.c2[i][0], sg.b_s2[i][0], sg.b_o2[i][0]);
-            f16* dst = bs + row * kStride + half * 32;
-#pragma unroll
-            for (int d = 0; d < 4; ++d) {
-              u32x4 o;
-#pragma unroll
-              for (int bb = 0; bb < 4; ++bb) {
-                const f32x2 nv = lk.v[i][4 * d + bb];
-                o[bb] = dk_pack2(dk_h(__fmul_rn(nv[0], amax)), dk_h(__fmul_rn(nv[1], amax)));
-              }
-              *reinterpret_cast<u32x4*>(dst + d * 8) = o;
-            }
+            dst = bs + (c >> 1) * B_LD + (c & 1) * 32;
           } else {
-            const int kg = c & 15, ng = c >> 4;
-            f16 v[4][8];
+            constexpr int CPR = BN / 32;
+            dst = bs + (c / CPR) * B_LD + 32 * (c % CPR);
+          }
+          const float amax = dk_absmax(lk.c2[i], sg.b_s2[i], sg.b_o2[i]);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) {
-              const float amax = dk_absmax(lk.c2[i][r], sg.b_s2[i][r], sg.b_o2[i][r]);
+          for (int d = 0; d < 4; ++d) {
+            u32x4 o;
 #pragma unroll
-              for (int bb = 0; bb < 4; ++bb) {
-                const f32x2 nv = lk.v[i][4 * r + bb];
-                v[r][2 * bb] = dk_h(__fmul_rn(nv[0], amax));
-                v[r][2 * bb + 1] = dk_h(__fmul_rn(nv[1], amax));
-              }
+            for (int bb = 0; bb < 4; ++bb) {
+              const f32x2 nv = lk.v[i][4 * d + bb];
+              o[bb] = dk_pack2(dk_h(__fmul_rn(nv[0], amax)), dk_h(__fmul_rn(nv[1], amax)));
             }
-#pragma unroll
-            for (int col = 0; col < 8; ++col) {
-              u32x2 o;
-              o[0] = dk_pack2(v[0][col], v[1][col]);
-              o[1] = dk_pack2(v[2][col], v[3][col]);
-              *reinterpret_cast<u32x2*>(bs + (8 * ng + col) * kStride + 4 * kg) = o;
-            }
+            *reinterpret_cast<u32x4*>(dst + d * 8) = o;
           }
         }
       }
@@ -275,21 +264,100 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
     }
     return;
   }
-  if (producer) return;  // split-K second launch: the consumers sum the partials
 
   // =========================== consumer waves ===========================
   const int wm = wave & 1, wn = wave >> 1;
   const int lrow = lane & 31;
   const int lk8 = 8 * (lane >> 5);
-  f32x16 acc[TM][TN];
-#pragma unroll
-  for (int i = 0; i < TM; ++i)
-#pragma unroll
-    for (int j = 0; j < TN; ++j)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  const int rsub = 4 * (lane >> 5);
+  // NN transposing reads: this lane's row and column offsets in the W tile (see compute)
+  const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
 
-  if (!p.reduce) {
+  // ---- epilogue of one 32 x 32 block (i, j) of this wave's sub-tile.  Lane layout of a 32 x 32
+  // fp32 MFMA result: column lane % 32, row 8 * (v / 4) + 4 * (lane / 32) + v % 4 for register v.
+  auto linear_block = [&](int i, int j, const f32x16& a) {
+    const bool has_lora = p.lz != nullptr;
+    f16* out16 = reinterpret_cast<f16*>(p.out);
+    float* out32 = reinterpret_cast<float*>(p.out);
+    const int64_t mrow0 = m0 + wm * WM + 32 * i;
+    const int64_t n = n0 + wn * WN + 32 * j + lrow;
+    f32x16 lo;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
+    if (has_lora) {
+      const int64_t zm = mrow0 + lrow;
+      for (int rc = 0; rc < p.rank; rc += 16) {
+        f16x8 zf, rf;
+        if (zm < M) {
+          zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk8);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
+        }
+        if (!TRANS) {
+          rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk8);
+        } else {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk8 + e) * N + n];
+        }
+        lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
+      }
+    }
+    const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) {
+      const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+      if (m >= M) continue;
+      const f16 y16 = dk_h(__fadd_rn(a[v], bias));
+      float r = (float)y16;
+      if (has_lora) {
+        float lf = (float)dk_h(lo[v]);
+        if (TRANS) {
+          if (p.mask) lf = p.mask[m * N + n] ? __fmul_rn(lf, p.keep_scale) : 0.0f;
+        } else {
+          lf = __fmul_rn(p.lora_scale, lf);
+        }
+        r = __fadd_rn(r, lf);
+      }
+      const int64_t o = m * p.ldo + n;
+      if (p.out_mode == DK_OUT_F16) {
+        out16[o] = dk_h(r);
+      } else if (p.out_mode == DK_OUT_F32) {
+        out32[o] = r;
+      } else {
+        out32[o] = __fadd_rn(out32[o], r);
+      }
+    }
+  };
+
+  if constexpr (REDUCE) {
+    // split-K, second launch: block (i, j) of every consumer sub-tile of the tile, the partials
+    // summed in split order (a fixed order, so the result is deterministic); the kernel boundary
+    // orders this launch after every partial store
+    static_assert(EPI == EPI_LINEAR, "split-K runs the linear epilogue only");
+    const int ij = b % per_tile;
+    const int i = ij / TN, j = ij % TN;
+    const float* all = p.part + (int64_t)tile * p.splits * TILE +
+                       ((wave * TM + i) * TN + j) * 16 * 64 + lane;
+    f32x16 a;
+#pragma unroll
+    for (int v = 0; v < 16; ++v) a[v] = all[v * 64];
+    for (int sp = 1; sp < p.splits; ++sp) {
+#pragma unroll
+      for (int v = 0; v < 16; ++v) a[v] += all[(int64_t)sp * TILE + v * 64];
+    }
+    linear_block(i, j, a);
+    return;
+  } else {
+    f32x16 acc[TM][TN];
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
     auto compute = [&](int buf) {
       const f16* as = As[buf];
       const f16* bs = Bs[buf];
@@ -300,8 +368,23 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
         for (int i = 0; i < TM; ++i)
           af[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk8);
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk8);
+        for (int j = 0; j < TN; ++j) {
+          if (!TRANS) {
+            bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk8);
+          } else {
+            // ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives element b of
+            // the 4-element rows addressed by lanes a, a + 4, a + 8, a + 12.  Lane 4j + a of
+            // group G addresses row k = 16 s + 8 (G / 2) + 4 h + j, columns from
+            // 16 (G % 2) + 4 a, so lane l gets W[k0 + 8 (l / 32) + 4 h + 0..3][l % 32]: two
+            // reads (h = 0, 1) give the 8 consecutive k of the MFMA operand.
+            const f16* base = bs + (16 * s + tr_k) * B_LD + wn * WN + 32 * j + tr_n;
+            const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(base)));
+            const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(base + 4 * B_LD)));
+            bf[j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          }
+        }
 #pragma unroll
         for (int i = 0; i < TM; ++i)
 #pragma unroll
@@ -330,135 +413,65 @@ __global__ __launch_bounds__(kThreads) void w4_gemm_kernel(GemmParams p) {
             mine[(((wave * TM + i) * TN + j) * 16 + v) * 64 + lane] = acc[i][j][v];
       return;
     }
-  } else {
-    // split-K, second launch: sum the partials in split order (a fixed order, so the result is
-    // deterministic); the kernel boundary orders it after every partial store
-    const float* all = p.part + (int64_t)tile * p.splits * TILE;
-#pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int idx = (((wave * TM + i) * TN + j) * 16 + v) * 64 + lane;
-          float s = 0.0f;
-          for (int sp = 0; sp < p.splits; ++sp) s += all[(int64_t)sp * TILE + idx];
-          acc[i][j][v] = s;
-        }
-  }
 
-  // ---- epilogue.  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
-  // 8 * (v / 4) + 4 * (lane / 32) + v % 4 for register v.
-  const int rsub = 4 * (lane >> 5);
-  if (EPI == EPI_LINEAR) {
-    const bool has_lora = p.lz != nullptr;
-    f16* out16 = reinterpret_cast<f16*>(p.out);
-    float* out32 = reinterpret_cast<float*>(p.out);
+    if constexpr (EPI == EPI_LINEAR) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t mrow0 = m0 + wm * WM + 32 * i;
+      for (int i = 0; i < TM; ++i)
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n0 + wn * WN + 32 * j + lrow;
-        f32x16 lo;
+        for (int j = 0; j < TN; ++j) linear_block(i, j, acc[i][j]);
+    } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+      f16* act = reinterpret_cast<f16*>(p.out);
+      const int64_t hcol = (n0 + wn * WN) / 2 + lrow;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
-        if (has_lora) {
-          const int64_t zm = mrow0 + lrow;
-          for (int rc = 0; rc < p.rank; rc += 16) {
-            f16x8 zf, rf;
-            if (zm < M) {
-              zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk8);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
-            }
-            if (!TRANS) {
-              rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk8);
-            } else {
-#pragma unroll
-              for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk8 + e) * N + n];
-            }
-            lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
-          }
-        }
-        const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+      for (int i = 0; i < TM; ++i) {
+        const int64_t mrow0 = m0 + wm * WM + 32 * i;
 #pragma unroll
         for (int v = 0; v < 16; ++v) {
           const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
           if (m >= M) continue;
-          const f16 y16 = dk_h(__fadd_rn(acc[i][j][v], bias));
-          float r = (float)y16;
-          if (has_lora) {
-            float lf = (float)dk_h(lo[v]);
-            if (TRANS) {
-              if (p.mask) lf = p.mask[m * N + n] ? __fmul_rn(lf, p.keep_scale) : 0.0f;
-            } else {
-              lf = __fmul_rn(p.lora_scale, lf);
-            }
-            r = __fadd_rn(r, lf);
-          }
-          const int64_t o = m * p.ldo + n;
-          if (p.out_mode == DK_OUT_F16) {
-            out16[o] = dk_h(r);
-          } else if (p.out_mode == DK_OUT_F32) {
-            out32[o] = r;
-          } else {
-            out32[o] = __fadd_rn(out32[o], r);
-          }
-        }
-      }
-    }
-  } else if (EPI == EPI_SWIGLU_FWD) {
-    f16* act = reinterpret_cast<f16*>(p.out);
-    const int64_t hcol = (n0 + wn * WN) / 2 + lrow;
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t mrow0 = m0 + wm * WM + 32 * i;
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
-        if (m >= M) continue;
-        const f16 g16 = dk_h(acc[i][0][v]);
-        const f16 u16 = dk_h(acc[i][1][v]);
-        float sig, silu;
-        dk_silu_parts((float)g16, &sig, &silu);
-        act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
-        if (p.gu) {
-          p.gu[m * 2 * p.inter + hcol] = g16;
-          p.gu[m * 2 * p.inter + p.inter + hcol] = u16;
-        }
-      }
-    }
-  } else {  // EPI_SWIGLU_BWD: N == inter
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t mrow0 = m0 + wm * WM + 32 * i;
-#pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const int64_t n = n0 + wn * WN + 32 * j + lrow;
-#pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
-          if (m >= M) continue;
-          const float da = (float)dk_h(acc[i][j][v]);
-          f16* gp = p.gu + m * 2 * p.inter + n;
-          const float g = (float)gp[0];
-          const float u = (float)gp[p.inter];
+          const f16 g16 = dk_h(acc[i][0][v]);
+          const f16 u16 = dk_h(acc[i][1][v]);
           float sig, silu;
-          dk_silu_parts(g, &sig, &silu);
-          gp[p.inter] = dk_h(da * silu);
-          gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
+          dk_silu_parts((float)g16, &sig, &silu);
+          act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
+          if (p.gu) {
+            p.gu[m * 2 * p.inter + hcol] = g16;
+            p.gu[m * 2 * p.inter + p.inter + hcol] = u16;
+          }
+        }
+      }
+    } else {  // EPI_SWIGLU_BWD: N == inter
+#pragma unroll
+      for (int i = 0; i < TM; ++i) {
+        const int64_t mrow0 = m0 + wm * WM + 32 * i;
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          const int64_t n = n0 + wn * WN + 32 * j + lrow;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) {
+            const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+            if (m >= M) continue;
+            const float da = (float)dk_h(acc[i][j][v]);
+            f16* gp = p.gu + m * 2 * p.inter + n;
+            const float g = (float)gp[0];
+            const float u = (float)gp[p.inter];
+            float sig, silu;
+            dk_silu_parts(g, &sig, &silu);
+            gp[p.inter] = dk_h(da * silu);
+            gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
+          }
         }
       }
     }
   }
 }
 
-// Launch plan: tile shape and split-K factor.  256 CUs; a 256 x 128 tile's 114 KB of LDS leaves
-// one workgroup per CU, the 128-row tiles two.  Shapes with too few tiles to fill the chip split
-// K when it is long (at least 16 steps per split, so the partial-tile traffic stays small next
-// to the MFMA work) and otherwise use narrower tiles.
+// Launch plan: tile shape and split-K factor.  256 CUs.  A 128-row tile's workgroup needs
+// 76.8 KB of LDS (60 KB at 64 columns) and at most 128 VGPRs, so two share a CU (512 slots); a
+// 256 x 128 tile needs a CU of its own and is used only when there are tiles for four rounds of
+// it.  Shapes with fewer tiles than slots split K (at least 8 steps per split) so that about
+// 768 workgroups run: the fp32 partial tiles cost one extra pass over the output in the second
+// launch, so short K (under 64 steps) prefers narrower tiles and splits only below 256 tiles.
 struct Plan {
   int bm, bn, splits;
   int64_t tiles;
@@ -467,18 +480,17 @@ struct Plan {
 Plan plan_for(int64_t M, int64_t N, int64_t K, int epi) {
   const int64_t nk = K / kBK;
   const int64_t mt256 = (M + 255) / 256, mt128 = (M + 127) / 128;
-  if (N % 128 == 0 && mt256 * (N / 128) >= 256) return {256, 128, 1, mt256 * (N / 128)};
+  if (N % 128 == 0 && mt256 * (N / 128) >= 1024) return {256, 128, 1, mt256 * (N / 128)};
   Plan pl{128, 128, 1, mt128 * (N / 128)};
   if (N % 128 != 0) pl = {128, 64, 1, mt128 * (N / 64)};
-  if (epi != EPI_LINEAR || pl.tiles >= 256) return pl;
-  if (nk >= 64) {
-    int64_t s = (512 + pl.tiles - 1) / pl.tiles;
-    if (s > nk / 16) s = nk / 16;
+  if (epi != EPI_LINEAR || pl.tiles >= 512) return pl;
+  if (pl.bn == 128 && nk < 64) pl = {128, 64, 1, mt128 * (N / 64)};
+  if ((pl.tiles < 256 && nk >= 16) || (pl.tiles < 512 && nk >= 64)) {
+    int64_t s = (768 + pl.tiles - 1) / pl.tiles;
+    if (s > nk / 8) s = nk / 8;
     if (s > 8) s = 8;
     if (s >= 2) pl.splits = (int)s;
-    return pl;
   }
-  if (pl.bn == 128) pl = {128, 64, 1, mt128 * (N / 64)};
   return pl;
 }
 
@@ -492,16 +504,18 @@ int launch(GemmParams p, int splits, hipStream_t stream) {
   p.tiles_n = (int)(p.N / BN);
   const int64_t tiles = ((p.M + BM - 1) / BM) * (int64_t)p.tiles_n;
   p.splits = splits;
-  p.reduce = 0;
-  if (tiles <= 0 || tiles * splits > 0x7fffffff) return DK_ERR_INVALID;
-  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)(tiles * splits)),
+  constexpr int blocks = (BM / 64) * (BN / 64);   // 32 x 32 blocks per consumer sub-tile
+  if (tiles <= 0 || tiles * (splits > blocks ? splits : blocks) > 0x7fffffff) return DK_ERR_INVALID;
+  if (splits > 1 && EPI != EPI_LINEAR) return DK_ERR_INVALID;
+  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, false>), dim3((unsigned)(tiles * splits)),
                      dim3(kThreads), 0, stream, p);
   DK_CHECK_LAUNCH();
-  if (splits > 1) {
-    p.reduce = 1;
-    hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI>), dim3((unsigned)tiles),
-                       dim3(kThreads), 0, stream, p);
-    DK_CHECK_LAUNCH();
+  if constexpr (EPI == EPI_LINEAR) {
+    if (splits > 1) {
+      hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, true>),
+                         dim3((unsigned)(tiles * blocks)), dim3(kRoleThreads), 0, stream, p);
+      DK_CHECK_LAUNCH();
+    }
   }
   return 0;
 }

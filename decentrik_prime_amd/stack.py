@@ -94,6 +94,7 @@ class NF4LinearStack:
         self.dx_o = torch.empty(m, D, dtype=f16, device=dev)
         self.dx_mlp = torch.empty(m, D, dtype=f16, device=dev)
         self.grads = [None] * n_layers
+        self.probe = None   # (operator name, [(start event, end event), ...]) or None
 
     @property
     def flops_per_step(self):
@@ -101,28 +102,50 @@ class NF4LinearStack:
 
     def forward_layer(self, i):
         L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
-        lora_down(x, lo["Aq"], lo["mq"], self.keep_scale, out=z["q"])
-        lora_down(x, lo["Av"], lo["mv"], self.keep_scale, out=z["v"])
-        linear_forward(x, L["q"], None, z["q"], lo["Bq"], self.s, out=o["q"])
-        linear_forward(x, L["k"], out=o["k"])
-        linear_forward(x, L["v"], None, z["v"], lo["Bv"], self.s, out=o["v"])
-        linear_forward(x, L["o"], out=o["o"])
-        gateup_swiglu_forward(x, L["gu"], act=self.act, gu=self.gu[i])
-        linear_forward(self.act, L["d"], out=o["y"])
+        op = self._op
+        op("lora_down", lora_down, x, lo["Aq"], lo["mq"], self.keep_scale, out=z["q"])
+        op("lora_down", lora_down, x, lo["Av"], lo["mv"], self.keep_scale, out=z["v"])
+        op("w4_linear_fwd q+lora", linear_forward, x, L["q"], None, z["q"], lo["Bq"], self.s,
+           out=o["q"])
+        op("w4_linear_fwd k", linear_forward, x, L["k"], out=o["k"])
+        op("w4_linear_fwd v+lora", linear_forward, x, L["v"], None, z["v"], lo["Bv"], self.s,
+           out=o["v"])
+        op("w4_linear_fwd o", linear_forward, x, L["o"], out=o["o"])
+        op("w4_gateup_swiglu_fwd", gateup_swiglu_forward, x, L["gu"], act=self.act, gu=self.gu[i])
+        op("w4_linear_fwd down", linear_forward, self.act, L["d"], out=o["y"])
 
     def backward_layer(self, i):
         L, lo, z, x, dy = self.layers[i], self.lora[i], self.z[i], self.x, self.dy
         gu = self.gu[i]
-        down_swiglu_backward(dy["d"], L["d"], gu)
-        linear_backward_dx(gu, L["gu"], out=self.dx_mlp)
-        linear_backward_dx(dy["o"], L["o"], out=self.dx_o)
-        daq, dbq, dzq = lora_grads(dy["q"], z["q"], x, lo["Bq"], self.s, lo["mq"], self.keep_scale)
-        dav, dbv, dzv = lora_grads(dy["v"], z["v"], x, lo["Bv"], self.s, lo["mv"], self.keep_scale)
-        linear_backward_dx(dy["q"], L["q"], dzq, lo["Aq"], lo["mq"], self.keep_scale, out=self.dx_qkv)
-        linear_backward_dx(dy["k"], L["k"], out=self.dx_qkv, accumulate=True)
-        linear_backward_dx(dy["v"], L["v"], dzv, lo["Av"], lo["mv"], self.keep_scale,
-                           out=self.dx_qkv, accumulate=True)
+        op = self._op
+        op("w4_down_swiglu_bwd", down_swiglu_backward, dy["d"], L["d"], gu)
+        op("w4_linear_bwd_dx gate|up", linear_backward_dx, gu, L["gu"], out=self.dx_mlp)
+        op("w4_linear_bwd_dx o", linear_backward_dx, dy["o"], L["o"], out=self.dx_o)
+        daq, dbq, dzq = op("lora_grads q", lora_grads, dy["q"], z["q"], x, lo["Bq"], self.s,
+                           lo["mq"], self.keep_scale)
+        dav, dbv, dzv = op("lora_grads v", lora_grads, dy["v"], z["v"], x, lo["Bv"], self.s,
+                           lo["mv"], self.keep_scale)
+        op("w4_linear_bwd_dx q+lora", linear_backward_dx, dy["q"], L["q"], dzq, lo["Aq"], lo["mq"],
+           self.keep_scale, out=self.dx_qkv)
+        op("w4_linear_bwd_dx k", linear_backward_dx, dy["k"], L["k"], out=self.dx_qkv,
+           accumulate=True)
+        op("w4_linear_bwd_dx v+lora", linear_backward_dx, dy["v"], L["v"], dzv, lo["Av"], lo["mv"],
+           self.keep_scale, out=self.dx_qkv, accumulate=True)
         self.grads[i] = (daq, dbq, dav, dbv)
+
+    def _op(self, name, fn, *args, **kwargs):
+        """Run one operator; when ``self.probe`` is ``(name, events)`` for this operator, bracket
+        it with a pair of timing events on the current stream (the stream it launches on)."""
+        probe = self.probe
+        if probe is None or probe[0] != name:
+            return fn(*args, **kwargs)
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        result = fn(*args, **kwargs)
+        e1.record()
+        probe[1].append((e0, e1))
+        return result
 
     def step(self):
         for i in range(self.n_layers):

@@ -46,7 +46,7 @@ const char* dk_error_string(int code);
 /* ------------------------------------------------------------------------------------------
  * NF4 dequant.  Replaces k_nf4.dequant_tensors / nf4_layer_dequant_kernel
  * (solution/k_nf4.py:40-57, 176-181): out[e] = fp16(NF4[nib(e)] * absmax[e / 64]) for every
- * element of n_qblocks * 64, bit-exact.  packed must be 4-byte aligned, out 16-byte aligned. */
+ * element of n_qblocks * 64, bit-exact.  packed and out must be 16-byte aligned. */
 int dk_nf4_dequant(const uint8_t* packed, const uint8_t* qabs, const float* scale2,
                    const float* offset2, const float* code2, const float* nf4, void* out_f16,
                    int64_t n_qblocks, hipStream_t stream);

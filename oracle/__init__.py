@@ -15,5 +15,4 @@ Modules:
           solution/k_rope.py:39-43, 54-58).
   mlp     gated SiLU forward/backward (solution/k_mlp.py:20-47) and the example SwiGLU
           (solution/swiglu.py:15-37).
-  configs seeded generators for the five benchmark configurations.
 """

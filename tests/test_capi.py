@@ -34,8 +34,11 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 100, 8, ctypes.byref(w), None, None, None, 0,
                                 2.0, ctypes.c_void_p(16), 100, None, 0, None) == _lib.DK_ERR_INVALID
     assert lib.dk_w4_linear_workspace(2048, ctypes.byref(w), 0) == 0
-    # misaligned packed pointer (needs 4 bytes) and fp16 output (needs 16 bytes)
+    # misaligned packed pointer and fp16 output (both need 16 bytes)
     assert lib.dk_nf4_dequant(ctypes.c_void_p(2), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
+                              ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_nf4_dequant(ctypes.c_void_p(4), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
     assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 32 * 1536 * 16 * 4

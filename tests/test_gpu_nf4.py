@@ -35,8 +35,10 @@ def test_dequant_golden_blocks(torch_dev):
     log("dequant golden nf4_blocks")
     g = dict(np.load(os.path.join(GOLD, "nf4_blocks.npz")))
     assert np.array_equal(_dequant(torch_dev, g), g["out"])
-    # prefix: two second-level blocks (partial last workgroup)
-    assert np.array_equal(_dequant(torch_dev, g, 512), g["out"][:512 * 64])
+    # prefixes: two second-level blocks, and counts that end inside a workgroup (128 first-level
+    # blocks each) or a second-level block
+    for nq in (512, 1, 3, 129, 700):
+        assert np.array_equal(_dequant(torch_dev, g, nq), g["out"][:nq * 64]), nq
 
 
 def test_dequant_golden_vproj(torch_dev):
