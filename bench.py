@@ -50,34 +50,36 @@ def kernel_table(torch, st, reps, only=None):
     `only`: a set of operator names to restrict the table to."""
     from decentrik_prime_amd import w4linear as W
     m, D, I, KV, r = st.m, 1536, 8960, 256, 16
+    QKV = D + 2 * KV
     L, lo, z, x, dy, o = st.layers[0], st.lora[0], st.z[0], st.x, st.dy, st.out
     ks, s = st.keep_scale, st.s
     gu = st.gu[0]
     gu_save = gu.clone()
+    dzq = (torch.randn(m, r, device=x.device) * 1e-2).half()
+    dzv = (torch.randn(m, r, device=x.device) * 1e-2).half()
     g = lambda mm, n, k: 2.0 * mm * n * k  # noqa: E731
     rows = [
         # name, fn, flops, bytes, launches per step (per layer)
         ("w4_gateup_swiglu_fwd", lambda: W.gateup_swiglu_forward(x, L["gu"], act=st.act, gu=gu),
          g(m, 2 * I, D), None, 1),
         ("w4_linear_fwd down", lambda: W.linear_forward(st.act, L["d"], out=o["y"]), g(m, D, I), None, 1),
-        ("w4_linear_fwd q+lora", lambda: W.linear_forward(x, L["q"], None, z["q"], lo["Bq"], s, out=o["q"]),
-         g(m, D, D) + g(m, D, r), None, 1),
+        ("w4_linear_fwd qkv+lora", lambda: W.linear_forward_lora(x, L["qkv"], lo["bias"], st.qkv_terms(0),
+                                                                 out=o["qkv"]),
+         g(m, QKV, D) + g(m, D, r) + g(m, KV, r), None, 1),
         ("w4_linear_fwd o", lambda: W.linear_forward(x, L["o"], out=o["o"]), g(m, D, D), None, 1),
-        ("w4_linear_fwd k", lambda: W.linear_forward(x, L["k"], out=o["k"]), g(m, KV, D), None, 1),
-        ("w4_linear_fwd v+lora", lambda: W.linear_forward(x, L["v"], None, z["v"], lo["Bv"], s, out=o["v"]),
-         g(m, KV, D) + g(m, KV, r), None, 1),
         ("w4_down_swiglu_bwd", lambda: W.down_swiglu_backward(dy["d"], L["d"], gu), g(m, I, D), None, 1),
         ("w4_linear_bwd_dx gate|up", lambda: W.linear_backward_dx(gu, L["gu"], out=st.dx_mlp),
          g(m, D, 2 * I), None, 1),
         ("w4_linear_bwd_dx o", lambda: W.linear_backward_dx(dy["o"], L["o"], out=st.dx_o), g(m, D, D), None, 1),
-        ("w4_linear_bwd_dx q+lora", lambda: W.linear_backward_dx(dy["q"], L["q"], z["q"], lo["Aq"], lo["mq"], ks,
-                                                                  out=st.dx_qkv), g(m, D, D) + g(m, D, r), None, 1),
-        ("w4_linear_bwd_dx k", lambda: W.linear_backward_dx(dy["k"], L["k"], out=st.dx_qkv, accumulate=True),
-         g(m, D, KV), None, 1),
+        ("w4_linear_bwd_dx qkv+lora", lambda: W.linear_backward_dx_lora(
+            dy["qkv"], L["qkv"], [(dzq, lo["Aq"], lo["mq"], ks), (dzv, lo["Av"], lo["mv"], ks)],
+            out=st.dx_qkv), g(m, D, QKV) + 2 * g(m, D, r), None, 1),
         ("lora_down", lambda: W.lora_down(x, lo["Aq"], lo["mq"], ks, out=z["q"]), g(m, r, D),
          m * D * 3 + r * D * 2 + m * r * 2, 2),
-        ("lora_grads q", lambda: W.lora_grads(dy["q"], z["q"], x, lo["Bq"], s, lo["mq"], ks),
+        ("lora_grads q", lambda: W.lora_grads(dy["qkv"][:, :D], z["q"], x, lo["Bq"], s, lo["mq"], ks),
          g(m, r, D) * 3, None, 1),
+        ("lora_grads v", lambda: W.lora_grads(dy["qkv"][:, D + KV:], z["v"], x, lo["Bv"], s, lo["mv"], ks),
+         g(m, r, KV) * 2 + g(m, r, D), None, 1),
     ]
     out = []
     for name, fn, flops, nbytes, per_layer in rows:

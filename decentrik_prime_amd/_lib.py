@@ -30,6 +30,15 @@ class NF4WeightC(ctypes.Structure):
 
 _W = ctypes.POINTER(NF4WeightC)
 
+
+class LoraTermC(ctypes.Structure):
+    """struct dk_lora_term."""
+    _fields_ = [("left", _c_p), ("right", _c_p), ("mask", _c_p), ("col_begin", _i64),
+                ("col_end", _i64), ("scale", _f32)]
+
+
+_T = ctypes.POINTER(LoraTermC)
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dk_error_string": (ctypes.c_char_p, [_int]),
@@ -44,10 +53,14 @@ SIGNATURES = {
                                 _c_p, _i64, _c_p]),
     "dk_w4_linear_bwd_dx": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _i64, _c_p, _f32, _c_p,
                                    _i64, _int, _c_p, _i64, _c_p]),
+    "dk_w4_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _W, _c_p, _T, _int, _i64, _c_p, _i64,
+                                     _c_p, _i64, _c_p]),
+    "dk_w4_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _W, _T, _int, _i64, _c_p, _i64, _int,
+                                        _c_p, _i64, _c_p]),
     "dk_w4_linear_workspace": (_i64, [_i64, _W, _int]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
-    "dk_lora_grads": (_int, [_c_p, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64, _i64,
-                             _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
+    "dk_lora_grads": (_int, [_c_p, _i64, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64,
+                             _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_w4_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _c_p]),
     "dk_w4_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p]),
 }

@@ -41,6 +41,7 @@ __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, fl
 // the result register v of lane l is row 4 * (l / 16) + v, column l % 16.
 template <int R, int MODE>
 __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restrict__ in,
+                                                             int64_t ld,
                                                              const uint8_t* __restrict__ mask,
                                                              float ks, const f16* __restrict__ wt,
                                                              float scale, f16* __restrict__ out,
@@ -60,7 +61,7 @@ __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restri
   if (MODE == 0) {
     for (int64_t s = w; s < cols / 32; s += kWaves) {
       const int64_t k = s * 32 + lk;
-      f16x8 a = *reinterpret_cast<const f16x8*>(in + m * cols + k);
+      f16x8 a = *reinterpret_cast<const f16x8*>(in + m * ld + k);
       if (mask) a = dropout8(a, mask + m * cols + k, ks);
 #pragma unroll
       for (int b = 0; b < RB; ++b) {
@@ -81,7 +82,7 @@ __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restri
       }
       __syncthreads();
       for (int s = w; s < kc / 32; s += kWaves) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(in + m * cols + c0 + s * 32 + lk);
+        const f16x8 a = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
 #pragma unroll
         for (int b = 0; b < RB; ++b) {
           const f16x8 bw = *reinterpret_cast<const f16x8*>(wT + (16 * b + lr) * (KC + 8) + s * 32 + lk);
@@ -110,7 +111,7 @@ __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restri
 // the first use, and are summed in a fixed order through LDS.  DROP: P is the dropout of x (mask
 // may be null).
 template <int R, bool DROP>
-__global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restrict__ P,
+__global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restrict__ P, int64_t ld,
                                                              const uint8_t* __restrict__ mask,
                                                              float ks, const f16* __restrict__ Q,
                                                              float* __restrict__ part,
@@ -136,7 +137,7 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restri
     const int rr = w * RW + u;
     const int rc = rr < nrows ? rr : nrows - 1;
     const int64_t m = r0 + rc;
-    const f16x2 pv = *reinterpret_cast<const f16x2*>(P + m * cols + nc);
+    const f16x2 pv = *reinterpret_cast<const f16x2*>(P + m * ld + nc);
     float a = (float)pv[0], b = (float)pv[1];
     if (DROP && mask) {
       const uint32_t mk = *reinterpret_cast<const uint16_t*>(mask + m * cols + nc);
@@ -208,14 +209,14 @@ __global__ __launch_bounds__(kThreads) void lora_finalize_kernel(const float* __
 }
 
 template <int MODE>
-int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, const uint8_t* mask, float ks,
-                  const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
+int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
+                  float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
   const dim3 grid((unsigned)((rows + kRowTile - 1) / kRowTile));
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE>), grid, dim3(kThreads), 0, stream, in, mask, ks, wt, scale, out, rows, cols); break;
-    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE>), grid, dim3(kThreads), 0, stream, in, mask, ks, wt, scale, out, rows, cols); break;
-    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE>), grid, dim3(kThreads), 0, stream, in, mask, ks, wt, scale, out, rows, cols); break;
-    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE>), grid, dim3(kThreads), 0, stream, in, mask, ks, wt, scale, out, rows, cols); break;
+    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
     default: return DK_ERR_INVALID;
   }
   DK_CHECK_LAUNCH();
@@ -223,15 +224,15 @@ int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, const uint8_t* m
 }
 
 template <bool DROP>
-int cols_dispatch(int64_t R, hipStream_t stream, const f16* P, const uint8_t* mask, float ks,
-                  const f16* Q, float* part, int64_t rows, int64_t cols) {
+int cols_dispatch(int64_t R, hipStream_t stream, const f16* P, int64_t ld, const uint8_t* mask,
+                  float ks, const f16* Q, float* part, int64_t rows, int64_t cols) {
   const dim3 grid((unsigned)((cols + kColsPerBlock - 1) / kColsPerBlock),
                   (unsigned)((rows + kChunkRows - 1) / kChunkRows));
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_cols_kernel<16, DROP>), grid, dim3(kThreads), 0, stream, P, mask, ks, Q, part, rows, cols); break;
-    case 32: hipLaunchKernelGGL((lora_cols_kernel<32, DROP>), grid, dim3(kThreads), 0, stream, P, mask, ks, Q, part, rows, cols); break;
-    case 48: hipLaunchKernelGGL((lora_cols_kernel<48, DROP>), grid, dim3(kThreads), 0, stream, P, mask, ks, Q, part, rows, cols); break;
-    case 64: hipLaunchKernelGGL((lora_cols_kernel<64, DROP>), grid, dim3(kThreads), 0, stream, P, mask, ks, Q, part, rows, cols); break;
+    case 16: hipLaunchKernelGGL((lora_cols_kernel<16, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
+    case 32: hipLaunchKernelGGL((lora_cols_kernel<32, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
+    case 48: hipLaunchKernelGGL((lora_cols_kernel<48, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
+    case 64: hipLaunchKernelGGL((lora_cols_kernel<64, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
     default: return DK_ERR_INVALID;
   }
   DK_CHECK_LAUNCH();
@@ -247,7 +248,7 @@ extern "C" int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale
   if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !a || !z) return DK_ERR_INVALID;
   if (!dk_aligned(x, 16) || !dk_aligned(a, 16) || (mask && !dk_aligned(mask, 8))) return DK_ERR_ALIGN;
   if (m == 0) return 0;
-  return rows_dispatch<0>(rank, stream, (const f16*)x, mask, mask ? keep_scale : 1.0f,
+  return rows_dispatch<0>(rank, stream, (const f16*)x, k, mask, mask ? keep_scale : 1.0f,
                           (const f16*)a, 1.0f, (f16*)z, m, k);
 }
 
@@ -258,13 +259,14 @@ extern "C" int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, 
   return chunks * cols * rank * (int64_t)sizeof(float);
 }
 
-extern "C" int dk_lora_grads(const void* dy, const void* z, const void* x, const uint8_t* mask,
+extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x,
+                             const uint8_t* mask,
                              float keep_scale, const void* lora_b, float lora_scale, int64_t m,
                              int64_t n_out, int64_t k, int64_t rank, float* da, float* db,
                              void* dz, void* ws, int64_t ws_bytes, hipStream_t stream) {
   if (m < 0 || n_out <= 0 || k <= 0 || n_out % 32 || k % 32 || !rank_ok(rank)) return DK_ERR_INVALID;
-  if (!dy || !z || !x || !lora_b || !da || !db || !dz) return DK_ERR_INVALID;
-  if (!dk_aligned(dy, 16) || !dk_aligned(x, 16) || !dk_aligned(lora_b, 16) ||
+  if (!dy || !z || !x || !lora_b || !da || !db || !dz || lddy < n_out) return DK_ERR_INVALID;
+  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(x, 16) || !dk_aligned(lora_b, 16) ||
       (mask && !dk_aligned(mask, 8)))
     return DK_ERR_ALIGN;
   if (m == 0) return 0;
@@ -273,17 +275,18 @@ extern "C" int dk_lora_grads(const void* dy, const void* z, const void* x, const
   const int64_t chunks = (m + kChunkRows - 1) / kChunkRows;
   float* part = (float*)ws;
   // dz = fp16(fp16(dY B) * s)
-  int e = rows_dispatch<1>(rank, stream, (const f16*)dy, nullptr, 1.0f, (const f16*)lora_b,
+  int e = rows_dispatch<1>(rank, stream, (const f16*)dy, lddy, nullptr, 1.0f, (const f16*)lora_b,
                            lora_scale, (f16*)dz, m, n_out);
   if (e) return e;
   // dB = fp32(fp16(dY^T z)) * s
-  e = cols_dispatch<false>(rank, stream, (const f16*)dy, nullptr, 1.0f, (const f16*)z, part, m, n_out);
+  e = cols_dispatch<false>(rank, stream, (const f16*)dy, lddy, nullptr, 1.0f, (const f16*)z, part, m,
+                           n_out);
   if (e) return e;
   hipLaunchKernelGGL(lora_finalize_kernel<false>, dim3((unsigned)((n_out * rank + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, stream, part, chunks, n_out, rank, lora_scale, db);
   DK_CHECK_LAUNCH();
   // dA = fp32(fp16(dz^T Xd))
-  e = cols_dispatch<true>(rank, stream, (const f16*)x, mask, ks, (const f16*)dz, part, m, k);
+  e = cols_dispatch<true>(rank, stream, (const f16*)x, k, mask, ks, (const f16*)dz, part, m, k);
   if (e) return e;
   hipLaunchKernelGGL(lora_finalize_kernel<true>, dim3((unsigned)((k * rank + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, stream, part, chunks, k, rank, 1.0f, da);

@@ -42,6 +42,17 @@ constexpr int kRoleThreads = 256;
 
 enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
 
+// One LoRA term of the LINEAR epilogue.  Forward: adds s * fp32(fp16(z B^T)) to output columns
+// [n_begin, n_end) (B holds the rows of those columns).  Backward: adds
+// (mask ? fp32(fp16(dz A)) * keep_scale : 0) to every column.
+struct LoraTerm {
+  const f16* z;         // [M][rank]: z (forward) or dz (backward)
+  const f16* r;         // forward: B [n_end - n_begin][rank]; backward: A [rank][N]
+  const uint8_t* mask;  // backward keep-mask [M][N] or null (no dropout, no scale)
+  int64_t n_begin, n_end;
+  float scale;          // forward: s; backward: keep_scale
+};
+
 struct GemmParams {
   const f16* a;
   int64_t lda;
@@ -54,12 +65,9 @@ struct GemmParams {
   const float* nf4;
   int64_t inter;        // SwiGLU: gate/up width I
   const f16* bias;      // [N] or null
-  const f16* lz;        // LoRA left factor [M][rank] (z forward, dz backward) or null
-  const f16* lr;        // LoRA right factor: forward B [N][rank]; backward A [rank][N]
+  LoraTerm lora[2];     // rank-r LoRA terms added in the LINEAR epilogue, in order
+  int n_lora;
   int64_t rank;
-  float lora_scale;
-  const uint8_t* mask;  // backward dropout keep-mask [M][N] or null
-  float keep_scale;
   void* out;
   int64_t ldo;
   int out_mode;
@@ -276,57 +284,86 @@ void w4_gemm_kernel(GemmParams p) {
 
   // ---- epilogue of one 32 x 32 block (i, j) of this wave's sub-tile.  Lane layout of a 32 x 32
   // fp32 MFMA result: column lane % 32, row 8 * (v / 4) + 4 * (lane / 32) + v % 4 for register v.
+  // this consumer wave's 2 KB of epilogue scratch in LDS: after the last K-step the A tile
+  // buffers are free (every producer store and consumer read is behind the final barrier)
+  uint8_t* escr;
+  if constexpr (REDUCE) {
+    __shared__ __attribute__((aligned(16))) uint8_t reduce_scr[4][2048];
+    escr = reduce_scr[wave];
+  } else {
+    escr = reinterpret_cast<uint8_t*>(As[0]) + wave * 2048;
+  }
+
   auto linear_block = [&](int i, int j, const f32x16& a) {
-    const bool has_lora = p.lz != nullptr;
     f16* out16 = reinterpret_cast<f16*>(p.out);
     float* out32 = reinterpret_cast<float*>(p.out);
     const int64_t mrow0 = m0 + wm * WM + 32 * i;
-    const int64_t n = n0 + wn * WN + 32 * j + lrow;
-    f32x16 lo;
+    const int64_t nb = n0 + wn * WN + 32 * j;  // first column of the block
+    const int64_t n = nb + lrow;
+    const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+    f32x16 res;
 #pragma unroll
-    for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
-    if (has_lora) {
+    for (int v = 0; v < 16; ++v) res[v] = (float)dk_h(__fadd_rn(a[v], bias));
+#pragma unroll
+    for (int t = 0; t < 2; ++t) {
+      if (t >= p.n_lora) break;
+      const LoraTerm& L = p.lora[t];
+      if (!TRANS && (nb < L.n_begin || nb >= L.n_end)) continue;
+      f32x16 lo;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
       const int64_t zm = mrow0 + lrow;
       for (int rc = 0; rc < p.rank; rc += 16) {
         f16x8 zf, rf;
         if (zm < M) {
-          zf = *reinterpret_cast<const f16x8*>(p.lz + zm * p.rank + rc + lk8);
+          zf = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
         } else {
 #pragma unroll
           for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
         }
         if (!TRANS) {
-          rf = *reinterpret_cast<const f16x8*>(p.lr + n * p.rank + rc + lk8);
+          rf = *reinterpret_cast<const f16x8*>(L.r + (n - L.n_begin) * p.rank + rc + lk8);
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) rf[e] = p.lr[(int64_t)(rc + lk8 + e) * N + n];
+          for (int e = 0; e < 8; ++e) rf[e] = L.r[(int64_t)(rc + lk8 + e) * N + n];
         }
         lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
       }
+      if (TRANS && L.mask) {
+        // the block's 32 x 32 keep-mask bytes: one coalesced 16-byte load per lane, staged in
+        // this wave's LDS scratch (rows of 48 bytes), then read per element
+        const int64_t mr = mrow0 + (lane >> 1);
+        u32x4 mw = u32x4{0u, 0u, 0u, 0u};
+        if (mr < M) mw = *reinterpret_cast<const u32x4*>(L.mask + mr * N + nb + 16 * (lane & 1));
+        __builtin_amdgcn_wave_barrier();
+        *reinterpret_cast<u32x4*>(escr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw;
+        __builtin_amdgcn_wave_barrier();
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int mloc = 8 * (v >> 2) + rsub + (v & 3);
+          const float lf = (float)dk_h(lo[v]);
+          res[v] = __fadd_rn(res[v], escr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
+        }
+        __builtin_amdgcn_wave_barrier();
+      } else {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const float lf = (float)dk_h(lo[v]);
+          res[v] = __fadd_rn(res[v], TRANS ? lf : __fmul_rn(L.scale, lf));
+        }
+      }
     }
-    const float bias = p.bias ? (float)p.bias[n] : 0.0f;
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
       const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
       if (m >= M) continue;
-      const f16 y16 = dk_h(__fadd_rn(a[v], bias));
-      float r = (float)y16;
-      if (has_lora) {
-        float lf = (float)dk_h(lo[v]);
-        if (TRANS) {
-          if (p.mask) lf = p.mask[m * N + n] ? __fmul_rn(lf, p.keep_scale) : 0.0f;
-        } else {
-          lf = __fmul_rn(p.lora_scale, lf);
-        }
-        r = __fadd_rn(r, lf);
-      }
       const int64_t o = m * p.ldo + n;
       if (p.out_mode == DK_OUT_F16) {
-        out16[o] = dk_h(r);
+        out16[o] = dk_h(res[v]);
       } else if (p.out_mode == DK_OUT_F32) {
-        out32[o] = r;
+        out32[o] = res[v];
       } else {
-        out32[o] = __fadd_rn(out32[o], r);
+        out32[o] = __fadd_rn(out32[o], res[v]);
       }
     }
   };
@@ -467,9 +504,9 @@ void w4_gemm_kernel(GemmParams p) {
 }
 
 // Launch plan: tile shape and split-K factor.  256 CUs.  A 128-row tile's workgroup needs
-// 76.8 KB of LDS (60 KB at 64 columns) and at most 128 VGPRs, so two share a CU (512 slots); a
-// 256 x 128 tile needs a CU of its own and is used only when there are tiles for four rounds of
-// it.  Shapes with fewer tiles than slots split K (at least 8 steps per split) so that about
+// 76.8 KB of LDS (60 KB at 64 columns) and at most 128 VGPRs, so two share a CU (512 slots).
+// (256 x 128 tiles, one workgroup per CU, measured slower at these shapes and are not
+// planned.)  Shapes with fewer tiles than slots split K (at least 8 steps per split) so that about
 // 768 workgroups run: the fp32 partial tiles cost one extra pass over the output in the second
 // launch, so short K (under 64 steps) prefers narrower tiles and splits only below 256 tiles.
 struct Plan {
@@ -479,8 +516,7 @@ struct Plan {
 
 Plan plan_for(int64_t M, int64_t N, int64_t K, int epi) {
   const int64_t nk = K / kBK;
-  const int64_t mt256 = (M + 255) / 256, mt128 = (M + 127) / 128;
-  if (N % 128 == 0 && mt256 * (N / 128) >= 1024) return {256, 128, 1, mt256 * (N / 128)};
+  const int64_t mt128 = (M + 127) / 128;
   Plan pl{128, 128, 1, mt128 * (N / 128)};
   if (N % 128 != 0) pl = {128, 64, 1, mt128 * (N / 64)};
   if (epi != EPI_LINEAR || pl.tiles >= 512) return pl;
@@ -533,7 +569,6 @@ int dispatch(GemmParams p, void* ws, int64_t ws_bytes, hipStream_t stream) {
       p.part = reinterpret_cast<float*>(ws);
     }
   }
-  if (pl.bm == 256) return launch<256, 128, TRANS, EPI>(p, pl.splits, stream);
   if (pl.bn == 128) return launch<128, 128, TRANS, EPI>(p, pl.splits, stream);
   if constexpr (EPI == EPI_SWIGLU_FWD) {
     return DK_ERR_INVALID;
@@ -556,26 +591,55 @@ void set_weight(GemmParams& p, const dk_nf4_weight* w) {
   p.nf4 = w->nf4;
 }
 
-int check_lora(const void* left, const void* right, int64_t rank) {
-  if ((left == nullptr) != (right == nullptr)) return DK_ERR_INVALID;
-  if (left && (rank < 16 || rank > 64 || rank % 16)) return DK_ERR_INVALID;
-  if (left && !dk_aligned(left, 16)) return DK_ERR_ALIGN;
+// Copies the caller's LoRA terms into the kernel parameters.  Forward terms cover disjoint
+// column ranges, multiples of 32 inside [0, n_cols); backward terms cover every column.
+int set_lora(GemmParams& p, const dk_lora_term* terms, int n_terms, int64_t rank, int64_t n_cols,
+             bool backward) {
+  if (n_terms < 0 || n_terms > 2 || (n_terms > 0 && !terms)) return DK_ERR_INVALID;
+  if (n_terms > 0 && (rank < 16 || rank > 64 || rank % 16)) return DK_ERR_INVALID;
+  p.n_lora = n_terms;
+  p.rank = rank;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_term& u = terms[t];
+    if (!u.left || !u.right) return DK_ERR_INVALID;
+    if (!dk_aligned(u.left, 16) || (!backward && !dk_aligned(u.right, 16))) return DK_ERR_ALIGN;
+    LoraTerm& L = p.lora[t];
+    L.z = (const f16*)u.left;
+    L.r = (const f16*)u.right;
+    if (backward) {
+      L.mask = u.mask;
+      L.scale = u.mask ? u.scale : 1.0f;
+      L.n_begin = 0;
+      L.n_end = n_cols;
+    } else {
+      if (u.mask) return DK_ERR_INVALID;
+      if (u.col_begin < 0 || u.col_end > n_cols || u.col_begin >= u.col_end ||
+          u.col_begin % 32 || u.col_end % 32)
+        return DK_ERR_INVALID;
+      for (int q = 0; q < t; ++q)
+        if (u.col_begin < p.lora[q].n_end && p.lora[q].n_begin < u.col_end) return DK_ERR_INVALID;
+      L.mask = nullptr;
+      L.scale = u.scale;
+      L.n_begin = u.col_begin;
+      L.n_end = u.col_end;
+    }
+  }
   return 0;
 }
 
 }  // namespace
 
-extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
-                                const void* bias, const void* z, const void* lora_b,
-                                int64_t rank, float lora_scale, void* y, int64_t ldy,
-                                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
+                                     const dk_nf4_weight* w, const void* bias,
+                                     const dk_lora_term* terms, int n_terms, int64_t rank,
+                                     void* y, int64_t ldy, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || !weight_ok(w) || !x || !y) return DK_ERR_INVALID;
   if (w->rows % 64 || w->cols % kBK || ldx < w->cols || ldy < w->rows) return DK_ERR_INVALID;
-  if (int e = check_lora(z, lora_b, rank)) return e;
-  if (z && !dk_aligned(lora_b, 16)) return DK_ERR_ALIGN;
   if (!dk_aligned(x, 16) || ldx % 8 || !dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
-  if (m == 0) return 0;
   GemmParams p = {};
+  if (int e = set_lora(p, terms, n_terms, rank, w->rows, false)) return e;
+  if (m == 0) return 0;
   p.a = (const f16*)x;
   p.lda = ldx;
   p.M = m;
@@ -583,14 +647,44 @@ extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_
   p.K = w->cols;
   set_weight(p, w);
   p.bias = (const f16*)bias;
-  p.lz = (const f16*)z;
-  p.lr = (const f16*)lora_b;
-  p.rank = rank;
-  p.lora_scale = lora_scale;
   p.out = y;
   p.ldo = ldy;
   p.out_mode = DK_OUT_F16;
   return dispatch<false, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
+                                const void* bias, const void* z, const void* lora_b,
+                                int64_t rank, float lora_scale, void* y, int64_t ldy,
+                                void* workspace, int64_t workspace_bytes, hipStream_t stream) {
+  if ((z == nullptr) != (lora_b == nullptr) || !weight_ok(w)) return DK_ERR_INVALID;
+  dk_lora_term t = {z, lora_b, nullptr, 0, w->rows, lora_scale};
+  return dk_w4_linear_fwd_lora(x, ldx, m, w, bias, &t, z ? 1 : 0, z ? rank : 0, y, ldy,
+                               workspace, workspace_bytes, stream);
+}
+
+extern "C" int dk_w4_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m,
+                                        const dk_nf4_weight* w, const dk_lora_term* terms,
+                                        int n_terms, int64_t rank, void* dx, int64_t lddx,
+                                        int out_mode, void* workspace, int64_t workspace_bytes,
+                                        hipStream_t stream) {
+  if (m < 0 || !weight_ok(w) || !dy || !dx) return DK_ERR_INVALID;
+  if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
+  if (w->cols % 64 || w->rows % kBK || lddy < w->rows || lddx < w->cols) return DK_ERR_INVALID;
+  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
+  GemmParams p = {};
+  if (int e = set_lora(p, terms, n_terms, rank, w->cols, true)) return e;
+  if (m == 0) return 0;
+  p.a = (const f16*)dy;
+  p.lda = lddy;
+  p.M = m;
+  p.N = w->cols;
+  p.K = w->rows;
+  set_weight(p, w);
+  p.out = dx;
+  p.ldo = lddx;
+  p.out_mode = out_mode;
+  return dispatch<true, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
@@ -598,28 +692,10 @@ extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
                                    int64_t rank, const uint8_t* mask, float keep_scale, void* dx,
                                    int64_t lddx, int out_mode, void* workspace,
                                    int64_t workspace_bytes, hipStream_t stream) {
-  if (m < 0 || !weight_ok(w) || !dy || !dx) return DK_ERR_INVALID;
-  if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
-  if (w->cols % 64 || w->rows % kBK || lddy < w->rows || lddx < w->cols) return DK_ERR_INVALID;
-  if (int e = check_lora(dz, lora_a, rank)) return e;
-  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(w->packed, 4)) return DK_ERR_ALIGN;
-  if (m == 0) return 0;
-  GemmParams p = {};
-  p.a = (const f16*)dy;
-  p.lda = lddy;
-  p.M = m;
-  p.N = w->cols;
-  p.K = w->rows;
-  set_weight(p, w);
-  p.lz = (const f16*)dz;
-  p.lr = (const f16*)lora_a;
-  p.rank = rank;
-  p.mask = mask;
-  p.keep_scale = mask ? keep_scale : 1.0f;
-  p.out = dx;
-  p.ldo = lddx;
-  p.out_mode = out_mode;
-  return dispatch<true, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
+  if ((dz == nullptr) != (lora_a == nullptr)) return DK_ERR_INVALID;
+  dk_lora_term t = {dz, lora_a, mask, 0, 0, keep_scale};
+  return dk_w4_linear_bwd_dx_lora(dy, lddy, m, w, &t, dz ? 1 : 0, dz ? rank : 0, dx, lddx,
+                                  out_mode, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
@@ -647,7 +723,7 @@ extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
                                      const dk_nf4_weight* w_down, void* gu, hipStream_t stream) {
   if (m < 0 || !weight_ok(w_down) || !dh || !gu) return DK_ERR_INVALID;
   if (w_down->cols % 64 || w_down->rows % kBK || lddh < w_down->rows) return DK_ERR_INVALID;
-  if (!dk_aligned(dh, 16) || lddh % 8 || !dk_aligned(w_down->packed, 4)) return DK_ERR_ALIGN;
+  if (!dk_aligned(dh, 16) || lddh % 8 || !dk_aligned(w_down->packed, 16)) return DK_ERR_ALIGN;
   if (m == 0) return 0;
   GemmParams p = {};
   p.a = (const f16*)dh;

@@ -4,15 +4,17 @@ Per layer (shapes of solution/fast_qwen.py:53 QWEN15: D = 1536, I = 8960, KV = 2
 with M packed tokens:
 
   forward   z_q = lora_down(X, A_q, mask_q)            z_v likewise        (rank-16 LoRA inputs)
-            q = X W_q^T + s z_q B_q^T,  k = X W_k^T,  v = X W_v^T + s z_v B_v^T
+            qkv = X W_qkv^T + b_qkv, + s z_q B_q^T on the q columns, + s z_v B_v^T on the v
+                  columns                               one GEMM over the q|k|v rows, as the
+                                                        reference's addmm (fast_qwen.py:947)
             o = X W_o^T                                 (X stands in for the attention output)
             act, gu = SwiGLU(X W_gu^T)                  gate|up as one GEMM, gu kept
             y = act W_d^T
   backward  gu <- SwiGLU'(dY_d W_d, gu)                 down^T GEMM + SwiGLU backward fused
             dX_mlp = gu W_gu                            [M, 2I] x [2I, D]
             dX_o = dY_o W_o
-            dA_q, dB_q, dz_q = lora_grads(dY_q, ...)    and the same for v
-            dX_qkv = dY_q W_q + mask_q ks dz_q A_q + dY_k W_k + dY_v W_v + mask_v ks dz_v A_v
+            dA_q, dB_q, dz_q = lora_grads(dQKV[:, q], ...)    and the same for v
+            dX_qkv = dQKV W_qkv + mask_q ks dz_q A_q + mask_v ks dz_v A_v    one NN GEMM
 
 The upstream gradients dY_* are fixed random tensors (the attention and norm backward that would
 produce them are not part of the linear stack).  The step's algorithmic work is
@@ -23,9 +25,11 @@ import torch
 
 from . import k_nf4, quant
 from .w4linear import (down_swiglu_backward, gateup_swiglu_forward, linear_backward_dx,
-                       linear_forward, lora_down, lora_grads)
+                       linear_backward_dx_lora, linear_forward, linear_forward_lora, lora_down,
+                       lora_grads)
 
 D, I, KV, R = 1536, 8960, 256, 16
+QKV = D + 2 * KV
 SHAPES = {"q_proj": (D, D), "k_proj": (KV, D), "v_proj": (KV, D), "o_proj": (D, D),
           "gate_proj": (I, D), "up_proj": (I, D), "down_proj": (D, I)}
 
@@ -66,9 +70,7 @@ class NF4LinearStack:
             packed, _ = k_nf4.repack_layer(linears, dev)
             self.layers.append(dict(
                 packed=packed,
-                q=packed.weight("q_proj", self.code2, self.nf4),
-                k=packed.weight("k_proj", self.code2, self.nf4),
-                v=packed.weight("v_proj", self.code2, self.nf4),
+                qkv=packed.weights(("q_proj", "k_proj", "v_proj"), self.code2, self.nf4),
                 o=packed.weight("o_proj", self.code2, self.nf4),
                 gu=packed.weights(("gate_proj", "up_proj"), self.code2, self.nf4),
                 d=packed.weight("down_proj", self.code2, self.nf4)))
@@ -78,14 +80,15 @@ class NF4LinearStack:
                 lo["A" + t] = ((torch.rand(R, D, generator=gen, device=dev) * 2 - 1) * bound).half()
                 lo["B" + t] = (torch.randn(out, R, generator=gen, device=dev) * 0.02).half()
                 lo["m" + t] = (torch.rand(m, D, generator=gen, device=dev) >= p_drop).to(torch.uint8)
+            lo["bias"] = (torch.randn(QKV, generator=gen, device=dev) * 0.02).half()
             self.lora.append(lo)
         self.x = torch.randn(m, D, generator=gen, device=dev).half()
         self.dy = {k: (torch.randn(m, n, generator=gen, device=dev) * 1e-2).half()
-                   for k, n in (("q", D), ("k", KV), ("v", KV), ("o", D), ("d", D))}
+                   for k, n in (("qkv", QKV), ("o", D), ("d", D))}
         self.save_gu = save_gu
         f16 = torch.float16
         self.out = {k: torch.empty(m, n, dtype=f16, device=dev)
-                    for k, n in (("q", D), ("k", KV), ("v", KV), ("o", D), ("y", D))}
+                    for k, n in (("qkv", QKV), ("o", D), ("y", D))}
         self.act = torch.empty(m, I, dtype=f16, device=dev)
         self.gu = [torch.empty(m, 2 * I, dtype=f16, device=dev) for _ in range(n_layers)]
         self.z = [{t: torch.empty(m, R, dtype=f16, device=dev) for t in ("q", "v")}
@@ -105,11 +108,8 @@ class NF4LinearStack:
         op = self._op
         op("lora_down", lora_down, x, lo["Aq"], lo["mq"], self.keep_scale, out=z["q"])
         op("lora_down", lora_down, x, lo["Av"], lo["mv"], self.keep_scale, out=z["v"])
-        op("w4_linear_fwd q+lora", linear_forward, x, L["q"], None, z["q"], lo["Bq"], self.s,
-           out=o["q"])
-        op("w4_linear_fwd k", linear_forward, x, L["k"], out=o["k"])
-        op("w4_linear_fwd v+lora", linear_forward, x, L["v"], None, z["v"], lo["Bv"], self.s,
-           out=o["v"])
+        op("w4_linear_fwd qkv+lora", linear_forward_lora, x, L["qkv"], lo["bias"],
+           self.qkv_terms(i), out=o["qkv"])
         op("w4_linear_fwd o", linear_forward, x, L["o"], out=o["o"])
         op("w4_gateup_swiglu_fwd", gateup_swiglu_forward, x, L["gu"], act=self.act, gu=self.gu[i])
         op("w4_linear_fwd down", linear_forward, self.act, L["d"], out=o["y"])
@@ -121,17 +121,20 @@ class NF4LinearStack:
         op("w4_down_swiglu_bwd", down_swiglu_backward, dy["d"], L["d"], gu)
         op("w4_linear_bwd_dx gate|up", linear_backward_dx, gu, L["gu"], out=self.dx_mlp)
         op("w4_linear_bwd_dx o", linear_backward_dx, dy["o"], L["o"], out=self.dx_o)
-        daq, dbq, dzq = op("lora_grads q", lora_grads, dy["q"], z["q"], x, lo["Bq"], self.s,
+        dqkv = dy["qkv"]
+        daq, dbq, dzq = op("lora_grads q", lora_grads, dqkv[:, :D], z["q"], x, lo["Bq"], self.s,
                            lo["mq"], self.keep_scale)
-        dav, dbv, dzv = op("lora_grads v", lora_grads, dy["v"], z["v"], x, lo["Bv"], self.s,
-                           lo["mv"], self.keep_scale)
-        op("w4_linear_bwd_dx q+lora", linear_backward_dx, dy["q"], L["q"], dzq, lo["Aq"], lo["mq"],
-           self.keep_scale, out=self.dx_qkv)
-        op("w4_linear_bwd_dx k", linear_backward_dx, dy["k"], L["k"], out=self.dx_qkv,
-           accumulate=True)
-        op("w4_linear_bwd_dx v+lora", linear_backward_dx, dy["v"], L["v"], dzv, lo["Av"], lo["mv"],
-           self.keep_scale, out=self.dx_qkv, accumulate=True)
+        dav, dbv, dzv = op("lora_grads v", lora_grads, dqkv[:, D + KV:], z["v"], x, lo["Bv"],
+                           self.s, lo["mv"], self.keep_scale)
+        op("w4_linear_bwd_dx qkv+lora", linear_backward_dx_lora, dqkv, L["qkv"],
+           [(dzq, lo["Aq"], lo["mq"], self.keep_scale), (dzv, lo["Av"], lo["mv"], self.keep_scale)],
+           out=self.dx_qkv)
         self.grads[i] = (daq, dbq, dav, dbv)
+
+    def qkv_terms(self, i):
+        """LoRA terms of layer i's fused QKV forward: q on columns [0, D), v on [D + KV, QKV)."""
+        lo, z = self.lora[i], self.z[i]
+        return [(z["q"], lo["Bq"], 0, D, self.s), (z["v"], lo["Bv"], D + KV, QKV, self.s)]
 
     def _op(self, name, fn, *args, **kwargs):
         """Run one operator; when ``self.probe`` is ``(name, events)`` for this operator, bracket

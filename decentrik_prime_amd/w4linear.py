@@ -160,6 +160,96 @@ def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=Non
     return out
 
 
+def _lora_terms(terms, m, backward, n_cols):
+    """ctypes array of dk_lora_term from (left, right, mask, col_begin, col_end, scale) tuples."""
+    if len(terms) > 2:
+        raise ValueError("at most two LoRA terms")
+    arr = (_lib.LoraTermC * max(1, len(terms)))()
+    rank = 0
+    keep = []
+    for i, (left, right, mask, c0, c1, scale) in enumerate(terms):
+        r = left.shape[1]
+        if rank and r != rank:
+            raise ValueError("LoRA terms must share the rank")
+        rank = r
+        _check16(left, "LoRA left factor", (m, r))
+        if backward:
+            _check16(right, "lora_A", (r, n_cols))
+            mask = _mask_ok(mask, (m, n_cols))
+        else:
+            _check16(right, "lora_B", (c1 - c0, r))
+            if mask is not None:
+                raise ValueError("forward LoRA terms take no mask")
+        if not left.is_contiguous() or not right.is_contiguous():
+            raise ValueError("LoRA factors must be contiguous")
+        keep += [left, right, mask]
+        arr[i] = _lib.LoraTermC(left.data_ptr(), right.data_ptr(),
+                                mask.data_ptr() if mask is not None else None, c0, c1, float(scale))
+    return arr, len(terms), rank, keep
+
+
+def linear_forward_lora(x, w, bias=None, terms=(), out=None):
+    """The fused linear forward with up to two LoRA terms on disjoint output-column ranges:
+    terms = [(z [M, r], lora_B [c1 - c0, r], col_begin c0, col_end c1, scale s), ...].  The fused
+    QKV projection passes the q term on columns [0, NQ*HD) and the v term on the last NKV*HD
+    columns (solution/fast_qwen.py:943-949)."""
+    _check16(x, "x")
+    m = x.shape[0]
+    if x.shape[1] != w.cols:
+        raise ValueError(f"x has {x.shape[1]} features, weight expects {w.cols}")
+    if bias is not None:
+        _check16(bias.view(1, -1), "bias", (1, w.rows))
+    arr, n, rank, _keep = _lora_terms([(z, b, None, c0, c1, s) for z, b, c0, c1, s in terms], m,
+                                      False, w.rows)
+    if out is None:
+        out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
+    _check16(out, "out", (m, w.rows))
+    ws, nbytes = _workspace(w, m, False, x.device)
+    rc = _lib.lib().dk_w4_linear_fwd_lora(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
+                                          arr, n, rank, _lib.ptr(out), out.stride(0), _lib.ptr(ws),
+                                          nbytes, _lib.stream_handle(x.device))
+    _lib.check(rc, "dk_w4_linear_fwd_lora")
+    return out
+
+
+def _dx_out(out, m, w, out_dtype, accumulate, device):
+    if out is None:
+        if accumulate:
+            raise ValueError("accumulate needs an output tensor")
+        out = torch.empty(m, w.cols, dtype=out_dtype, device=device)
+    if out.dtype == torch.float16:
+        mode = _lib.DK_OUT_F16
+        if accumulate:
+            raise ValueError("accumulation is into fp32 only")
+    elif out.dtype == torch.float32:
+        mode = _lib.DK_OUT_F32_ACCUM if accumulate else _lib.DK_OUT_F32
+    else:
+        raise ValueError("dX is fp16 or fp32")
+    if tuple(out.shape) != (m, w.cols) or out.stride(1) != 1:
+        raise ValueError("dX output has the wrong shape or layout")
+    return out, mode
+
+
+def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, accumulate=False):
+    """dX = fp32(fp16(dy W)) + sum over terms of (mask ? fp32(fp16(dz A)) * keep_scale : 0),
+    terms = [(dz [M, r], lora_A [r, in], mask [M, in] or None, keep_scale), ...] added in order
+    (the QKV backward: dy1 = mm(dqkv, W_qkv) plus the lq and lv terms of rms_backward,
+    solution/fast_qwen.py:1364, 1376-1380)."""
+    _check16(dy, "dy")
+    m = dy.shape[0]
+    if dy.shape[1] != w.rows:
+        raise ValueError(f"dy has {dy.shape[1]} columns, weight has {w.rows} rows")
+    arr, n, rank, _keep = _lora_terms([(dz, a, mk, 0, 0, ks) for dz, a, mk, ks in terms], m,
+                                      True, w.cols)
+    out, mode = _dx_out(out, m, w, out_dtype, accumulate, dy.device)
+    ws, nbytes = _workspace(w, m, True, dy.device)
+    rc = _lib.lib().dk_w4_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), arr, n, rank,
+                                             _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws),
+                                             nbytes, _lib.stream_handle(dy.device))
+    _lib.check(rc, "dk_w4_linear_bwd_dx_lora")
+    return out
+
+
 def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, out=None,
                        out_dtype=torch.float32, accumulate=False):
     """dX = fp32(fp16(dy W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0).
@@ -179,20 +269,7 @@ def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, o
         if not dz.is_contiguous() or not lora_A.is_contiguous():
             raise ValueError("dz and lora_A must be contiguous")
     mask = _mask_ok(mask, (m, w.cols))
-    if out is None:
-        if accumulate:
-            raise ValueError("accumulate needs an output tensor")
-        out = torch.empty(m, w.cols, dtype=out_dtype, device=dy.device)
-    if out.dtype == torch.float16:
-        mode = _lib.DK_OUT_F16
-        if accumulate:
-            raise ValueError("accumulation is into fp32 only")
-    elif out.dtype == torch.float32:
-        mode = _lib.DK_OUT_F32_ACCUM if accumulate else _lib.DK_OUT_F32
-    else:
-        raise ValueError("dX is fp16 or fp32")
-    if tuple(out.shape) != (m, w.cols) or out.stride(1) != 1:
-        raise ValueError("dX output has the wrong shape or layout")
+    out, mode = _dx_out(out, m, w, out_dtype, accumulate, dy.device)
     ws, nbytes = _workspace(w, m, True, dy.device)
     rc = _lib.lib().dk_w4_linear_bwd_dx(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), _lib.ptr(dz),
                                         _lib.ptr(lora_A), r, _lib.ptr(mask), float(keep_scale),
@@ -204,8 +281,10 @@ def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, o
 
 def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
     """(dA fp32 [r, in], dB fp32 [out, r], dz fp16 [M, r]) with
-    dB = fp32(fp16(dy^T z)) s, dz = fp16(fp16(dy B) s), dA = fp32(fp16(dz^T drop(x)))."""
-    for t, nm in ((dy, "dy"), (z, "z"), (x, "x"), (lora_B, "lora_B")):
+    dB = fp32(fp16(dy^T z)) s, dz = fp16(fp16(dy B) s), dA = fp32(fp16(dz^T drop(x))).
+    dy may be a column slice (row stride > out), like the reference's gq = qkv[:, :NQ*HD]."""
+    _check16(dy, "dy")
+    for t, nm in ((z, "z"), (x, "x"), (lora_B, "lora_B")):
         _check16(t, nm)
         if not t.is_contiguous():
             raise ValueError(f"{nm} must be contiguous")
@@ -222,7 +301,8 @@ def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
     dz = torch.empty(m, r, dtype=torch.float16, device=dev)
     nbytes = int(L.dk_lora_grads_workspace(m, n_out, k, r))
     ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev)
-    rc = L.dk_lora_grads(_lib.ptr(dy), _lib.ptr(z), _lib.ptr(x), _lib.ptr(mask), float(keep_scale),
+    rc = L.dk_lora_grads(_lib.ptr(dy), dy.stride(0), _lib.ptr(z), _lib.ptr(x), _lib.ptr(mask),
+                         float(keep_scale),
                          _lib.ptr(lora_B), float(lora_scale), m, n_out, k, r, _lib.ptr(da),
                          _lib.ptr(db), _lib.ptr(dz), _lib.ptr(ws), nbytes, _lib.stream_handle(dev))
     _lib.check(rc, "dk_lora_grads")

@@ -101,6 +101,32 @@ int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight*
                      float lora_scale, void* y, int64_t ldy, void* workspace,
                      int64_t workspace_bytes, hipStream_t stream);
 
+/* One rank-r LoRA term of a fused linear (used by the *_lora entry points, at most two each).
+ * Forward:  adds s * fp32(fp16(left right^T)) to output columns [col_begin, col_end) (multiples of
+ *           32, disjoint between terms); left = z [m, rank], right = B [col_end - col_begin, rank],
+ *           mask NULL, scale = s.
+ * Backward: adds (mask ? fp32(fp16(left right)) * scale : 0) to every column of dX, terms in
+ *           order; left = dz [m, rank], right = A [rank, w.cols], mask [m, w.cols] uint8 or NULL
+ *           (no dropout: the term is added unscaled), scale = keep_scale; col_* ignored. */
+typedef struct dk_lora_term {
+  const void* left;
+  const void* right;
+  const uint8_t* mask;
+  int64_t col_begin;
+  int64_t col_end;
+  float scale;
+} dk_lora_term;
+
+/* The fused linear forward with up to two LoRA terms on disjoint output-column ranges.  Replaces
+ * the fused QKV projection: qkv = addmm(bias_qkv, x, W_qkv^T) with the q and v LoRA adds of
+ * qkv_epilogue_forward (solution/fast_qwen.py:943-949; solution/k_rope.py:39-43, 54-58), w being
+ * the q|k|v rows of the repacked layer.  Rounding per term as in dk_w4_linear_fwd, terms added in
+ * order.  Other arguments and rules as dk_w4_linear_fwd. */
+int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
+                          const void* bias, const dk_lora_term* terms, int n_terms,
+                          int64_t rank, void* y, int64_t ldy, void* workspace,
+                          int64_t workspace_bytes, hipStream_t stream);
+
 /* Workspace bytes the fused linear needs at m rows (0: no split-K for this shape);
  * backward = 0 for dk_w4_linear_fwd, 1 for dk_w4_linear_bwd_dx.  No counterpart in the
  * reference (cuBLAS manages its own workspace); part of the drop-in for its torch.mm calls. */
@@ -124,15 +150,26 @@ int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m, const dk_nf4_we
                         float keep_scale, void* dx, int64_t lddx, int out_mode,
                         void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* The backward dX GEMM with up to two LoRA dX terms (each with its own dropout mask).  Replaces
+ * dy1 = mm(dqkv, W_qkv) and the lq/lv adds of rms_backward (solution/fast_qwen.py:1364,
+ * 1376-1380; solution/k_norm.py:64-70):
+ *   dX = fp32(fp16(dY W)) + (mq ? fp32(fp16(dz_q A_q)) * ks : 0) + (mv ? ... : 0)
+ * Other arguments and rules as dk_w4_linear_bwd_dx. */
+int dk_w4_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const dk_nf4_weight* w,
+                             const dk_lora_term* terms, int n_terms, int64_t rank, void* dx,
+                             int64_t lddx, int out_mode, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream);
+
 /* LoRA parameter gradients and the LoRA-down gradient.  Replaces
  * solution/fast_qwen.py:1369-1374:
  *   dB = fp32(fp16(dY^T z)) * s              [w_rows, rank] fp32
  *   dz = fp16(fp16(dY B) * s)                [m, rank] fp16
  *   dA = fp32(fp16(dz^T Xd)), Xd as in dk_lora_down   [rank, k] fp32
- * dy [m, n_out] fp16, z [m, rank], x [m, k], mask [m, k] (NULL = no dropout), lora_b
- * [n_out, rank].  ws: fp32 scratch of dk_lora_grads_workspace(m, n_out, k, rank) bytes. */
+ * dy [m, n_out] fp16 with row stride lddy (a column slice of dQKV: gq = qkv[:, :NQ*HD]),
+ * z [m, rank], x [m, k], mask [m, k] (NULL = no dropout), lora_b [n_out, rank].
+ * ws: fp32 scratch of dk_lora_grads_workspace(m, n_out, k, rank) bytes. */
 int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank);
-int dk_lora_grads(const void* dy, const void* z, const void* x, const uint8_t* mask,
+int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x, const uint8_t* mask,
                   float keep_scale, const void* lora_b, float lora_scale, int64_t m,
                   int64_t n_out, int64_t k, int64_t rank, float* da, float* db, void* dz,
                   void* ws, int64_t ws_bytes, hipStream_t stream);

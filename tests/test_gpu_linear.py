@@ -152,6 +152,70 @@ def test_backward_config3(torch, name, rows, m):
     _scaled_close(host(d16), ref["dx_base"], "dx fp16")
 
 
+@pytest.mark.parametrize("m", [2048, 200])
+def test_fused_qkv_forward_backward(torch, m):
+    """The reference's fused QKV projection (solution/fast_qwen.py:943-949, 1364-1380): one GEMM
+    over the q|k|v rows with the q and v LoRA terms on their column ranges, and one dX GEMM with
+    both masked LoRA dX terms; LoRA gradients from column slices of dQKV."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"fused QKV forward + backward, two LoRA terms, M={m}")
+    D, KV = 1536, 256
+    q = nf4_weight(D + 2 * KV, D, seed=107)
+    wq, wk, wv = q["deq"][:D], q["deq"][D:D + KV], q["deq"][D + KV:]
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, seed=11)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, seed=12)
+    rng = np.random.default_rng(13)
+    bias = (rng.standard_normal(D + 2 * KV) * 0.1).astype(F16)
+    dqkv = (rng.standard_normal((m, D + 2 * KV)) * 1e-2).astype(F16)
+    ks = linear.keep_scale(0.05)
+    yq, zq = linear.linear_fwd(x, wq, bias[:D], mq, ks, aq, bq, 2.0)
+    yk, _ = linear.linear_fwd(x, wk, bias[D:D + KV])
+    yv, zv = linear.linear_fwd(x, wv, bias[D + KV:], mv, ks, av, bv, 2.0)
+    w = to_w4(q)
+    tzq = w4linear.lora_down(cuda16(x), cuda16(aq), cuda(mq), ks)
+    tzv = w4linear.lora_down(cuda16(x), cuda16(av), cuda(mv), ks)
+    qkv = w4linear.linear_forward_lora(cuda16(x), w, cuda16(bias),
+                                       [(tzq, cuda16(bq), 0, D, 2.0),
+                                        (tzv, cuda16(bv), D + KV, D + 2 * KV, 2.0)])
+    torch.cuda.synchronize()
+    assert_close(host(qkv), np.concatenate([yq, yk, yv], axis=1), RTOL, ATOL, "qkv")
+    # backward
+    rq = linear.linear_bwd(dqkv[:, :D], wq, zq, x, mq, ks, aq, bq, 2.0)
+    rv = linear.linear_bwd(dqkv[:, D + KV:], wv, zv, x, mv, ks, av, bv, 2.0)
+    tq = np.where(mq != 0, (rq["lx"].astype(np.float32) * np.float32(ks)).astype(np.float32), 0)
+    tv = np.where(mv != 0, (rv["lx"].astype(np.float32) * np.float32(ks)).astype(np.float32), 0)
+    dx_ref = ((linear.mm16(dqkv, q["deq"]).astype(np.float32) + tq).astype(np.float32) + tv)
+    g = cuda16(dqkv)
+    daq, dbq, dzq = w4linear.lora_grads(g[:, :D], cuda16(zq), cuda16(x), cuda16(bq), 2.0,
+                                        cuda(mq), ks)
+    dav, dbv, dzv = w4linear.lora_grads(g[:, D + KV:], cuda16(zv), cuda16(x), cuda16(bv), 2.0,
+                                        cuda(mv), ks)
+    dx = w4linear.linear_backward_dx_lora(g, w, [(dzq, cuda16(aq), cuda(mq), ks),
+                                                 (dzv, cuda16(av), cuda(mv), ks)])
+    torch.cuda.synchronize()
+    for got, ref, nm in ((dzq, rq["dZ"], "dz_q"), (daq, rq["dA"], "dA_q"), (dbq, rq["dB"], "dB_q"),
+                         (dzv, rv["dZ"], "dz_v"), (dav, rv["dA"], "dA_v"), (dbv, rv["dB"], "dB_v")):
+        _scaled_close(host(got), ref, nm)
+    _scaled_close(host(dx), dx_ref, "dX qkv")
+
+
+def test_lora_term_argument_errors(torch):
+    from decentrik_prime_amd import w4linear
+    log("fused linear LoRA-term argument checks")
+    q = nf4_weight(512, 256, seed=108)
+    w = to_w4(q)
+    x = torch.zeros(64, 256, dtype=torch.float16, device="cuda")
+    z = torch.zeros(64, 16, dtype=torch.float16, device="cuda")
+    b = torch.zeros(256, 16, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):   # overlapping column ranges
+        w4linear.linear_forward_lora(x, w, None, [(z, b, 0, 256, 2.0), (z, b, 128, 384, 2.0)])
+    with pytest.raises(ValueError):   # range not a multiple of 32
+        w4linear.linear_forward_lora(x, w, None, [(z, b[:240], 16, 256, 2.0)])
+    with pytest.raises(ValueError):   # beyond the output columns
+        w4linear.linear_forward_lora(x, w, None, [(z, b, 384, 640, 2.0)])
+
+
 def test_mlp_config2(torch):
     from decentrik_prime_amd import w4linear
     from oracle import linear, mlp
