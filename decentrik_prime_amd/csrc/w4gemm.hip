@@ -37,8 +37,10 @@ namespace {
 constexpr int kBK = 64;
 constexpr int kStride = kBK + 8;  // halves per K-contiguous LDS row (144 bytes)
 constexpr int kPadT = 16;         // NN: halves of padding per N-contiguous LDS row of the W tile
-constexpr int kThreads = 512;     // 4 consumer + 4 producer waves
-constexpr int kRoleThreads = 256;
+// Waves per role: consumers are WAVES_M x 2 (64-row strips), producers as many; 128-row tiles
+// run 512 threads, 256-row tiles 1024.
+template <int BM>
+constexpr int role_threads() { return (BM / 64) * 2 * 64; }
 
 enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
 
@@ -63,6 +65,7 @@ struct GemmParams {
   const float* offset2;
   const float* code2;
   const float* nf4;
+  const f16* w16;       // two-phase: the weight dequantised to fp16, stored order ([N][K] NT, [K][N] NN)
   int64_t inter;        // SwiGLU: gate/up width I
   const f16* bias;      // [N] or null
   LoraTerm lora[2];     // rank-r LoRA terms added in the LINEAR epilogue, in order
@@ -72,25 +75,32 @@ struct GemmParams {
   int64_t ldo;
   int out_mode;
   f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
-  int tiles_n;
+  int tiles_m, tiles_n;
+  int m_fastest;        // tile order: row tiles fastest (1) or column tiles fastest (0)
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
 };
 
 // REDUCE: the split-K second launch (consumer waves only): sum the partials, then the epilogue.
-// 128-row tiles are held to 128 VGPRs (4 waves per SIMD: two workgroups per CU).
-template <int BM, int BN, bool TRANS, int EPI, bool REDUCE>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(BM == 128 ? 4 : 2)))
+// Every tile runs 4 waves per SIMD (two 512-thread or one 1024-thread workgroup per CU), so the
+// kernel is held to 128 VGPRs.
+// F16B: W is read as fp16 from p.w16 (the two-phase path) instead of NF4 sections.
+template <int BM, int BN, bool TRANS, int EPI, bool REDUCE, bool F16B>
+__global__ __launch_bounds__(2 * role_threads<BM>()) __attribute__((amdgpu_waves_per_eu(4)))
 void w4_gemm_kernel(GemmParams p) {
-  constexpr int WM = BM / 2, WN = BN / 2;
+  constexpr int ROLE = role_threads<BM>();         // threads per role
+  constexpr int WAVES_M = BM / 64, WAVES_N = 2;    // consumer waves
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int A_CHUNKS = BM * kBK / 8 / kRoleThreads;
-  constexpr int B_UNITS = BN / 128 > 0 ? BN / 128 : 1;
-  constexpr int B_ACTIVE = BN * 2;  // 16-byte packed chunks (32 weights) per W tile
+  constexpr int A_CHUNKS = BM * kBK / 8 / ROLE;    // 16-byte A chunks per producer thread
+  constexpr int BU = BN * kBK / ROLE;              // W weights per producer thread per step
+  constexpr int BU_WORDS = BU / 8;                 // packed dwords per unit
   constexpr int B_LD = TRANS ? BN + kPadT : kStride;   // halves per LDS row of the W tile
   constexpr int B_HALVES = TRANS ? kBK * B_LD : BN * kStride;
   constexpr int TILE = BM * BN;
   static_assert(TM >= 1 && TN >= 1, "tile too small");
+  static_assert(BU == 16 || BU == 32, "a W unit is 16 or 32 weights of one stored row");
+  static_assert(A_CHUNKS >= 1 && BM * kBK / 8 == A_CHUNKS * ROLE, "A tile split");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
 
   __shared__ __attribute__((aligned(16))) f16 As[2][BM * kStride];
@@ -102,12 +112,13 @@ void w4_gemm_kernel(GemmParams p) {
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const bool producer = wave >= 4;
+  const bool producer = wave >= ROLE / 64;   // wave-uniform
 
   // XCD-aware tile order: workgroups are dealt to the 8 XCDs round-robin, so give each XCD a
-  // contiguous run of tiles, N fastest: an XCD keeps one band of A rows in its L2 while the
-  // packed W tiles (a quarter of the bytes per row) stream past it.  With split-K the splits of
-  // one tile are consecutive, so they share an XCD and its L2.
+  // contiguous run of tiles.  Packed W (one phase): column tiles fastest, so an XCD keeps one band
+  // of A rows in its L2 while the packed W tiles (a quarter of the bytes per row) stream past it.
+  // fp16 W (two phase): row tiles fastest (see launch).  With split-K the splits of one tile are
+  // consecutive, so they share an XCD and its L2.
   int b = blockIdx.x;
   const int nb = gridDim.x;
   if ((nb & 7) == 0) b = (b & 7) * (nb >> 3) + (b >> 3);
@@ -116,8 +127,8 @@ void w4_gemm_kernel(GemmParams p) {
   const int per_tile = REDUCE ? TM * TN : p.splits;
   const int split = REDUCE ? 0 : b % per_tile;
   const int tile = b / per_tile;
-  const int64_t m0 = (int64_t)(tile / p.tiles_n) * BM;
-  const int64_t n0 = (int64_t)(tile % p.tiles_n) * BN;
+  const int64_t m0 = (int64_t)(p.m_fastest ? tile % p.tiles_m : tile / p.tiles_n) * BM;
+  const int64_t n0 = (int64_t)(p.m_fastest ? tile / p.tiles_m : tile % p.tiles_n) * BN;
   const int64_t M = p.M, N = p.N, K = p.K;
   const int nk_all = (int)(K / kBK);
   const int ks0 = (int)((int64_t)nk_all * split / p.splits);
@@ -125,57 +136,89 @@ void w4_gemm_kernel(GemmParams p) {
 
   if (!REDUCE && producer) {
     // =========================== producer waves ===========================
-    const int pt = tid - kRoleThreads;
-    pair_lut[pt] = f32x2{p.nf4[pt >> 4], p.nf4[pt & 15]};
-    c2t[pt] = p.code2[pt];
+    const int pt = tid - ROLE;
+    if (!F16B && pt < 256) {
+      pair_lut[pt] = f32x2{p.nf4[pt >> 4], p.nf4[pt & 15]};
+      c2t[pt] = p.code2[pt];
+    }
 
+    constexpr int B_TOTAL = BN * kBK / BU;                   // W units per tile (a power of 2)
+    constexpr int B_UNITS = B_TOTAL / ROLE > 0 ? B_TOTAL / ROLE : 1;  // units per thread
+    constexpr int UPR = TRANS ? BN / BU : kBK / BU;   // units per W-tile row
+    constexpr int B16 = F16B ? BN * kBK / 8 / ROLE : 1;   // fp16 W chunks (16 bytes) per thread
     struct Stage {
       u32x4 a_reg[A_CHUNKS];
-      uint32_t b_word[B_UNITS][4];
+      uint32_t b_word[B_UNITS][BU_WORDS];
       uint32_t b_code[B_UNITS];
       float b_s2[B_UNITS];
       float b_o2[B_UNITS];
+      u32x4 b16[B16];
     };
+    // fp16 W chunk c of the tile: NT row n (8 chunks of 8 k), NN row k (BN / 8 chunks of 8 n)
+    constexpr int B16_PER_ROW = TRANS ? BN / 8 : kBK / 8;
     struct Looked {
-      f32x2 v[B_UNITS][16];
+      f32x2 v[B_UNITS][BU / 2];
       float c2[B_UNITS];
     };
 
     // Every load is unconditional (rows past M read row M - 1, whose products land only in
-    // output rows that are never stored; steps past the last repeat it; surplus threads of a
-    // narrow B tile repeat a valid chunk), so the compiler counts outstanding loads exactly and
-    // waits only for the stage it consumes.
+    // output rows that are never stored; steps past the last repeat it), so the compiler counts
+    // outstanding loads exactly and waits only for the stage it consumes.
     auto load_tiles = [&](Stage& sg, int kt) {
       const int64_t k0 = (int64_t)(ks0 + (kt < nk ? kt : nk - 1)) * kBK;
 #pragma unroll
       for (int i = 0; i < A_CHUNKS; ++i) {
-        const int c = pt + kRoleThreads * i;
+        const int c = pt + ROLE * i;
         const int row = c >> 3, col8 = c & 7;
         const int64_t gm = m0 + row < M ? m0 + row : M - 1;
         sg.a_reg[i] = *reinterpret_cast<const u32x4*>(p.a + gm * p.lda + k0 + col8 * 8);
       }
+      if constexpr (F16B) {
+#pragma unroll
+        for (int i = 0; i < B16; ++i) {
+          const int c = pt + ROLE * i;
+          const int row = c / B16_PER_ROW, off = (c % B16_PER_ROW) * 8;
+          int64_t src;
+          if (!TRANS) {
+            int64_t n = n0 + row;
+            if (EPI == EPI_SWIGLU_FWD) {
+              const int64_t g = n >> 6, w = n & 63;
+              n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
+            }
+            src = n * K + k0 + off;
+          } else {
+            src = (k0 + row) * N + n0 + off;
+          }
+          sg.b16[i] = *reinterpret_cast<const u32x4*>(p.w16 + src);
+        }
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < B_UNITS; ++i) {
-        // one 16-byte chunk of packed nibbles = 32 consecutive weights of a stored row, inside
-        // one first-level block.  NT: row n of W, k half `half`; NN: row k of W, columns
-        // 32 * chunk of the tile.
-        const int c = (pt + kRoleThreads * i) & (B_ACTIVE - 1);
+        // unit c: BU consecutive weights of one stored row, inside one first-level block.
+        // NT: row n of W (K contiguous); NN: row k of W (N contiguous).
+        const int c = (pt + ROLE * i) & (B_TOTAL - 1);
+        const int row = c / UPR, off = (c % UPR) * BU;
         int64_t elem;
         if (!TRANS) {
-          const int row = c >> 1, half = c & 1;
           int64_t n = n0 + row;
           if (EPI == EPI_SWIGLU_FWD) {
             const int64_t g = n >> 6, w = n & 63;
             n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
           }
-          elem = n * K + k0 + half * 32;
+          elem = n * K + k0 + off;
         } else {
-          constexpr int CPR = BN / 32;   // chunks per W-tile row
-          elem = (k0 + c / CPR) * N + n0 + 32 * (c % CPR);
+          elem = (k0 + row) * N + n0 + off;
         }
-        const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
+        if constexpr (BU_WORDS == 4) {
+          const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (elem >> 1));
 #pragma unroll
-        for (int d = 0; d < 4; ++d) sg.b_word[i][d] = v[d];
+          for (int d = 0; d < 4; ++d) sg.b_word[i][d] = v[d];
+        } else {
+          const u32x2 v = *reinterpret_cast<const u32x2*>(p.packed + (elem >> 1));
+          sg.b_word[i][0] = v[0];
+          sg.b_word[i][1] = v[1];
+        }
         const int64_t q = elem >> 6;
         sg.b_code[i] = p.qabs[q];
         sg.b_s2[i] = p.scale2[q >> 8];
@@ -184,10 +227,11 @@ void w4_gemm_kernel(GemmParams p) {
     };
 
     auto look_up = [&](const Stage& sg, Looked& lk) {
+      if constexpr (F16B) return;
 #pragma unroll
       for (int i = 0; i < B_UNITS; ++i) {
 #pragma unroll
-        for (int d = 0; d < 4; ++d)
+        for (int d = 0; d < BU_WORDS; ++d)
 #pragma unroll
           for (int bb = 0; bb < 4; ++bb) lk.v[i][4 * d + bb] = pair_lut[(sg.b_word[i][d] >> (8 * bb)) & 0xffu];
         lk.c2[i] = c2t[sg.b_code[i]];
@@ -199,26 +243,28 @@ void w4_gemm_kernel(GemmParams p) {
       f16* bs = Bs[buf];
 #pragma unroll
       for (int i = 0; i < A_CHUNKS; ++i) {
-        const int c = pt + kRoleThreads * i;
+        const int c = pt + ROLE * i;
         const int row = c >> 3, col8 = c & 7;
         *reinterpret_cast<u32x4*>(as + row * kStride + col8 * 8) = sg.a_reg[i];
       }
+      if constexpr (F16B) {
+#pragma unroll
+        for (int i = 0; i < B16; ++i) {
+          const int c = pt + ROLE * i;
+          *reinterpret_cast<u32x4*>(bs + (c / B16_PER_ROW) * B_LD + (c % B16_PER_ROW) * 8) = sg.b16[i];
+        }
+        return;
+      }
 #pragma unroll
       for (int i = 0; i < B_UNITS; ++i) {
-        const int c = pt + kRoleThreads * i;
-        if (c < B_ACTIVE) {
-          // NT: W-tile row n holds k contiguous (the MFMA operand layout); NN: W-tile row k
-          // holds n contiguous (the consumers read it with transposing LDS loads)
-          f16* dst;
-          if (!TRANS) {
-            dst = bs + (c >> 1) * B_LD + (c & 1) * 32;
-          } else {
-            constexpr int CPR = BN / 32;
-            dst = bs + (c / CPR) * B_LD + 32 * (c % CPR);
-          }
+        // NT: W-tile row n holds k contiguous (the MFMA operand layout); NN: W-tile row k holds
+        // n contiguous (the consumers read it with transposing LDS loads)
+        const int c = pt + ROLE * i;
+        if (c < B_TOTAL) {
+          f16* dst = bs + (c / UPR) * B_LD + (c % UPR) * BU;
           const float amax = dk_absmax(lk.c2[i], sg.b_s2[i], sg.b_o2[i]);
 #pragma unroll
-          for (int d = 0; d < 4; ++d) {
+          for (int d = 0; d < BU_WORDS; ++d) {
             u32x4 o;
 #pragma unroll
             for (int bb = 0; bb < 4; ++bb) {
@@ -236,6 +282,31 @@ void w4_gemm_kernel(GemmParams p) {
     // step j + 1 into the other buffer; each load has two steps of MFMA time to land.  Steps past
     // the last repeat it into a buffer that is not read again: no branch around memory
     // operations inside the loop.
+    if constexpr (F16B) {
+      // fp16 W: 32 registers per stage, so two stages.  Step j + 1 is in one stage while step
+      // j + 2 loads into the other; each load has one step of MFMA time to land.
+      Stage s0, s1;
+      Looked lk;
+      load_tiles(s0, 0);
+      load_tiles(s1, 1);
+      __syncthreads();
+      store_tiles(s0, lk, 0);
+      __syncthreads();  // step 0 in buffer 0
+      int j = 0;
+      for (; j + 2 <= nk; j += 2) {
+        load_tiles(s0, j + 2);
+        store_tiles(s1, lk, (j + 1) & 1);
+        __syncthreads();
+        load_tiles(s1, j + 3);
+        store_tiles(s0, lk, j & 1);
+        __syncthreads();
+      }
+      if (j < nk) {
+        store_tiles(s1, lk, (j + 1) & 1);
+        __syncthreads();
+      }
+      return;
+    }
     Stage s0, s1, s2;
     Looked lk;
     load_tiles(s0, 0);
@@ -274,7 +345,7 @@ void w4_gemm_kernel(GemmParams p) {
   }
 
   // =========================== consumer waves ===========================
-  const int wm = wave & 1, wn = wave >> 1;
+  const int wm = wave % WAVES_M, wn = wave / WAVES_M;
   const int lrow = lane & 31;
   const int lk8 = 8 * (lane >> 5);
   const int rsub = 4 * (lane >> 5);
@@ -284,14 +355,17 @@ void w4_gemm_kernel(GemmParams p) {
 
   // ---- epilogue of one 32 x 32 block (i, j) of this wave's sub-tile.  Lane layout of a 32 x 32
   // fp32 MFMA result: column lane % 32, row 8 * (v / 4) + 4 * (lane / 32) + v % 4 for register v.
-  // this consumer wave's 2 KB of epilogue scratch in LDS: after the last K-step the A tile
-  // buffers are free (every producer store and consumer read is behind the final barrier)
+  // this consumer wave's 4 KB of epilogue scratch in LDS (keep-mask bytes at 0, a LoRA A slice
+  // at 2048): after the last K-step the A tile buffers are free (every producer store and
+  // consumer read is behind the final barrier)
+  constexpr int kEpiScratch = 4096;
+  static_assert(WAVES_M * WAVES_N * kEpiScratch <= BM * kStride * 2, "epilogue scratch");
   uint8_t* escr;
   if constexpr (REDUCE) {
-    __shared__ __attribute__((aligned(16))) uint8_t reduce_scr[4][2048];
+    __shared__ __attribute__((aligned(16))) uint8_t reduce_scr[WAVES_M * WAVES_N][kEpiScratch];
     escr = reduce_scr[wave];
   } else {
-    escr = reinterpret_cast<uint8_t*>(As[0]) + wave * 2048;
+    escr = reinterpret_cast<uint8_t*>(As[0]) + wave * kEpiScratch;
   }
 
   auto linear_block = [&](int i, int j, const f32x16& a) {
@@ -324,8 +398,22 @@ void w4_gemm_kernel(GemmParams p) {
         if (!TRANS) {
           rf = *reinterpret_cast<const f16x8*>(L.r + (n - L.n_begin) * p.rank + rc + lk8);
         } else {
-#pragma unroll
-          for (int e = 0; e < 8; ++e) rf[e] = L.r[(int64_t)(rc + lk8 + e) * N + n];
+          // A[rc .. rc + 16][nb .. nb + 32] staged row-major in LDS (one 16-byte load per lane,
+          // rows of 48 halves) and read back rank-contiguous with transposing reads, as the W
+          // tile of the main loop
+          f16* ascr = reinterpret_cast<f16*>(escr + 2048);
+          const f16x8 av = *reinterpret_cast<const f16x8*>(
+              L.r + (int64_t)(rc + (lane >> 2)) * N + nb + 8 * (lane & 3));
+          __builtin_amdgcn_wave_barrier();
+          *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = av;
+          __builtin_amdgcn_wave_barrier();
+          const f16* base = ascr + tr_k * 48 + tr_n;
+          const f16x4 lo4 = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(base)));
+          const f16x4 hi4 = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(base + 4 * 48)));
+          rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+          __builtin_amdgcn_wave_barrier();
         }
         lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
       }
@@ -395,46 +483,61 @@ void w4_gemm_kernel(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
 
-    auto compute = [&](int buf) {
+    struct Frags {
+      f16x8 a[TM], b[TN];
+    };
+    // the MFMA operands of K sub-step s (16 wide) of LDS buffer buf
+    auto load_frags = [&](Frags& f, int buf, int s) {
       const f16* as = As[buf];
       const f16* bs = Bs[buf];
 #pragma unroll
-      for (int s = 0; s < kBK / 16; ++s) {
-        f16x8 af[TM], bf[TN];
+      for (int i = 0; i < TM; ++i)
+        f.a[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk8);
 #pragma unroll
-        for (int i = 0; i < TM; ++i)
-          af[i] = *reinterpret_cast<const f16x8*>(as + (wm * WM + 32 * i + lrow) * kStride + 16 * s + lk8);
-#pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if (!TRANS) {
-            bf[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk8);
-          } else {
-            // ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives element b of
-            // the 4-element rows addressed by lanes a, a + 4, a + 8, a + 12.  Lane 4j + a of
-            // group G addresses row k = 16 s + 8 (G / 2) + 4 h + j, columns from
-            // 16 (G % 2) + 4 a, so lane l gets W[k0 + 8 (l / 32) + 4 h + 0..3][l % 32]: two
-            // reads (h = 0, 1) give the 8 consecutive k of the MFMA operand.
-            const f16* base = bs + (16 * s + tr_k) * B_LD + wn * WN + 32 * j + tr_n;
-            const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4*)(base)));
-            const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-                (__attribute__((address_space(3))) i16x4*)(base + 4 * B_LD)));
-            bf[j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-          }
+      for (int j = 0; j < TN; ++j) {
+        if (!TRANS) {
+          f.b[j] = *reinterpret_cast<const f16x8*>(bs + (wn * WN + 32 * j + lrow) * kStride + 16 * s + lk8);
+        } else {
+          // ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives element b of the
+          // 4-element rows addressed by lanes a, a + 4, a + 8, a + 12.  Lane 4j + a of group G
+          // addresses row k = 16 s + 8 (G / 2) + 4 h + j, columns from 16 (G % 2) + 4 a, so lane
+          // l gets W[k0 + 8 (l / 32) + 4 h + 0..3][l % 32]: two reads (h = 0, 1) give the 8
+          // consecutive k of the MFMA operand.
+          const f16* base = bs + (16 * s + tr_k) * B_LD + wn * WN + 32 * j + tr_n;
+          const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(base)));
+          const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4*)(base + 4 * B_LD)));
+          f.b[j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
         }
-#pragma unroll
-        for (int i = 0; i < TM; ++i)
-#pragma unroll
-          for (int j = 0; j < TN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(af[i], bf[j], acc[i][j], 0, 0, 0);
       }
     };
-    // the same number of barriers as the producers: 2 before step 0, one per step
+    auto mma = [&](const Frags& f) {
+#pragma unroll
+      for (int i = 0; i < TM; ++i)
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(f.a[i], f.b[j], acc[i][j], 0, 0, 0);
+    };
+    // The same number of barriers as the producers: 2 before step 0, one per step.  Software
+    // pipelined by one K sub-step: the operands of sub-step s + 1 are read while the MFMAs of s
+    // run.  The step's last operands are in registers at its barrier (which waits for every LDS
+    // read), so its last MFMAs run after the barrier, beside the first reads of the next step.
     __syncthreads();
     __syncthreads();
+    Frags f0, f1;
+    load_frags(f0, 0, 0);
     for (int kt = 0; kt < nk; ++kt) {
-      compute(kt & 1);
+      const int buf = kt & 1;
+      load_frags(f1, buf, 1);
+      mma(f0);
+      load_frags(f0, buf, 2);
+      mma(f1);
+      load_frags(f1, buf, 3);
+      mma(f0);
       __syncthreads();
+      if (kt + 1 < nk) load_frags(f0, buf ^ 1, 0);
+      mma(f1);
     }
 
     // split-K, first launch: store the fp32 partial tile (lane-major, so each register store is
@@ -530,51 +633,88 @@ Plan plan_for(int64_t M, int64_t N, int64_t K, int epi) {
   return pl;
 }
 
+// Two-phase path: with many row tiles, dequantising each W tile once per row tile (in LDS) costs
+// more LDS bandwidth than the MFMAs can hide, so for wide outputs (many W tiles) from
+// kTwoPhaseRows rows on, the weight is first dequantised once into the workspace at HBM rate
+// (nf4_dequant_kernel) and the GEMM reads fp16 W.  Measured on MI355X at M = 2048: gate|up
+// forward (N = 17920) 174 -> 153 us, down backward (N = 8960) 139 -> 132 us; the N = 1536 and
+// 2048 outputs are as fast or faster in one phase.
+constexpr int64_t kTwoPhaseRows = 512;
+constexpr int64_t kTwoPhaseCols = 4096;
+
+bool two_phase(int64_t M, int64_t N) { return M >= kTwoPhaseRows && N >= kTwoPhaseCols; }
+
+int64_t round256(int64_t b) { return (b + 255) / 256 * 256; }
+
 int64_t plan_workspace(const Plan& pl) {
   if (pl.splits <= 1) return 0;
   return pl.tiles * pl.splits * pl.bm * pl.bn * (int64_t)sizeof(float);
 }
 
-template <int BM, int BN, bool TRANS, int EPI>
+// Workspace of one GEMM: [split-K partial tiles | fp16 weight (two-phase)].
+int64_t gemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
+  if (M <= 0) return 0;
+  const int64_t part = plan_workspace(plan_for(M, N, K, epi));
+  const int64_t w16 = two_phase(M, N) ? N * K * (int64_t)sizeof(f16) : 0;
+  return w16 ? round256(part) + w16 : part;
+}
+
+template <int BM, int BN, bool TRANS, int EPI, bool F16B>
 int launch(GemmParams p, int splits, hipStream_t stream) {
   p.tiles_n = (int)(p.N / BN);
-  const int64_t tiles = ((p.M + BM - 1) / BM) * (int64_t)p.tiles_n;
+  p.tiles_m = (int)((p.M + BM - 1) / BM);
+  // fp16 W (two-phase) is 4x the bytes of packed W: with row tiles fastest, each XCD's run of
+  // tiles covers a band of columns for every row tile, so each XCD reads its slice of W once
+  p.m_fastest = F16B ? 1 : 0;
+  const int64_t tiles = (int64_t)p.tiles_m * p.tiles_n;
   p.splits = splits;
-  constexpr int blocks = (BM / 64) * (BN / 64);   // 32 x 32 blocks per consumer sub-tile
+  constexpr int blocks = 2 * (BN / 64);   // 32 x 32 blocks per consumer sub-tile (64 x BN/2)
   if (tiles <= 0 || tiles * (splits > blocks ? splits : blocks) > 0x7fffffff) return DK_ERR_INVALID;
   if (splits > 1 && EPI != EPI_LINEAR) return DK_ERR_INVALID;
-  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, false>), dim3((unsigned)(tiles * splits)),
-                     dim3(kThreads), 0, stream, p);
+  hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, false, F16B>),
+                     dim3((unsigned)(tiles * splits)), dim3(2 * role_threads<BM>()), 0, stream, p);
   DK_CHECK_LAUNCH();
   if constexpr (EPI == EPI_LINEAR) {
     if (splits > 1) {
-      hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, true>),
-                         dim3((unsigned)(tiles * blocks)), dim3(kRoleThreads), 0, stream, p);
+      hipLaunchKernelGGL((w4_gemm_kernel<BM, BN, TRANS, EPI, true, false>),
+                         dim3((unsigned)(tiles * blocks)), dim3(role_threads<BM>()), 0, stream, p);
       DK_CHECK_LAUNCH();
     }
   }
   return 0;
 }
 
-// Runs the plan; without a workspace the plan's split-K is dropped (same kernel, one split).
-template <bool TRANS, int EPI>
-int dispatch(GemmParams p, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  Plan pl = plan_for(p.M, p.N, p.K, EPI);
-  if (pl.splits > 1) {
-    if (ws == nullptr) {
-      pl.splits = 1;
-    } else {
-      if (ws_bytes < plan_workspace(pl)) return DK_ERR_WORKSPACE;
-      if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
-      p.part = reinterpret_cast<float*>(ws);
-    }
-  }
-  if (pl.bn == 128) return launch<128, 128, TRANS, EPI>(p, pl.splits, stream);
+template <bool TRANS, int EPI, bool F16B>
+int launch_plan(const Plan& pl, GemmParams p, hipStream_t stream) {
+  if (pl.bm == 256) return launch<256, 128, TRANS, EPI, F16B>(p, pl.splits, stream);
+  if (pl.bn == 128) return launch<128, 128, TRANS, EPI, F16B>(p, pl.splits, stream);
   if constexpr (EPI == EPI_SWIGLU_FWD) {
     return DK_ERR_INVALID;
   } else {
-    return launch<128, 64, TRANS, EPI>(p, pl.splits, stream);
+    return launch<128, 64, TRANS, EPI, F16B>(p, pl.splits, stream);
   }
+}
+
+// Runs the plan.  Without a workspace: one phase (W dequantised in LDS), no split-K.  With one
+// (at least gemm_workspace bytes): split-K partials and, on the two-phase shapes, the weight
+// dequantised to fp16 in the workspace first (both launches on `stream`, in order).
+template <bool TRANS, int EPI>
+int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  Plan pl = plan_for(p.M, p.N, p.K, EPI);
+  if (ws == nullptr) {
+    pl.splits = 1;
+    return launch_plan<TRANS, EPI, false>(pl, p, stream);
+  }
+  if (ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI)) return DK_ERR_WORKSPACE;
+  if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
+  if (pl.splits > 1) p.part = reinterpret_cast<float*>(ws);
+  if (!two_phase(p.M, p.N)) return launch_plan<TRANS, EPI, false>(pl, p, stream);
+  f16* w16 = reinterpret_cast<f16*>(reinterpret_cast<char*>(ws) + round256(plan_workspace(pl)));
+  if (int e = dk_nf4_dequant(w->packed, w->qabs, w->scale2, w->offset2, w->code2, w->nf4, w16,
+                             w->rows * w->cols / DK_QBLOCK, stream))
+    return e;
+  p.w16 = w16;
+  return launch_plan<TRANS, EPI, true>(pl, p, stream);
 }
 
 bool weight_ok(const dk_nf4_weight* w) {
@@ -602,7 +742,8 @@ int set_lora(GemmParams& p, const dk_lora_term* terms, int n_terms, int64_t rank
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_term& u = terms[t];
     if (!u.left || !u.right) return DK_ERR_INVALID;
-    if (!dk_aligned(u.left, 16) || (!backward && !dk_aligned(u.right, 16))) return DK_ERR_ALIGN;
+    if (!dk_aligned(u.left, 16) || !dk_aligned(u.right, 16)) return DK_ERR_ALIGN;
+    if (backward && u.mask && !dk_aligned(u.mask, 16)) return DK_ERR_ALIGN;
     LoraTerm& L = p.lora[t];
     L.z = (const f16*)u.left;
     L.r = (const f16*)u.right;
@@ -650,7 +791,7 @@ extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
   p.out = y;
   p.ldo = ldy;
   p.out_mode = DK_OUT_F16;
-  return dispatch<false, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
+  return dispatch<false, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
@@ -684,7 +825,7 @@ extern "C" int dk_w4_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m,
   p.out = dx;
   p.ldo = lddx;
   p.out_mode = out_mode;
-  return dispatch<true, EPI_LINEAR>(p, workspace, workspace_bytes, stream);
+  return dispatch<true, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
@@ -700,6 +841,7 @@ extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
 
 extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
                                        const dk_nf4_weight* w_gu, void* act, void* gu_out,
+                                       void* workspace, int64_t workspace_bytes,
                                        hipStream_t stream) {
   if (m < 0 || !weight_ok(w_gu) || !x || !act) return DK_ERR_INVALID;
   if (w_gu->rows % 128 || w_gu->cols % kBK || ldx < w_gu->cols) return DK_ERR_INVALID;
@@ -716,11 +858,12 @@ extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
   p.out = act;
   p.ldo = p.inter;
   p.gu = (f16*)gu_out;
-  return dispatch<false, EPI_SWIGLU_FWD>(p, nullptr, 0, stream);
+  return dispatch<false, EPI_SWIGLU_FWD>(p, w_gu, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
-                                     const dk_nf4_weight* w_down, void* gu, hipStream_t stream) {
+                                     const dk_nf4_weight* w_down, void* gu, void* workspace,
+                                     int64_t workspace_bytes, hipStream_t stream) {
   if (m < 0 || !weight_ok(w_down) || !dh || !gu) return DK_ERR_INVALID;
   if (w_down->cols % 64 || w_down->rows % kBK || lddh < w_down->rows) return DK_ERR_INVALID;
   if (!dk_aligned(dh, 16) || lddh % 8 || !dk_aligned(w_down->packed, 16)) return DK_ERR_ALIGN;
@@ -734,11 +877,20 @@ extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
   p.inter = w_down->cols;
   set_weight(p, w_down);
   p.gu = (f16*)gu;
-  return dispatch<true, EPI_SWIGLU_BWD>(p, nullptr, 0, stream);
+  return dispatch<true, EPI_SWIGLU_BWD>(p, w_down, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op) {
+  if (m <= 0 || !weight_ok(w)) return 0;
+  switch (op) {
+    case DK_OP_LINEAR_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_LINEAR);
+    case DK_OP_LINEAR_BWD_DX: return gemm_workspace(m, w->cols, w->rows, EPI_LINEAR);
+    case DK_OP_GATEUP_SWIGLU_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_SWIGLU_FWD);
+    case DK_OP_DOWN_SWIGLU_BWD: return gemm_workspace(m, w->cols, w->rows, EPI_SWIGLU_BWD);
+    default: return 0;
+  }
 }
 
 extern "C" int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward) {
-  if (m <= 0 || !weight_ok(w)) return 0;
-  const int64_t n = backward ? w->cols : w->rows, k = backward ? w->rows : w->cols;
-  return plan_workspace(plan_for(m, n, k, EPI_LINEAR));
+  return dk_w4_workspace(m, w, backward ? DK_OP_LINEAR_BWD_DX : DK_OP_LINEAR_FWD);
 }

@@ -80,10 +80,11 @@ _WS = {}
 _WS_LOCK = threading.Lock()
 
 
-def _workspace(w, m, backward, device):
-    """Split-K scratch for a fused linear (None when the shape needs none): one buffer per
-    (device, stream), grown on demand.  Kernels on one stream run in order, so they share it."""
-    nbytes = int(_lib.lib().dk_w4_linear_workspace(m, w.c_ref(), int(backward)))
+def _workspace(w, m, op, device):
+    """Scratch of a fused NF4 GEMM (split-K partials and the two-phase fp16 weight; None when the
+    shape needs none): one buffer per (device, stream), grown on demand.  Kernels on one stream
+    run in order, so they share it."""
+    nbytes = int(_lib.lib().dk_w4_workspace(m, w.c_ref(), int(op)))
     if nbytes == 0:
         return None, 0
     key = (device, torch.cuda.current_stream(device).cuda_stream)
@@ -151,7 +152,7 @@ def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=Non
     if out is None:
         out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
     _check16(out, "out", (m, w.rows))
-    ws, nbytes = _workspace(w, m, False, x.device)
+    ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_FWD, x.device)
     rc = _lib.lib().dk_w4_linear_fwd(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
                                      _lib.ptr(z), _lib.ptr(lora_B), r, float(lora_scale),
                                      _lib.ptr(out), out.stride(0), _lib.ptr(ws), nbytes,
@@ -204,7 +205,7 @@ def linear_forward_lora(x, w, bias=None, terms=(), out=None):
     if out is None:
         out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
     _check16(out, "out", (m, w.rows))
-    ws, nbytes = _workspace(w, m, False, x.device)
+    ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_FWD, x.device)
     rc = _lib.lib().dk_w4_linear_fwd_lora(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
                                           arr, n, rank, _lib.ptr(out), out.stride(0), _lib.ptr(ws),
                                           nbytes, _lib.stream_handle(x.device))
@@ -242,7 +243,7 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
     arr, n, rank, _keep = _lora_terms([(dz, a, mk, 0, 0, ks) for dz, a, mk, ks in terms], m,
                                       True, w.cols)
     out, mode = _dx_out(out, m, w, out_dtype, accumulate, dy.device)
-    ws, nbytes = _workspace(w, m, True, dy.device)
+    ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
     rc = _lib.lib().dk_w4_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), arr, n, rank,
                                              _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws),
                                              nbytes, _lib.stream_handle(dy.device))
@@ -270,7 +271,7 @@ def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, o
             raise ValueError("dz and lora_A must be contiguous")
     mask = _mask_ok(mask, (m, w.cols))
     out, mode = _dx_out(out, m, w, out_dtype, accumulate, dy.device)
-    ws, nbytes = _workspace(w, m, True, dy.device)
+    ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
     rc = _lib.lib().dk_w4_linear_bwd_dx(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), _lib.ptr(dz),
                                         _lib.ptr(lora_A), r, _lib.ptr(mask), float(keep_scale),
                                         _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws), nbytes,
@@ -329,8 +330,10 @@ def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True):
         _check16(gu, "gu", (m, 2 * inter))
         if not gu.is_contiguous():
             raise ValueError("gu must be contiguous")
+    ws, nbytes = _workspace(w_gu, m, _lib.DK_OP_GATEUP_SWIGLU_FWD, dev)
     rc = _lib.lib().dk_w4_gateup_swiglu_fwd(_lib.ptr(x), x.stride(0), m, w_gu.c_ref(), _lib.ptr(act),
-                                            _lib.ptr(gu), _lib.stream_handle(dev))
+                                            _lib.ptr(gu), _lib.ptr(ws), nbytes,
+                                            _lib.stream_handle(dev))
     _lib.check(rc, "dk_w4_gateup_swiglu_fwd")
     return act, gu
 
@@ -341,8 +344,10 @@ def down_swiglu_backward(dh, w_down, gu):
     _check16(gu, "gu", (dh.shape[0], 2 * w_down.cols))
     if dh.shape[1] != w_down.rows or not gu.is_contiguous():
         raise ValueError("down backward: shapes do not match")
+    ws, nbytes = _workspace(w_down, dh.shape[0], _lib.DK_OP_DOWN_SWIGLU_BWD, dh.device)
     rc = _lib.lib().dk_w4_down_swiglu_bwd(_lib.ptr(dh), dh.stride(0), dh.shape[0], w_down.c_ref(),
-                                          _lib.ptr(gu), _lib.stream_handle(dh.device))
+                                          _lib.ptr(gu), _lib.ptr(ws), nbytes,
+                                          _lib.stream_handle(dh.device))
     _lib.check(rc, "dk_w4_down_swiglu_bwd")
     return gu
 

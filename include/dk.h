@@ -93,9 +93,10 @@ int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const voi
  * x [m, w.cols] fp16 (row stride ldx elements), y [m, w.rows] fp16 (row stride ldy),
  * bias [w.rows] fp16 or NULL, z [m, rank] fp16 and lora_b [w.rows, rank] fp16, or both NULL.
  * w.rows % 64 == 0, w.cols % 64 == 0.
- * workspace: scratch of dk_w4_linear_workspace(m, w, 0) bytes, 256-byte aligned, for the
- * split-K partial tiles (a second launch on the same stream sums them in a fixed order and runs
- * the epilogue); NULL runs without split-K.  Launches that overlap in time must not share it. */
+ * workspace: scratch of dk_w4_workspace(m, w, DK_OP_LINEAR_FWD) bytes, 256-byte aligned, for
+ * the split-K partial tiles (a second launch on the same stream sums them in a fixed order and
+ * runs the epilogue) and the two-phase fp16 weight; NULL runs in one phase without split-K.
+ * Launches that overlap in time must not share it. */
 int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
                      const void* bias, const void* z, const void* lora_b, int64_t rank,
                      float lora_scale, void* y, int64_t ldy, void* workspace,
@@ -127,9 +128,21 @@ int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const dk_nf4_we
                           int64_t rank, void* y, int64_t ldy, void* workspace,
                           int64_t workspace_bytes, hipStream_t stream);
 
-/* Workspace bytes the fused linear needs at m rows (0: no split-K for this shape);
- * backward = 0 for dk_w4_linear_fwd, 1 for dk_w4_linear_bwd_dx.  No counterpart in the
- * reference (cuBLAS manages its own workspace); part of the drop-in for its torch.mm calls. */
+/* Workspace of the fused NF4 GEMMs.  No counterpart in the reference (cuBLAS manages its own);
+ * it stands in for the reference's fp16 dequant workspace (solution/fast_qwen.py:398-418).
+ * It holds split-K partial tiles and, from 512 rows on for outputs of at least 4096 columns, the
+ * weight dequantised to fp16 once per call (the "two-phase" path: dequant at HBM rate, then the
+ * MFMA GEMM on fp16 W), which at many row tiles is faster than dequantising each W tile again for
+ * every row tile.  Without a
+ * workspace (NULL) every entry point still runs, in one phase with the dequant in LDS.
+ * Bytes needed at m rows for operation op (0: none). */
+#define DK_OP_LINEAR_FWD 0         /* dk_w4_linear_fwd, dk_w4_linear_fwd_lora */
+#define DK_OP_LINEAR_BWD_DX 1      /* dk_w4_linear_bwd_dx, dk_w4_linear_bwd_dx_lora */
+#define DK_OP_GATEUP_SWIGLU_FWD 2  /* dk_w4_gateup_swiglu_fwd */
+#define DK_OP_DOWN_SWIGLU_BWD 3    /* dk_w4_down_swiglu_bwd */
+int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op);
+
+/* dk_w4_workspace(m, w, backward ? DK_OP_LINEAR_BWD_DX : DK_OP_LINEAR_FWD). */
 int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward);
 
 /* Output modes of the backward dX GEMM. */
@@ -144,7 +157,7 @@ int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward);
  *   dX = fp32(fp16(dY W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0)
  * dy [m, w.rows] fp16 (row stride lddy), dx [m, w.cols] (row stride lddx) in out_mode,
  * dz [m, rank] fp16, lora_a [rank, w.cols] fp16 and mask [m, w.cols] uint8, or all NULL.
- * workspace as for dk_w4_linear_fwd, sized by dk_w4_linear_workspace(m, w, 1). */
+ * workspace as for dk_w4_linear_fwd, sized by dk_w4_workspace(m, w, DK_OP_LINEAR_BWD_DX). */
 int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m, const dk_nf4_weight* w,
                         const void* dz, const void* lora_a, int64_t rank, const uint8_t* mask,
                         float keep_scale, void* dx, int64_t lddx, int out_mode,
@@ -179,16 +192,19 @@ int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x, co
  *   g = fp16(X Wg^T), u = fp16(X Wu^T), act = fp16(silu(g) * u)
  * w_gu is [2 * inter, k]: the gate rows then the up rows (the repacked layer's gate|up order,
  * solution/k_nf4.py:7-9).  act [m, inter]; gu_out [m, 2 * inter] receives [g | u] when not NULL
- * (the saved gate|up of the backward).  inter % 32 == 0, k % 64 == 0. */
+ * (the saved gate|up of the backward).  inter % 32 == 0, k % 64 == 0.  workspace as for
+ * dk_w4_linear_fwd, sized by dk_w4_workspace(m, w_gu, DK_OP_GATEUP_SWIGLU_FWD), or NULL. */
 int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w_gu,
-                            void* act, void* gu_out, hipStream_t stream);
+                            void* act, void* gu_out, void* workspace, int64_t workspace_bytes,
+                            hipStream_t stream);
 
 /* Down-projection backward fused with the gated-SiLU backward.  Replaces dact = dh W_d and
  * gated_silu_backward (solution/fast_qwen.py:1310-1312; solution/k_mlp.py:32-47):
  *   dact = fp16(dh W_d);  gu <- [dact * u * sig * (1 + g * (1 - sig)) | dact * silu(g)]
- * dh [m, w_down.rows] fp16, w_down [d_model, inter], gu [m, 2 * inter] in/out. */
+ * dh [m, w_down.rows] fp16, w_down [d_model, inter], gu [m, 2 * inter] in/out.  workspace as
+ * for dk_w4_linear_fwd, sized by dk_w4_workspace(m, w_down, DK_OP_DOWN_SWIGLU_BWD), or NULL. */
 int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const dk_nf4_weight* w_down,
-                          void* gu, hipStream_t stream);
+                          void* gu, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -34,6 +34,15 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 100, 8, ctypes.byref(w), None, None, None, 0,
                                 2.0, ctypes.c_void_p(16), 100, None, 0, None) == _lib.DK_ERR_INVALID
     assert lib.dk_w4_linear_workspace(2048, ctypes.byref(w), 0) == 0
+    # workspace sizes (no device access): split-K partials, and the fp16 weight of the two-phase
+    # path (from 512 rows on, outputs of 4096 columns or more)
+    wq = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 1536, 1536)
+    wgu = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 17920, 1536)
+    assert lib.dk_w4_workspace(2048, ctypes.byref(wq), _lib.DK_OP_LINEAR_FWD) == 0
+    assert lib.dk_w4_workspace(256, ctypes.byref(wq), _lib.DK_OP_LINEAR_FWD) == 48 * 3 * 128 * 64 * 4
+    assert lib.dk_w4_workspace(2048, ctypes.byref(wgu), _lib.DK_OP_GATEUP_SWIGLU_FWD) == 17920 * 1536 * 2
+    assert lib.dk_w4_workspace(256, ctypes.byref(wgu), _lib.DK_OP_GATEUP_SWIGLU_FWD) == 0
+    assert lib.dk_w4_workspace(2048, ctypes.byref(wq), 7) == 0
     # misaligned packed pointer and fp16 output (both need 16 bytes)
     assert lib.dk_nf4_dequant(ctypes.c_void_p(2), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),

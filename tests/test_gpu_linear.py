@@ -216,14 +216,17 @@ def test_lora_term_argument_errors(torch):
         w4linear.linear_forward_lora(x, w, None, [(z, b, 384, 640, 2.0)])
 
 
-def test_mlp_config2(torch):
+@pytest.mark.parametrize("m", [2048, 700, 300])
+def test_mlp_config2(torch, m):
+    """M = 2048 and 700 take the two-phase path (gate|up and down^T dequantised to fp16 once);
+    300 rows stay in one phase."""
     from decentrik_prime_amd import w4linear
     from oracle import linear, mlp
-    log("config 2: gate|up SwiGLU forward + down, M=2048")
+    log(f"config 2: gate|up SwiGLU forward + down, M={m}")
     I = 8960
     qg = nf4_weight(2 * I, 1536, seed=104)          # gate rows then up rows
     qd = nf4_weight(1536, I, seed=105)
-    x = np.random.default_rng(3).standard_normal((2048, 1536)).astype(F16)
+    x = np.random.default_rng(3).standard_normal((m, 1536)).astype(F16)
     gu_ref, h_ref, _ = mlp.mlp_fwd(x, qg["deq"], qd["deq"])
     act, gu = w4linear.gateup_swiglu_forward(cuda16(x), to_w4(qg))
     torch.cuda.synchronize()
@@ -234,7 +237,7 @@ def test_mlp_config2(torch):
     y_ref = linear.mm16(host(act), qd["deq"].T)
     assert_close(host(y), y_ref, RTOL, ATOL, "down")
     # backward: down^T fused with the SwiGLU backward, then gate|up^T
-    dh = (np.random.default_rng(4).standard_normal((2048, 1536)) * 1e-2).astype(F16)
+    dh = (np.random.default_rng(4).standard_normal((m, 1536)) * 1e-2).astype(F16)
     gu_np = host(gu)
     dgu_ref, dx_ref = mlp.mlp_bwd(dh, gu_np, qg["deq"], qd["deq"])
     w4linear.down_swiglu_backward(cuda16(dh), to_w4(qd), gu)
