@@ -1,14 +1,14 @@
 // Rank-r LoRA kernels around the NF4 linear (r = 16 in the reference; r in {16, 32, 48, 64}).
 //
-// Row reductions (MFMA v_mfma_f32_16x16x32_f16; a workgroup owns 16 token rows and its 4 waves
+// Row reductions (MFMA v_mfma_f32_16x16x32_f16; a workgroup owns 16 token rows and its 8 waves
 // split K, summed in a fixed order through LDS):
 //   down:  Xd = fp16(mask ? fp32(x) * ks : 0);  z[m][r] = fp16(sum_k Xd[m][k] A[r][k])
 //          (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944)
 //   dz:    dz[m][r] = fp16(fp32(fp16(sum_n dY[m][n] B[n][r])) * s)
 //          (solution/fast_qwen.py:1370, 1373: mm(gq, B).mul_(s) on an fp16 tensor)
-//          B is staged transposed in LDS so its MFMA operand is K-contiguous.
+//          B is staged in LDS as stored and read K-contiguous with transposing LDS reads.
 // Column reductions over the token rows, in two deterministic passes (fixed-order partial sums
-// per 64-row chunk into a workspace, then one finalize pass):
+// per 128-row chunk into a workspace, MFMA on LDS-staged tiles, then one finalize pass):
 //   dB[n][r] = fp32(fp16(sum_m dY[m][n] z[m][r])) * s       (solution/fast_qwen.py:1369)
 //   dA[r][k] = fp32(fp16(sum_m dz[m][r] Xd[m][k]))           (solution/fast_qwen.py:1371)
 // Products of two fp16 values are exact in fp32; only the order of the fp32 sums differs from a
@@ -20,7 +20,8 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / 64;
 constexpr int kRowTile = 16;     // rows per workgroup of the row reductions
-constexpr int kChunkRows = 64;   // rows per partial sum of the column reductions
+constexpr int kRowThreads = 512; // 8 waves split K in the row reductions
+constexpr int kChunkRows = 128;  // rows per partial sum of the column reductions
 constexpr int kColsPerBlock = 128;
 
 __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, float ks) {
@@ -36,57 +37,88 @@ __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, fl
 
 // MODE 0 (down): out[m][r] = fp16(sum_k Xd[m][k] W[r][k]), W = A [R][cols].
 // MODE 1 (dz):   out[m][r] = fp16(fp16(sum_k in[m][k] W[k][r]) * scale), W = B [cols][R], staged
-//                transposed in LDS.
+//                row-major in LDS and read k-contiguous with ds_read_b64_tr_b16 (see
+//                lora_cols_kernel for the lane layout).
 // 16x16x32 MFMA operand layout: lane l holds row/column l % 16 and k = 8 * (l / 16) + [0, 8);
-// the result register v of lane l is row 4 * (l / 16) + v, column l % 16.
-template <int R, int MODE>
-__global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restrict__ in,
-                                                             int64_t ld,
-                                                             const uint8_t* __restrict__ mask,
-                                                             float ks, const f16* __restrict__ wt,
-                                                             float scale, f16* __restrict__ out,
-                                                             int64_t rows, int64_t cols) {
+// the result register v of lane l is row 4 * (l / 16) + v, column l % 16.  The 8 waves split K
+// and issue the loads of kBatch steps before their MFMAs; their sums are added in a fixed order.
+template <int R, int MODE, bool MASKED>
+__global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(const f16* __restrict__ in,
+                                                                int64_t ld,
+                                                                const uint8_t* __restrict__ mask,
+                                                                float ks, const f16* __restrict__ wt,
+                                                                float scale, f16* __restrict__ out,
+                                                                int64_t rows, int64_t cols) {
   constexpr int RB = R / 16;
-  constexpr int KC = 1024;  // columns of B^T staged per pass (MODE 1)
-  __shared__ float red[kWaves * 16 * R];
-  __shared__ __attribute__((aligned(16))) f16 wT[MODE == 1 ? R * (KC + 8) : 8];
+  constexpr int NW = kRowThreads / 64;
+  constexpr int kBatch = 4;
+  constexpr int KC = 768;        // rows of B staged per pass (MODE 1)
+  constexpr int BLD = R + 8;     // halves per staged B row
+  __shared__ float red[NW * 16 * R];
+  __shared__ __attribute__((aligned(16))) f16 Bs[MODE == 1 ? KC * BLD : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   const int64_t row0 = (int64_t)blockIdx.x * kRowTile;
   const int lr = lane & 15, lk = 8 * (lane >> 4);
   const int64_t m = row0 + lr < rows ? row0 + lr : rows - 1;   // clamped: its sums are not stored
+  const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
   f32x4 acc[RB];
 #pragma unroll
   for (int b = 0; b < RB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
 
   if (MODE == 0) {
-    for (int64_t s = w; s < cols / 32; s += kWaves) {
-      const int64_t k = s * 32 + lk;
-      f16x8 a = *reinterpret_cast<const f16x8*>(in + m * ld + k);
-      if (mask) a = dropout8(a, mask + m * cols + k, ks);
+    const int64_t steps = cols / 32;
+    for (int64_t s0 = w; s0 < steps; s0 += NW * kBatch) {
+      f16x8 a[kBatch], bw[kBatch][RB];
 #pragma unroll
-      for (int b = 0; b < RB; ++b) {
-        const f16x8 bw = *reinterpret_cast<const f16x8*>(wt + (int64_t)(16 * b + lr) * cols + k);
-        acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, acc[b], 0, 0, 0);
+      for (int u = 0; u < kBatch; ++u) {
+        const int64_t s = s0 + (int64_t)u * NW;
+        const int64_t k = (s < steps ? s : steps - 1) * 32 + lk;   // clamped; not accumulated
+        a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + k);
+        if (MASKED) a[u] = dropout8(a[u], mask + m * cols + k, ks);
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+          bw[u][b] = *reinterpret_cast<const f16x8*>(wt + (int64_t)(16 * b + lr) * cols + k);
+      }
+#pragma unroll
+      for (int u = 0; u < kBatch; ++u) {
+        if (s0 + (int64_t)u * NW >= steps) break;
+#pragma unroll
+        for (int b = 0; b < RB; ++b)
+          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bw[u][b], acc[b], 0, 0, 0);
       }
     }
   } else {
     for (int64_t c0 = 0; c0 < cols; c0 += KC) {
       const int kc = (int)(cols - c0 < KC ? cols - c0 : KC);
-      __syncthreads();  // the previous pass has finished reading wT
-      // B^T columns [c0, c0 + kc) into LDS: 8 consecutive r of one k per thread, scattered
-      for (int i = tid; i < kc * (R / 8); i += kThreads) {
+      __syncthreads();  // the previous pass has finished reading Bs
+      for (int i = tid; i < kc * (R / 8); i += kRowThreads) {
         const int kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
-        const f16x8 v = *reinterpret_cast<const f16x8*>(wt + (c0 + kk) * R + r8);
-#pragma unroll
-        for (int e = 0; e < 8; ++e) wT[(r8 + e) * (KC + 8) + kk] = v[e];
+        *reinterpret_cast<f16x8*>(Bs + kk * BLD + r8) =
+            *reinterpret_cast<const f16x8*>(wt + (c0 + kk) * R + r8);
       }
       __syncthreads();
-      for (int s = w; s < kc / 32; s += kWaves) {
-        const f16x8 a = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
+      const int steps = kc / 32;
+      for (int s0 = w; s0 < steps; s0 += NW * kBatch) {
+        f16x8 a[kBatch];
 #pragma unroll
-        for (int b = 0; b < RB; ++b) {
-          const f16x8 bw = *reinterpret_cast<const f16x8*>(wT + (16 * b + lr) * (KC + 8) + s * 32 + lk);
-          acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bw, acc[b], 0, 0, 0);
+        for (int u = 0; u < kBatch; ++u) {
+          const int s = s0 + u * NW < steps ? s0 + u * NW : steps - 1;
+          a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
+        }
+#pragma unroll
+        for (int u = 0; u < kBatch; ++u) {
+          const int s = s0 + u * NW;
+          if (s >= steps) break;
+#pragma unroll
+          for (int b = 0; b < RB; ++b) {
+            const f16* base = Bs + (s * 32 + trow) * BLD + 16 * b + tcol;
+            const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(base)));
+            const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                (__attribute__((address_space(3))) i16x4*)(base + 4 * BLD)));
+            const f16x8 bw = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+            acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bw, acc[b], 0, 0, 0);
+          }
         }
       }
     }
@@ -96,90 +128,114 @@ __global__ __launch_bounds__(kThreads) void lora_rows_kernel(const f16* __restri
 #pragma unroll
     for (int v = 0; v < 4; ++v) red[(w * 16 + 4 * (lane >> 4) + v) * R + 16 * b + lr] = acc[b][v];
   __syncthreads();
-  for (int i = tid; i < 16 * R; i += kThreads) {
+  for (int i = tid; i < 16 * R; i += kRowThreads) {
     const int rr = i / R, r = i % R;
     if (row0 + rr >= rows) continue;
     float sum = 0.0f;
 #pragma unroll
-    for (int ww = 0; ww < kWaves; ++ww) sum += red[(ww * 16 + rr) * R + r];
+    for (int ww = 0; ww < NW; ++ww) sum += red[(ww * 16 + rr) * R + r];
     out[(row0 + rr) * R + r] = MODE == 0 ? dk_h(sum) : dk_h(__fmul_rn((float)dk_h(sum), scale));
   }
 }
 
-// Partial column sums over one 64-row chunk: part[chunk][n][r] = sum_m P[m][n] Q[m][r].  A block
-// owns 128 columns (two per lane); its 4 waves take 16 rows each, all 16 loads in flight before
-// the first use, and are summed in a fixed order through LDS.  DROP: P is the dropout of x (mask
-// may be null).
+// Partial column sums over one kChunkRows-row chunk: part[chunk][c][r] = sum_m P[m][c] Q[m][r]
+// (P = dropout(x) with the keep-mask when DROP).  A workgroup stages its P tile (kChunkRows rows x
+// 128 columns, 16-byte coalesced loads, the dropout applied on the way) and the Q rows in LDS
+// row-major, then v_mfma_f32_16x16x32_f16 runs with both operands read M-contiguous by
+// ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives element b of the 4-element
+// rows addressed by lanes a, a + 4, a + 8, a + 12, so lane l addressing row
+// 8 (l / 16) + 4 h + (l % 16) / 4, column 4 (l % 4) receives rows 8 (l / 16) + 4 h + 0..3 of
+// column l % 16, and two reads (h = 0, 1) give the 8 consecutive rows of the MFMA operand.
 template <int R, bool DROP>
 __global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restrict__ P, int64_t ld,
                                                              const uint8_t* __restrict__ mask,
                                                              float ks, const f16* __restrict__ Q,
                                                              float* __restrict__ part,
                                                              int64_t rows, int64_t cols) {
-  constexpr int RW = kChunkRows / kWaves;  // rows per wave
-  __shared__ __attribute__((aligned(16))) float qs[kChunkRows][R];
-  __shared__ float red[kWaves - 1][64][2 * R + 1];
-  const int64_t chunk = blockIdx.y;
-  const int64_t r0 = chunk * kChunkRows;
-  const int nrows = (int)(rows - r0 < kChunkRows ? rows - r0 : kChunkRows);
-  for (int i = threadIdx.x; i < kChunkRows * R; i += kThreads) {
-    const int rr = i / R, r = i % R;
-    qs[rr][r] = rr < nrows ? (float)Q[(r0 + rr) * R + r] : 0.0f;
-  }
-  __syncthreads();
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-  const int64_t n = (int64_t)blockIdx.x * kColsPerBlock + 2 * lane;
-  const bool live = n < cols;
-  const int64_t nc = live ? n : 0;
-  float p0[RW], p1[RW];
+  constexpr int PLD = kColsPerBlock + 16;   // halves per staged P row
+  constexpr int QLD = R + 16;               // halves per staged Q row
+  constexpr int P_CHUNKS = kChunkRows * kColsPerBlock / 8 / kThreads;   // 16-byte chunks per thread
+  __shared__ __attribute__((aligned(16))) f16 Ps[kChunkRows * PLD];
+  __shared__ __attribute__((aligned(16))) f16 Qs[kChunkRows * QLD];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  const int64_t c0 = (int64_t)blockIdx.x * kColsPerBlock;
+  const int64_t r0 = (int64_t)blockIdx.y * kChunkRows;
+  // P tile: every load issued before the first store (rows past the end read as zero)
+  f16x8 pv[P_CHUNKS];
+  u32x2 mv[P_CHUNKS];
 #pragma unroll
-  for (int u = 0; u < RW; ++u) {
-    const int rr = w * RW + u;
-    const int rc = rr < nrows ? rr : nrows - 1;
-    const int64_t m = r0 + rc;
-    const f16x2 pv = *reinterpret_cast<const f16x2*>(P + m * ld + nc);
-    float a = (float)pv[0], b = (float)pv[1];
-    if (DROP && mask) {
-      const uint32_t mk = *reinterpret_cast<const uint16_t*>(mask + m * cols + nc);
-      a = (mk & 0xffu) ? (float)dk_h(__fmul_rn(a, ks)) : 0.0f;
-      b = (mk >> 8) ? (float)dk_h(__fmul_rn(b, ks)) : 0.0f;
-    }
-    p0[u] = rr < nrows ? a : 0.0f;
-    p1[u] = rr < nrows ? b : 0.0f;
-  }
-  float acc0[R], acc1[R];
+  for (int i = 0; i < P_CHUNKS; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / (kColsPerBlock / 8), c8 = c % (kColsPerBlock / 8);
+    const int64_t m = r0 + row;
+    if (m < rows && c0 + 8 * c8 < cols) {
+      pv[i] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + 8 * c8);
+      if (DROP) mv[i] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + 8 * c8);
+    } else {
 #pragma unroll
-  for (int r = 0; r < R; ++r) acc0[r] = acc1[r] = 0.0f;
-#pragma unroll
-  for (int u = 0; u < RW; ++u) {
-    const float* q = qs[w * RW + u];
-#pragma unroll
-    for (int r = 0; r < R; ++r) {
-      acc0[r] += p0[u] * q[r];
-      acc1[r] += p1[u] * q[r];
+      for (int e = 0; e < 8; ++e) pv[i][e] = (f16)0.0f;
+      if (DROP) mv[i] = u32x2{0u, 0u};
     }
   }
-  if (w > 0) {
+  for (int i = tid; i < kChunkRows * R / 8; i += kThreads) {
+    const int row = i / (R / 8), r8 = (i % (R / 8)) * 8;
+    const int64_t m = r0 + row;
+    f16x8 q;
+    if (m < rows) {
+      q = *reinterpret_cast<const f16x8*>(Q + m * R + r8);
+    } else {
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      red[w - 1][lane][r] = acc0[r];
-      red[w - 1][lane][R + r] = acc1[r];
+      for (int e = 0; e < 8; ++e) q[e] = (f16)0.0f;
     }
+    *reinterpret_cast<f16x8*>(Qs + row * QLD + r8) = q;
   }
-  __syncthreads();
-  if (w == 0 && live) {
-    float* dst = part + (chunk * cols + n) * R;
 #pragma unroll
-    for (int r = 0; r < R; ++r) {
-      float s0 = acc0[r], s1 = acc1[r];
+  for (int i = 0; i < P_CHUNKS; ++i) {
+    const int c = tid + kThreads * i;
+    const int row = c / (kColsPerBlock / 8), c8 = c % (kColsPerBlock / 8);
+    f16x8 v = pv[i];
+    if (DROP) {
 #pragma unroll
-      for (int v = 0; v < kWaves - 1; ++v) {
-        s0 += red[v][lane][r];
-        s1 += red[v][lane][R + r];
+      for (int e = 0; e < 8; ++e) {
+        const uint32_t keep = (mv[i][e >> 2] >> (8 * (e & 3))) & 0xffu;
+        v[e] = keep ? dk_h(__fmul_rn((float)v[e], ks)) : (f16)0.0f;
       }
-      dst[r] = s0;
-      dst[R + r] = s1;
     }
+    *reinterpret_cast<f16x8*>(Ps + row * PLD + 8 * c8) = v;
+  }
+  __syncthreads();
+  // wave w: column blocks 2w, 2w + 1 (16 columns each), all R / 16 rank blocks
+  const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
+  auto tr8 = [&](const f16* base, int ldh) {
+    const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(base)));
+    const f16x4 hi = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+        (__attribute__((address_space(3))) i16x4*)(base + 4 * ldh)));
+    return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+  };
+#pragma unroll
+  for (int cb = 0; cb < 2; ++cb) {
+    const int cbase = (2 * w + cb) * 16;
+    f32x4 acc[R / 16];
+#pragma unroll
+    for (int rb = 0; rb < R / 16; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+    for (int kb = 0; kb < kChunkRows / 32; ++kb) {
+      const f16x8 a = tr8(Ps + (32 * kb + trow) * PLD + cbase + tcol, PLD);
+#pragma unroll
+      for (int rb = 0; rb < R / 16; ++rb) {
+        const f16x8 bq = tr8(Qs + (32 * kb + trow) * QLD + 16 * rb + tcol, QLD);
+        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, acc[rb], 0, 0, 0);
+      }
+    }
+    // result register v of lane l: column cbase + 4 (l / 16) + v, rank 16 rb + l % 16
+#pragma unroll
+    for (int rb = 0; rb < R / 16; ++rb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) {
+        const int64_t c = c0 + cbase + 4 * (lane >> 4) + v;
+        if (c < cols) part[((int64_t)blockIdx.y * cols + c) * R + 16 * rb + (lane & 15)] = acc[rb][v];
+      }
   }
 }
 
@@ -208,19 +264,26 @@ __global__ __launch_bounds__(kThreads) void lora_finalize_kernel(const float* __
   if (TRANSPOSE) out[r * cols + n] = v; else out[i] = v;
 }
 
-template <int MODE>
-int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
-                  float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
-  const dim3 grid((unsigned)((rows + kRowTile - 1) / kRowTile));
+template <int MODE, bool MASKED>
+int rows_launch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
+                float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
+  const dim3 grid((unsigned)((rows + kRowTile - 1) / kRowTile)), block(kRowThreads);
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE>), grid, dim3(kThreads), 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
     default: return DK_ERR_INVALID;
   }
   DK_CHECK_LAUNCH();
   return 0;
+}
+
+template <int MODE>
+int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
+                  float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
+  if (MODE == 0 && mask) return rows_launch<MODE, true>(R, stream, in, ld, mask, ks, wt, scale, out, rows, cols);
+  return rows_launch<MODE, false>(R, stream, in, ld, mask, ks, wt, scale, out, rows, cols);
 }
 
 template <bool DROP>
@@ -286,7 +349,9 @@ extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const 
                      dim3(kThreads), 0, stream, part, chunks, n_out, rank, lora_scale, db);
   DK_CHECK_LAUNCH();
   // dA = fp32(fp16(dz^T Xd))
-  e = cols_dispatch<true>(rank, stream, (const f16*)x, k, mask, ks, (const f16*)dz, part, m, k);
+  e = mask ? cols_dispatch<true>(rank, stream, (const f16*)x, k, mask, ks, (const f16*)dz, part, m, k)
+           : cols_dispatch<false>(rank, stream, (const f16*)x, k, nullptr, 1.0f, (const f16*)dz, part,
+                                  m, k);
   if (e) return e;
   hipLaunchKernelGGL(lora_finalize_kernel<true>, dim3((unsigned)((k * rank + kThreads - 1) / kThreads)),
                      dim3(kThreads), 0, stream, part, chunks, k, rank, 1.0f, da);

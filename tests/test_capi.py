@@ -50,7 +50,7 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_nf4_dequant(ctypes.c_void_p(4), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
-    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 32 * 1536 * 16 * 4
+    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * 1536 * 16 * 4
     assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
     with pytest.raises(ValueError):
         _lib.check(_lib.DK_ERR_INVALID, "probe")
