@@ -58,22 +58,43 @@ def kernel_table(torch, st, reps, only=None):
     dzq = (torch.randn(m, r, device=x.device) * 1e-2).half()
     dzv = (torch.randn(m, r, device=x.device) * 1e-2).half()
     g = lambda mm, n, k: 2.0 * mm * n * k  # noqa: E731
-    rows = [
-        # name, fn, flops, bytes, launches per step (per layer)
-        ("w4_gateup_swiglu_fwd", lambda: W.gateup_swiglu_forward(x, L["gu"], act=st.act, gu=gu),
-         g(m, 2 * I, D), None, 1),
-        ("w4_linear_fwd down", lambda: W.linear_forward(st.act, L["d"], out=o["y"]), g(m, D, I), None, 1),
-        ("w4_linear_fwd qkv+lora", lambda: W.linear_forward_lora(x, L["qkv"], lo["bias"], st.qkv_terms(0),
-                                                                 out=o["qkv"]),
-         g(m, QKV, D) + g(m, D, r) + g(m, KV, r), None, 1),
-        ("w4_linear_fwd o", lambda: W.linear_forward(x, L["o"], out=o["o"]), g(m, D, D), None, 1),
-        ("w4_down_swiglu_bwd", lambda: W.down_swiglu_backward(dy["d"], L["d"], gu), g(m, I, D), None, 1),
-        ("w4_linear_bwd_dx gate|up", lambda: W.linear_backward_dx(gu, L["gu"], out=st.dx_mlp),
-         g(m, D, 2 * I), None, 1),
-        ("w4_linear_bwd_dx o", lambda: W.linear_backward_dx(dy["o"], L["o"], out=st.dx_o), g(m, D, D), None, 1),
-        ("w4_linear_bwd_dx qkv+lora", lambda: W.linear_backward_dx_lora(
+    # fp16 copies of layer 0's weights: the operand of the dk_h16_* entry points, as the
+    # side-stream dequant leaves it
+    h = {k: L[k].dequantize() for k in st.KINDS}
+    dq_bytes = lambda w: w.rows * w.cols * (0.5 + 1 / 64 + 8 / 16384 + 2)  # noqa: E731
+    gemms = [
+        # kind, name suffix, fn(w16), flops
+        ("gu", "_gateup_swiglu_fwd",
+         lambda w16: W.gateup_swiglu_forward(x, L["gu"], act=st.act, gu=gu, w16=w16), g(m, 2 * I, D)),
+        ("d", "_linear_fwd down", lambda w16: W.linear_forward(st.act, L["d"], out=o["y"], w16=w16),
+         g(m, D, I)),
+        ("qkv", "_linear_fwd qkv+lora", lambda w16: W.linear_forward_lora(
+            x, L["qkv"], lo["bias"], st.qkv_terms(0), out=o["qkv"], w16=w16),
+         g(m, QKV, D) + g(m, D, r) + g(m, KV, r)),
+        ("o", "_linear_fwd o", lambda w16: W.linear_forward(x, L["o"], out=o["o"], w16=w16), g(m, D, D)),
+        ("d", "_down_swiglu_bwd", lambda w16: W.down_swiglu_backward(dy["d"], L["d"], gu, w16=w16),
+         g(m, I, D)),
+        ("gu", "_linear_bwd_dx gate|up",
+         lambda w16: W.linear_backward_dx(gu, L["gu"], out=st.dx_mlp, w16=w16), g(m, D, 2 * I)),
+        ("o", "_linear_bwd_dx o",
+         lambda w16: W.linear_backward_dx(dy["o"], L["o"], out=st.dx_o, w16=w16), g(m, D, D)),
+        ("qkv", "_linear_bwd_dx qkv+lora", lambda w16: W.linear_backward_dx_lora(
             dy["qkv"], L["qkv"], [(dzq, lo["Aq"], lo["mq"], ks), (dzv, lo["Av"], lo["mv"], ks)],
-            out=st.dx_qkv), g(m, D, QKV) + 2 * g(m, D, r), None, 1),
+            out=st.dx_qkv, w16=w16), g(m, D, QKV) + 2 * g(m, D, r)),
+    ]
+    rows = []
+    for kind, suffix, fn, flops in gemms:
+        # both forms; the one the step runs counts once per layer, the other is reported only
+        used = "h16" if kind in st.ahead else "w4"
+        rows.append(("w4" + suffix, (lambda f: lambda: f(None))(fn), flops, None,
+                     int(used == "w4")))
+        rows.append(("h16" + suffix, (lambda f, k: lambda: f(h[k]))(fn, kind), flops, None,
+                     int(used == "h16")))
+    for kind in st.KINDS:
+        # the side-stream dequant of one weight (HBM-bound; overlaps the GEMMs in the step)
+        rows.append((f"dequant {kind}", (lambda k: lambda: L[k].dequantize(out=h[k]))(kind), 0.0,
+                     dq_bytes(L[kind]), 0))
+    rows += [
         ("lora_down", lambda: W.lora_down(x, lo["Aq"], lo["mq"], ks, out=z["q"]), g(m, r, D),
          m * D * 3 + r * D * 2 + m * r * 2, 2),
         ("lora_grads q", lambda: W.lora_grads(dy["qkv"][:, :D], z["q"], x, lo["Bq"], s, lo["mq"], ks),
@@ -87,12 +108,15 @@ def kernel_table(torch, st, reps, only=None):
             continue
         ms = time_op(torch, fn, reps)
         row = {"kernel": name, "avg_us": round(ms * 1e3, 2), "launches_per_layer": per_layer,
-               "gflop": round(flops / 1e9, 3), "tflops": round(flops / (ms * 1e-3) / 1e12, 1),
-               "frac_fp16_peak": round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)}
+               "gflop": round(flops / 1e9, 3)}
+        if flops:
+            row["tflops"] = round(flops / (ms * 1e-3) / 1e12, 1)
+            row["frac_fp16_peak"] = round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)
         if nbytes:
             row["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         out.append(row)
     gu.copy_(gu_save)
+    del h
     return out
 
 
@@ -364,17 +388,20 @@ def main():
     kernels = None
     if not args.no_kernels:
         # each operator in isolation first: the one with the largest share of the step is the
-        # dominant kernel, whose launches are then timed inside the timed steps
+        # dominant kernel, whose launches are then timed inside the last timed step (timing
+        # events in every step would cost the step about 3%)
         kernels = kernel_table(torch, st, args.reps)
         dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
-        st.probe = (dom["kernel"], [])
+        probe = (dom["kernel"], [])
         print(f"[bench] kernel table done; dominant operator {dom['kernel']}", file=sys.stderr,
               flush=True)
     torch.cuda.synchronize()
     e0, e1 = _events(torch)
     t0 = time.perf_counter()
     e0.record()
-    for _ in range(args.steps):
+    for k in range(args.steps):
+        if kernels is not None and k == args.steps - 1:
+            st.probe = probe
         st.step()
     e1.record()
     torch.cuda.synchronize()
@@ -405,8 +432,8 @@ def main():
             "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
             "traffic": traffic["bytes"] if traffic else None,
             "per_launch": f"{dom['gflop']} GFLOP algorithmic / {live_ms * 1e3:.2f} us average over "
-                          f"{len(events)} launches inside the timed steps (HIP events on the launch "
-                          f"stream); {dom['avg_us']} us in isolation",
+                          f"{len(events)} launches inside the last timed step (HIP events on the "
+                          f"launch stream); {dom['avg_us']} us in isolation",
             "traffic_source": (f"{traffic['source']}: FETCH_SIZE {traffic['fetch']} B + WRITE_SIZE "
                                f"{traffic['write']} B per call, scaled by a copy of known size")
                               if traffic else None}

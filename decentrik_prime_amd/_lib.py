@@ -60,6 +60,14 @@ SIGNATURES = {
                                         _c_p, _i64, _c_p]),
     "dk_w4_linear_workspace": (_i64, [_i64, _W, _int]),
     "dk_w4_workspace": (_i64, [_i64, _W, _int]),
+    "dk_h16_workspace": (_i64, [_i64, _i64, _i64, _int]),
+    "dk_h16_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
+                                      _c_p, _i64, _c_p, _i64, _c_p]),
+    "dk_h16_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64, _c_p,
+                                         _i64, _int, _c_p, _i64, _c_p]),
+    "dk_h16_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64,
+                                        _c_p]),
+    "dk_h16_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "dk_lora_grads": (_int, [_c_p, _i64, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64,
                              _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),

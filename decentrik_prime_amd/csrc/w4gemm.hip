@@ -768,6 +768,108 @@ int set_lora(GemmParams& p, const dk_lora_term* terms, int n_terms, int64_t rank
   return 0;
 }
 
+
+// ---- parameter set-up shared by the NF4 (dk_w4_*) and fp16 (dk_h16_*) entry points; rows x
+// cols is the stored weight shape [out, in].
+
+int linear_fwd_params(GemmParams& p, const void* x, int64_t ldx, int64_t m, int64_t rows,
+                      int64_t cols, const void* bias, const dk_lora_term* terms, int n_terms,
+                      int64_t rank, void* y, int64_t ldy) {
+  if (m < 0 || !x || !y || rows <= 0 || cols <= 0) return DK_ERR_INVALID;
+  if (rows % 64 || cols % kBK || ldx < cols || ldy < rows) return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16) || ldx % 8) return DK_ERR_ALIGN;
+  if (int e = set_lora(p, terms, n_terms, rank, rows, false)) return e;
+  p.a = (const f16*)x;
+  p.lda = ldx;
+  p.M = m;
+  p.N = rows;
+  p.K = cols;
+  p.bias = (const f16*)bias;
+  p.out = y;
+  p.ldo = ldy;
+  p.out_mode = DK_OUT_F16;
+  return 0;
+}
+
+int linear_bwd_params(GemmParams& p, const void* dy, int64_t lddy, int64_t m, int64_t rows,
+                      int64_t cols, const dk_lora_term* terms, int n_terms, int64_t rank,
+                      void* dx, int64_t lddx, int out_mode) {
+  if (m < 0 || !dy || !dx || rows <= 0 || cols <= 0) return DK_ERR_INVALID;
+  if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
+  if (cols % 64 || rows % kBK || lddy < rows || lddx < cols) return DK_ERR_INVALID;
+  if (!dk_aligned(dy, 16) || lddy % 8) return DK_ERR_ALIGN;
+  if (int e = set_lora(p, terms, n_terms, rank, cols, true)) return e;
+  p.a = (const f16*)dy;
+  p.lda = lddy;
+  p.M = m;
+  p.N = cols;
+  p.K = rows;
+  p.out = dx;
+  p.ldo = lddx;
+  p.out_mode = out_mode;
+  return 0;
+}
+
+int gateup_params(GemmParams& p, const void* x, int64_t ldx, int64_t m, int64_t rows,
+                  int64_t cols, void* act, void* gu_out) {
+  if (m < 0 || !x || !act || rows <= 0 || cols <= 0) return DK_ERR_INVALID;
+  if (rows % 128 || cols % kBK || ldx < cols) return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16) || ldx % 8) return DK_ERR_ALIGN;
+  p.a = (const f16*)x;
+  p.lda = ldx;
+  p.M = m;
+  p.N = rows;  // logical columns: 2 * inter, interleaved in groups of 32
+  p.K = cols;
+  p.inter = rows / 2;
+  p.out = act;
+  p.ldo = p.inter;
+  p.gu = (f16*)gu_out;
+  return 0;
+}
+
+int down_bwd_params(GemmParams& p, const void* dh, int64_t lddh, int64_t m, int64_t rows,
+                    int64_t cols, void* gu) {
+  if (m < 0 || !dh || !gu || rows <= 0 || cols <= 0) return DK_ERR_INVALID;
+  if (cols % 64 || rows % kBK || lddh < rows) return DK_ERR_INVALID;
+  if (!dk_aligned(dh, 16) || lddh % 8) return DK_ERR_ALIGN;
+  p.a = (const f16*)dh;
+  p.lda = lddh;
+  p.M = m;
+  p.N = cols;  // inter
+  p.K = rows;  // d_model
+  p.inter = cols;
+  p.gu = (f16*)gu;
+  return 0;
+}
+
+// fp16 weight: the plan's split-K (partials in the workspace when one is given), one phase.
+template <bool TRANS, int EPI>
+int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (!w16) return DK_ERR_INVALID;
+  if (!dk_aligned(w16, 16)) return DK_ERR_ALIGN;
+  if (p.M == 0) return 0;
+  p.w16 = (const f16*)w16;
+  Plan pl = plan_for(p.M, p.N, p.K, EPI);
+  if (ws == nullptr) {
+    pl.splits = 1;
+  } else if (pl.splits > 1) {
+    if (ws_bytes < plan_workspace(pl)) return DK_ERR_WORKSPACE;
+    if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
+    p.part = reinterpret_cast<float*>(ws);
+  }
+  return launch_plan<TRANS, EPI, true>(pl, p, stream);
+}
+
+template <bool TRANS, int EPI>
+int dispatch_w4(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes,
+                hipStream_t stream) {
+  if (!weight_ok(w)) return DK_ERR_INVALID;
+  if (!dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
+  if (p.M == 0) return 0;
+  set_weight(p, w);
+  return dispatch<TRANS, EPI>(p, w, ws, ws_bytes, stream);
+}
+
 }  // namespace
 
 extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
@@ -775,23 +877,11 @@ extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
                                      const dk_lora_term* terms, int n_terms, int64_t rank,
                                      void* y, int64_t ldy, void* workspace,
                                      int64_t workspace_bytes, hipStream_t stream) {
-  if (m < 0 || !weight_ok(w) || !x || !y) return DK_ERR_INVALID;
-  if (w->rows % 64 || w->cols % kBK || ldx < w->cols || ldy < w->rows) return DK_ERR_INVALID;
-  if (!dk_aligned(x, 16) || ldx % 8 || !dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
+  if (!weight_ok(w)) return DK_ERR_INVALID;
   GemmParams p = {};
-  if (int e = set_lora(p, terms, n_terms, rank, w->rows, false)) return e;
-  if (m == 0) return 0;
-  p.a = (const f16*)x;
-  p.lda = ldx;
-  p.M = m;
-  p.N = w->rows;
-  p.K = w->cols;
-  set_weight(p, w);
-  p.bias = (const f16*)bias;
-  p.out = y;
-  p.ldo = ldy;
-  p.out_mode = DK_OUT_F16;
-  return dispatch<false, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
+  if (int e = linear_fwd_params(p, x, ldx, m, w->rows, w->cols, bias, terms, n_terms, rank, y, ldy))
+    return e;
+  return dispatch_w4<false, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_weight* w,
@@ -809,23 +899,12 @@ extern "C" int dk_w4_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m,
                                         int n_terms, int64_t rank, void* dx, int64_t lddx,
                                         int out_mode, void* workspace, int64_t workspace_bytes,
                                         hipStream_t stream) {
-  if (m < 0 || !weight_ok(w) || !dy || !dx) return DK_ERR_INVALID;
-  if (out_mode < DK_OUT_F16 || out_mode > DK_OUT_F32_ACCUM) return DK_ERR_INVALID;
-  if (w->cols % 64 || w->rows % kBK || lddy < w->rows || lddx < w->cols) return DK_ERR_INVALID;
-  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(w->packed, 16)) return DK_ERR_ALIGN;
+  if (!weight_ok(w)) return DK_ERR_INVALID;
   GemmParams p = {};
-  if (int e = set_lora(p, terms, n_terms, rank, w->cols, true)) return e;
-  if (m == 0) return 0;
-  p.a = (const f16*)dy;
-  p.lda = lddy;
-  p.M = m;
-  p.N = w->cols;
-  p.K = w->rows;
-  set_weight(p, w);
-  p.out = dx;
-  p.ldo = lddx;
-  p.out_mode = out_mode;
-  return dispatch<true, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
+  if (int e = linear_bwd_params(p, dy, lddy, m, w->rows, w->cols, terms, n_terms, rank, dx, lddx,
+                                out_mode))
+    return e;
+  return dispatch_w4<true, EPI_LINEAR>(p, w, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_linear_bwd_dx(const void* dy, int64_t lddy, int64_t m,
@@ -843,41 +922,70 @@ extern "C" int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m,
                                        const dk_nf4_weight* w_gu, void* act, void* gu_out,
                                        void* workspace, int64_t workspace_bytes,
                                        hipStream_t stream) {
-  if (m < 0 || !weight_ok(w_gu) || !x || !act) return DK_ERR_INVALID;
-  if (w_gu->rows % 128 || w_gu->cols % kBK || ldx < w_gu->cols) return DK_ERR_INVALID;
-  if (!dk_aligned(x, 16) || ldx % 8 || !dk_aligned(w_gu->packed, 16)) return DK_ERR_ALIGN;
-  if (m == 0) return 0;
+  if (!weight_ok(w_gu)) return DK_ERR_INVALID;
   GemmParams p = {};
-  p.a = (const f16*)x;
-  p.lda = ldx;
-  p.M = m;
-  p.N = w_gu->rows;  // logical columns: 2 * inter, interleaved in groups of 32
-  p.K = w_gu->cols;
-  p.inter = w_gu->rows / 2;
-  set_weight(p, w_gu);
-  p.out = act;
-  p.ldo = p.inter;
-  p.gu = (f16*)gu_out;
-  return dispatch<false, EPI_SWIGLU_FWD>(p, w_gu, workspace, workspace_bytes, stream);
+  if (int e = gateup_params(p, x, ldx, m, w_gu->rows, w_gu->cols, act, gu_out)) return e;
+  return dispatch_w4<false, EPI_SWIGLU_FWD>(p, w_gu, workspace, workspace_bytes, stream);
 }
 
 extern "C" int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m,
                                      const dk_nf4_weight* w_down, void* gu, void* workspace,
                                      int64_t workspace_bytes, hipStream_t stream) {
-  if (m < 0 || !weight_ok(w_down) || !dh || !gu) return DK_ERR_INVALID;
-  if (w_down->cols % 64 || w_down->rows % kBK || lddh < w_down->rows) return DK_ERR_INVALID;
-  if (!dk_aligned(dh, 16) || lddh % 8 || !dk_aligned(w_down->packed, 16)) return DK_ERR_ALIGN;
-  if (m == 0) return 0;
+  if (!weight_ok(w_down)) return DK_ERR_INVALID;
   GemmParams p = {};
-  p.a = (const f16*)dh;
-  p.lda = lddh;
-  p.M = m;
-  p.N = w_down->cols;  // inter
-  p.K = w_down->rows;  // d_model
-  p.inter = w_down->cols;
-  set_weight(p, w_down);
-  p.gu = (f16*)gu;
-  return dispatch<true, EPI_SWIGLU_BWD>(p, w_down, workspace, workspace_bytes, stream);
+  if (int e = down_bwd_params(p, dh, lddh, m, w_down->rows, w_down->cols, gu)) return e;
+  return dispatch_w4<true, EPI_SWIGLU_BWD>(p, w_down, workspace, workspace_bytes, stream);
+}
+
+// ---- fp16 weights (the reference's GEMMs on its dequantised workspace)
+
+extern "C" int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const void* w16,
+                                      int64_t rows, int64_t cols, const void* bias,
+                                      const dk_lora_term* terms, int n_terms, int64_t rank,
+                                      void* y, int64_t ldy, void* workspace,
+                                      int64_t workspace_bytes, hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = linear_fwd_params(p, x, ldx, m, rows, cols, bias, terms, n_terms, rank, y, ldy))
+    return e;
+  return dispatch_h16<false, EPI_LINEAR>(p, w16, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
+                                         int64_t rows, int64_t cols, const dk_lora_term* terms,
+                                         int n_terms, int64_t rank, void* dx, int64_t lddx,
+                                         int out_mode, void* workspace, int64_t workspace_bytes,
+                                         hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = linear_bwd_params(p, dy, lddy, m, rows, cols, terms, n_terms, rank, dx, lddx,
+                                out_mode))
+    return e;
+  return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16,
+                                        int64_t rows, int64_t cols, void* act, void* gu_out,
+                                        void* workspace, int64_t workspace_bytes,
+                                        hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = gateup_params(p, x, ldx, m, rows, cols, act, gu_out)) return e;
+  return dispatch_h16<false, EPI_SWIGLU_FWD>(p, w16, workspace, workspace_bytes, stream);
+}
+
+extern "C" int dk_h16_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const void* w16,
+                                      int64_t rows, int64_t cols, void* gu, void* workspace,
+                                      int64_t workspace_bytes, hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = down_bwd_params(p, dh, lddh, m, rows, cols, gu)) return e;
+  return dispatch_h16<true, EPI_SWIGLU_BWD>(p, w16, workspace, workspace_bytes, stream);
+}
+
+extern "C" int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op) {
+  if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  switch (op) {
+    case DK_OP_LINEAR_FWD: return plan_workspace(plan_for(m, rows, cols, EPI_LINEAR));
+    case DK_OP_LINEAR_BWD_DX: return plan_workspace(plan_for(m, cols, rows, EPI_LINEAR));
+    default: return 0;
+  }
 }
 
 extern "C" int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op) {

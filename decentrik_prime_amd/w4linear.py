@@ -95,6 +95,27 @@ def _workspace(w, m, op, device):
     return buf, nbytes
 
 
+def _h16_workspace(m, rows, cols, op, device):
+    """Split-K scratch of an fp16-weight GEMM (None when the shape needs none)."""
+    nbytes = int(_lib.lib().dk_h16_workspace(m, rows, cols, int(op)))
+    if nbytes == 0:
+        return None, 0
+    key = (device, torch.cuda.current_stream(device).cuda_stream)
+    with _WS_LOCK:
+        buf = _WS.get(key)
+        if buf is None or buf.numel() < nbytes:
+            buf = _WS[key] = torch.empty(nbytes, dtype=torch.uint8, device=device)
+    return buf, nbytes
+
+
+def _check_w16(w16, w):
+    """An fp16 copy of NF4 weight w ([rows, cols] or flat), contiguous, on its device."""
+    if w16.dtype != torch.float16 or not w16.is_cuda or not w16.is_contiguous():
+        raise ValueError("w16 must be a contiguous CUDA fp16 tensor")
+    if w16.numel() != w.rows * w.cols:
+        raise ValueError(f"w16 has {w16.numel()} elements, the weight {w.rows} x {w.cols}")
+
+
 def _check16(t, name, shape=None):
     if t.dtype != torch.float16 or not t.is_cuda:
         raise ValueError(f"{name} must be a CUDA fp16 tensor, got {t.dtype} on {t.device}")
@@ -131,9 +152,14 @@ def lora_down(x, lora_A, mask=None, keep_scale=1.0, out=None):
     return out
 
 
-def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None):
+def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None, w16=None):
     """y = fp16(fp32(fp16(x W^T + bias)) + s * fp32(fp16(z B^T)))  (LoRA part optional).
-    x [M, in] fp16, w a W4 [out, in], z [M, r], lora_B [out, r]."""
+    x [M, in] fp16, w a W4 [out, in], z [M, r], lora_B [out, r]; w16 as in linear_forward_lora."""
+    if w16 is not None:
+        if (z is None) != (lora_B is None):
+            raise ValueError("z and lora_B go together")
+        terms = [(z, lora_B, 0, w.rows, lora_scale)] if z is not None else []
+        return linear_forward_lora(x, w, bias, terms, out, w16=w16)
     _check16(x, "x")
     m = x.shape[0]
     if x.shape[1] != w.cols:
@@ -189,11 +215,12 @@ def _lora_terms(terms, m, backward, n_cols):
     return arr, len(terms), rank, keep
 
 
-def linear_forward_lora(x, w, bias=None, terms=(), out=None):
+def linear_forward_lora(x, w, bias=None, terms=(), out=None, w16=None):
     """The fused linear forward with up to two LoRA terms on disjoint output-column ranges:
     terms = [(z [M, r], lora_B [c1 - c0, r], col_begin c0, col_end c1, scale s), ...].  The fused
     QKV projection passes the q term on columns [0, NQ*HD) and the v term on the last NKV*HD
-    columns (solution/fast_qwen.py:943-949)."""
+    columns (solution/fast_qwen.py:943-949).  w16: the weight already dequantised to fp16 (the
+    reference's workspace view), or None to read the NF4 sections."""
     _check16(x, "x")
     m = x.shape[0]
     if x.shape[1] != w.cols:
@@ -205,6 +232,15 @@ def linear_forward_lora(x, w, bias=None, terms=(), out=None):
     if out is None:
         out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
     _check16(out, "out", (m, w.rows))
+    if w16 is not None:
+        _check_w16(w16, w)
+        ws, nbytes = _h16_workspace(m, w.rows, w.cols, _lib.DK_OP_LINEAR_FWD, x.device)
+        rc = _lib.lib().dk_h16_linear_fwd_lora(_lib.ptr(x), x.stride(0), m, _lib.ptr(w16), w.rows,
+                                               w.cols, _lib.ptr(bias), arr, n, rank, _lib.ptr(out),
+                                               out.stride(0), _lib.ptr(ws), nbytes,
+                                               _lib.stream_handle(x.device))
+        _lib.check(rc, "dk_h16_linear_fwd_lora")
+        return out
     ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_FWD, x.device)
     rc = _lib.lib().dk_w4_linear_fwd_lora(_lib.ptr(x), x.stride(0), m, w.c_ref(), _lib.ptr(bias),
                                           arr, n, rank, _lib.ptr(out), out.stride(0), _lib.ptr(ws),
@@ -231,7 +267,8 @@ def _dx_out(out, m, w, out_dtype, accumulate, device):
     return out, mode
 
 
-def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, accumulate=False):
+def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, accumulate=False,
+                            w16=None):
     """dX = fp32(fp16(dy W)) + sum over terms of (mask ? fp32(fp16(dz A)) * keep_scale : 0),
     terms = [(dz [M, r], lora_A [r, in], mask [M, in] or None, keep_scale), ...] added in order
     (the QKV backward: dy1 = mm(dqkv, W_qkv) plus the lq and lv terms of rms_backward,
@@ -243,6 +280,15 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
     arr, n, rank, _keep = _lora_terms([(dz, a, mk, 0, 0, ks) for dz, a, mk, ks in terms], m,
                                       True, w.cols)
     out, mode = _dx_out(out, m, w, out_dtype, accumulate, dy.device)
+    if w16 is not None:
+        _check_w16(w16, w)
+        ws, nbytes = _h16_workspace(m, w.rows, w.cols, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
+        rc = _lib.lib().dk_h16_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, _lib.ptr(w16),
+                                                  w.rows, w.cols, arr, n, rank, _lib.ptr(out),
+                                                  out.stride(0), mode, _lib.ptr(ws), nbytes,
+                                                  _lib.stream_handle(dy.device))
+        _lib.check(rc, "dk_h16_linear_bwd_dx_lora")
+        return out
     ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
     rc = _lib.lib().dk_w4_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, w.c_ref(), arr, n, rank,
                                              _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws),
@@ -252,10 +298,16 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
 
 
 def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, out=None,
-                       out_dtype=torch.float32, accumulate=False):
+                       out_dtype=torch.float32, accumulate=False, w16=None):
     """dX = fp32(fp16(dy W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0).
     dy [M, out] fp16, w a W4 [out, in], dz [M, r], lora_A [r, in], mask [M, in].
-    out_dtype float16 rounds dX to fp16; accumulate=True adds into an fp32 `out`."""
+    out_dtype float16 rounds dX to fp16; accumulate=True adds into an fp32 `out`; w16 as in
+    linear_forward_lora."""
+    if w16 is not None:
+        if (dz is None) != (lora_A is None):
+            raise ValueError("dz and lora_A go together")
+        terms = [(dz, lora_A, mask, keep_scale)] if dz is not None else []
+        return linear_backward_dx_lora(dy, w, terms, out, out_dtype, accumulate, w16=w16)
     _check16(dy, "dy")
     m = dy.shape[0]
     if dy.shape[1] != w.rows:
@@ -310,7 +362,7 @@ def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
     return da, db, dz
 
 
-def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True):
+def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None):
     """gate|up as one NF4 GEMM with the gated-SiLU epilogue.  w_gu is [2I, in] (gate rows then up
     rows).  Returns (act [M, I], gu [M, 2I] or None)."""
     _check16(x, "x")
@@ -330,6 +382,13 @@ def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True):
         _check16(gu, "gu", (m, 2 * inter))
         if not gu.is_contiguous():
             raise ValueError("gu must be contiguous")
+    if w16 is not None:
+        _check_w16(w16, w_gu)
+        rc = _lib.lib().dk_h16_gateup_swiglu_fwd(_lib.ptr(x), x.stride(0), m, _lib.ptr(w16),
+                                                 w_gu.rows, w_gu.cols, _lib.ptr(act), _lib.ptr(gu),
+                                                 None, 0, _lib.stream_handle(dev))
+        _lib.check(rc, "dk_h16_gateup_swiglu_fwd")
+        return act, gu
     ws, nbytes = _workspace(w_gu, m, _lib.DK_OP_GATEUP_SWIGLU_FWD, dev)
     rc = _lib.lib().dk_w4_gateup_swiglu_fwd(_lib.ptr(x), x.stride(0), m, w_gu.c_ref(), _lib.ptr(act),
                                             _lib.ptr(gu), _lib.ptr(ws), nbytes,
@@ -338,12 +397,19 @@ def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True):
     return act, gu
 
 
-def down_swiglu_backward(dh, w_down, gu):
+def down_swiglu_backward(dh, w_down, gu, w16=None):
     """dact = fp16(dh W_down), then gu <- [dgate | dup] in place.  Returns gu."""
     _check16(dh, "dh")
     _check16(gu, "gu", (dh.shape[0], 2 * w_down.cols))
     if dh.shape[1] != w_down.rows or not gu.is_contiguous():
         raise ValueError("down backward: shapes do not match")
+    if w16 is not None:
+        _check_w16(w16, w_down)
+        rc = _lib.lib().dk_h16_down_swiglu_bwd(_lib.ptr(dh), dh.stride(0), dh.shape[0], _lib.ptr(w16),
+                                               w_down.rows, w_down.cols, _lib.ptr(gu), None, 0,
+                                               _lib.stream_handle(dh.device))
+        _lib.check(rc, "dk_h16_down_swiglu_bwd")
+        return gu
     ws, nbytes = _workspace(w_down, dh.shape[0], _lib.DK_OP_DOWN_SWIGLU_BWD, dh.device)
     rc = _lib.lib().dk_w4_down_swiglu_bwd(_lib.ptr(dh), dh.stride(0), dh.shape[0], w_down.c_ref(),
                                           _lib.ptr(gu), _lib.ptr(ws), nbytes,

@@ -206,6 +206,31 @@ int dk_w4_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const dk_nf4_
 int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const dk_nf4_weight* w_down,
                           void* gu, void* workspace, int64_t workspace_bytes, hipStream_t stream);
 
+/* ------------------------------------------------------------------------------------------
+ * The same GEMMs and epilogues on a weight already dequantised to fp16 (w16 [rows][cols], stored
+ * like the NF4 weight: [out, in], in contiguous, 16-byte aligned).  These are the reference's
+ * GEMMs on its dequantised workspace (torch.mm/addmm on views filled by k_nf4.dequant_range on a
+ * side stream ahead of use, solution/fast_qwen.py:694-756, 943-947, 1093-1112, 1310-1364): a
+ * caller dequantises the next weight with dk_nf4_dequant on a second stream while the current
+ * GEMM runs, and orders the two streams with events.  Arguments, rounding and rules as the dk_w4_*
+ * entry point of the same name; workspace (split-K partials only) sized by dk_h16_workspace, or
+ * NULL. */
+int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op);
+int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
+                           int64_t cols, const void* bias, const dk_lora_term* terms, int n_terms,
+                           int64_t rank, void* y, int64_t ldy, void* workspace,
+                           int64_t workspace_bytes, hipStream_t stream);
+int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
+                              int64_t rows, int64_t cols, const dk_lora_term* terms, int n_terms,
+                              int64_t rank, void* dx, int64_t lddx, int out_mode, void* workspace,
+                              int64_t workspace_bytes, hipStream_t stream);
+int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
+                             int64_t cols, void* act, void* gu_out, void* workspace,
+                             int64_t workspace_bytes, hipStream_t stream);
+int dk_h16_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const void* w16,
+                           int64_t rows, int64_t cols, void* gu, void* workspace,
+                           int64_t workspace_bytes, hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -50,6 +50,26 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_nf4_dequant(ctypes.c_void_p(4), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16),
                               ctypes.c_void_p(16), 4, None) == _lib.DK_ERR_ALIGN
+    # fp16-weight GEMMs: split-K partials only (no fp16 copy of the weight to make)
+    assert lib.dk_h16_workspace(256, 1536, 1536, _lib.DK_OP_LINEAR_FWD) == 48 * 3 * 128 * 64 * 4
+    assert lib.dk_h16_workspace(2048, 2048, 1536, _lib.DK_OP_LINEAR_FWD) == 0
+    assert lib.dk_h16_workspace(2048, 17920, 1536, _lib.DK_OP_GATEUP_SWIGLU_FWD) == 0
+    assert lib.dk_h16_workspace(0, 1536, 1536, _lib.DK_OP_LINEAR_FWD) == 0
+    p16 = ctypes.c_void_p(16)
+    assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, None, 1536, 1536, None, None, 0, 0, p16, 1536,
+                                      None, 0, None) == _lib.DK_ERR_INVALID     # no weight
+    assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, ctypes.c_void_p(8), 1536, 1536, None, None, 0,
+                                      0, p16, 1536, None, 0, None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, p16, 1000, 1536, None, None, 0, 0, p16, 1536,
+                                      None, 0, None) == _lib.DK_ERR_INVALID     # rows % 64
+    assert lib.dk_h16_linear_bwd_dx_lora(p16, 1536, 8, p16, 1536, 1536, None, 0, 0, p16, 1536, 9,
+                                         None, 0, None) == _lib.DK_ERR_INVALID  # output mode
+    assert lib.dk_h16_gateup_swiglu_fwd(p16, 1536, 8, p16, 17920 + 64, 1536, p16, None, None, 0,
+                                        None) == _lib.DK_ERR_INVALID            # rows % 128
+    assert lib.dk_h16_down_swiglu_bwd(p16, 1536, 8, p16, 1536, 8960, None, None, 0,
+                                      None) == _lib.DK_ERR_INVALID              # no gu
+    assert lib.dk_h16_linear_fwd_lora(p16, 1536, 0, p16, 1536, 1536, None, None, 0, 0, p16, 1536,
+                                      None, 0, None) == 0                       # zero rows
     assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * 1536 * 16 * 4
     assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
     with pytest.raises(ValueError):

@@ -1,0 +1,193 @@
+"""GPU parity of the fp16-weight GEMM entry points (dk_h16_*, the GEMMs that read a weight already
+dequantised to fp16, as the reference's GEMMs read its dequantised workspace,
+solution/fast_qwen.py:694-756) and of the dequant-ahead schedule of the linear stack.
+
+The fp16 weight is the GPU dequant of the NF4 weight (bit-exact with the oracle's, pinned by
+test_gpu_nf4).  The GEMMs run the same tile plan and MFMA order as their NF4 counterparts, so the
+outputs must be bit-identical to the dk_w4_* results; they are also checked against the oracle at
+rtol 1e-2 / atol 2e-2 (relative to the output scale for the small-valued gradients)."""
+
+import numpy as np
+import pytest
+
+from tests.helpers import assert_close, cuda, cuda16, host, log, lora_inputs, nf4_weight, to_w4
+
+pytestmark = pytest.mark.gpu
+RTOL, ATOL = 1e-2, 2e-2
+F16 = np.float16
+
+
+def _scaled_close(got, want, what):
+    s = float(np.abs(want).max()) or 1.0
+    assert_close(np.asarray(got, np.float64) / s, np.asarray(want, np.float64) / s, RTOL, ATOL, what)
+
+
+def _same(a, b, what):
+    """Bit-identical tensors (fp16 / fp32 / uint8 alike)."""
+    a, b = host(a), host(b)
+    assert a.shape == b.shape and a.dtype == b.dtype, what
+    if not np.array_equal(a.view(np.uint8), b.view(np.uint8)):
+        bad = np.argwhere(a != b)
+        raise AssertionError(f"{what}: {len(bad)} of {a.size} differ; first at {bad[0].tolist()}: "
+                             f"{a[tuple(bad[0])]} vs {b[tuple(bad[0])]}")
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    return t
+
+
+@pytest.mark.parametrize("m", [2048, 200])
+def test_h16_fused_qkv(torch, m):
+    """Fused QKV forward (two column-range LoRA terms, bias) and the dX GEMM with both masked LoRA
+    terms, on the fp16 weight."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"h16 fused QKV forward + dX, M={m}")
+    D, KV = 1536, 256
+    q = nf4_weight(D + 2 * KV, D, seed=207)
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, seed=21)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, seed=22)
+    rng = np.random.default_rng(23)
+    bias = (rng.standard_normal(D + 2 * KV) * 0.1).astype(F16)
+    dqkv = (rng.standard_normal((m, D + 2 * KV)) * 1e-2).astype(F16)
+    ks = linear.keep_scale(0.05)
+    w = to_w4(q)
+    w16 = w.dequantize()
+    tzq = w4linear.lora_down(cuda16(x), cuda16(aq), cuda(mq), ks)
+    tzv = w4linear.lora_down(cuda16(x), cuda16(av), cuda(mv), ks)
+    terms = [(tzq, cuda16(bq), 0, D, 2.0), (tzv, cuda16(bv), D + KV, D + 2 * KV, 2.0)]
+    y4 = w4linear.linear_forward_lora(cuda16(x), w, cuda16(bias), terms)
+    y16 = w4linear.linear_forward_lora(cuda16(x), w, cuda16(bias), terms, w16=w16)
+    torch.cuda.synchronize()
+    _same(y16, y4, "qkv h16 vs w4")
+    yq, _ = linear.linear_fwd(x, q["deq"][:D], bias[:D], mq, ks, aq, bq, 2.0)
+    yk, _ = linear.linear_fwd(x, q["deq"][D:D + KV], bias[D:D + KV])
+    yv, _ = linear.linear_fwd(x, q["deq"][D + KV:], bias[D + KV:], mv, ks, av, bv, 2.0)
+    assert_close(host(y16), np.concatenate([yq, yk, yv], axis=1), RTOL, ATOL, "qkv vs oracle")
+    g = cuda16(dqkv)
+    dzq = (torch.randn(m, 16, device="cuda") * 1e-2).half()
+    dzv = (torch.randn(m, 16, device="cuda") * 1e-2).half()
+    bterms = [(dzq, cuda16(aq), cuda(mq), ks), (dzv, cuda16(av), cuda(mv), ks)]
+    dx4 = w4linear.linear_backward_dx_lora(g, w, bterms)
+    dx16 = w4linear.linear_backward_dx_lora(g, w, bterms, w16=w16)
+    torch.cuda.synchronize()
+    _same(dx16, dx4, "dX qkv h16 vs w4")
+    mm = lambda a, b: linear.mm16(a, b).astype(np.float32)  # noqa: E731
+    tq = np.where(mq != 0, mm(host(dzq), aq) * np.float32(ks), 0).astype(np.float32)
+    tv = np.where(mv != 0, mm(host(dzv), av) * np.float32(ks), 0).astype(np.float32)
+    _scaled_close(host(dx16), (mm(dqkv, q["deq"]) + tq) + tv, "dX qkv vs oracle")
+
+
+def test_h16_o_projection(torch):
+    """1536 x 1536 at M = 2048: 128 x 64 tiles with split-K in both directions; fp16 dX output
+    and fp32 accumulation into an existing dX."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log("h16 o projection forward + dX (split-K), M=2048")
+    q = nf4_weight(1536, 1536, seed=208)
+    rng = np.random.default_rng(24)
+    x = rng.standard_normal((2048, 1536)).astype(F16)
+    dy = (rng.standard_normal((2048, 1536)) * 1e-2).astype(F16)
+    w = to_w4(q)
+    w16 = w.dequantize()
+    y4 = w4linear.linear_forward(cuda16(x), w)
+    y16 = w4linear.linear_forward(cuda16(x), w, w16=w16)
+    d4 = w4linear.linear_backward_dx(cuda16(dy), w, out_dtype=torch.float16)
+    d16 = w4linear.linear_backward_dx(cuda16(dy), w, out_dtype=torch.float16, w16=w16)
+    acc = torch.ones(2048, 1536, dtype=torch.float32, device="cuda")
+    w4linear.linear_backward_dx(cuda16(dy), w, out=acc, accumulate=True, w16=w16)
+    torch.cuda.synchronize()
+    _same(y16, y4, "o forward h16 vs w4")
+    _same(d16, d4, "o dX h16 vs w4")
+    assert_close(host(y16), linear.mm16(x, q["deq"].T), RTOL, ATOL, "o forward vs oracle")
+    ref = linear.mm16(dy, q["deq"])
+    _scaled_close(host(d16), ref, "o dX vs oracle")
+    _scaled_close(host(acc) - 1.0, ref.astype(np.float32), "o dX accumulate")
+
+
+@pytest.mark.parametrize("m", [2048, 300])
+def test_h16_mlp(torch, m):
+    """gate|up SwiGLU forward, down forward, down^T + SwiGLU backward and gate|up^T on fp16
+    weights."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear, mlp
+    log(f"h16 MLP forward + backward, M={m}")
+    I = 8960
+    qg = nf4_weight(2 * I, 1536, seed=204)
+    qd = nf4_weight(1536, I, seed=205)
+    wg, wd = to_w4(qg), to_w4(qd)
+    g16, d16 = wg.dequantize(), wd.dequantize()
+    x = np.random.default_rng(25).standard_normal((m, 1536)).astype(F16)
+    act4, gu4 = w4linear.gateup_swiglu_forward(cuda16(x), wg)
+    act16, gu16 = w4linear.gateup_swiglu_forward(cuda16(x), wg, w16=g16)
+    torch.cuda.synchronize()
+    _same(gu16, gu4, "gu h16 vs w4")
+    _same(act16, act4, "act h16 vs w4")
+    gu_ref, h_ref, _ = mlp.mlp_fwd(x, qg["deq"], qd["deq"])
+    assert_close(host(gu16), gu_ref, RTOL, ATOL, "gu vs oracle")
+    assert_close(host(act16), h_ref, RTOL, ATOL, "act vs oracle")
+    y4 = w4linear.linear_forward(act16, wd)
+    y16 = w4linear.linear_forward(act16, wd, w16=d16)
+    torch.cuda.synchronize()
+    _same(y16, y4, "down h16 vs w4")
+    assert_close(host(y16), linear.mm16(host(act16), qd["deq"].T), RTOL, ATOL, "down vs oracle")
+    dh = (np.random.default_rng(26).standard_normal((m, 1536)) * 1e-2).astype(F16)
+    gu_np = host(gu16)
+    w4linear.down_swiglu_backward(cuda16(dh), wd, gu4)
+    w4linear.down_swiglu_backward(cuda16(dh), wd, gu16, w16=d16)
+    torch.cuda.synchronize()
+    _same(gu16, gu4, "dgu h16 vs w4")
+    dgu_ref, dx_ref = mlp.mlp_bwd(dh, gu_np, qg["deq"], qd["deq"])
+    _scaled_close(host(gu16), dgu_ref, "dgu vs oracle")
+    dx4 = w4linear.linear_backward_dx(gu4, wg, out_dtype=torch.float16)
+    dx16 = w4linear.linear_backward_dx(gu16, wg, out_dtype=torch.float16, w16=g16)
+    torch.cuda.synchronize()
+    _same(dx16, dx4, "dX mlp h16 vs w4")
+    _scaled_close(host(dx16), dx_ref, "dX mlp vs oracle chain")
+
+
+def test_h16_argument_checks(torch):
+    from decentrik_prime_amd import w4linear
+    log("h16 argument checks")
+    q = nf4_weight(512, 256, seed=209)
+    w = to_w4(q)
+    x = torch.zeros(64, 256, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):   # wrong element count
+        w4linear.linear_forward(x, w, w16=torch.zeros(512 * 128, dtype=torch.float16, device="cuda"))
+    with pytest.raises(ValueError):   # wrong dtype
+        w4linear.linear_forward(x, w, w16=torch.zeros(512, 256, dtype=torch.float32, device="cuda"))
+    with pytest.raises(ValueError):   # not contiguous
+        w4linear.linear_forward(x, w, w16=torch.zeros(256, 512, dtype=torch.float16,
+                                                         device="cuda").t())
+
+
+def test_stack_dequant_ahead_matches_nf4_reads(torch):
+    """Three layers, M = 512, two steps: every weight dequantised one use ahead, in order on the
+    compute stream or on a side stream, gives bit-identical outputs and LoRA gradients to the
+    schedule that reads NF4 directly (same seed, so the same weights and inputs)."""
+    from decentrik_prime_amd.stack import NF4LinearStack
+    log("stack: dequant-ahead schedules vs NF4 reads, 3 layers, M=512, 2 steps")
+    configs = (((), "main"), (NF4LinearStack.KINDS, "main"), (("gu", "d"), "side"),
+               (NF4LinearStack.KINDS, "side"))
+    runs = {}
+    for ahead, where in configs:
+        st = NF4LinearStack(n_layers=3, m=512, seed=3, device="cuda", ahead=ahead, dq_stream=where)
+        results = []
+        for _ in range(2):
+            st.step()
+            torch.cuda.synchronize()
+            results.append([t.clone() for t in (st.out["qkv"], st.out["o"], st.out["y"],
+                                                 st.dx_qkv, st.dx_o, st.dx_mlp)]
+                           + [g.clone() for gr in st.grads for g in gr]
+                           + [gu.clone() for gu in st.gu])
+        runs[(ahead, where)] = results
+        del st
+    names = (["qkv", "o", "y", "dx_qkv", "dx_o", "dx_mlp"]
+             + [f"grad{i}.{j}" for i in range(3) for j in range(4)] + [f"dgu{i}" for i in range(3)])
+    base = runs[configs[0]]
+    for cfg in configs[1:]:
+        for step in range(2):
+            for name, a, b in zip(names, base[step], runs[cfg][step]):
+                _same(b, a, f"{cfg} step {step} {name}")
