@@ -1,0 +1,57 @@
+// Parameters shared by the fused GEMM kernels (w4gemm.hip: NF4 or fp16 weights, warp-specialised
+// 128-row tiles; hgemm.hip: fp16 weights, 256 x 256 tiles fed by LDS-DMA loads).
+#pragma once
+#include "dk_common.h"
+
+namespace dk {
+
+enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
+
+// One LoRA term of the LINEAR epilogue.  Forward: adds s * fp32(fp16(z B^T)) to output columns
+// [n_begin, n_end) (B holds the rows of those columns).  Backward: adds
+// (mask ? fp32(fp16(dz A)) * keep_scale : 0) to every column.
+struct LoraTerm {
+  const f16* z;         // [M][rank]: z (forward) or dz (backward)
+  const f16* r;         // forward: B [n_end - n_begin][rank]; backward: A [rank][N]
+  const uint8_t* mask;  // backward keep-mask [M][N] or null (no dropout, no scale)
+  int64_t n_begin, n_end;
+  float scale;          // forward: s; backward: keep_scale
+};
+
+struct GemmParams {
+  const f16* a;
+  int64_t lda;
+  int64_t M, N, K;
+  const uint8_t* packed;
+  const uint8_t* qabs;
+  const float* scale2;
+  const float* offset2;
+  const float* code2;
+  const float* nf4;
+  const f16* w16;       // two-phase: the weight dequantised to fp16, stored order ([N][K] NT, [K][N] NN)
+  int64_t inter;        // SwiGLU: gate/up width I
+  const f16* bias;      // [N] or null
+  LoraTerm lora[2];     // rank-r LoRA terms added in the LINEAR epilogue, in order
+  int n_lora;
+  int64_t rank;
+  void* out;
+  int64_t ldo;
+  int out_mode;
+  f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
+  int tiles_m, tiles_n;
+  int m_fastest;        // tile order: row tiles fastest (1) or column tiles fastest (0)
+  int splits;           // split-K factor (1: none)
+  float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
+};
+
+// Runs the GEMM of `p` (fp16 weight p.w16) on the 256 x 256-tile kernel when the shape suits it:
+// output columns a multiple of 256, K a multiple of 32, and either at least one tile per CU or
+// (LINEAR, at least 1024 rows) a split-K that fills the CUs, whose fp32 partials need
+// hgemm_workspace bytes of `ws`.  Returns kHgemmDeclined without launching anything otherwise,
+// a HIP error code, or 0.
+constexpr int kHgemmDeclined = -1000;
+template <bool TRANS, int EPI>
+int hgemm_launch(const GemmParams& p, void* ws, int64_t ws_bytes, hipStream_t stream);
+int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi);
+
+}  // namespace dk

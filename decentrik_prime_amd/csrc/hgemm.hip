@@ -1,0 +1,552 @@
+// fp16-weight GEMMs with the fused epilogues on 256 x 256 tiles (gfx950).
+//
+//   NT (TRANS = false): C[m][n] = sum_k A[m][k] * W[n][k]      W = p.w16 stored [N][K]
+//   NN (TRANS = true):  C[m][n] = sum_k A[m][k] * W[k][n]      W = p.w16 stored [K][N]
+//
+// One 512-thread workgroup per CU owns a 256 x 256 tile of C: 8 waves (2 x 4), each a 128 x 64
+// block of v_mfma_f32_32x32x16_f16 results.  Per output FLOP that is half the operand bytes of a
+// 128 x 128 tile, and the operand bytes between L2 and the CUs are what bounds these GEMMs on
+// MI355X.  K is walked in steps of 32.  Operands go from global memory straight into LDS with
+// global_load_lds_dwordx4 (LDS DMA: no registers, no LDS write instructions), four steps ahead,
+// into a ring of four stages (4 x 32 KB).  Each wave waits only for its own loads (vmcnt), and one
+// barrier per step both publishes the step's tiles and frees the stage read in the step before.
+// The MFMA operands of the next 16-wide sub-step are read while the MFMAs of the current one run.
+//
+// LDS layout: A tiles and NT W tiles are rows of 32 halves (64 bytes) whose four 16-byte chunks
+// are XOR-swizzled by row (swz_k), so the b128 operand reads of 16 consecutive rows hit distinct
+// banks.  NN W tiles are rows of 256 halves (N contiguous) with chunks swizzled by k (swz_n); the
+// consumers build each K-contiguous operand from two ds_read_b64_tr_b16 (transposing) reads.
+// The DMA writes 64 consecutive 16-byte chunks per instruction, so the swizzle is applied to the
+// global addresses each lane loads.
+//
+// Tiles are dealt M-fastest inside each XCD's contiguous run of workgroups.  When the tile count
+// leaves a last round at most half full, those last tiles run as four 128 x 128 sub-tiles each
+// (8 waves of 32 x 64), so the final round is short instead of mostly idle.
+//
+// Epilogues as in w4gemm.hip (the same per-element rounding): LINEAR with up to two LoRA terms
+// and the three output modes, SWIGLU_FWD (gate/up rows interleaved in groups of 32 so g and u of
+// an output share a lane), SWIGLU_BWD (in place on gu).
+#include "gemm_common.h"
+
+namespace dk {
+namespace {
+
+constexpr int kBK = 32;                      // K per step
+constexpr int kStages = 4;                   // LDS ring depth (= load distance in steps)
+constexpr int kThreads = 512;
+constexpr int kTile = 256;
+constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 16 KB
+constexpr int kEpiScratch = 4096;            // bytes of LDS per wave for the epilogue
+
+__device__ __forceinline__ unsigned lds_offset(const void* p) {
+  return (unsigned)(size_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane.  Written as inline assembly
+// so that the compiler does not guard every later LDS read with a wait for it: the kernel tracks
+// these loads itself with vmcnt waits.  M0 (the LDS address) is saved and restored around it.
+__device__ __forceinline__ void dma16(const void* src, unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+__device__ __forceinline__ f16x4 read_tr(const f16* p) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+                                       (__attribute__((address_space(3))) i16x4*)(p)));
+}
+
+// chunk swizzles: 64-byte rows (conflict-free for 8- and 16-lane LDS passes of b128 reads of
+// consecutive rows) and N-contiguous rows of the NN W tile (transposing reads of 4 rows x 32
+// columns hit distinct banks)
+__device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
+
+// The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
+// element is (mw0, nw0).  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
+// 8 (v / 4) + 4 (lane / 32) + v % 4 for register v.  escr: this wave's 4 KB of LDS scratch.
+template <bool TRANS, int EPI, int TM, int TN>
+__device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
+                                              int64_t mw0, int64_t nw0, uint8_t* escr) {
+  const int lane = threadIdx.x & 63;
+  const int lrow = lane & 31;
+  const int lk8 = 8 * (lane >> 5);
+  const int rsub = 4 * (lane >> 5);
+  const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const int64_t M = p.M, N = p.N;
+
+  if constexpr (EPI == EPI_LINEAR) {
+    f16* out16 = reinterpret_cast<f16*>(p.out);
+    float* out32 = reinterpret_cast<float*>(p.out);
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const f32x16& a = acc[i][j];
+        const int64_t mrow0 = mw0 + 32 * i;
+        const int64_t nb = nw0 + 32 * j;
+        const int64_t n = nb + lrow;
+        const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+        f32x16 res;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) res[v] = (float)dk_h(__fadd_rn(a[v], bias));
+        for (int t = 0; t < p.n_lora; ++t) {
+          const LoraTerm& L = p.lora[t];
+          if (!TRANS && (nb < L.n_begin || nb >= L.n_end)) continue;
+          f32x16 lo;
+#pragma unroll
+          for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
+          const int64_t zm = mrow0 + lrow;
+          for (int rc = 0; rc < p.rank; rc += 16) {
+            f16x8 zf, rf;
+            if (zm < M) {
+              zf = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
+            } else {
+#pragma unroll
+              for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
+            }
+            if (!TRANS) {
+              rf = *reinterpret_cast<const f16x8*>(L.r + (n - L.n_begin) * p.rank + rc + lk8);
+            } else {
+              // A[rc .. rc + 16][nb .. nb + 32] staged row-major (rows of 48 halves), read back
+              // rank-contiguous with transposing reads
+              f16* ascr = reinterpret_cast<f16*>(escr + 2048);
+              const f16x8 av = *reinterpret_cast<const f16x8*>(
+                  L.r + (int64_t)(rc + (lane >> 2)) * N + nb + 8 * (lane & 3));
+              __builtin_amdgcn_wave_barrier();
+              *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = av;
+              __builtin_amdgcn_wave_barrier();
+              const f16* base = ascr + tr_k * 48 + tr_n;
+              const f16x4 lo4 = read_tr(base), hi4 = read_tr(base + 4 * 48);
+              rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+              __builtin_amdgcn_wave_barrier();
+            }
+            lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
+          }
+          if (TRANS && L.mask) {
+            // the block's 32 x 32 keep-mask bytes: one 16-byte load per lane, staged in LDS
+            // (rows of 48 bytes), then read per element
+            const int64_t mr = mrow0 + (lane >> 1);
+            u32x4 mw = u32x4{0u, 0u, 0u, 0u};
+            if (mr < M) mw = *reinterpret_cast<const u32x4*>(L.mask + mr * N + nb + 16 * (lane & 1));
+            __builtin_amdgcn_wave_barrier();
+            *reinterpret_cast<u32x4*>(escr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw;
+            __builtin_amdgcn_wave_barrier();
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const int mloc = 8 * (v >> 2) + rsub + (v & 3);
+              const float lf = (float)dk_h(lo[v]);
+              res[v] = __fadd_rn(res[v], escr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
+            }
+            __builtin_amdgcn_wave_barrier();
+          } else {
+#pragma unroll
+            for (int v = 0; v < 16; ++v) {
+              const float lf = (float)dk_h(lo[v]);
+              res[v] = __fadd_rn(res[v], TRANS ? lf : __fmul_rn(L.scale, lf));
+            }
+          }
+        }
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+          if (m >= M) continue;
+          const int64_t o = m * p.ldo + n;
+          if (p.out_mode == DK_OUT_F16) {
+            out16[o] = dk_h(res[v]);
+          } else if (p.out_mode == DK_OUT_F32) {
+            out32[o] = res[v];
+          } else {
+            out32[o] = __fadd_rn(out32[o], res[v]);
+          }
+        }
+      }
+    }
+  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+    f16* act = reinterpret_cast<f16*>(p.out);
+    const int64_t hcol = nw0 / 2 + lrow;
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t mrow0 = mw0 + 32 * i;
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+        if (m >= M) continue;
+        const f16 g16 = dk_h(acc[i][0][v]);
+        const f16 u16 = dk_h(acc[i][1][v]);
+        float sig, silu;
+        dk_silu_parts((float)g16, &sig, &silu);
+        act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
+        if (p.gu) {
+          p.gu[m * 2 * p.inter + hcol] = g16;
+          p.gu[m * 2 * p.inter + p.inter + hcol] = u16;
+        }
+      }
+    }
+  } else {  // EPI_SWIGLU_BWD: N == inter
+#pragma unroll
+    for (int i = 0; i < TM; ++i) {
+      const int64_t mrow0 = mw0 + 32 * i;
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const int64_t n = nw0 + 32 * j + lrow;
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+          if (m >= M) continue;
+          const float da = (float)dk_h(acc[i][j][v]);
+          f16* gp = p.gu + m * 2 * p.inter + n;
+          const float g = (float)gp[0];
+          const float u = (float)gp[p.inter];
+          float sig, silu;
+          dk_silu_parts(g, &sig, &silu);
+          gp[p.inter] = dk_h(da * silu);
+          gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
+        }
+      }
+    }
+  }
+}
+
+template <bool TRANS, int EPI, int BM, int BN, int WAVES_M>
+__device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64_t n0, int kt0,
+                                          int nk, float* part, f16* As, f16* Bs) {
+  constexpr int WAVES_N = 8 / WAVES_M;
+  constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
+  constexpr int TM = WM / 32, TN = WN / 32;
+  constexpr int LA = BM * 4 / kThreads;     // A chunks per lane per stage
+  constexpr int LB = BN * 4 / kThreads;     // W chunks per lane per stage
+  constexpr int LOADS = LA + LB;            // DMA instructions per lane per stage
+  constexpr int NCH = BN / 8;               // NN: 16-byte chunks per W-tile row
+  static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile shape");
+  static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
+  static_assert((TM * TN) % LOADS == 0, "DMA interleave");
+
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t M = p.M, N = p.N, K = p.K;
+
+  // ---- DMA sources (first K step kt0; nk steps): instruction j of wave w fills the stage's chunks [(8 j + w) 64, +64)
+  const f16* a_src[LA];
+  const f16* b_src[LB];
+#pragma unroll
+  for (int j = 0; j < LA; ++j) {
+    const int q = (j * 8 + wave) * 64 + lane;
+    const int row = q >> 2, c = (q & 3) ^ swz_k(q >> 2);
+    const int64_t gm = m0 + row < M ? m0 + row : M - 1;   // rows past M: never stored
+    a_src[j] = p.a + gm * p.lda + (int64_t)kt0 * kBK + c * 8;
+  }
+#pragma unroll
+  for (int j = 0; j < LB; ++j) {
+    const int q = (j * 8 + wave) * 64 + lane;
+    if (!TRANS) {
+      const int row = q >> 2, c = (q & 3) ^ swz_k(q >> 2);
+      int64_t n = n0 + row;
+      if (EPI == EPI_SWIGLU_FWD) {
+        const int64_t g = n >> 6, w = n & 63;
+        n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
+      }
+      b_src[j] = p.w16 + n * K + (int64_t)kt0 * kBK + c * 8;
+    } else {
+      const int k = q / NCH, c = (q % NCH) ^ swz_n(q / NCH);
+      b_src[j] = p.w16 + ((int64_t)kt0 * kBK + k) * N + n0 + c * 8;
+    }
+  }
+  // load d (0 .. LOADS-1) of step kt into stage st
+  auto issue = [&](int kt, int st, int d) {
+    if (d < LA) {
+      const unsigned dst = __builtin_amdgcn_readfirstlane(
+          lds_offset(As + st * kStageHalves + (d * 8 + wave) * 512));
+      dma16(a_src[d] + (int64_t)kt * kBK, dst);
+    } else {
+      const int j = d - LA;
+      const unsigned dst = __builtin_amdgcn_readfirstlane(
+          lds_offset(Bs + st * kStageHalves + (j * 8 + wave) * 512));
+      dma16(b_src[j] + (TRANS ? (int64_t)kt * kBK * N : (int64_t)kt * kBK), dst);
+    }
+  };
+  // wait until at most `later` stages of this lane's loads are still in flight
+  auto wait_loads = [&](int later) {
+    if (later >= 3) wait_vmem<3 * LOADS>();
+    else if (later == 2) wait_vmem<2 * LOADS>();
+    else if (later == 1) wait_vmem<LOADS>();
+    else wait_vmem<0>();
+  };
+
+  // ---- MFMA operands
+  const int wm = wave / WAVES_N, wn = wave % WAVES_N;
+  const int lrow = lane & 31;
+  const int hx = swz_k(lane & 15);
+  const int fo[2] = {lrow * kBK + ((0 + (lane >> 5)) ^ hx) * 8,
+                     lrow * kBK + ((2 + (lane >> 5)) ^ hx) * 8};
+  const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
+  const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  int nn_off[TN];
+#pragma unroll
+  for (int j = 0; j < TN; ++j) {
+    const int n = wn * WN + 32 * j + tr_n;
+    nn_off[j] = tr_k * BN + (((n >> 3) ^ swz_n(tr_k)) * 8) + (n & 7);
+  }
+
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+  f16x8 fa[2][TM], fb[2][TN];
+
+  auto read_frags = [&](int st, int s, int buf) {
+    const f16* as = As + st * kStageHalves + wm * WM * kBK + fo[s];
+#pragma unroll
+    for (int i = 0; i < TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kBK);
+    if (!TRANS) {
+      const f16* bs = Bs + st * kStageHalves + wn * WN * kBK + fo[s];
+#pragma unroll
+      for (int j = 0; j < TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kBK);
+    } else {
+      // ds_read_b64_tr_b16: lane l receives W[16 s + 8 (l / 32) + 4 h + 0..3][column l % 32] of
+      // the 32 columns the lanes of its 16-lane group address; h = 0, 1 give 8 consecutive k
+#pragma unroll
+      for (int j = 0; j < TN; ++j) {
+        const f16* q = Bs + st * kStageHalves + 16 * s * BN + nn_off[j];
+        const f16x4 lo = read_tr(q), hi = read_tr(q + 4 * BN);
+        fb[buf][j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+      }
+    }
+  };
+  auto mfmas = [&](int buf) {
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+        acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
+  };
+  // one operand read after each of the first MFMAs of a sub-step
+  constexpr int NREAD = TM + (TRANS ? 2 * TN : TN);
+  auto interleave = [&]() {
+#pragma unroll
+    for (int i = 0; i < TM * TN; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+      if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    }
+  };
+
+  // ---- main loop.  Step kt lives in stage kt % 4.  In step kt: read sub-step 1's operands
+  // under sub-step 0's MFMAs; wait for this wave's loads of step kt + 1 and for every wave's
+  // last read of stage kt % 4 (one barrier); refill that stage with step kt + 4, spreading the
+  // DMA instructions between sub-step 1's MFMAs, which run beside the reads of step kt + 1.
+#pragma unroll
+  for (int s = 0; s < kStages; ++s)
+    if (s < nk)
+#pragma unroll
+      for (int d = 0; d < LOADS; ++d) issue(s, s, d);
+  wait_loads(nk < kStages ? nk - 1 : kStages - 1);
+  __syncthreads();
+  read_frags(0, 0, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & (kStages - 1);
+    read_frags(st, 1, 1);
+    mfmas(0);
+    interleave();
+    wait_loads((nk - 1) - (kt + 1) < 2 ? (nk - 1) - (kt + 1) : 2);
+    __syncthreads();
+    if (kt + 1 < nk) read_frags((kt + 1) & (kStages - 1), 0, 0);
+    const bool refill = kt + kStages < nk;
+#pragma unroll
+    for (int q = 0; q < TM * TN; ++q) {
+      acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
+                                                                 acc[q / TN][q % TN], 0, 0, 0);
+      constexpr int PER = TM * TN / LOADS;
+      if (refill && q % PER == PER - 1) issue(kt + kStages, st, q / PER);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+  // every wave is past the last barrier, after which no wave reads a stage and no load is in
+  // flight: the A stages are free for the per-wave epilogue scratch
+
+  if (part) {
+    // split-K: this wave's fp32 partial blocks, lane-major (each register store is 256
+    // contiguous bytes); the reduce launch sums the splits and runs the epilogue
+    float* mine = part + (int64_t)wave * TM * TN * 1024 + lane;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) mine[((i * TN + j) * 16 + v) * 64] = acc[i][j][v];
+    return;
+  }
+  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN,
+                                    reinterpret_cast<uint8_t*>(As) + wave * kEpiScratch);
+}
+
+// Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
+// tiles as 128 x 128 quarters.  With split-K (p.splits > 1, LINEAR only) workgroup b runs split
+// b % splits of tile b / splits and stores its fp32 partial tile at p.part.  Tiles are numbered
+// M-fastest.
+template <bool TRANS, int EPI>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
+  __shared__ __attribute__((aligned(1024))) f16 As[kStages * kStageHalves];
+  __shared__ __attribute__((aligned(1024))) f16 Bs[kStages * kStageHalves];
+  const int nk_all = (int)(p.K / kBK);
+  int b = blockIdx.x;
+  if (b < main_tiles) {
+    // workgroups are dealt to the 8 XCDs round-robin: give each XCD a contiguous run of tiles
+    if ((main_tiles & 7) == 0) b = (b & 7) * (main_tiles >> 3) + (b >> 3);
+    const int tile = b / p.splits, split = b % p.splits;
+    const int64_t m0 = (int64_t)(tile % p.tiles_m) * kTile;
+    const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile;
+    const int kt0 = (int)((int64_t)nk_all * split / p.splits);
+    const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - kt0;
+    float* part = p.splits > 1 ? p.part + (int64_t)b * kTile * kTile : nullptr;
+    gemm_tile<TRANS, EPI, 256, 256, 2>(p, m0, n0, kt0, nk, part, As, Bs);
+  } else {
+    int t = b - main_tiles;
+    if ((tail_wgs & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
+    const int parent = main_tiles + t / 4, quarter = t % 4;
+    const int64_t m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
+    const int64_t n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
+    if (m0 >= p.M) return;
+    gemm_tile<TRANS, EPI, 128, 128, 4>(p, m0, n0, 0, nk_all, nullptr, As, Bs);
+  }
+}
+
+// Split-K, second launch: one wave per 128 x 64 wave block of a 256 x 256 tile sums the split
+// partials in split order (fixed, so the result is deterministic) and runs the epilogue.  The
+// kernel boundary orders it after every partial store.
+template <bool TRANS, int EPI>
+__global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
+  __shared__ __attribute__((aligned(16))) uint8_t escr[kEpiScratch];
+  constexpr int TM = 4, TN = 2;
+  const int lane = threadIdx.x;
+  const int tile = blockIdx.x / 8, wave = blockIdx.x % 8;
+  const int64_t m0 = (int64_t)(tile % p.tiles_m) * kTile + (wave / 4) * 128;
+  const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile + (wave % 4) * 64;
+  if (m0 >= p.M) return;
+  const float* src = p.part + (int64_t)tile * p.splits * kTile * kTile + wave * TM * TN * 1024 + lane;
+  f32x16 acc[TM][TN];
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = src[((i * TN + j) * 16 + v) * 64];
+  for (int sp = 1; sp < p.splits; ++sp) {
+    const float* q = src + (int64_t)sp * kTile * kTile;
+#pragma unroll
+    for (int i = 0; i < TM; ++i)
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) acc[i][j][v] += q[((i * TN + j) * 16 + v) * 64];
+  }
+  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0, n0, escr);
+}
+
+int cu_count() {
+  static int cached[64] = {};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 0;
+  if (!cached[dev]) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess) return 0;
+    cached[dev] = n;
+  }
+  return cached[dev];
+}
+
+// The launch shape of a GEMM on this kernel, or ok = false.
+struct HPlan {
+  bool ok;
+  int64_t tiles_m, tiles_n, main_wgs, tail_wgs;
+  int splits;
+};
+
+HPlan hplan(int64_t M, int64_t N, int64_t K, int epi) {
+  HPlan h{false, 0, 0, 0, 0, 1};
+  if (M <= 0 || N % kTile || K % kBK || K < kBK) return h;
+  const int cus = cu_count();
+  if (cus <= 0) return h;
+  h.tiles_m = (M + kTile - 1) / kTile;
+  h.tiles_n = N / kTile;
+  const int64_t tiles = h.tiles_m * h.tiles_n;
+  if (tiles * 4 > 0x7fffffff) return h;
+  if (tiles >= cus) {
+    // a last round at most half full runs as 128 x 128 quarters
+    h.main_wgs = tiles;
+    const int64_t rest = tiles % cus;
+    if (rest > 0 && rest <= cus / 2) {
+      h.main_wgs = tiles - rest;
+      h.tail_wgs = 4 * rest;
+    }
+    h.ok = true;
+    return h;
+  }
+  // fewer tiles than CUs: split K so that the splits fill the CUs once.  The fp32 partials cost
+  // two passes over splits x tiles x 256 KB, which only long K (4096 or more) repays; LINEAR
+  // only, at least 4 row tiles
+  if (epi != EPI_LINEAR || h.tiles_m < 4 || K < 4096) return h;
+  int64_t s = cus / tiles;
+  if (s > K / kBK / 8) s = K / kBK / 8;
+  if (s < 2) return h;
+  h.splits = (int)s;
+  h.main_wgs = tiles * s;
+  h.ok = true;
+  return h;
+}
+
+}  // namespace
+
+int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
+  const HPlan h = hplan(M, N, K, epi);
+  if (!h.ok || h.splits == 1) return 0;
+  return h.main_wgs * kTile * kTile * (int64_t)sizeof(float);
+}
+
+template <bool TRANS, int EPI>
+int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (!p0.w16) return kHgemmDeclined;
+  const HPlan h = hplan(p0.M, p0.N, p0.K, EPI);
+  if (!h.ok) return kHgemmDeclined;
+  GemmParams p = p0;
+  p.tiles_m = (int)h.tiles_m;
+  p.tiles_n = (int)h.tiles_n;
+  p.splits = h.splits;
+  if (h.splits > 1) {
+    // the partials go to the caller's workspace; without room for them, decline
+    if (!ws || ws_bytes < h.main_wgs * kTile * kTile * (int64_t)sizeof(float) || !dk_aligned(ws, 256))
+      return kHgemmDeclined;
+    p.part = reinterpret_cast<float*>(ws);
+  }
+  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>), dim3((unsigned)(h.main_wgs + h.tail_wgs)),
+                     dim3(kThreads), 0, stream, p, (int)h.main_wgs, (int)h.tail_wgs);
+  DK_CHECK_LAUNCH();
+  if (h.splits > 1) {
+    hipLaunchKernelGGL((hgemm_reduce_kernel<TRANS, EPI>),
+                       dim3((unsigned)(h.tiles_m * h.tiles_n * 8)), dim3(64), 0, stream, p);
+    DK_CHECK_LAUNCH();
+  }
+  return 0;
+}
+
+template int hgemm_launch<false, EPI_LINEAR>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_LINEAR>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<false, EPI_SWIGLU_FWD>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_SWIGLU_BWD>(const GemmParams&, void*, int64_t, hipStream_t);
+
+}  // namespace dk

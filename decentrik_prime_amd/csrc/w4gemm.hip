@@ -30,7 +30,9 @@
 // Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
 // (the REDUCE instance: consumer waves only, no LDS) sums them in split order and runs the
 // epilogue.
-#include "dk_common.h"
+#include "gemm_common.h"
+
+using namespace dk;
 
 namespace {
 
@@ -41,45 +43,6 @@ constexpr int kPadT = 16;         // NN: halves of padding per N-contiguous LDS 
 // run 512 threads, 256-row tiles 1024.
 template <int BM>
 constexpr int role_threads() { return (BM / 64) * 2 * 64; }
-
-enum { EPI_LINEAR = 0, EPI_SWIGLU_FWD = 1, EPI_SWIGLU_BWD = 2 };
-
-// One LoRA term of the LINEAR epilogue.  Forward: adds s * fp32(fp16(z B^T)) to output columns
-// [n_begin, n_end) (B holds the rows of those columns).  Backward: adds
-// (mask ? fp32(fp16(dz A)) * keep_scale : 0) to every column.
-struct LoraTerm {
-  const f16* z;         // [M][rank]: z (forward) or dz (backward)
-  const f16* r;         // forward: B [n_end - n_begin][rank]; backward: A [rank][N]
-  const uint8_t* mask;  // backward keep-mask [M][N] or null (no dropout, no scale)
-  int64_t n_begin, n_end;
-  float scale;          // forward: s; backward: keep_scale
-};
-
-struct GemmParams {
-  const f16* a;
-  int64_t lda;
-  int64_t M, N, K;
-  const uint8_t* packed;
-  const uint8_t* qabs;
-  const float* scale2;
-  const float* offset2;
-  const float* code2;
-  const float* nf4;
-  const f16* w16;       // two-phase: the weight dequantised to fp16, stored order ([N][K] NT, [K][N] NN)
-  int64_t inter;        // SwiGLU: gate/up width I
-  const f16* bias;      // [N] or null
-  LoraTerm lora[2];     // rank-r LoRA terms added in the LINEAR epilogue, in order
-  int n_lora;
-  int64_t rank;
-  void* out;
-  int64_t ldo;
-  int out_mode;
-  f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
-  int tiles_m, tiles_n;
-  int m_fastest;        // tile order: row tiles fastest (1) or column tiles fastest (0)
-  int splits;           // split-K factor (1: none)
-  float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
-};
 
 // REDUCE: the split-K second launch (consumer waves only): sum the partials, then the epilogue.
 // Every tile runs 4 waves per SIMD (two 512-thread or one 1024-thread workgroup per CU), so the
@@ -714,6 +677,8 @@ int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, h
                              w->rows * w->cols / DK_QBLOCK, stream))
     return e;
   p.w16 = w16;
+  const int big = hgemm_launch<TRANS, EPI>(p, nullptr, 0, stream);
+  if (big != kHgemmDeclined) return big;
   return launch_plan<TRANS, EPI, true>(pl, p, stream);
 }
 
@@ -842,13 +807,16 @@ int down_bwd_params(GemmParams& p, const void* dh, int64_t lddh, int64_t m, int6
   return 0;
 }
 
-// fp16 weight: the plan's split-K (partials in the workspace when one is given), one phase.
+// fp16 weight: the 256 x 256-tile kernel where the shape suits it (no workspace), else the plan's
+// split-K (partials in the workspace when one is given), one phase.
 template <bool TRANS, int EPI>
 int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes, hipStream_t stream) {
   if (!w16) return DK_ERR_INVALID;
   if (!dk_aligned(w16, 16)) return DK_ERR_ALIGN;
   if (p.M == 0) return 0;
   p.w16 = (const f16*)w16;
+  const int big = hgemm_launch<TRANS, EPI>(p, ws, ws_bytes, stream);
+  if (big != kHgemmDeclined) return big;
   Plan pl = plan_for(p.M, p.N, p.K, EPI);
   if (ws == nullptr) {
     pl.splits = 1;
@@ -981,11 +949,15 @@ extern "C" int dk_h16_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, c
 
 extern "C" int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op) {
   if (m <= 0 || rows <= 0 || cols <= 0) return 0;
+  // the 256 x 256-tile kernel's split-K partials where it takes the shape, else the plan's
+  int64_t n = 0, k = 0;
   switch (op) {
-    case DK_OP_LINEAR_FWD: return plan_workspace(plan_for(m, rows, cols, EPI_LINEAR));
-    case DK_OP_LINEAR_BWD_DX: return plan_workspace(plan_for(m, cols, rows, EPI_LINEAR));
+    case DK_OP_LINEAR_FWD: n = rows; k = cols; break;
+    case DK_OP_LINEAR_BWD_DX: n = cols; k = rows; break;
     default: return 0;
   }
+  const int64_t big = hgemm_workspace(m, n, k, EPI_LINEAR);
+  return big > 0 ? big : plan_workspace(plan_for(m, n, k, EPI_LINEAR));
 }
 
 extern "C" int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op) {

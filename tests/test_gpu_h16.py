@@ -3,9 +3,11 @@ dequantised to fp16, as the reference's GEMMs read its dequantised workspace,
 solution/fast_qwen.py:694-756) and of the dequant-ahead schedule of the linear stack.
 
 The fp16 weight is the GPU dequant of the NF4 weight (bit-exact with the oracle's, pinned by
-test_gpu_nf4).  The GEMMs run the same tile plan and MFMA order as their NF4 counterparts, so the
-outputs must be bit-identical to the dk_w4_* results; they are also checked against the oracle at
-rtol 1e-2 / atol 2e-2 (relative to the output scale for the small-valued gradients)."""
+test_gpu_nf4).  Where both entry points run the same kernel and tile plan (every shape here but
+the long-K ones, which the fp16 path splits differently) the outputs must be bit-identical to the
+dk_w4_* results; the long-K ones must agree to within fp32 summation-order differences (two fp16
+ulps).  All are also checked against the oracle at rtol 1e-2 / atol 2e-2 (relative to the output
+scale for the small-valued gradients)."""
 
 import numpy as np
 import pytest
@@ -30,6 +32,16 @@ def _same(a, b, what):
         bad = np.argwhere(a != b)
         raise AssertionError(f"{what}: {len(bad)} of {a.size} differ; first at {bad[0].tolist()}: "
                              f"{a[tuple(bad[0])]} vs {b[tuple(bad[0])]}")
+
+
+def _near(a, b, what):
+    """Equal up to the rounding of a different fp32 summation order: two fp16 ulps of the value
+    (fp16 outputs) or 2e-6 relative to the tensor's scale (fp32 outputs)."""
+    a, b = host(a).astype(np.float64), host(b).astype(np.float64)
+    scale = float(np.abs(b).max()) or 1.0
+    tol = 2 * 2.0 ** -10 * np.abs(b) + 2e-6 * scale
+    bad = np.abs(a - b) > tol
+    assert not bad.any(), f"{what}: {bad.sum()} of {a.size} differ beyond summation-order rounding"
 
 
 @pytest.fixture(scope="module")
@@ -131,7 +143,7 @@ def test_h16_mlp(torch, m):
     y4 = w4linear.linear_forward(act16, wd)
     y16 = w4linear.linear_forward(act16, wd, w16=d16)
     torch.cuda.synchronize()
-    _same(y16, y4, "down h16 vs w4")
+    _near(y16, y4, "down h16 vs w4")      # K = 8960: split differently
     assert_close(host(y16), linear.mm16(host(act16), qd["deq"].T), RTOL, ATOL, "down vs oracle")
     dh = (np.random.default_rng(26).standard_normal((m, 1536)) * 1e-2).astype(F16)
     gu_np = host(gu16)
@@ -144,7 +156,7 @@ def test_h16_mlp(torch, m):
     dx4 = w4linear.linear_backward_dx(gu4, wg, out_dtype=torch.float16)
     dx16 = w4linear.linear_backward_dx(gu16, wg, out_dtype=torch.float16, w16=g16)
     torch.cuda.synchronize()
-    _same(dx16, dx4, "dX mlp h16 vs w4")
+    _near(dx16, dx4, "dX mlp h16 vs w4")  # K = 17920: split differently
     _scaled_close(host(dx16), dx_ref, "dX mlp vs oracle chain")
 
 
