@@ -95,12 +95,13 @@ def kernel_table(torch, st, reps, only=None):
         rows.append((f"dequant {kind}", (lambda k: lambda: L[k].dequantize(out=h[k]))(kind), 0.0,
                      dq_bytes(L[kind]), 0))
     rows += [
-        ("lora_down", lambda: W.lora_down(x, lo["Aq"], lo["mq"], ks, out=z["q"]), g(m, r, D),
-         m * D * 3 + r * D * 2 + m * r * 2, 2),
-        ("lora_grads q", lambda: W.lora_grads(dy["qkv"][:, :D], z["q"], x, lo["Bq"], s, lo["mq"], ks),
-         g(m, r, D) * 3, None, 1),
-        ("lora_grads v", lambda: W.lora_grads(dy["qkv"][:, D + KV:], z["v"], x, lo["Bv"], s, lo["mv"], ks),
-         g(m, r, KV) * 2 + g(m, r, D), None, 1),
+        ("lora_down q+v", lambda: W.lora_down_multi(
+            x, [(lo["Aq"], lo["mq"], ks), (lo["Av"], lo["mv"], ks)], outs=[z["q"], z["v"]]),
+         2 * g(m, r, D), m * D * 2 + 2 * m * D + 2 * r * D * 2 + 2 * m * r * 2, 1),
+        ("lora_grads q+v", lambda: W.lora_grads_multi(
+            x, [(dy["qkv"][:, :D], z["q"], lo["Bq"], s, lo["mq"], ks),
+                (dy["qkv"][:, D + KV:], z["v"], lo["Bv"], s, lo["mv"], ks)]),
+         g(m, r, D) * 3 + g(m, r, KV) * 2 + g(m, r, D), None, 1),
     ]
     out = []
     for name, fn, flops, nbytes, per_layer in rows:

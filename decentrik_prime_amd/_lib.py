@@ -40,6 +40,18 @@ class LoraTermC(ctypes.Structure):
 
 _T = ctypes.POINTER(LoraTermC)
 
+
+class LoraDownTermC(ctypes.Structure):
+    """struct dk_lora_down_term."""
+    _fields_ = [("mask", _c_p), ("keep_scale", _f32), ("a", _c_p), ("z", _c_p)]
+
+
+class LoraGradsTermC(ctypes.Structure):
+    """struct dk_lora_grads_term."""
+    _fields_ = [("dy", _c_p), ("lddy", _i64), ("n_out", _i64), ("z", _c_p), ("lora_b", _c_p),
+                ("lora_scale", _f32), ("mask", _c_p), ("keep_scale", _f32), ("da", _c_p),
+                ("db", _c_p), ("dz", _c_p)]
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dk_error_string": (ctypes.c_char_p, [_int]),
@@ -69,6 +81,10 @@ SIGNATURES = {
                                         _c_p]),
     "dk_h16_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
+    "dk_lora_down_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraDownTermC), _int, _c_p]),
+    "dk_lora_grads_multi_workspace": (_i64, [_i64, _i64, _i64, ctypes.POINTER(_i64), _int]),
+    "dk_lora_grads_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraGradsTermC), _int,
+                                   _c_p, _i64, _c_p]),
     "dk_lora_grads": (_int, [_c_p, _i64, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64,
                              _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_w4_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _c_p, _i64, _c_p]),

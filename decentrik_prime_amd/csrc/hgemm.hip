@@ -426,36 +426,38 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   }
 }
 
-// Split-K, second launch: one wave per 128 x 64 wave block of a 256 x 256 tile sums the split
-// partials in split order (fixed, so the result is deterministic) and runs the epilogue.  The
-// kernel boundary orders it after every partial store.
+// Split-K, second launch: one wave per 32 x 32 block of a 256 x 256 tile (64 per tile) sums the
+// block's split partials in split order (fixed, so the result is deterministic) and runs the
+// epilogue on it.  The kernel boundary orders it after every partial store.
 template <bool TRANS, int EPI>
 __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
   __shared__ __attribute__((aligned(16))) uint8_t escr[kEpiScratch];
-  constexpr int TM = 4, TN = 2;
+  constexpr int TM = 4, TN = 2;   // the blocks of one 128 x 64 wave block of the first launch
   const int lane = threadIdx.x;
-  const int tile = blockIdx.x / 8, wave = blockIdx.x % 8;
-  const int64_t m0 = (int64_t)(tile % p.tiles_m) * kTile + (wave / 4) * 128;
-  const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile + (wave % 4) * 64;
+  const int tile = blockIdx.x / 64, blk = blockIdx.x % 64;
+  const int wave = blk / (TM * TN), i = (blk / TN) % TM, j = blk % TN;
+  const int64_t m0 = (int64_t)(tile % p.tiles_m) * kTile + (wave / 4) * 128 + 32 * i;
+  const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile + (wave % 4) * 64 + 32 * j;
   if (m0 >= p.M) return;
-  const float* src = p.part + (int64_t)tile * p.splits * kTile * kTile + wave * TM * TN * 1024 + lane;
-  f32x16 acc[TM][TN];
+  const float* src = p.part + (int64_t)tile * p.splits * kTile * kTile +
+                     (wave * TM * TN + i * TN + j) * 1024 + lane;
+  f32x16 acc[1][1];
+  float v_all[8][16];
+  // all splits' loads first (up to 8 in flight per register), then the sum in split order
+  int sp = 0;
+  for (; sp < p.splits; sp += 8) {
 #pragma unroll
-  for (int i = 0; i < TM; ++i)
+    for (int u = 0; u < 8; ++u)
+      if (sp + u < p.splits)
 #pragma unroll
-    for (int j = 0; j < TN; ++j)
+        for (int v = 0; v < 16; ++v) v_all[u][v] = src[(int64_t)(sp + u) * kTile * kTile + v * 64];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) acc[i][j][v] = src[((i * TN + j) * 16 + v) * 64];
-  for (int sp = 1; sp < p.splits; ++sp) {
-    const float* q = src + (int64_t)sp * kTile * kTile;
+    for (int u = 0; u < 8; ++u)
+      if (sp + u < p.splits)
 #pragma unroll
-    for (int i = 0; i < TM; ++i)
-#pragma unroll
-      for (int j = 0; j < TN; ++j)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] += q[((i * TN + j) * 16 + v) * 64];
+        for (int v = 0; v < 16; ++v) acc[0][0][v] = sp + u == 0 ? v_all[u][v] : acc[0][0][v] + v_all[u][v];
   }
-  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0, n0, escr);
+  wave_epilogue<TRANS, EPI, 1, 1>(p, acc, m0, n0, escr);
 }
 
 int cu_count() {
@@ -538,7 +540,7 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   DK_CHECK_LAUNCH();
   if (h.splits > 1) {
     hipLaunchKernelGGL((hgemm_reduce_kernel<TRANS, EPI>),
-                       dim3((unsigned)(h.tiles_m * h.tiles_n * 8)), dim3(64), 0, stream, p);
+                       dim3((unsigned)(h.tiles_m * h.tiles_n * 64)), dim3(64), 0, stream, p);
     DK_CHECK_LAUNCH();
   }
   return 0;

@@ -23,6 +23,7 @@ constexpr int kRowTile = 16;     // rows per workgroup of the row reductions
 constexpr int kRowThreads = 512; // 8 waves split K in the row reductions
 constexpr int kChunkRows = 128;  // rows per partial sum of the column reductions
 constexpr int kColsPerBlock = 128;
+constexpr int kMaxJobs = 2;      // LoRA terms per launch (q and v of the fused QKV projection)
 
 __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, float ks) {
   f16x8 out;
@@ -42,13 +43,34 @@ __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, fl
 // 16x16x32 MFMA operand layout: lane l holds row/column l % 16 and k = 8 * (l / 16) + [0, 8);
 // the result register v of lane l is row 4 * (l / 16) + v, column l % 16.  The 8 waves split K
 // and issue the loads of kBatch steps before their MFMAs; their sums are added in a fixed order.
+// Up to kMaxJobs independent problems over the same rows run in one launch (the q and v LoRA
+// terms of the fused QKV projection); workgroup b serves job b / ceil(rows / kRowTile).
+struct RowsJob {
+  const f16* in;
+  int64_t ld;
+  const uint8_t* mask;
+  float ks;
+  const f16* wt;
+  float scale;
+  f16* out;
+  int64_t cols;
+};
+struct RowsJobs {
+  RowsJob j[kMaxJobs];
+};
+
 template <int R, int MODE, bool MASKED>
-__global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(const f16* __restrict__ in,
-                                                                int64_t ld,
-                                                                const uint8_t* __restrict__ mask,
-                                                                float ks, const f16* __restrict__ wt,
-                                                                float scale, f16* __restrict__ out,
-                                                                int64_t rows, int64_t cols) {
+__global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, int64_t rows) {
+  const int64_t per_job = (rows + kRowTile - 1) / kRowTile;
+  const RowsJob& J = jobs.j[blockIdx.x / per_job];
+  const f16* __restrict__ in = J.in;
+  const int64_t ld = J.ld;
+  const uint8_t* __restrict__ mask = J.mask;
+  const float ks = J.ks;
+  const f16* __restrict__ wt = J.wt;
+  const float scale = J.scale;
+  f16* __restrict__ out = J.out;
+  const int64_t cols = J.cols;
   constexpr int RB = R / 16;
   constexpr int NW = kRowThreads / 64;
   constexpr int kBatch = 4;
@@ -57,7 +79,7 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(const f16* __res
   __shared__ float red[NW * 16 * R];
   __shared__ __attribute__((aligned(16))) f16 Bs[MODE == 1 ? KC * BLD : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t row0 = (int64_t)blockIdx.x * kRowTile;
+  const int64_t row0 = (int64_t)(blockIdx.x % per_job) * kRowTile;
   const int lr = lane & 15, lk = 8 * (lane >> 4);
   const int64_t m = row0 + lr < rows ? row0 + lr : rows - 1;   // clamped: its sums are not stored
   const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
@@ -146,19 +168,40 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(const f16* __res
 // rows addressed by lanes a, a + 4, a + 8, a + 12, so lane l addressing row
 // 8 (l / 16) + 4 h + (l % 16) / 4, column 4 (l % 4) receives rows 8 (l / 16) + 4 h + 0..3 of
 // column l % 16, and two reads (h = 0, 1) give the 8 consecutive rows of the MFMA operand.
+// Jobs as for the row reductions: column blocks [bx0, next job's bx0) of grid.x serve job j.
+struct ColsJob {
+  const f16* P;
+  int64_t ld;
+  const uint8_t* mask;
+  float ks;
+  const f16* Q;
+  float* part;
+  int64_t cols;
+  int bx0;
+};
+struct ColsJobs {
+  ColsJob j[kMaxJobs];
+  int n;
+};
+
 template <int R, bool DROP>
-__global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restrict__ P, int64_t ld,
-                                                             const uint8_t* __restrict__ mask,
-                                                             float ks, const f16* __restrict__ Q,
-                                                             float* __restrict__ part,
-                                                             int64_t rows, int64_t cols) {
+__global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int64_t rows) {
+  const int jb = (jobs.n > 1 && (int)blockIdx.x >= jobs.j[1].bx0) ? 1 : 0;
+  const ColsJob& J = jobs.j[jb];
+  const f16* __restrict__ P = J.P;
+  const int64_t ld = J.ld;
+  const uint8_t* __restrict__ mask = J.mask;
+  const float ks = J.ks;
+  const f16* __restrict__ Q = J.Q;
+  float* __restrict__ part = J.part;
+  const int64_t cols = J.cols;
   constexpr int PLD = kColsPerBlock + 16;   // halves per staged P row
   constexpr int QLD = R + 16;               // halves per staged Q row
   constexpr int P_CHUNKS = kChunkRows * kColsPerBlock / 8 / kThreads;   // 16-byte chunks per thread
   __shared__ __attribute__((aligned(16))) f16 Ps[kChunkRows * PLD];
   __shared__ __attribute__((aligned(16))) f16 Qs[kChunkRows * QLD];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t c0 = (int64_t)blockIdx.x * kColsPerBlock;
+  const int64_t c0 = (int64_t)(blockIdx.x - J.bx0) * kColsPerBlock;
   const int64_t r0 = (int64_t)blockIdx.y * kChunkRows;
   // P tile: every load issued before the first store (rows past the end read as zero)
   f16x8 pv[P_CHUNKS];
@@ -239,15 +282,33 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(const f16* __restri
   }
 }
 
-// out = fp32(fp16(sum over chunks of part[chunk][n][r])) * scale, stored [n][r] or, TRANSPOSE,
-// [r][n].
-template <bool TRANSPOSE>
-__global__ __launch_bounds__(kThreads) void lora_finalize_kernel(const float* __restrict__ part,
-                                                                 int64_t n_chunks, int64_t cols,
-                                                                 int64_t R, float scale,
-                                                                 float* __restrict__ out) {
-  const int64_t i = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+// out = fp32(fp16(sum over chunks of part[chunk][n][r])) * scale, stored [n][r] or, transposed,
+// [r][n].  Up to kMaxFinal jobs per launch; job j owns the threads from its t0 (a multiple of the
+// workgroup size) on.
+constexpr int kMaxFinal = 2 * kMaxJobs;
+struct FinalJob {
+  const float* part;
+  int64_t cols;
+  float scale;
+  float* out;
+  int transpose;
+  int64_t t0;
+};
+struct FinalJobs {
+  FinalJob j[kMaxFinal];
+  int n;
+};
+
+__global__ __launch_bounds__(kThreads) void lora_finalize_kernel(FinalJobs jobs, int64_t n_chunks,
+                                                                 int64_t R) {
+  const int64_t gi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
+  int jb = 0;
+  for (int q = 1; q < jobs.n; ++q)
+    if (gi >= jobs.j[q].t0) jb = q;
+  const FinalJob& J = jobs.j[jb];
+  const int64_t i = gi - J.t0, cols = J.cols;
   if (i >= cols * R) return;
+  const float* __restrict__ part = J.part;
   // 8 loads in flight at a time, added in chunk order
   float s = 0.0f;
   int64_t c = 0;
@@ -259,45 +320,52 @@ __global__ __launch_bounds__(kThreads) void lora_finalize_kernel(const float* __
     for (int u = 0; u < 8; ++u) s += v[u];
   }
   for (; c < n_chunks; ++c) s += part[c * cols * R + i];
-  const float v = __fmul_rn((float)dk_h(s), scale);
+  const float v = __fmul_rn((float)dk_h(s), J.scale);
   const int64_t n = i / R, r = i % R;
-  if (TRANSPOSE) out[r * cols + n] = v; else out[i] = v;
+  if (J.transpose) J.out[r * cols + n] = v; else J.out[i] = v;
 }
 
 template <int MODE, bool MASKED>
-int rows_launch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
-                float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
-  const dim3 grid((unsigned)((rows + kRowTile - 1) / kRowTile)), block(kRowThreads);
+int rows_launch(int64_t R, hipStream_t stream, const RowsJobs& jobs, int n_jobs, int64_t rows) {
+  const dim3 grid((unsigned)(n_jobs * ((rows + kRowTile - 1) / kRowTile))), block(kRowThreads);
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
-    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE, MASKED>), grid, block, 0, stream, in, ld, mask, ks, wt, scale, out, rows, cols); break;
+    case 16: hipLaunchKernelGGL((lora_rows_kernel<16, MODE, MASKED>), grid, block, 0, stream, jobs, rows); break;
+    case 32: hipLaunchKernelGGL((lora_rows_kernel<32, MODE, MASKED>), grid, block, 0, stream, jobs, rows); break;
+    case 48: hipLaunchKernelGGL((lora_rows_kernel<48, MODE, MASKED>), grid, block, 0, stream, jobs, rows); break;
+    case 64: hipLaunchKernelGGL((lora_rows_kernel<64, MODE, MASKED>), grid, block, 0, stream, jobs, rows); break;
     default: return DK_ERR_INVALID;
   }
   DK_CHECK_LAUNCH();
   return 0;
 }
 
-template <int MODE>
-int rows_dispatch(int64_t R, hipStream_t stream, const f16* in, int64_t ld, const uint8_t* mask,
-                  float ks, const f16* wt, float scale, f16* out, int64_t rows, int64_t cols) {
-  if (MODE == 0 && mask) return rows_launch<MODE, true>(R, stream, in, ld, mask, ks, wt, scale, out, rows, cols);
-  return rows_launch<MODE, false>(R, stream, in, ld, mask, ks, wt, scale, out, rows, cols);
-}
-
 template <bool DROP>
-int cols_dispatch(int64_t R, hipStream_t stream, const f16* P, int64_t ld, const uint8_t* mask,
-                  float ks, const f16* Q, float* part, int64_t rows, int64_t cols) {
-  const dim3 grid((unsigned)((cols + kColsPerBlock - 1) / kColsPerBlock),
-                  (unsigned)((rows + kChunkRows - 1) / kChunkRows));
+int cols_launch(int64_t R, hipStream_t stream, ColsJobs jobs, int64_t rows) {
+  int bx = 0;
+  for (int q = 0; q < jobs.n; ++q) {
+    jobs.j[q].bx0 = bx;
+    bx += (int)((jobs.j[q].cols + kColsPerBlock - 1) / kColsPerBlock);
+  }
+  const dim3 grid((unsigned)bx, (unsigned)((rows + kChunkRows - 1) / kChunkRows));
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_cols_kernel<16, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
-    case 32: hipLaunchKernelGGL((lora_cols_kernel<32, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
-    case 48: hipLaunchKernelGGL((lora_cols_kernel<48, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
-    case 64: hipLaunchKernelGGL((lora_cols_kernel<64, DROP>), grid, dim3(kThreads), 0, stream, P, ld, mask, ks, Q, part, rows, cols); break;
+    case 16: hipLaunchKernelGGL((lora_cols_kernel<16, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 32: hipLaunchKernelGGL((lora_cols_kernel<32, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 48: hipLaunchKernelGGL((lora_cols_kernel<48, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 64: hipLaunchKernelGGL((lora_cols_kernel<64, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
     default: return DK_ERR_INVALID;
   }
+  DK_CHECK_LAUNCH();
+  return 0;
+}
+
+int finalize_launch(FinalJobs jobs, int64_t n_chunks, int64_t R, hipStream_t stream) {
+  int64_t t = 0;
+  for (int q = 0; q < jobs.n; ++q) {
+    jobs.j[q].t0 = t;
+    t += (jobs.j[q].cols * R + kThreads - 1) / kThreads * kThreads;
+  }
+  hipLaunchKernelGGL(lora_finalize_kernel, dim3((unsigned)(t / kThreads)), dim3(kThreads), 0, stream,
+                     jobs, n_chunks, R);
   DK_CHECK_LAUNCH();
   return 0;
 }
@@ -306,55 +374,143 @@ bool rank_ok(int64_t r) { return r >= 16 && r <= 64 && r % 16 == 0; }
 
 }  // namespace
 
-extern "C" int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const void* a,
-                            void* z, int64_t m, int64_t k, int64_t rank, hipStream_t stream) {
-  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !a || !z) return DK_ERR_INVALID;
-  if (!dk_aligned(x, 16) || !dk_aligned(a, 16) || (mask && !dk_aligned(mask, 8))) return DK_ERR_ALIGN;
+extern "C" int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t rank,
+                                  const dk_lora_down_term* terms, int n_terms, hipStream_t stream) {
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !terms || n_terms < 1 ||
+      n_terms > kMaxJobs)
+    return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
+  int masked = 0;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_down_term& u = terms[t];
+    if (!u.a || !u.z) return DK_ERR_INVALID;
+    if (!dk_aligned(u.a, 16) || (u.mask && !dk_aligned(u.mask, 8))) return DK_ERR_ALIGN;
+    masked += u.mask != nullptr;
+  }
   if (m == 0) return 0;
-  return rows_dispatch<0>(rank, stream, (const f16*)x, k, mask, mask ? keep_scale : 1.0f,
-                          (const f16*)a, 1.0f, (f16*)z, m, k);
+  auto job = [&](const dk_lora_down_term& u) {
+    return RowsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f, (const f16*)u.a, 1.0f,
+                   (f16*)u.z, k};
+  };
+  if (masked == 0 || masked == n_terms) {
+    RowsJobs jobs = {};
+    for (int t = 0; t < n_terms; ++t) jobs.j[t] = job(terms[t]);
+    return masked ? rows_launch<0, true>(rank, stream, jobs, n_terms, m)
+                  : rows_launch<0, false>(rank, stream, jobs, n_terms, m);
+  }
+  for (int t = 0; t < n_terms; ++t) {   // masked and unmasked terms: one launch each
+    RowsJobs jobs = {};
+    jobs.j[0] = job(terms[t]);
+    const int e = terms[t].mask ? rows_launch<0, true>(rank, stream, jobs, 1, m)
+                                : rows_launch<0, false>(rank, stream, jobs, 1, m);
+    if (e) return e;
+  }
+  return 0;
 }
 
-extern "C" int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank) {
-  if (m <= 0) return 0;
+extern "C" int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const void* a,
+                            void* z, int64_t m, int64_t k, int64_t rank, hipStream_t stream) {
+  const dk_lora_down_term t = {mask, keep_scale, a, z};
+  return dk_lora_down_multi(x, m, k, rank, &t, 1, stream);
+}
+
+extern "C" int64_t dk_lora_grads_multi_workspace(int64_t m, int64_t k, int64_t rank,
+                                                 const int64_t* n_outs, int n_terms) {
+  if (m <= 0 || k <= 0 || rank <= 0 || !n_outs || n_terms < 1 || n_terms > kMaxJobs) return 0;
   const int64_t chunks = (m + kChunkRows - 1) / kChunkRows;
-  const int64_t cols = n_out > k ? n_out : k;
+  int64_t cols = 0;
+  for (int t = 0; t < n_terms; ++t) cols += (n_outs[t] > 0 ? n_outs[t] : 0) + k;
   return chunks * cols * rank * (int64_t)sizeof(float);
 }
 
-extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x,
-                             const uint8_t* mask,
-                             float keep_scale, const void* lora_b, float lora_scale, int64_t m,
-                             int64_t n_out, int64_t k, int64_t rank, float* da, float* db,
-                             void* dz, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (m < 0 || n_out <= 0 || k <= 0 || n_out % 32 || k % 32 || !rank_ok(rank)) return DK_ERR_INVALID;
-  if (!dy || !z || !x || !lora_b || !da || !db || !dz || lddy < n_out) return DK_ERR_INVALID;
-  if (!dk_aligned(dy, 16) || lddy % 8 || !dk_aligned(x, 16) || !dk_aligned(lora_b, 16) ||
-      (mask && !dk_aligned(mask, 8)))
-    return DK_ERR_ALIGN;
+extern "C" int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank) {
+  return dk_lora_grads_multi_workspace(m, k, rank, &n_out, 1);
+}
+
+extern "C" int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t rank,
+                                   const dk_lora_grads_term* terms, int n_terms, void* ws,
+                                   int64_t ws_bytes, hipStream_t stream) {
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !terms || n_terms < 1 ||
+      n_terms > kMaxJobs)
+    return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
+  int64_t n_outs[kMaxJobs];
+  int masked = 0;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_grads_term& u = terms[t];
+    if (u.n_out <= 0 || u.n_out % 32 || !u.dy || !u.z || !u.lora_b || !u.da || !u.db || !u.dz ||
+        u.lddy < u.n_out)
+      return DK_ERR_INVALID;
+    if (!dk_aligned(u.dy, 16) || u.lddy % 8 || !dk_aligned(u.lora_b, 16) ||
+        (u.mask && !dk_aligned(u.mask, 8)))
+      return DK_ERR_ALIGN;
+    n_outs[t] = u.n_out;
+    masked += u.mask != nullptr;
+  }
   if (m == 0) return 0;
-  if (!ws || ws_bytes < dk_lora_grads_workspace(m, n_out, k, rank)) return DK_ERR_WORKSPACE;
-  const float ks = mask ? keep_scale : 1.0f;
+  if (!ws || ws_bytes < dk_lora_grads_multi_workspace(m, k, rank, n_outs, n_terms))
+    return DK_ERR_WORKSPACE;
   const int64_t chunks = (m + kChunkRows - 1) / kChunkRows;
-  float* part = (float*)ws;
+  // partial sums: [dB of every term | dA of every term], each chunks x cols x rank fp32
+  float* part_db[kMaxJobs];
+  float* part_da[kMaxJobs];
+  float* next = (float*)ws;
+  for (int t = 0; t < n_terms; ++t) { part_db[t] = next; next += chunks * n_outs[t] * rank; }
+  for (int t = 0; t < n_terms; ++t) { part_da[t] = next; next += chunks * k * rank; }
   // dz = fp16(fp16(dY B) * s)
-  int e = rows_dispatch<1>(rank, stream, (const f16*)dy, lddy, nullptr, 1.0f, (const f16*)lora_b,
-                           lora_scale, (f16*)dz, m, n_out);
+  RowsJobs rj = {};
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_grads_term& u = terms[t];
+    rj.j[t] = RowsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.lora_b, u.lora_scale,
+                      (f16*)u.dz, u.n_out};
+  }
+  int e = rows_launch<1, false>(rank, stream, rj, n_terms, m);
   if (e) return e;
   // dB = fp32(fp16(dY^T z)) * s
-  e = cols_dispatch<false>(rank, stream, (const f16*)dy, lddy, nullptr, 1.0f, (const f16*)z, part, m,
-                           n_out);
+  ColsJobs cb = {};
+  cb.n = n_terms;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_grads_term& u = terms[t];
+    cb.j[t] = ColsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.z, part_db[t], u.n_out, 0};
+  }
+  e = cols_launch<false>(rank, stream, cb, m);
   if (e) return e;
-  hipLaunchKernelGGL(lora_finalize_kernel<false>, dim3((unsigned)((n_out * rank + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, part, chunks, n_out, rank, lora_scale, db);
-  DK_CHECK_LAUNCH();
-  // dA = fp32(fp16(dz^T Xd))
-  e = mask ? cols_dispatch<true>(rank, stream, (const f16*)x, k, mask, ks, (const f16*)dz, part, m, k)
-           : cols_dispatch<false>(rank, stream, (const f16*)x, k, nullptr, 1.0f, (const f16*)dz, part,
-                                  m, k);
-  if (e) return e;
-  hipLaunchKernelGGL(lora_finalize_kernel<true>, dim3((unsigned)((k * rank + kThreads - 1) / kThreads)),
-                     dim3(kThreads), 0, stream, part, chunks, k, rank, 1.0f, da);
-  DK_CHECK_LAUNCH();
-  return 0;
+  // dA = fp32(fp16(dz^T Xd)), Xd the dropout of x with the term's mask
+  auto da_job = [&](int t) {
+    const dk_lora_grads_term& u = terms[t];
+    return ColsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f, (const f16*)u.dz,
+                   part_da[t], k, 0};
+  };
+  if (masked == 0 || masked == n_terms) {
+    ColsJobs ca = {};
+    ca.n = n_terms;
+    for (int t = 0; t < n_terms; ++t) ca.j[t] = da_job(t);
+    e = masked ? cols_launch<true>(rank, stream, ca, m) : cols_launch<false>(rank, stream, ca, m);
+    if (e) return e;
+  } else {
+    for (int t = 0; t < n_terms; ++t) {
+      ColsJobs ca = {};
+      ca.n = 1;
+      ca.j[0] = da_job(t);
+      e = terms[t].mask ? cols_launch<true>(rank, stream, ca, m) : cols_launch<false>(rank, stream, ca, m);
+      if (e) return e;
+    }
+  }
+  FinalJobs fj = {};
+  fj.n = 2 * n_terms;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_grads_term& u = terms[t];
+    fj.j[t] = FinalJob{part_db[t], u.n_out, u.lora_scale, u.db, 0, 0};
+    fj.j[n_terms + t] = FinalJob{part_da[t], k, 1.0f, u.da, 1, 0};
+  }
+  return finalize_launch(fj, chunks, rank, stream);
+}
+
+extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x,
+                             const uint8_t* mask, float keep_scale, const void* lora_b,
+                             float lora_scale, int64_t m, int64_t n_out, int64_t k, int64_t rank,
+                             float* da, float* db, void* dz, void* ws, int64_t ws_bytes,
+                             hipStream_t stream) {
+  const dk_lora_grads_term t = {dy, lddy, n_out, z, lora_b, lora_scale, mask, keep_scale, da, db, dz};
+  return dk_lora_grads_multi(x, m, k, rank, &t, 1, ws, ws_bytes, stream);
 }

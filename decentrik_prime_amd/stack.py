@@ -3,7 +3,7 @@
 Per layer (shapes of solution/fast_qwen.py:53 QWEN15: D = 1536, I = 8960, KV = 256, r = 16),
 with M packed tokens:
 
-  forward   z_q = lora_down(X, A_q, mask_q)            z_v likewise        (rank-16 LoRA inputs)
+  forward   z_q = lora_down(X, A_q, mask_q)            z_v likewise, one launch (rank-16 inputs)
             qkv = X W_qkv^T + b_qkv, + s z_q B_q^T on the q columns, + s z_v B_v^T on the v
                   columns                               one GEMM over the q|k|v rows, as the
                                                         reference's addmm (fast_qwen.py:947)
@@ -13,7 +13,7 @@ with M packed tokens:
   backward  gu <- SwiGLU'(dY_d W_d, gu)                 down^T GEMM + SwiGLU backward fused
             dX_mlp = gu W_gu                            [M, 2I] x [2I, D]
             dX_o = dY_o W_o
-            dA_q, dB_q, dz_q = lora_grads(dQKV[:, q], ...)    and the same for v
+            dA_q, dB_q, dz_q = lora_grads(dQKV[:, q], ...)    and v, in shared launches
             dX_qkv = dQKV W_qkv + mask_q ks dz_q A_q + mask_v ks dz_v A_v    one NN GEMM
 
 The upstream gradients dY_* are fixed random tensors (the attention and norm backward that would
@@ -37,8 +37,8 @@ import torch
 from . import k_nf4, quant
 from .schedule import DequantAhead
 from .w4linear import (down_swiglu_backward, gateup_swiglu_forward, linear_backward_dx,
-                       linear_backward_dx_lora, linear_forward, linear_forward_lora, lora_down,
-                       lora_grads)
+                       linear_backward_dx_lora, linear_forward, linear_forward_lora,
+                       lora_down_multi, lora_grads_multi)
 
 D, I, KV, R = 1536, 8960, 256, 16
 QKV = D + 2 * KV
@@ -146,8 +146,9 @@ class NF4LinearStack:
     def forward_layer(self, i):
         L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
         op, nm, w16, done = self._op, self.op_name, self._w16, self._done
-        op("lora_down", lora_down, x, lo["Aq"], lo["mq"], self.keep_scale, out=z["q"])
-        op("lora_down", lora_down, x, lo["Av"], lo["mv"], self.keep_scale, out=z["v"])
+        op("lora_down q+v", lora_down_multi, x,
+           [(lo["Aq"], lo["mq"], self.keep_scale), (lo["Av"], lo["mv"], self.keep_scale)],
+           outs=[z["q"], z["v"]])
         op(nm("qkv", "_linear_fwd qkv+lora"), linear_forward_lora, x, L["qkv"], lo["bias"],
            self.qkv_terms(i), out=o["qkv"], w16=w16("qkv", i))
         done("qkv", i + 1)
@@ -173,10 +174,10 @@ class NF4LinearStack:
            w16=w16("o", i))
         done("o", i - 1)
         dqkv = dy["qkv"]
-        daq, dbq, dzq = op("lora_grads q", lora_grads, dqkv[:, :D], z["q"], x, lo["Bq"], self.s,
-                           lo["mq"], self.keep_scale)
-        dav, dbv, dzv = op("lora_grads v", lora_grads, dqkv[:, D + KV:], z["v"], x, lo["Bv"],
-                           self.s, lo["mv"], self.keep_scale)
+        (daq, dbq, dzq), (dav, dbv, dzv) = op(
+            "lora_grads q+v", lora_grads_multi, x,
+            [(dqkv[:, :D], z["q"], lo["Bq"], self.s, lo["mq"], self.keep_scale),
+             (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, lo["mv"], self.keep_scale)])
         op(nm("qkv", "_linear_bwd_dx qkv+lora"), linear_backward_dx_lora, dqkv, L["qkv"],
            [(dzq, lo["Aq"], lo["mq"], self.keep_scale), (dzv, lo["Av"], lo["mv"], self.keep_scale)],
            out=self.dx_qkv, w16=w16("qkv", i))

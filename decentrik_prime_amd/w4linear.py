@@ -2,12 +2,14 @@
 
 These replace the reference's dequant-to-workspace + ``torch.mm``/``addmm`` call sites and the
 LoRA lines around them (solution/fast_qwen.py:943-947, 1037, 1080-1112, 1310-1383;
-solution/k_norm.py:49-53, 65-71; solution/k_rope.py:39-43, 54-58).  The NF4 weight is never
-materialised in fp16: each GEMM workgroup dequantises its W tile into LDS (``dk_w4_*`` in
-libdk.so).  Every op runs on ``torch.cuda.current_stream()`` and allocates only its outputs
-(and, for the LoRA gradients, a small fp32 partial-sum workspace) through torch.
+solution/k_norm.py:49-53, 65-71; solution/k_rope.py:39-43, 54-58).  A GEMM either reads the NF4
+sections and dequantises its W tiles on the fly (``dk_w4_*`` in libdk.so) or, given ``w16``,
+reads an fp16 copy of the weight dequantised ahead (``dk_h16_*``, the reference's dequantised
+workspace).  Every op runs on ``torch.cuda.current_stream()`` and allocates only its outputs and
+scratch (split-K partials, LoRA partial sums) through torch.
 """
 
+import ctypes
 import threading
 
 import torch
@@ -150,6 +152,35 @@ def lora_down(x, lora_A, mask=None, keep_scale=1.0, out=None):
                                  _lib.ptr(out), m, k, r, _lib.stream_handle(x.device))
     _lib.check(rc, "dk_lora_down")
     return out
+
+
+def lora_down_multi(x, terms, outs=None):
+    """lora_down of one or two adapters on the same x in shared launches (the q and v adapters
+    of the fused QKV projection): terms = [(lora_A [r, K], mask or None, keep_scale), ...].
+    Returns [z, ...], each exactly as lora_down computes it."""
+    _check16(x, "x")
+    m, k = x.shape
+    if not x.is_contiguous():
+        raise ValueError("lora_down_multi: x must be contiguous")
+    if not 1 <= len(terms) <= 2:
+        raise ValueError("lora_down_multi takes one or two terms")
+    r = terms[0][0].shape[0]
+    arr = (_lib.LoraDownTermC * len(terms))()
+    keep, zs = [], []
+    for t, (a, mask, ks) in enumerate(terms):
+        _check16(a, "lora_A")
+        if tuple(a.shape) != (r, k) or not a.is_contiguous():
+            raise ValueError("lora_down_multi: every lora_A must be a contiguous [r, K]")
+        mask = _mask_ok(mask, (m, k))
+        z = outs[t] if outs is not None else torch.empty(m, r, dtype=torch.float16, device=x.device)
+        _check16(z, "z", (m, r))
+        arr[t] = _lib.LoraDownTermC(_lib.ptr(mask), float(ks), _lib.ptr(a), _lib.ptr(z))
+        keep.append((a, mask))
+        zs.append(z)
+    rc = _lib.lib().dk_lora_down_multi(_lib.ptr(x), m, k, r, arr, len(terms),
+                                       _lib.stream_handle(x.device))
+    _lib.check(rc, "dk_lora_down_multi")
+    return zs
 
 
 def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None, w16=None):
@@ -360,6 +391,49 @@ def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
                          _lib.ptr(db), _lib.ptr(dz), _lib.ptr(ws), nbytes, _lib.stream_handle(dev))
     _lib.check(rc, "dk_lora_grads")
     return da, db, dz
+
+
+def lora_grads_multi(x, terms):
+    """lora_grads of one or two adapters on the same x in shared launches: terms =
+    [(dy, z, lora_B, lora_scale, mask or None, keep_scale), ...].  Returns [(dA, dB, dz), ...],
+    each exactly as lora_grads computes it."""
+    _check16(x, "x")
+    if not x.is_contiguous():
+        raise ValueError("x must be contiguous")
+    if not 1 <= len(terms) <= 2:
+        raise ValueError("lora_grads_multi takes one or two terms")
+    m, k = x.shape
+    r = terms[0][1].shape[1]
+    dev = x.device
+    arr = (_lib.LoraGradsTermC * len(terms))()
+    n_outs = (ctypes.c_int64 * len(terms))()
+    keep, res = [], []
+    for t, (dy, z, lora_B, s, mask, ks) in enumerate(terms):
+        _check16(dy, "dy")
+        for u, nm in ((z, "z"), (lora_B, "lora_B")):
+            _check16(u, nm)
+            if not u.is_contiguous():
+                raise ValueError(f"{nm} must be contiguous")
+        n_out = dy.shape[1]
+        if dy.shape[0] != m or tuple(z.shape) != (m, r) or tuple(lora_B.shape) != (n_out, r):
+            raise ValueError("lora_grads_multi: inconsistent shapes")
+        mask = _mask_ok(mask, (m, k))
+        da = torch.empty(r, k, dtype=torch.float32, device=dev)
+        db = torch.empty(n_out, r, dtype=torch.float32, device=dev)
+        dz = torch.empty(m, r, dtype=torch.float16, device=dev)
+        arr[t] = _lib.LoraGradsTermC(_lib.ptr(dy), dy.stride(0), n_out, _lib.ptr(z),
+                                     _lib.ptr(lora_B), float(s), _lib.ptr(mask), float(ks),
+                                     _lib.ptr(da), _lib.ptr(db), _lib.ptr(dz))
+        n_outs[t] = n_out
+        keep.append((dy, mask))
+        res.append((da, db, dz))
+    L = _lib.lib()
+    nbytes = int(L.dk_lora_grads_multi_workspace(m, k, r, n_outs, len(terms)))
+    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev)
+    rc = L.dk_lora_grads_multi(_lib.ptr(x), m, k, r, arr, len(terms), _lib.ptr(ws), nbytes,
+                               _lib.stream_handle(dev))
+    _lib.check(rc, "dk_lora_grads_multi")
+    return res
 
 
 def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None):

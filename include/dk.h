@@ -187,6 +187,41 @@ int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x, co
                   int64_t n_out, int64_t k, int64_t rank, float* da, float* db, void* dz,
                   void* ws, int64_t ws_bytes, hipStream_t stream);
 
+/* One or two LoRA adapters on the same input x in shared launches: the q and v adapters of the
+ * fused QKV projection (solution/fast_qwen.py:943-944 forward, 1364-1380 backward), each term
+ * computed exactly as by dk_lora_down / dk_lora_grads (same kernels, same summation order), x
+ * read by both terms' workgroups of one launch.  No counterpart in the reference as one call:
+ * it batches the per-adapter calls above. */
+typedef struct dk_lora_down_term {
+  const uint8_t* mask;  /* [m, k] keep-mask or NULL */
+  float keep_scale;
+  const void* a;        /* lora_A [rank, k] fp16 */
+  void* z;              /* [m, rank] fp16 out */
+} dk_lora_down_term;
+int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t rank,
+                       const dk_lora_down_term* terms, int n_terms, hipStream_t stream);
+
+typedef struct dk_lora_grads_term {
+  const void* dy;       /* [m, n_out] fp16, row stride lddy (a column slice of dQKV) */
+  int64_t lddy;
+  int64_t n_out;
+  const void* z;        /* [m, rank] fp16 */
+  const void* lora_b;   /* [n_out, rank] fp16 */
+  float lora_scale;
+  const uint8_t* mask;  /* [m, k] keep-mask or NULL */
+  float keep_scale;
+  float* da;            /* [rank, k] fp32 out */
+  float* db;            /* [n_out, rank] fp32 out */
+  void* dz;             /* [m, rank] fp16 out */
+} dk_lora_grads_term;
+/* ws: fp32 scratch of dk_lora_grads_multi_workspace(m, k, rank, n_outs, n_terms) bytes, n_outs
+ * the terms' n_out in order. */
+int64_t dk_lora_grads_multi_workspace(int64_t m, int64_t k, int64_t rank, const int64_t* n_outs,
+                                      int n_terms);
+int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t rank,
+                        const dk_lora_grads_term* terms, int n_terms, void* ws, int64_t ws_bytes,
+                        hipStream_t stream);
+
 /* gate|up as one NF4 GEMM with the gated-SiLU epilogue.  Replaces the gate and up GEMMs and
  * gated_silu_forward (solution/fast_qwen.py:1080-1108; solution/k_mlp.py:20-29):
  *   g = fp16(X Wg^T), u = fp16(X Wu^T), act = fp16(silu(g) * u)

@@ -70,7 +70,21 @@ def test_argument_errors_come_back_before_launch():
                                       None) == _lib.DK_ERR_INVALID              # no gu
     assert lib.dk_h16_linear_fwd_lora(p16, 1536, 0, p16, 1536, 1536, None, None, 0, 0, p16, 1536,
                                       None, 0, None) == 0                       # zero rows
-    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * 1536 * 16 * 4
+    # LoRA gradient partial sums: 16 row chunks x (n_out + k) columns x rank fp32, per term
+    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * (1536 + 1536) * 16 * 4
+    n_outs = (ctypes.c_int64 * 2)(1536, 256)
+    assert lib.dk_lora_grads_multi_workspace(2048, 1536, 16, n_outs, 2) == \
+        16 * (1536 + 256 + 2 * 1536) * 16 * 4
+    assert lib.dk_lora_grads_multi_workspace(2048, 1536, 16, n_outs, 3) == 0
+    down = (_lib.LoraDownTermC * 3)()
+    assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 3, None) == _lib.DK_ERR_INVALID  # 3 terms
+    assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_INVALID  # no A / z
+    down[0] = _lib.LoraDownTermC(None, 1.0, ctypes.c_void_p(8), p16)
+    assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_ALIGN
+    grads = (_lib.LoraGradsTermC * 1)()
+    assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
+    grads[0] = _lib.LoraGradsTermC(p16, 64, 64, p16, p16, 2.0, None, 1.0, p16, p16, p16)
+    assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_WORKSPACE
     assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
     with pytest.raises(ValueError):
         _lib.check(_lib.DK_ERR_INVALID, "probe")

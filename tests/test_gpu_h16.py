@@ -160,6 +160,41 @@ def test_h16_mlp(torch, m):
     _scaled_close(host(dx16), dx_ref, "dX mlp vs oracle chain")
 
 
+@pytest.mark.parametrize("m", [2048, 200])
+def test_lora_multi_matches_single(torch, m):
+    """The q and v adapters in shared launches (dk_lora_down_multi / dk_lora_grads_multi) give
+    bit-identical results to one call per adapter, and those match the oracle."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"LoRA q+v shared launches vs one call each, M={m}")
+    D, KV = 1536, 256
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, seed=31)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, seed=32)
+    ks = linear.keep_scale(0.05)
+    dqkv = (np.random.default_rng(33).standard_normal((m, D + 2 * KV)) * 1e-2).astype(F16)
+    tx, g = cuda16(x), cuda16(dqkv)
+    t = {k: cuda16(v) for k, v in (("aq", aq), ("av", av), ("bq", bq), ("bv", bv))}
+    tmq, tmv = cuda(mq), cuda(mv)
+    zq1 = w4linear.lora_down(tx, t["aq"], tmq, ks)
+    zv1 = w4linear.lora_down(tx, t["av"], tmv, ks)
+    zq2, zv2 = w4linear.lora_down_multi(tx, [(t["aq"], tmq, ks), (t["av"], tmv, ks)])
+    torch.cuda.synchronize()
+    _same(zq2, zq1, "z_q")
+    _same(zv2, zv1, "z_v")
+    single = [w4linear.lora_grads(g[:, :D], zq1, tx, t["bq"], 2.0, tmq, ks),
+              w4linear.lora_grads(g[:, D + KV:], zv1, tx, t["bv"], 2.0, tmv, ks)]
+    multi = w4linear.lora_grads_multi(tx, [(g[:, :D], zq1, t["bq"], 2.0, tmq, ks),
+                                           (g[:, D + KV:], zv1, t["bv"], 2.0, tmv, ks)])
+    torch.cuda.synchronize()
+    for term, (one, both) in zip("qv", zip(single, multi)):
+        for nm, a, b in zip(("dA", "dB", "dz"), both, one):
+            _same(a, b, f"{nm}_{term}")
+    assert_close(host(zq1), linear.lora_down(x, mq, ks, aq), 2e-3, 2e-3, "z_q vs oracle")
+    ref = linear.linear_bwd(dqkv[:, :D], np.zeros((D, D), F16), host(zq1), x, mq, ks, aq, bq, 2.0)
+    for nm, got in zip(("dA", "dB", "dZ"), multi[0]):
+        _scaled_close(host(got), ref[nm], f"{nm}_q vs oracle")
+
+
 def test_h16_argument_checks(torch):
     from decentrik_prime_amd import w4linear
     log("h16 argument checks")
