@@ -33,7 +33,14 @@ static inline bool dk_aligned(const void* p, uintptr_t a) {
 }
 
 // fp32 -> fp16, round to nearest even (v_cvt_f16_f32 under the default round mode).
-__device__ __forceinline__ f16 dk_h(float x) { return (f16)x; }
+// fp16 of an fp32 value, rounded the way the reference rounds: the fp32 result of the producing
+// multiply or add first, then fp16.  The empty asm keeps the compiler from folding that multiply
+// or add and this conversion into one v_fma_mix*_f16, which rounds the exact result straight to
+// fp16 and differs in the last fp16 bit for about 1 input in 10^4.
+__device__ __forceinline__ f16 dk_h(float x) {
+  asm("" : "+v"(x));
+  return (f16)x;
+}
 
 // Logistic parts of the gated SiLU for the GEMM epilogues: e = 1 + exp(-g), sig = 1/e and
 // silu = g/e through one hardware reciprocal (v_rcp_f32, about 1 ulp) instead of two IEEE

@@ -31,12 +31,14 @@
 namespace dk {
 namespace {
 
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
 constexpr int kBK = 32;                      // K per step
 constexpr int kStages = 4;                   // LDS ring depth (= load distance in steps)
 constexpr int kThreads = 512;
 constexpr int kTile = 256;
 constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 16 KB
-constexpr int kEpiScratch = 4096;            // bytes of LDS per wave for the epilogue
+constexpr int kEpiScratch = 16384;           // bytes of LDS per wave for the epilogue
 
 __device__ __forceinline__ unsigned lds_offset(const void* p) {
   return (unsigned)(size_t)(__attribute__((address_space(3))) const void*)p;
@@ -75,10 +77,19 @@ __device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
 
 // The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
 // element is (mw0, nw0).  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
-// 8 (v / 4) + 4 (lane / 32) + v % 4 for register v.  escr: this wave's 4 KB of LDS scratch.
+// 8 (v / 4) + 4 (lane / 32) + v % 4 for register v.  Each 32-row strip i is finished in
+// registers (bias, LoRA terms, fp16 rounding), staged in this wave's LDS scratch `escr`
+// (kEpiScratch bytes) and written back as 16-byte vectors of 8 consecutive columns, so that the
+// global traffic (and the gate/up reads of the SwiGLU backward) moves in whole 16-byte pieces.
 template <bool TRANS, int EPI, int TM, int TN>
 __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
                                               int64_t mw0, int64_t nw0, uint8_t* escr) {
+  constexpr int COLS = 32 * TN;          // columns of a strip
+  constexpr int SLD = COLS + 8;          // floats per staged row: the two half-waves' rows
+                                         // (4 apart) land 32 banks apart
+  constexpr int SEGS = COLS / 8;         // 8-column segments per row
+  constexpr int ROWS_PER_PASS = 64 / SEGS;
+  static_assert(32 * SLD * 4 + 3072 <= kEpiScratch, "epilogue scratch");
   const int lane = threadIdx.x & 63;
   const int lrow = lane & 31;
   const int lk8 = 8 * (lane >> 5);
@@ -86,22 +97,35 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   const int64_t M = p.M, N = p.N;
+  float* stage = reinterpret_cast<float*>(escr);
+  uint8_t* mscr = escr + 32 * SLD * 4;   // keep-mask bytes (rows of 48 bytes)
+  f16* ascr = reinterpret_cast<f16*>(mscr + 1536);   // LoRA A slice (rows of 48 halves)
+  const int seg = lane % SEGS, srow = lane / SEGS;   // read-back position of this lane
 
-  if constexpr (EPI == EPI_LINEAR) {
-    f16* out16 = reinterpret_cast<f16*>(p.out);
-    float* out32 = reinterpret_cast<float*>(p.out);
+  // registers -> staged strip (the values, already rounded where the output is fp16)
+  auto stage_block = [&](int j, const f32x16& r) {
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
+    for (int v = 0; v < 16; ++v) stage[(8 * (v >> 2) + rsub + (v & 3)) * SLD + 32 * j + lrow] = r[v];
+  };
+  auto staged8 = [&](int row, int col) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(stage + row * SLD + col);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(stage + row * SLD + col + 4);
+    return f32x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
+  };
+
+#pragma unroll
+  for (int i = 0; i < TM; ++i) {
+    const int64_t mrow0 = mw0 + 32 * i;
+    if constexpr (EPI == EPI_LINEAR) {
+      f32x16 res[TN];
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
         const f32x16& a = acc[i][j];
-        const int64_t mrow0 = mw0 + 32 * i;
         const int64_t nb = nw0 + 32 * j;
         const int64_t n = nb + lrow;
         const float bias = p.bias ? (float)p.bias[n] : 0.0f;
-        f32x16 res;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) res[v] = (float)dk_h(__fadd_rn(a[v], bias));
+        for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(__fadd_rn(a[v], bias));
         for (int t = 0; t < p.n_lora; ++t) {
           const LoraTerm& L = p.lora[t];
           if (!TRANS && (nb < L.n_begin || nb >= L.n_end)) continue;
@@ -122,7 +146,6 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
             } else {
               // A[rc .. rc + 16][nb .. nb + 32] staged row-major (rows of 48 halves), read back
               // rank-contiguous with transposing reads
-              f16* ascr = reinterpret_cast<f16*>(escr + 2048);
               const f16x8 av = *reinterpret_cast<const f16x8*>(
                   L.r + (int64_t)(rc + (lane >> 2)) * N + nb + 8 * (lane & 3));
               __builtin_amdgcn_wave_barrier();
@@ -142,80 +165,138 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
             u32x4 mw = u32x4{0u, 0u, 0u, 0u};
             if (mr < M) mw = *reinterpret_cast<const u32x4*>(L.mask + mr * N + nb + 16 * (lane & 1));
             __builtin_amdgcn_wave_barrier();
-            *reinterpret_cast<u32x4*>(escr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw;
+            *reinterpret_cast<u32x4*>(mscr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw;
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const int mloc = 8 * (v >> 2) + rsub + (v & 3);
               const float lf = (float)dk_h(lo[v]);
-              res[v] = __fadd_rn(res[v], escr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
+              res[j][v] = __fadd_rn(res[j][v], mscr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
             }
             __builtin_amdgcn_wave_barrier();
           } else {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const float lf = (float)dk_h(lo[v]);
-              res[v] = __fadd_rn(res[v], TRANS ? lf : __fmul_rn(L.scale, lf));
+              res[j][v] = __fadd_rn(res[j][v], TRANS ? lf : __fmul_rn(L.scale, lf));
             }
           }
         }
+        if (p.out_mode == DK_OUT_F16) {
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
-          if (m >= M) continue;
-          const int64_t o = m * p.ldo + n;
-          if (p.out_mode == DK_OUT_F16) {
-            out16[o] = dk_h(res[v]);
-          } else if (p.out_mode == DK_OUT_F32) {
-            out32[o] = res[v];
-          } else {
-            out32[o] = __fadd_rn(out32[o], res[v]);
-          }
+          for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(res[j][v]);
         }
       }
-    }
-  } else if constexpr (EPI == EPI_SWIGLU_FWD) {
-    f16* act = reinterpret_cast<f16*>(p.out);
-    const int64_t hcol = nw0 / 2 + lrow;
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t mrow0 = mw0 + 32 * i;
+      for (int j = 0; j < TN; ++j) stage_block(j, res[j]);
+      __builtin_amdgcn_wave_barrier();
+#pragma unroll
+      for (int q = 0; q < 32 / ROWS_PER_PASS; ++q) {
+        const int row = srow + q * ROWS_PER_PASS;
+        const int64_t m = mrow0 + row;
+        if (m >= M) continue;
+        const f32x8_t r = staged8(row, 8 * seg);
+        const int64_t o = m * p.ldo + nw0 + 8 * seg;
+        if (p.out_mode == DK_OUT_F16) {
+          f16x8 h;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[e] = (f16)r[e];
+          *reinterpret_cast<f16x8*>(reinterpret_cast<f16*>(p.out) + o) = h;
+        } else {
+          float* dst = reinterpret_cast<float*>(p.out) + o;
+          f32x4 lo4 = f32x4{r[0], r[1], r[2], r[3]}, hi4 = f32x4{r[4], r[5], r[6], r[7]};
+          if (p.out_mode == DK_OUT_F32_ACCUM) {
+            const f32x4 p0 = *reinterpret_cast<const f32x4*>(dst);
+            const f32x4 p1 = *reinterpret_cast<const f32x4*>(dst + 4);
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+              lo4[e] = __fadd_rn(p0[e], lo4[e]);
+              hi4[e] = __fadd_rn(p1[e], hi4[e]);
+            }
+          }
+          *reinterpret_cast<f32x4*>(dst) = lo4;
+          *reinterpret_cast<f32x4*>(dst + 4) = hi4;
+        }
+      }
+      __builtin_amdgcn_wave_barrier();
+    } else if constexpr (EPI == EPI_SWIGLU_FWD) {
+      // block 0: the gate values, block 1: the up values of the same 32 hidden units
+      f32x16 g, u;
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
+        g[v] = (float)dk_h(acc[i][0][v]);
+        u[v] = (float)dk_h(acc[i][1][v]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      stage_block(0, g);
+      stage_block(1, u);
+      __builtin_amdgcn_wave_barrier();
+      // 32 rows x 4 segments of 8 hidden units: 2 per lane
+      const int hseg = lane & 3, hrow = lane >> 2;
+      const int64_t hcol = nw0 / 2 + 8 * hseg;
+#pragma unroll
+      for (int q = 0; q < 2; ++q) {
+        const int row = hrow + 16 * q;
+        const int64_t m = mrow0 + row;
         if (m >= M) continue;
-        const f16 g16 = dk_h(acc[i][0][v]);
-        const f16 u16 = dk_h(acc[i][1][v]);
-        float sig, silu;
-        dk_silu_parts((float)g16, &sig, &silu);
-        act[m * p.ldo + hcol] = dk_h(silu * (float)u16);
+        const f32x8_t gv = staged8(row, 8 * hseg), uv = staged8(row, 32 + 8 * hseg);
+        f16x8 ah, gh, uh;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          float sig, silu;
+          dk_silu_parts(gv[e], &sig, &silu);
+          ah[e] = dk_h(silu * uv[e]);
+          gh[e] = (f16)gv[e];
+          uh[e] = (f16)uv[e];
+        }
+        *reinterpret_cast<f16x8*>(reinterpret_cast<f16*>(p.out) + m * p.ldo + hcol) = ah;
         if (p.gu) {
-          p.gu[m * 2 * p.inter + hcol] = g16;
-          p.gu[m * 2 * p.inter + p.inter + hcol] = u16;
+          *reinterpret_cast<f16x8*>(p.gu + m * 2 * p.inter + hcol) = gh;
+          *reinterpret_cast<f16x8*>(p.gu + m * 2 * p.inter + p.inter + hcol) = uh;
         }
       }
-    }
-  } else {  // EPI_SWIGLU_BWD: N == inter
-#pragma unroll
-    for (int i = 0; i < TM; ++i) {
-      const int64_t mrow0 = mw0 + 32 * i;
+      __builtin_amdgcn_wave_barrier();
+    } else {  // EPI_SWIGLU_BWD: N == inter; dact = fp16(acc), then the gated-SiLU backward on gu
+      __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const int64_t n = nw0 + 32 * j + lrow;
+        f32x16 d;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) {
-          const int64_t m = mrow0 + 8 * (v >> 2) + rsub + (v & 3);
-          if (m >= M) continue;
-          const float da = (float)dk_h(acc[i][j][v]);
-          f16* gp = p.gu + m * 2 * p.inter + n;
-          const float g = (float)gp[0];
-          const float u = (float)gp[p.inter];
+        for (int v = 0; v < 16; ++v) d[v] = (float)dk_h(acc[i][j][v]);
+        stage_block(j, d);
+      }
+      __builtin_amdgcn_wave_barrier();
+      constexpr int PASSES = 32 / ROWS_PER_PASS;
+      f16x8 gq[PASSES], uq[PASSES];
+      // every pass's gate/up loads first, then the arithmetic and the stores
+#pragma unroll
+      for (int q = 0; q < PASSES; ++q) {
+        const int64_t m = mrow0 + srow + q * ROWS_PER_PASS;
+        const f16* gp = p.gu + (m < M ? m : M - 1) * 2 * p.inter + nw0 + 8 * seg;
+        gq[q] = *reinterpret_cast<const f16x8*>(gp);
+        uq[q] = *reinterpret_cast<const f16x8*>(gp + p.inter);
+      }
+#pragma unroll
+      for (int q = 0; q < PASSES; ++q) {
+        const int row = srow + q * ROWS_PER_PASS;
+        const int64_t m = mrow0 + row;
+        if (m >= M) continue;
+        const f32x8_t da = staged8(row, 8 * seg);
+        f16x8 dg, du;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const float g = (float)gq[q][e], u = (float)uq[q][e];
           float sig, silu;
           dk_silu_parts(g, &sig, &silu);
-          gp[p.inter] = dk_h(da * silu);
-          gp[0] = dk_h((da * u) * sig * (1.0f + g * (1.0f - sig)));
+          du[e] = dk_h(da[e] * silu);
+          dg[e] = dk_h((da[e] * u) * sig * (1.0f + g * (1.0f - sig)));
         }
+        f16* gp = p.gu + m * 2 * p.inter + nw0 + 8 * seg;
+        *reinterpret_cast<f16x8*>(gp) = dg;
+        *reinterpret_cast<f16x8*>(gp + p.inter) = du;
       }
+      __builtin_amdgcn_wave_barrier();
     }
   }
 }
@@ -376,7 +457,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     }
   }
   // every wave is past the last barrier, after which no wave reads a stage and no load is in
-  // flight: the A stages are free for the per-wave epilogue scratch
+  // flight: the stages are free for the per-wave epilogue scratch
 
   if (part) {
     // split-K: this wave's fp32 partial blocks, lane-major (each register store is 256
@@ -390,8 +471,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
         for (int v = 0; v < 16; ++v) mine[((i * TN + j) * 16 + v) * 64] = acc[i][j][v];
     return;
   }
-  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN,
-                                    reinterpret_cast<uint8_t*>(As) + wave * kEpiScratch);
+  // the epilogue scratch: 16 KB per wave, waves 0-3 in the A stages, 4-7 in the W stages
+  uint8_t* escr = reinterpret_cast<uint8_t*>(wave < 4 ? As : Bs) + (wave & 3) * kEpiScratch;
+  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN, escr);
 }
 
 // Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
@@ -502,12 +584,21 @@ HPlan hplan(int64_t M, int64_t N, int64_t K, int epi) {
   // fewer tiles than CUs: split K so that the splits fill the CUs once.  The fp32 partials cost
   // two passes over splits x tiles x 256 KB, which only long K (4096 or more) repays; LINEAR
   // only, at least 4 row tiles
-  if (epi != EPI_LINEAR || h.tiles_m < 4 || K < 4096) return h;
-  int64_t s = cus / tiles;
-  if (s > K / kBK / 8) s = K / kBK / 8;
-  if (s < 2) return h;
-  h.splits = (int)s;
-  h.main_wgs = tiles * s;
+  if (epi == EPI_LINEAR && h.tiles_m >= 4 && K >= 4096) {
+    int64_t s = cus / tiles;
+    if (s > K / kBK / 8) s = K / kBK / 8;
+    if (s >= 2) {
+      h.splits = (int)s;
+      h.main_wgs = tiles * s;
+      h.ok = true;
+      return h;
+    }
+  }
+  // otherwise every tile as 128 x 128 quarters, when they fill at least half the CUs
+  const int64_t quarters = (M + 127) / 128 * (N / 128);
+  if (quarters * 2 < cus) return h;
+  h.main_wgs = 0;
+  h.tail_wgs = 4 * tiles;
   h.ok = true;
   return h;
 }
@@ -520,9 +611,19 @@ int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
   return h.main_wgs * kTile * kTile * (int64_t)sizeof(float);
 }
 
+// The epilogue writes 16-byte vectors of 8 consecutive columns.
+static bool vector_outputs_ok(const GemmParams& p, int epi) {
+  if (epi == EPI_LINEAR)
+    return dk_aligned(p.out, 16) && p.ldo % (p.out_mode == DK_OUT_F16 ? 8 : 4) == 0;
+  if (epi == EPI_SWIGLU_FWD)
+    return dk_aligned(p.out, 16) && p.ldo % 8 == 0 && (!p.gu || dk_aligned(p.gu, 16)) &&
+           p.inter % 8 == 0;
+  return dk_aligned(p.gu, 16) && p.inter % 8 == 0;
+}
+
 template <bool TRANS, int EPI>
 int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (!p0.w16) return kHgemmDeclined;
+  if (!p0.w16 || !vector_outputs_ok(p0, EPI)) return kHgemmDeclined;
   const HPlan h = hplan(p0.M, p0.N, p0.K, EPI);
   if (!h.ok) return kHgemmDeclined;
   GemmParams p = p0;
