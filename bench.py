@@ -91,9 +91,14 @@ def kernel_table(torch, st, reps, only=None):
         rows.append(("h16" + suffix, (lambda f, k: lambda: f(h[k]))(fn, kind), flops, None,
                      int(used == "h16")))
     for kind in st.KINDS:
-        # the side-stream dequant of one weight (HBM-bound; overlaps the GEMMs in the step)
+        # the dequant of one weight into its fp16 slot (HBM-bound)
         rows.append((f"dequant {kind}", (lambda k: lambda: L[k].dequantize(out=h[k]))(kind), 0.0,
-                     dq_bytes(L[kind]), 0))
+                     dq_bytes(L[kind]), 0 if st.whole_layer else 2))
+    # the whole layer in one launch (forward and backward of every layer)
+    from decentrik_prime_amd import k_nf4
+    hl = torch.empty(L["packed"].numel, dtype=torch.float16, device=x.device)
+    rows.append(("dequant layer", lambda: k_nf4.dequant_layer(L["packed"], st.code2, st.nf4, hl), 0.0,
+                 L["packed"].numel * (0.5 + 1 / 64 + 8 / 16384 + 2), 2 if st.whole_layer else 0))
     rows += [
         ("lora_down q+v", lambda: W.lora_down_multi(
             x, [(lo["Aq"], lo["mq"], ks), (lo["Av"], lo["mv"], ks)], outs=[z["q"], z["v"]]),
@@ -117,7 +122,7 @@ def kernel_table(torch, st, reps, only=None):
             row["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
         out.append(row)
     gu.copy_(gu_save)
-    del h
+    del h, hl
     return out
 
 

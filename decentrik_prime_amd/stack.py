@@ -25,7 +25,10 @@ read the slot (dk_h16_*); the other kinds read the NF4 sections directly (dk_w4_
 reference's workspace schedule (solution/fast_qwen.py:694-756): right after layer i's GEMM reads
 kind k's slot, the dequant of kind k for the next layer in step order (i + 1 forward, i - 1
 backward) is issued, and a weight still resident is not dequantised again (the last layer at the
-forward/backward turn, layer 0 between steps).  ``dq_stream="side"`` runs those dequants on a
+forward/backward turn, layer 0 between steps).  ``ahead="layer"`` (the default) keeps one slot
+for the whole layer instead and dequantises all seven weights of a layer in one launch (the
+reference's dequant_layer, solution/k_nf4.py:176-181): the small q|k|v and o dequants are
+launch-bound on their own.  ``dq_stream="side"`` runs those dequants on a
 stream of their own, overlapping the GEMMs in between; ``"main"`` (the default) issues them in
 order on the compute stream.  Measured on MI355X (28 layers, M = 2048) the in-order form is
 1.3 ms per step faster: each GEMM holds all of a CU's registers at two workgroups per CU, so a
@@ -58,6 +61,19 @@ def layer_flops(m, d=D, inter=I, kv=KV, r=R):
 FLOP_PER_LAYER_M2048 = layer_flops(2048)
 
 
+class _WholeLayer:
+    """All seven weights of layer i as one dequant job into the whole-layer slot."""
+
+    def __init__(self, stack, i):
+        self.stack, self.i = stack, i
+        self.rows, self.cols = stack.layers[i]["packed"].numel, 1
+
+    def dequantize(self, out):
+        st = self.stack
+        k_nf4.dequant_layer(st.layers[self.i]["packed"], st.code2, st.nf4, out.view(-1))
+        return out
+
+
 class NF4LinearStack:
     """Random-init NF4 weights (W ~ N(0, 0.02), quantised on the GPU), rank-16 LoRA on q and v,
     and synthetic activations, all resident on `device`."""
@@ -65,7 +81,7 @@ class NF4LinearStack:
     KINDS = ("qkv", "o", "gu", "d")
 
     def __init__(self, n_layers=28, m=2048, seed=0, device="cuda", p_drop=0.05, lora_scale=2.0,
-                 save_gu=True, ahead=("qkv", "o", "gu", "d"), dq_stream="main"):
+                 save_gu=True, ahead="layer", dq_stream="main"):
         self.n_layers, self.m, self.device = n_layers, m, torch.device(device)
         self.s = float(lora_scale)
         self.keep_scale = 1.0 / float(torch.tensor(1.0 - p_drop, dtype=torch.float32))
@@ -112,28 +128,49 @@ class NF4LinearStack:
         self.dx_mlp = torch.empty(m, D, dtype=f16, device=dev)
         self.grads = [None] * n_layers
         self.probe = None   # (operator name, [(start event, end event), ...]) or None
-        unknown = set(ahead) - set(self.KINDS)
-        if unknown:
-            raise ValueError(f"unknown weight kinds {sorted(unknown)}")
-        self.ahead = tuple(ahead)
-        self.dq = (DequantAhead(dev, {k: self.layers[0][k].rows * self.layers[0][k].cols
-                                      for k in self.ahead}, dq_stream) if self.ahead else None)
+        self.whole_layer = ahead == "layer"
+        if self.whole_layer:
+            self.ahead = self.KINDS
+            pk = self.layers[0]["packed"]
+            first = {"qkv": "q_proj", "o": "o_proj", "gu": "gate_proj", "d": "down_proj"}
+            self.views = {k: (pk.segments[first[k]][0], self.layers[0][k].rows * self.layers[0][k].cols)
+                          for k in self.KINDS}
+            self.dq = DequantAhead(dev, {"layer": pk.numel}, dq_stream)
+        else:
+            unknown = set(ahead) - set(self.KINDS)
+            if unknown:
+                raise ValueError(f"unknown weight kinds {sorted(unknown)}")
+            self.ahead = tuple(ahead)
+            self.dq = (DequantAhead(dev, {k: self.layers[0][k].rows * self.layers[0][k].cols
+                                          for k in self.ahead}, dq_stream) if self.ahead else None)
 
     @property
     def flops_per_step(self):
         return self.n_layers * layer_flops(self.m)
 
     def _w16(self, kind, i):
-        """Layer i's fp16 weight of `kind` from its side-stream slot, or None for an NF4 read."""
+        """Layer i's fp16 weight of `kind` from its slot, or None for an NF4 read."""
         if kind not in self.ahead:
             return None
+        if self.whole_layer:
+            self.dq.issue("layer", i, _WholeLayer(self, i))     # no-op when already resident
+            start, n = self.views[kind]
+            return self.dq.take("layer", i)[start:start + n]
         key = (i, kind)
         self.dq.issue(kind, key, self.layers[i][kind])     # no-op when already resident
         return self.dq.take(kind, key)
 
     def _done(self, kind, nxt):
-        """The slot of `kind` has had its last reader; dequantise layer `nxt`'s weight into it."""
+        """The slot of `kind` has had its last reader; dequantise layer `nxt`'s weight into it
+        (whole-layer slot: after the last weight of the layer in step order)."""
         if kind not in self.ahead:
+            return
+        if self.whole_layer:
+            if kind != ("d" if self._forward else "qkv"):    # the layer's last weight
+                return
+            self.dq.release("layer")
+            if 0 <= nxt < self.n_layers:
+                self.dq.issue("layer", nxt, _WholeLayer(self, nxt))
             return
         self.dq.release(kind)
         if 0 <= nxt < self.n_layers:
@@ -144,6 +181,7 @@ class NF4LinearStack:
         return ("h16" if kind in self.ahead else "w4") + base
 
     def forward_layer(self, i):
+        self._forward = True
         L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
         op, nm, w16, done = self._op, self.op_name, self._w16, self._done
         op("lora_down q+v", lora_down_multi, x,
@@ -162,6 +200,7 @@ class NF4LinearStack:
         done("d", i + 1)
 
     def backward_layer(self, i):
+        self._forward = False
         L, lo, z, x, dy = self.layers[i], self.lora[i], self.z[i], self.x, self.dy
         gu = self.gu[i]
         op, nm, w16, done = self._op, self.op_name, self._w16, self._done

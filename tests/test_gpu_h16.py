@@ -211,13 +211,14 @@ def test_h16_argument_checks(torch):
 
 
 def test_stack_dequant_ahead_matches_nf4_reads(torch):
-    """Three layers, M = 512, two steps: every weight dequantised one use ahead, in order on the
-    compute stream or on a side stream, gives bit-identical outputs and LoRA gradients to the
-    schedule that reads NF4 directly (same seed, so the same weights and inputs)."""
+    """Three layers, M = 512, two steps: every weight dequantised one use ahead (per weight kind
+    or the whole layer in one launch), in order on the compute stream or on a side stream, gives
+    bit-identical outputs and LoRA gradients to the schedule that reads NF4 directly (same seed,
+    so the same weights and inputs)."""
     from decentrik_prime_amd.stack import NF4LinearStack
     log("stack: dequant-ahead schedules vs NF4 reads, 3 layers, M=512, 2 steps")
     configs = (((), "main"), (NF4LinearStack.KINDS, "main"), (("gu", "d"), "side"),
-               (NF4LinearStack.KINDS, "side"))
+               (NF4LinearStack.KINDS, "side"), ("layer", "main"), ("layer", "side"))
     runs = {}
     for ahead, where in configs:
         st = NF4LinearStack(n_layers=3, m=512, seed=3, device="cuda", ahead=ahead, dq_stream=where)
