@@ -6,15 +6,18 @@
 // One 512-thread workgroup per CU owns a 256 x 256 tile of C: 8 waves (2 x 4), each a 128 x 64
 // block of v_mfma_f32_32x32x16_f16 results.  Per output FLOP that is half the operand bytes of a
 // 128 x 128 tile, and the operand bytes between L2 and the CUs are what bounds these GEMMs on
-// MI355X.  K is walked in steps of 32.  Operands go from global memory straight into LDS with
-// global_load_lds_dwordx4 (LDS DMA: no registers, no LDS write instructions), four steps ahead,
-// into a ring of four stages (4 x 32 KB).  Each wave waits only for its own loads (vmcnt), and one
-// barrier per step both publishes the step's tiles and frees the stage read in the step before.
-// The MFMA operands of the next 16-wide sub-step are read while the MFMAs of the current one run.
+// MI355X.  K is walked in steps of 64.  Operands go from global memory straight into LDS with
+// global_load_lds_dwordx4 (LDS DMA: no registers, no LDS write instructions) into two stages
+// (2 x 64 KB): the loads of step k + 2 go out during the last MFMAs of step k, into the stage
+// step k has just finished reading.  Each wave waits only for its own loads (vmcnt), and one
+// barrier per step both publishes the next step's tiles and frees the stage just read.  The MFMA
+// operands of the next 16-wide sub-step are read while the MFMAs of the current one run.
+// (Measured on MI355X: 64-wide steps in two stages run about 8% faster than 32-wide steps in a
+// four-stage ring; the barriers, not the load distance, are what costs.)
 //
-// LDS layout: A tiles and NT W tiles are rows of 32 halves (64 bytes) whose four 16-byte chunks
-// are XOR-swizzled by row (swz_k), so the b128 operand reads of 16 consecutive rows hit distinct
-// banks.  NN W tiles are rows of 256 halves (N contiguous) with chunks swizzled by k (swz_n); the
+// LDS layout: A tiles and NT W tiles are rows of 64 halves (128 bytes) whose eight 16-byte
+// chunks are XOR-swizzled by row (swz_k), so the b128 operand reads of 16 consecutive rows hit
+// distinct banks.  NN W tiles are rows of 256 halves (N contiguous) with chunks swizzled by k (swz_n); the
 // consumers build each K-contiguous operand from two ds_read_b64_tr_b16 (transposing) reads.
 // The DMA writes 64 consecutive 16-byte chunks per instruction, so the swizzle is applied to the
 // global addresses each lane loads.
@@ -33,11 +36,11 @@ namespace {
 
 typedef float f32x8_t __attribute__((ext_vector_type(8)));
 
-constexpr int kBK = 32;                      // K per step
-constexpr int kStages = 4;                   // LDS ring depth (= load distance in steps)
+constexpr int kBK = 64;                      // K per step
+constexpr int kStages = 2;                   // LDS stages
 constexpr int kThreads = 512;
 constexpr int kTile = 256;
-constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 16 KB
+constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 32 KB
 constexpr int kEpiScratch = 16384;           // bytes of LDS per wave for the epilogue
 
 __device__ __forceinline__ unsigned lds_offset(const void* p) {
@@ -69,10 +72,10 @@ __device__ __forceinline__ f16x4 read_tr(const f16* p) {
                                        (__attribute__((address_space(3))) i16x4*)(p)));
 }
 
-// chunk swizzles: 64-byte rows (conflict-free for 8- and 16-lane LDS passes of b128 reads of
+// chunk swizzles: 128-byte rows (conflict-free for 8- and 16-lane LDS passes of b128 reads of
 // consecutive rows) and N-contiguous rows of the NN W tile (transposing reads of 4 rows x 32
 // columns hit distinct banks)
-__device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 3) ^ ((r >> 3) & 1); }
+__device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
 __device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
 
 // The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
@@ -307,13 +310,12 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   constexpr int WAVES_N = 8 / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int LA = BM * 4 / kThreads;     // A chunks per lane per stage
-  constexpr int LB = BN * 4 / kThreads;     // W chunks per lane per stage
+  constexpr int LA = BM * 8 / kThreads;     // A chunks per lane per stage
+  constexpr int LB = BN * 8 / kThreads;     // W chunks per lane per stage
   constexpr int LOADS = LA + LB;            // DMA instructions per lane per stage
   constexpr int NCH = BN / 8;               // NN: 16-byte chunks per W-tile row
   static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile shape");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
-  static_assert((TM * TN) % LOADS == 0, "DMA interleave");
 
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -325,7 +327,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 #pragma unroll
   for (int j = 0; j < LA; ++j) {
     const int q = (j * 8 + wave) * 64 + lane;
-    const int row = q >> 2, c = (q & 3) ^ swz_k(q >> 2);
+    const int row = q >> 3, c = (q & 7) ^ swz_k(q >> 3);
     const int64_t gm = m0 + row < M ? m0 + row : M - 1;   // rows past M: never stored
     a_src[j] = p.a + gm * p.lda + (int64_t)kt0 * kBK + c * 8;
   }
@@ -333,7 +335,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   for (int j = 0; j < LB; ++j) {
     const int q = (j * 8 + wave) * 64 + lane;
     if (!TRANS) {
-      const int row = q >> 2, c = (q & 3) ^ swz_k(q >> 2);
+      const int row = q >> 3, c = (q & 7) ^ swz_k(q >> 3);
       int64_t n = n0 + row;
       if (EPI == EPI_SWIGLU_FWD) {
         const int64_t g = n >> 6, w = n & 63;
@@ -358,20 +360,14 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       dma16(b_src[j] + (TRANS ? (int64_t)kt * kBK * N : (int64_t)kt * kBK), dst);
     }
   };
-  // wait until at most `later` stages of this lane's loads are still in flight
-  auto wait_loads = [&](int later) {
-    if (later >= 3) wait_vmem<3 * LOADS>();
-    else if (later == 2) wait_vmem<2 * LOADS>();
-    else if (later == 1) wait_vmem<LOADS>();
-    else wait_vmem<0>();
-  };
 
   // ---- MFMA operands
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int lrow = lane & 31;
   const int hx = swz_k(lane & 15);
-  const int fo[2] = {lrow * kBK + ((0 + (lane >> 5)) ^ hx) * 8,
-                     lrow * kBK + ((2 + (lane >> 5)) ^ hx) * 8};
+  int fo[4];
+#pragma unroll
+  for (int q = 0; q < 4; ++q) fo[q] = lrow * kBK + ((2 * q + (lane >> 5)) ^ hx) * 8;
   const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
   const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
   int nn_off[TN];
@@ -426,33 +422,44 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     }
   };
 
-  // ---- main loop.  Step kt lives in stage kt % 4.  In step kt: read sub-step 1's operands
-  // under sub-step 0's MFMAs; wait for this wave's loads of step kt + 1 and for every wave's
-  // last read of stage kt % 4 (one barrier); refill that stage with step kt + 4, spreading the
-  // DMA instructions between sub-step 1's MFMAs, which run beside the reads of step kt + 1.
+  // ---- main loop.  Step kt lives in stage kt % 2.  In step kt: each sub-step's MFMAs run beside
+  // the operand reads of the next; before the last sub-step, wait for this wave's loads of step
+  // kt + 1 and for every wave's last read of stage kt % 2 (one barrier), then refill that stage
+  // with step kt + 2, spreading the DMA instructions between the last sub-step's MFMAs, which
+  // run beside the first reads of step kt + 1.
 #pragma unroll
-  for (int s = 0; s < kStages; ++s)
-    if (s < nk)
+  for (int d = 0; d < LOADS; ++d) issue(0, 0, d);
+  if (nk > 1) {
 #pragma unroll
-      for (int d = 0; d < LOADS; ++d) issue(s, s, d);
-  wait_loads(nk < kStages ? nk - 1 : kStages - 1);
+    for (int d = 0; d < LOADS; ++d) issue(1, 1, d);
+    wait_vmem<LOADS>();
+  } else {
+    wait_vmem<0>();
+  }
   __syncthreads();
   read_frags(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & (kStages - 1);
+    const int st = kt & 1;
     read_frags(st, 1, 1);
     mfmas(0);
     interleave();
-    wait_loads((nk - 1) - (kt + 1) < 2 ? (nk - 1) - (kt + 1) : 2);
+    read_frags(st, 2, 0);
+    mfmas(1);
+    interleave();
+    read_frags(st, 3, 1);
+    mfmas(0);
+    interleave();
+    wait_vmem<0>();
     __syncthreads();
-    if (kt + 1 < nk) read_frags((kt + 1) & (kStages - 1), 0, 0);
-    const bool refill = kt + kStages < nk;
+    if (kt + 1 < nk) read_frags(st ^ 1, 0, 0);
+    const bool refill = kt + 2 < nk;
 #pragma unroll
     for (int q = 0; q < TM * TN; ++q) {
       acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
                                                                  acc[q / TN][q % TN], 0, 0, 0);
-      constexpr int PER = TM * TN / LOADS;
-      if (refill && q % PER == PER - 1) issue(kt + kStages, st, q / PER);
+#pragma unroll
+      for (int d = q * LOADS / (TM * TN); d < (q + 1) * LOADS / (TM * TN); ++d)
+        if (refill) issue(kt + 2, st, d);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
