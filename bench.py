@@ -286,7 +286,8 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
     dispatch), each scaled by what the same counter reads for the calibration copy of
     `copy_bytes` read + `copy_bytes` written (the __amd_rocclr_copyBuffer dispatches within a
     factor of two of the largest one: nothing else in the run copies a quarter as much).
-    groups: [(operator name, kernel-name substring, operator calls in the run)]."""
+    groups: [(operator name, kernel-name substring, operator calls in the run, grid size in
+    workgroups or None for any)]."""
     out = []
     scaled = {}
     for label, db, counter in (("fetch", fetch_db, "FETCH_SIZE"), ("write", write_db, "WRITE_SIZE")):
@@ -299,8 +300,9 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
         factor = copy_bytes / (kib_avg * 1024.0)
         out.append(f"{counter}: calibration copy {copy_bytes} B -> {kib_avg:.0f} KiB per dispatch "
                    f"(n={len(kib)}), scale factor {factor:.4f}")
-        for op, pattern, calls in groups:
-            sel = {k: v for k, v in rows.items() if pattern in k[1]}
+        for op, pattern, calls, wgs_only in groups:
+            sel = {k: v for k, v in rows.items()
+                   if pattern in k[1] and (wgs_only is None or k[2] == wgs_only)}
             per_kernel = {}
             for k, v in sel.items():
                 per_kernel.setdefault((k[1], k[2]), []).append(v)
@@ -310,7 +312,7 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
             per_call = sum(sel.values()) * 1024.0 * factor / calls
             scaled[(op, label)] = per_call
             out.append(f"  {op}: {label} {per_call:.4g} B per operator call (scaled, {calls} calls)")
-    for op, _, _ in groups:
+    for op, _, _, _ in groups:
         f, w = scaled[(op, "fetch")], scaled[(op, "write")]
         out.append(f"TRAFFIC {op} | fetch {f:.0f} | write {w:.0f} | total {f + w:.0f}")
     return "\n".join(out)
@@ -353,7 +355,8 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="print HBM traffic per operator call from FETCH_SIZE / WRITE_SIZE runs")
     ap.add_argument("--group", action="append", default=[],
-                    help="with --summarize-pmc: 'operator=kernel-name substring@calls'")
+                    help="with --summarize-pmc: 'operator=kernel-name substring[#grid]@calls' "
+                         "(grid: only dispatches of that many workgroups)")
     args = ap.parse_args()
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))
@@ -363,7 +366,11 @@ def main():
         for g in args.group:
             op, rest = g.split("=", 1)
             pattern, calls = rest.rsplit("@", 1)
-            groups.append((op, pattern, int(calls)))
+            wgs = None
+            if "#" in pattern:
+                pattern, wgs = pattern.rsplit("#", 1)
+                wgs = int(wgs)
+            groups.append((op, pattern, int(calls), wgs))
         print(summarize_pmc(*args.summarize_pmc, groups))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:

@@ -485,8 +485,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 
 // Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
 // tiles as 128 x 128 quarters.  With split-K (p.splits > 1, LINEAR only) workgroup b runs split
-// b % splits of tile b / splits and stores its fp32 partial tile at p.part.  Tiles are numbered
-// M-fastest.
+// b / tiles of tile b % tiles and stores its fp32 partial tile at p.part[tile][split].  Tiles
+// are numbered M-fastest.
 template <bool TRANS, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
@@ -497,12 +497,16 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   if (b < main_tiles) {
     // workgroups are dealt to the 8 XCDs round-robin: give each XCD a contiguous run of tiles
     if ((main_tiles & 7) == 0) b = (b & 7) * (main_tiles >> 3) + (b >> 3);
-    const int tile = b / p.splits, split = b % p.splits;
+    // split-K: the splits are the slowest index, so an XCD's run covers neighbouring tiles of
+    // one K range, which share A and W slices in its L2
+    const int tiles = main_tiles / p.splits;
+    const int tile = b % tiles, split = b / tiles;
     const int64_t m0 = (int64_t)(tile % p.tiles_m) * kTile;
     const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile;
     const int kt0 = (int)((int64_t)nk_all * split / p.splits);
     const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - kt0;
-    float* part = p.splits > 1 ? p.part + (int64_t)b * kTile * kTile : nullptr;
+    float* part =
+        p.splits > 1 ? p.part + ((int64_t)tile * p.splits + split) * kTile * kTile : nullptr;
     gemm_tile<TRANS, EPI, 256, 256, 2>(p, m0, n0, kt0, nk, part, As, Bs);
   } else {
     int t = b - main_tiles;
