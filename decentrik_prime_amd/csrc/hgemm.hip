@@ -43,6 +43,10 @@ constexpr int kTile = 256;
 constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 32 KB
 constexpr int kEpiScratch = 16384;           // bytes of LDS per wave for the epilogue
 
+// Epilogue scratch of a wave with TN 32-column blocks per strip: the staged strip (32 rows of
+// 32 TN + 8 floats) plus the keep-mask and LoRA A slices (1536 bytes each).
+constexpr int epi_scratch_bytes(int tn) { return 32 * (32 * tn + 8) * 4 + 3072; }
+
 __device__ __forceinline__ unsigned lds_offset(const void* p) {
   return (unsigned)(size_t)(__attribute__((address_space(3))) const void*)p;
 }
@@ -82,7 +86,7 @@ __device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
 // element is (mw0, nw0).  Lane layout of a 32 x 32 fp32 MFMA result: column lane % 32, row
 // 8 (v / 4) + 4 (lane / 32) + v % 4 for register v.  Each 32-row strip i is finished in
 // registers (bias, LoRA terms, fp16 rounding), staged in this wave's LDS scratch `escr`
-// (kEpiScratch bytes) and written back as 16-byte vectors of 8 consecutive columns, so that the
+// (epi_scratch_bytes(TN) bytes) and written back as 16-byte vectors of 8 consecutive columns, so that the
 // global traffic (and the gate/up reads of the SwiGLU backward) moves in whole 16-byte pieces.
 template <bool TRANS, int EPI, int TM, int TN>
 __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
@@ -92,7 +96,8 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
                                          // (4 apart) land 32 banks apart
   constexpr int SEGS = COLS / 8;         // 8-column segments per row
   constexpr int ROWS_PER_PASS = 64 / SEGS;
-  static_assert(32 * SLD * 4 + 3072 <= kEpiScratch, "epilogue scratch");
+  static_assert(32 * SLD * 4 + 3072 == epi_scratch_bytes(TN) && epi_scratch_bytes(TN) <= kEpiScratch,
+                "epilogue scratch");
   const int lane = threadIdx.x & 63;
   const int lrow = lane & 31;
   const int lk8 = 8 * (lane >> 5);
@@ -524,7 +529,8 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
 // epilogue on it.  The kernel boundary orders it after every partial store.
 template <bool TRANS, int EPI>
 __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
-  __shared__ __attribute__((aligned(16))) uint8_t escr[kEpiScratch];
+  // 8 KB of LDS per one-wave workgroup, so that 20 of them fit a CU
+  __shared__ __attribute__((aligned(16))) uint8_t escr[epi_scratch_bytes(1)];
   constexpr int TM = 4, TN = 2;   // the blocks of one 128 x 64 wave block of the first launch
   const int lane = threadIdx.x;
   const int tile = blockIdx.x / 64, blk = blockIdx.x % 64;
@@ -535,17 +541,16 @@ __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
   const float* src = p.part + (int64_t)tile * p.splits * kTile * kTile +
                      (wave * TM * TN + i * TN + j) * 1024 + lane;
   f32x16 acc[1][1];
-  float v_all[8][16];
-  // all splits' loads first (up to 8 in flight per register), then the sum in split order
-  int sp = 0;
-  for (; sp < p.splits; sp += 8) {
+  float v_all[4][16];
+  // four splits' loads in flight at a time, then their sum in split order
+  for (int sp = 0; sp < p.splits; sp += 4) {
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 4; ++u)
       if (sp + u < p.splits)
 #pragma unroll
         for (int v = 0; v < 16; ++v) v_all[u][v] = src[(int64_t)(sp + u) * kTile * kTile + v * 64];
 #pragma unroll
-    for (int u = 0; u < 8; ++u)
+    for (int u = 0; u < 4; ++u)
       if (sp + u < p.splits)
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[0][0][v] = sp + u == 0 ? v_all[u][v] : acc[0][0][v] + v_all[u][v];
