@@ -309,9 +309,14 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   }
 }
 
-template <bool TRANS, int EPI, int BM, int BN, int WAVES_M>
+// NST: LDS stages of this tile shape in the kernel's 2 x 64 KB (256 x 256: 2, 128 x 128: 4, so
+// the smaller tiles, whose steps are a quarter as long, still load three steps ahead).
+template <bool TRANS, int EPI, int BM, int BN, int WAVES_M, int NST>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64_t n0, int kt0,
                                           int nk, float* part, f16* As, f16* Bs) {
+  constexpr int SA = BM * kBK, SB = BN * kBK;   // halves per stage of A and of W
+  static_assert(NST * SA <= kStages * kStageHalves && NST * SB <= kStages * kStageHalves &&
+                (NST & (NST - 1)) == 0 && NST >= 2, "LDS stages");
   constexpr int WAVES_N = 8 / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
@@ -356,12 +361,12 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   auto issue = [&](int kt, int st, int d) {
     if (d < LA) {
       const unsigned dst = __builtin_amdgcn_readfirstlane(
-          lds_offset(As + st * kStageHalves + (d * 8 + wave) * 512));
+          lds_offset(As + st * SA + (d * 8 + wave) * 512));
       dma16(a_src[d] + (int64_t)kt * kBK, dst);
     } else {
       const int j = d - LA;
       const unsigned dst = __builtin_amdgcn_readfirstlane(
-          lds_offset(Bs + st * kStageHalves + (j * 8 + wave) * 512));
+          lds_offset(Bs + st * SB + (j * 8 + wave) * 512));
       dma16(b_src[j] + (TRANS ? (int64_t)kt * kBK * N : (int64_t)kt * kBK), dst);
     }
   };
@@ -392,11 +397,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   f16x8 fa[2][TM], fb[2][TN];
 
   auto read_frags = [&](int st, int s, int buf) {
-    const f16* as = As + st * kStageHalves + wm * WM * kBK + fo[s];
+    const f16* as = As + st * SA + wm * WM * kBK + fo[s];
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kBK);
     if (!TRANS) {
-      const f16* bs = Bs + st * kStageHalves + wn * WN * kBK + fo[s];
+      const f16* bs = Bs + st * SB + wn * WN * kBK + fo[s];
 #pragma unroll
       for (int j = 0; j < TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kBK);
     } else {
@@ -404,7 +409,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       // the 32 columns the lanes of its 16-lane group address; h = 0, 1 give 8 consecutive k
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
-        const f16* q = Bs + st * kStageHalves + 16 * s * BN + nn_off[j];
+        const f16* q = Bs + st * SB + 16 * s * BN + nn_off[j];
         const f16x4 lo = read_tr(q), hi = read_tr(q + 4 * BN);
         fb[buf][j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
       }
@@ -427,24 +432,29 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     }
   };
 
-  // ---- main loop.  Step kt lives in stage kt % 2.  In step kt: each sub-step's MFMAs run beside
-  // the operand reads of the next; before the last sub-step, wait for this wave's loads of step
-  // kt + 1 and for every wave's last read of stage kt % 2 (one barrier), then refill that stage
-  // with step kt + 2, spreading the DMA instructions between the last sub-step's MFMAs, which
-  // run beside the first reads of step kt + 1.
+  // wait until at most `later` steps of this lane's loads are still in flight
+  auto wait_loads = [&](int later) {
+    if (NST > 3 && later >= 3) wait_vmem<3 * LOADS>();
+    else if (NST > 2 && later >= 2) wait_vmem<2 * LOADS>();
+    else if (later >= 1) wait_vmem<LOADS>();
+    else wait_vmem<0>();
+  };
+
+  // ---- main loop.  Step kt lives in stage kt % NST.  In step kt: each sub-step's MFMAs run
+  // beside the operand reads of the next; before the last sub-step, wait for this wave's loads of
+  // step kt + 1 and for every wave's last read of stage kt % NST (one barrier), then refill that
+  // stage with step kt + NST, spreading the DMA instructions between the last sub-step's MFMAs,
+  // which run beside the first reads of step kt + 1.
 #pragma unroll
-  for (int d = 0; d < LOADS; ++d) issue(0, 0, d);
-  if (nk > 1) {
+  for (int s0 = 0; s0 < NST; ++s0)
+    if (s0 < nk)
 #pragma unroll
-    for (int d = 0; d < LOADS; ++d) issue(1, 1, d);
-    wait_vmem<LOADS>();
-  } else {
-    wait_vmem<0>();
-  }
+      for (int d = 0; d < LOADS; ++d) issue(s0, s0, d);
+  wait_loads((nk < NST ? nk : NST) - 1);
   __syncthreads();
   read_frags(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
-    const int st = kt & 1;
+    const int st = kt & (NST - 1);
     read_frags(st, 1, 1);
     mfmas(0);
     interleave();
@@ -454,17 +464,18 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     read_frags(st, 3, 1);
     mfmas(0);
     interleave();
-    wait_vmem<0>();
+    // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
+    wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
     __syncthreads();
-    if (kt + 1 < nk) read_frags(st ^ 1, 0, 0);
-    const bool refill = kt + 2 < nk;
+    if (kt + 1 < nk) read_frags((kt + 1) & (NST - 1), 0, 0);
+    const bool refill = kt + NST < nk;
 #pragma unroll
     for (int q = 0; q < TM * TN; ++q) {
       acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
                                                                  acc[q / TN][q % TN], 0, 0, 0);
 #pragma unroll
       for (int d = q * LOADS / (TM * TN); d < (q + 1) * LOADS / (TM * TN); ++d)
-        if (refill) issue(kt + 2, st, d);
+        if (refill) issue(kt + NST, st, d);
       __builtin_amdgcn_sched_barrier(0);
     }
   }
@@ -512,7 +523,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - kt0;
     float* part =
         p.splits > 1 ? p.part + ((int64_t)tile * p.splits + split) * kTile * kTile : nullptr;
-    gemm_tile<TRANS, EPI, 256, 256, 2>(p, m0, n0, kt0, nk, part, As, Bs);
+    gemm_tile<TRANS, EPI, 256, 256, 2, 2>(p, m0, n0, kt0, nk, part, As, Bs);
   } else {
     int t = b - main_tiles;
     if ((tail_wgs & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
@@ -520,7 +531,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     const int64_t m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
     const int64_t n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
     if (m0 >= p.M) return;
-    gemm_tile<TRANS, EPI, 128, 128, 4>(p, m0, n0, 0, nk_all, nullptr, As, Bs);
+    gemm_tile<TRANS, EPI, 128, 128, 4, 4>(p, m0, n0, 0, nk_all, nullptr, As, Bs);
   }
 }
 
