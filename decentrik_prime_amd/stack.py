@@ -128,6 +128,10 @@ class NF4LinearStack:
         self.dx_mlp = torch.empty(m, D, dtype=f16, device=dev)
         self.grads = [None] * n_layers
         self.probe = None   # (operator name, [(start event, end event), ...]) or None
+        self._setup_schedule(ahead, dq_stream)
+
+    def _setup_schedule(self, ahead, dq_stream):
+        """The fp16 slots of the dequant-ahead schedule (see the module docstring)."""
         self.whole_layer = ahead == "layer"
         if self.whole_layer:
             self.ahead = self.KINDS
@@ -135,14 +139,15 @@ class NF4LinearStack:
             first = {"qkv": "q_proj", "o": "o_proj", "gu": "gate_proj", "d": "down_proj"}
             self.views = {k: (pk.segments[first[k]][0], self.layers[0][k].rows * self.layers[0][k].cols)
                           for k in self.KINDS}
-            self.dq = DequantAhead(dev, {"layer": pk.numel}, dq_stream)
+            self.dq = DequantAhead(self.device, {"layer": pk.numel}, dq_stream)
         else:
             unknown = set(ahead) - set(self.KINDS)
             if unknown:
                 raise ValueError(f"unknown weight kinds {sorted(unknown)}")
             self.ahead = tuple(ahead)
-            self.dq = (DequantAhead(dev, {k: self.layers[0][k].rows * self.layers[0][k].cols
-                                          for k in self.ahead}, dq_stream) if self.ahead else None)
+            self.dq = (DequantAhead(self.device, {k: self.layers[0][k].rows * self.layers[0][k].cols
+                                                  for k in self.ahead}, dq_stream)
+                       if self.ahead else None)
 
     @property
     def flops_per_step(self):
