@@ -94,11 +94,14 @@ def kernel_table(torch, st, reps, only=None):
         # the dequant of one weight into its fp16 slot (HBM-bound)
         rows.append((f"dequant {kind}", (lambda k: lambda: L[k].dequantize(out=h[k]))(kind), 0.0,
                      dq_bytes(L[kind]), 0 if st.whole_layer else 2))
-    # the whole layer in one launch (forward and backward of every layer)
+    # the whole layer in one launch (forward and backward of every layer; with the carried
+    # schedule the forward's only: the backward's rides on the GEMM launches, whose in-step times
+    # include it)
     from decentrik_prime_amd import k_nf4
     hl = torch.empty(L["packed"].numel, dtype=torch.float16, device=x.device)
+    per_layer = (1 if getattr(st, "carried", False) else 2) if st.whole_layer else 0
     rows.append(("dequant layer", lambda: k_nf4.dequant_layer(L["packed"], st.code2, st.nf4, hl), 0.0,
-                 L["packed"].numel * (0.5 + 1 / 64 + 8 / 16384 + 2), 2 if st.whole_layer else 0))
+                 L["packed"].numel * (0.5 + 1 / 64 + 8 / 16384 + 2), per_layer))
     rows += [
         ("lora_down q+v", lambda: W.lora_down_multi(
             x, [(lo["Aq"], lo["mq"], ks), (lo["Av"], lo["mv"], ks)], outs=[z["q"], z["v"]]),

@@ -52,6 +52,16 @@ class LoraGradsTermC(ctypes.Structure):
                 ("lora_scale", _f32), ("mask", _c_p), ("keep_scale", _f32), ("da", _c_p),
                 ("db", _c_p), ("dz", _c_p)]
 
+
+class SideDequantC(ctypes.Structure):
+    """struct dk_side_dequant."""
+    _fields_ = [("packed", _c_p), ("qabs", _c_p), ("scale2", _c_p), ("offset2", _c_p),
+                ("code2", _c_p), ("nf4", _c_p), ("out", _c_p), ("sb0", _i64), ("sb1", _i64),
+                ("wgs", ctypes.c_int32)]
+
+
+_S = ctypes.POINTER(SideDequantC)
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dk_error_string": (ctypes.c_char_p, [_int]),
@@ -74,12 +84,13 @@ SIGNATURES = {
     "dk_w4_workspace": (_i64, [_i64, _W, _int]),
     "dk_h16_workspace": (_i64, [_i64, _i64, _i64, _int]),
     "dk_h16_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
-                                      _c_p, _i64, _c_p, _i64, _c_p]),
+                                      _c_p, _i64, _c_p, _i64, _S, _c_p]),
     "dk_h16_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64, _c_p,
-                                         _i64, _int, _c_p, _i64, _c_p]),
+                                         _i64, _int, _c_p, _i64, _S, _c_p]),
     "dk_h16_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64,
-                                        _c_p]),
-    "dk_h16_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _c_p]),
+                                        _S, _c_p]),
+    "dk_h16_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _S,
+                                      _c_p]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "dk_lora_down_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraDownTermC), _int, _c_p]),
     "dk_lora_grads_multi_workspace": (_i64, [_i64, _i64, _i64, ctypes.POINTER(_i64), _int]),

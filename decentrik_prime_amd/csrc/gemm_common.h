@@ -1,7 +1,7 @@
 // Parameters shared by the fused GEMM kernels (w4gemm.hip: NF4 or fp16 weights, warp-specialised
 // 128-row tiles; hgemm.hip: fp16 weights, 256 x 256 tiles fed by LDS-DMA loads).
 #pragma once
-#include "dk_common.h"
+#include "nf4_dev.h"
 
 namespace dk {
 
@@ -42,13 +42,15 @@ struct GemmParams {
   int m_fastest;        // tile order: row tiles fastest (1) or column tiles fastest (0)
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
+  SideDequant side;     // dequant work carried by the launch's last side.wgs workgroups
 };
 
 // Runs the GEMM of `p` (fp16 weight p.w16) on the 256 x 256-tile kernel when the shape suits it:
-// output columns a multiple of 256, K a multiple of 32, and either at least one tile per CU or
-// (LINEAR, at least 1024 rows) a split-K that fills the CUs, whose fp32 partials need
-// hgemm_workspace bytes of `ws`.  Returns kHgemmDeclined without launching anything otherwise,
-// a HIP error code, or 0.
+// output columns a multiple of 256, K a multiple of 64, and either at least one tile per CU, or
+// (LINEAR, at least 4 row tiles, K of 4096 or more) a split-K that fills the CUs, whose fp32
+// partials need hgemm_workspace bytes of `ws`, or 128 x 128 tiles that fill at least half the
+// CUs.  p.side's workgroups (if any) join the launch.  Returns kHgemmDeclined without launching
+// anything otherwise, a HIP error code, or 0.
 constexpr int kHgemmDeclined = -1000;
 template <bool TRANS, int EPI>
 int hgemm_launch(const GemmParams& p, void* ws, int64_t ws_bytes, hipStream_t stream);

@@ -29,6 +29,11 @@
 // Epilogues as in w4gemm.hip (the same per-element rounding): LINEAR with up to two LoRA terms
 // and the three output modes, SWIGLU_FWD (gate/up rows interleaved in groups of 32 so g and u of
 // an output share a lane), SWIGLU_BWD (in place on gu).
+//
+// A launch may carry NF4 dequant work (GemmParams::side, nf4_dev.h) on extra workgroups after the
+// tiles: the hardware dispatches workgroups in order, so they start on the CUs that a last round
+// of tiles (or a grid smaller than the CU count) leaves idle, and the dequant of the next layer's
+// weights runs under this GEMM instead of in a launch of its own.
 #include "gemm_common.h"
 
 namespace dk {
@@ -126,74 +131,104 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
     const int64_t mrow0 = mw0 + 32 * i;
     if constexpr (EPI == EPI_LINEAR) {
       f32x16 res[TN];
+      float bias[TN];
 #pragma unroll
-      for (int j = 0; j < TN; ++j) {
-        const f32x16& a = acc[i][j];
-        const int64_t nb = nw0 + 32 * j;
-        const int64_t n = nb + lrow;
-        const float bias = p.bias ? (float)p.bias[n] : 0.0f;
+      for (int j = 0; j < TN; ++j) bias[j] = p.bias ? (float)p.bias[nw0 + 32 * j + lrow] : 0.0f;
 #pragma unroll
-        for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(__fadd_rn(a[v], bias));
-        for (int t = 0; t < p.n_lora; ++t) {
-          const LoraTerm& L = p.lora[t];
-          if (!TRANS && (nb < L.n_begin || nb >= L.n_end)) continue;
-          f32x16 lo;
+      for (int j = 0; j < TN; ++j)
 #pragma unroll
-          for (int v = 0; v < 16; ++v) lo[v] = 0.0f;
-          const int64_t zm = mrow0 + lrow;
-          for (int rc = 0; rc < p.rank; rc += 16) {
-            f16x8 zf, rf;
-            if (zm < M) {
-              zf = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
-            } else {
+        for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(__fadd_rn(acc[i][j][v], bias[j]));
+      // LoRA terms, one at a time.  Every global load a term needs in this strip (the z rows, the
+      // B rows or A columns of each block, the keep-mask bytes) is issued before the first is
+      // used, so a term costs one memory round trip rather than one per block and operand.
+      const int64_t zm = mrow0 + lrow;
+      for (int t = 0; t < p.n_lora; ++t) {
+        const LoraTerm& L = p.lora[t];
+        bool on[TN];
 #pragma unroll
-              for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
-            }
-            if (!TRANS) {
-              rf = *reinterpret_cast<const f16x8*>(L.r + (n - L.n_begin) * p.rank + rc + lk8);
-            } else {
-              // A[rc .. rc + 16][nb .. nb + 32] staged row-major (rows of 48 halves), read back
+        for (int j = 0; j < TN; ++j)
+          on[j] = TRANS || (nw0 + 32 * j >= L.n_begin && nw0 + 32 * j < L.n_end);
+        f32x16 lo[TN];
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) lo[j][v] = 0.0f;
+        u32x4 mw[TN];
+        const bool masked = TRANS && L.mask;
+        if (masked) {
+          // the blocks' 32 x 32 keep-mask bytes: one 16-byte load per lane and block
+          const int64_t mr = mrow0 + (lane >> 1);
+#pragma unroll
+          for (int j = 0; j < TN; ++j)
+            mw[j] = mr < M ? *reinterpret_cast<const u32x4*>(L.mask + mr * N + nw0 + 32 * j +
+                                                              16 * (lane & 1))
+                           : u32x4{0u, 0u, 0u, 0u};
+        }
+        for (int rc = 0; rc < p.rank; rc += 16) {
+          f16x8 zf, rr[TN];
+          if (zm < M) {
+            zf = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
+          } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            if (!on[j]) continue;
+            if (!TRANS)   // B row of this lane's column, ranks rc + lk8 ..
+              rr[j] = *reinterpret_cast<const f16x8*>(L.r + (nw0 + 32 * j + lrow - L.n_begin) * p.rank +
+                                                     rc + lk8);
+            else          // A[rc + lane / 4][8 columns of the block]
+              rr[j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N + nw0 +
+                                                     32 * j + 8 * (lane & 3));
+          }
+#pragma unroll
+          for (int j = 0; j < TN; ++j) {
+            if (!on[j]) continue;
+            f16x8 rf = rr[j];
+            if (TRANS) {
+              // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
               // rank-contiguous with transposing reads
-              const f16x8 av = *reinterpret_cast<const f16x8*>(
-                  L.r + (int64_t)(rc + (lane >> 2)) * N + nb + 8 * (lane & 3));
               __builtin_amdgcn_wave_barrier();
-              *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = av;
+              *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr[j];
               __builtin_amdgcn_wave_barrier();
               const f16* base = ascr + tr_k * 48 + tr_n;
               const f16x4 lo4 = read_tr(base), hi4 = read_tr(base + 4 * 48);
               rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
               __builtin_amdgcn_wave_barrier();
             }
-            lo = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo, 0, 0, 0);
+            lo[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo[j], 0, 0, 0);
           }
-          if (TRANS && L.mask) {
-            // the block's 32 x 32 keep-mask bytes: one 16-byte load per lane, staged in LDS
-            // (rows of 48 bytes), then read per element
-            const int64_t mr = mrow0 + (lane >> 1);
-            u32x4 mw = u32x4{0u, 0u, 0u, 0u};
-            if (mr < M) mw = *reinterpret_cast<const u32x4*>(L.mask + mr * N + nb + 16 * (lane & 1));
+        }
+#pragma unroll
+        for (int j = 0; j < TN; ++j) {
+          if (!on[j]) continue;
+          if (masked) {
+            // staged in LDS (rows of 48 bytes), then read per element
             __builtin_amdgcn_wave_barrier();
-            *reinterpret_cast<u32x4*>(mscr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw;
+            *reinterpret_cast<u32x4*>(mscr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw[j];
             __builtin_amdgcn_wave_barrier();
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
               const int mloc = 8 * (v >> 2) + rsub + (v & 3);
-              const float lf = (float)dk_h(lo[v]);
+              const float lf = (float)dk_h(lo[j][v]);
               res[j][v] = __fadd_rn(res[j][v], mscr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
             }
             __builtin_amdgcn_wave_barrier();
           } else {
 #pragma unroll
             for (int v = 0; v < 16; ++v) {
-              const float lf = (float)dk_h(lo[v]);
+              const float lf = (float)dk_h(lo[j][v]);
               res[j][v] = __fadd_rn(res[j][v], TRANS ? lf : __fmul_rn(L.scale, lf));
             }
           }
         }
-        if (p.out_mode == DK_OUT_F16) {
+      }
+      if (p.out_mode == DK_OUT_F16) {
+#pragma unroll
+        for (int j = 0; j < TN; ++j)
 #pragma unroll
           for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(res[j][v]);
-        }
       }
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -375,7 +410,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;
   const int lrow = lane & 31;
   const int hx = swz_k(lane & 15);
-  int fo[4];
+  int fo[4];   // operand offset of each 16-wide sub-step
 #pragma unroll
   for (int q = 0; q < 4; ++q) fo[q] = lrow * kBK + ((2 * q + (lane >> 5)) ^ hx) * 8;
   const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
@@ -396,7 +431,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
   f16x8 fa[2][TM], fb[2][TN];
 
-  auto read_frags = [&](int st, int s, int buf) {
+  auto read_frags = [&](int st, int s, int buf) {   // sub-step s of stage st
     const f16* as = As + st * SA + wm * WM * kBK + fo[s];
 #pragma unroll
     for (int i = 0; i < TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kBK);
@@ -446,31 +481,28 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   // stage with step kt + NST, spreading the DMA instructions between the last sub-step's MFMAs,
   // which run beside the first reads of step kt + 1.
 #pragma unroll
-  for (int s0 = 0; s0 < NST; ++s0)
-    if (s0 < nk)
+  for (int q = 0; q < NST; ++q)
+    if (q < nk)
 #pragma unroll
-      for (int d = 0; d < LOADS; ++d) issue(s0, s0, d);
+      for (int d = 0; d < LOADS; ++d) issue(q, q, d);
   wait_loads((nk < NST ? nk : NST) - 1);
   __syncthreads();
   read_frags(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & (NST - 1);
-    read_frags(st, 1, 1);
-    mfmas(0);
-    interleave();
-    read_frags(st, 2, 0);
-    mfmas(1);
-    interleave();
-    read_frags(st, 3, 1);
-    mfmas(0);
-    interleave();
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+      read_frags(st, j + 1, (j + 1) & 1);
+      mfmas(j & 1);
+      interleave();
+    }
     // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
     wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
     __syncthreads();
     if (kt + 1 < nk) read_frags((kt + 1) & (NST - 1), 0, 0);
     const bool refill = kt + NST < nk;
 #pragma unroll
-    for (int q = 0; q < TM * TN; ++q) {
+    for (int q = 0; q < TM * TN; ++q) {   // sub-step 3 (buffer 1)
       acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
                                                                  acc[q / TN][q % TN], 0, 0, 0);
 #pragma unroll
@@ -502,12 +534,19 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 // Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
 // tiles as 128 x 128 quarters.  With split-K (p.splits > 1, LINEAR only) workgroup b runs split
 // b / tiles of tile b % tiles and stores its fp32 partial tile at p.part[tile][split].  Tiles
-// are numbered M-fastest.
+// are numbered M-fastest.  The p.side.wgs workgroups after the tiles run the launch's dequant
+// work; dispatched last, they take the CUs the tiles leave idle.
 template <bool TRANS, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   __shared__ __attribute__((aligned(1024))) f16 As[kStages * kStageHalves];
   __shared__ __attribute__((aligned(1024))) f16 Bs[kStages * kStageHalves];
+  static_assert(side_dequant_lds <= kStages * kStageHalves * 2 && kSideThreads == kThreads,
+                "side dequant in the kernel's LDS");
+  if ((int)blockIdx.x >= main_tiles + tail_wgs) {
+    side_dequant(p.side, (int)blockIdx.x - main_tiles - tail_wgs, reinterpret_cast<uint8_t*>(As));
+    return;
+  }
   const int nk_all = (int)(p.K / kBK);
   int b = blockIdx.x;
   if (b < main_tiles) {
@@ -663,13 +702,26 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
       return kHgemmDeclined;
     p.part = reinterpret_cast<float*>(ws);
   }
-  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>), dim3((unsigned)(h.main_wgs + h.tail_wgs)),
+  // carried dequant: the given workgroup count, or (auto) the CUs the last round leaves idle
+  int side = 0;
+  if (p.side.sb1 > p.side.sb0 && p.side.wgs != 0) {
+    side = p.side.wgs;
+    if (side < 0) {
+      const int rest = (int)((h.main_wgs + h.tail_wgs) % cu_count());
+      side = rest ? cu_count() - rest : 0;
+      if (side < 16) side = 16;
+    }
+    p.side.wgs = side;
+  }
+  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>), dim3((unsigned)(h.main_wgs + h.tail_wgs + side)),
                      dim3(kThreads), 0, stream, p, (int)h.main_wgs, (int)h.tail_wgs);
   DK_CHECK_LAUNCH();
-  if (h.splits > 1) {
-    hipLaunchKernelGGL((hgemm_reduce_kernel<TRANS, EPI>),
-                       dim3((unsigned)(h.tiles_m * h.tiles_n * 64)), dim3(64), 0, stream, p);
-    DK_CHECK_LAUNCH();
+  if constexpr (EPI == EPI_LINEAR) {   // hplan splits K for the LINEAR epilogue only
+    if (h.splits > 1) {
+      hipLaunchKernelGGL((hgemm_reduce_kernel<TRANS, EPI>),
+                         dim3((unsigned)(h.tiles_m * h.tiles_n * 64)), dim3(64), 0, stream, p);
+      DK_CHECK_LAUNCH();
+    }
   }
   return 0;
 }

@@ -6,34 +6,22 @@
 // uniform (scalar loads).  The 64 output bytes of a lane are staged in LDS and written back
 // lane-contiguous, so every store instruction of a wave writes 1 KiB contiguous.  HBM traffic:
 // 2.516 bytes per weight (0.5 packed + 1/64 code + 8/16384 scale/offset in, 2 out).
-#include "dk_common.h"
+#include "nf4_dev.h"
 
 namespace {
 
 constexpr int kDqThreads = 256;
 constexpr int kDqQuadsPerBlock = kDqThreads;   // 8192 weights = half a second-level block
 
-__device__ __forceinline__ u32x4 dequant_word(uint32_t w, float a, const float* lut) {
-  u32x4 o;
-#pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    const uint32_t byte = (w >> (8 * b)) & 0xffu;
-    const f16 even = dk_h(__fmul_rn(lut[byte >> 4], a));   // element 2j: high nibble
-    const f16 odd = dk_h(__fmul_rn(lut[byte & 15u], a));
-    o[b] = dk_pack2(even, odd);
-  }
-  return o;
-}
-
 __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
     const u32x4* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ scale2, const float* __restrict__ offset2,
     const float* __restrict__ code2, const float* __restrict__ nf4, u32x4* __restrict__ out,
     int64_t n_quads) {
-  __shared__ float lut[16];
+  __shared__ f32x2 pairs[256];
   // per wave: 64 lanes x 4 chunks of 16 bytes, one pad chunk per 64 against bank conflicts
   __shared__ u32x4 stage[kDqThreads / 64][64 * 4 + 4];
-  if (threadIdx.x < 16) lut[threadIdx.x] = nf4[threadIdx.x];
+  dk_fill_pairs(pairs, nf4, threadIdx.x);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t first = (int64_t)blockIdx.x * kDqQuadsPerBlock;
   const int64_t sb = first >> 9;                    // 512 quads per second-level block
@@ -42,11 +30,11 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
   const int64_t tc = t < n_quads ? t : n_quads - 1;   // clamped: its result is not stored
   const u32x4 w = __builtin_nontemporal_load(packed + tc);
   const float amax = dk_absmax(code2[qabs[tc >> 1]], s2, o2);
-  __syncthreads();   // lut
+  __syncthreads();   // pairs
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = lane * 4 + j;
-    stage[wave][idx + (idx >> 6)] = dequant_word(w[j], amax, lut);
+    stage[wave][idx + (idx >> 6)] = dk_dequant_word(w[j], amax, pairs);
   }
   __syncthreads();
   const int64_t chunk0 = (first + wave * 64) * 4;     // first 8-weight chunk of this wave

@@ -807,13 +807,50 @@ int down_bwd_params(GemmParams& p, const void* dh, int64_t lddh, int64_t m, int6
   return 0;
 }
 
+// Checks the dequant work a launch carries and copies it into the kernel parameters.
+int set_side(GemmParams& p, const dk_side_dequant* side) {
+  p.side = SideDequant{};
+  if (!side || side->wgs == 0 || side->sb0 == side->sb1) return 0;
+  if ((side->wgs < 1 && side->wgs != DK_SIDE_WGS_AUTO) || side->wgs > 1024 || side->sb0 < 0 ||
+      side->sb1 < side->sb0)
+    return DK_ERR_INVALID;
+  if (!side->packed || !side->qabs || !side->scale2 || !side->offset2 || !side->code2 ||
+      !side->nf4 || !side->out)
+    return DK_ERR_INVALID;
+  if (!dk_aligned(side->packed, 16) || !dk_aligned(side->out, 16)) return DK_ERR_ALIGN;
+  p.side.packed = reinterpret_cast<const u32x4*>(side->packed);
+  p.side.qabs = side->qabs;
+  p.side.scale2 = side->scale2;
+  p.side.offset2 = side->offset2;
+  p.side.code2 = side->code2;
+  p.side.nf4 = side->nf4;
+  p.side.out = reinterpret_cast<u32x4*>(side->out);
+  p.side.sb0 = side->sb0;
+  p.side.sb1 = side->sb1;
+  p.side.wgs = side->wgs;
+  return 0;
+}
+
+// The carried dequant as a launch of its own, for GEMMs that do not run on the 256 x 256-tile
+// kernel (the same blocks, bit for bit).
+int side_alone(const SideDequant& s, hipStream_t stream) {
+  if (s.wgs == 0) return 0;
+  const int64_t q0 = s.sb0 * DK_QBLOCK2;
+  return dk_nf4_dequant(reinterpret_cast<const uint8_t*>(s.packed) + q0 * 32, s.qabs + q0,
+                        s.scale2 + s.sb0, s.offset2 + s.sb0, s.code2, s.nf4,
+                        reinterpret_cast<f16*>(s.out) + q0 * DK_QBLOCK, (s.sb1 - s.sb0) * DK_QBLOCK2,
+                        stream);
+}
+
 // fp16 weight: the 256 x 256-tile kernel where the shape suits it (no workspace), else the plan's
 // split-K (partials in the workspace when one is given), one phase.
 template <bool TRANS, int EPI>
-int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes, hipStream_t stream) {
+int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes,
+                 const dk_side_dequant* side, hipStream_t stream) {
   if (!w16) return DK_ERR_INVALID;
   if (!dk_aligned(w16, 16)) return DK_ERR_ALIGN;
-  if (p.M == 0) return 0;
+  if (int e = set_side(p, side)) return e;
+  if (p.M == 0) return side_alone(p.side, stream);
   p.w16 = (const f16*)w16;
   const int big = hgemm_launch<TRANS, EPI>(p, ws, ws_bytes, stream);
   if (big != kHgemmDeclined) return big;
@@ -825,7 +862,8 @@ int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes, hipS
     if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
     p.part = reinterpret_cast<float*>(ws);
   }
-  return launch_plan<TRANS, EPI, true>(pl, p, stream);
+  if (int e = launch_plan<TRANS, EPI, true>(pl, p, stream)) return e;
+  return side_alone(p.side, stream);
 }
 
 template <bool TRANS, int EPI>
@@ -911,40 +949,42 @@ extern "C" int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, con
                                       int64_t rows, int64_t cols, const void* bias,
                                       const dk_lora_term* terms, int n_terms, int64_t rank,
                                       void* y, int64_t ldy, void* workspace,
-                                      int64_t workspace_bytes, hipStream_t stream) {
+                                      int64_t workspace_bytes, const dk_side_dequant* side,
+                                      hipStream_t stream) {
   GemmParams p = {};
   if (int e = linear_fwd_params(p, x, ldx, m, rows, cols, bias, terms, n_terms, rank, y, ldy))
     return e;
-  return dispatch_h16<false, EPI_LINEAR>(p, w16, workspace, workspace_bytes, stream);
+  return dispatch_h16<false, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream);
 }
 
 extern "C" int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
                                          int64_t rows, int64_t cols, const dk_lora_term* terms,
                                          int n_terms, int64_t rank, void* dx, int64_t lddx,
                                          int out_mode, void* workspace, int64_t workspace_bytes,
-                                         hipStream_t stream) {
+                                         const dk_side_dequant* side, hipStream_t stream) {
   GemmParams p = {};
   if (int e = linear_bwd_params(p, dy, lddy, m, rows, cols, terms, n_terms, rank, dx, lddx,
                                 out_mode))
     return e;
-  return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, stream);
+  return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream);
 }
 
 extern "C" int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16,
                                         int64_t rows, int64_t cols, void* act, void* gu_out,
                                         void* workspace, int64_t workspace_bytes,
-                                        hipStream_t stream) {
+                                        const dk_side_dequant* side, hipStream_t stream) {
   GemmParams p = {};
   if (int e = gateup_params(p, x, ldx, m, rows, cols, act, gu_out)) return e;
-  return dispatch_h16<false, EPI_SWIGLU_FWD>(p, w16, workspace, workspace_bytes, stream);
+  return dispatch_h16<false, EPI_SWIGLU_FWD>(p, w16, workspace, workspace_bytes, side, stream);
 }
 
 extern "C" int dk_h16_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const void* w16,
                                       int64_t rows, int64_t cols, void* gu, void* workspace,
-                                      int64_t workspace_bytes, hipStream_t stream) {
+                                      int64_t workspace_bytes, const dk_side_dequant* side,
+                                      hipStream_t stream) {
   GemmParams p = {};
   if (int e = down_bwd_params(p, dh, lddh, m, rows, cols, gu)) return e;
-  return dispatch_h16<true, EPI_SWIGLU_BWD>(p, w16, workspace, workspace_bytes, stream);
+  return dispatch_h16<true, EPI_SWIGLU_BWD>(p, w16, workspace, workspace_bytes, side, stream);
 }
 
 extern "C" int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op) {

@@ -181,6 +181,30 @@ def dequant_layer(layer, code2, nf4, out):
                            code2, nf4, out)
 
 
+def side_dequant(layer, code2, nf4, out, sb0, sb1, wgs):
+    """The dk_side_dequant a fp16-weight GEMM launch carries (w4linear's ``side=`` argument):
+    second-level blocks [sb0, sb1) of `layer` (GPU-resident) into the whole-layer fp16 buffer
+    `out` (weight e at out[e]), on `wgs` extra workgroups of the launch (-1: as many as the CUs
+    its last round of tiles leaves idle, at least 16).  This is the reference's
+    dequant ahead of use (dequant_range on dq_stream, solution/fast_qwen.py:729-731) moved into
+    the launch of the GEMM it overlaps.  Returns the ctypes struct; `layer`, `out` and the tables
+    must outlive the launch."""
+    sb0, sb1, wgs = int(sb0), int(sb1), int(wgs)
+    n_sb = layer.n_qblocks // 256
+    if not (0 <= sb0 <= sb1 <= n_sb) or not (wgs == -1 or 0 <= wgs <= 1024):
+        raise ValueError(f"side dequant of blocks [{sb0}, {sb1}) of {n_sb} on {wgs} workgroups")
+    for t, dt in ((layer.packed, torch.uint8), (layer.qabs, torch.uint8),
+                  (layer.scale2, torch.float32), (layer.offset2, torch.float32),
+                  (code2, torch.float32), (nf4, torch.float32), (out, torch.float16)):
+        if t.dtype != dt or not t.is_cuda:
+            raise ValueError(f"dequant operand has dtype {t.dtype} on {t.device}, expected CUDA {dt}")
+    if out.numel() < layer.n_qblocks * 64 or not out.is_contiguous():
+        raise ValueError("side dequant output is not a contiguous whole-layer buffer")
+    return _lib.SideDequantC(_lib.ptr(layer.packed), _lib.ptr(layer.qabs), _lib.ptr(layer.scale2),
+                             _lib.ptr(layer.offset2), _lib.ptr(code2), _lib.ptr(nf4),
+                             _lib.ptr(out), sb0, sb1, wgs)
+
+
 def dequant_range(layer, q0, q1, code2, nf4, out, dst=None):
     """Dequantise first-level blocks [q0, q1) of `layer` into `out` at their own position, or at
     element offset `dst`.  q0 and q1 must be multiples of RANGE_ALIGN (q1 may be the layer end)

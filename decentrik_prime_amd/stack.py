@@ -25,7 +25,7 @@ read the slot (dk_h16_*); the other kinds read the NF4 sections directly (dk_w4_
 reference's workspace schedule (solution/fast_qwen.py:694-756): right after layer i's GEMM reads
 kind k's slot, the dequant of kind k for the next layer in step order (i + 1 forward, i - 1
 backward) is issued, and a weight still resident is not dequantised again (the last layer at the
-forward/backward turn, layer 0 between steps).  ``ahead="layer"`` (the default) keeps one slot
+forward/backward turn, layer 0 between steps).  ``ahead="layer"`` keeps one slot
 for the whole layer instead and dequantises all seven weights of a layer in one launch (the
 reference's dequant_layer, solution/k_nf4.py:176-181): the small q|k|v and o dequants are
 launch-bound on their own.  ``dq_stream="side"`` runs those dequants on a
@@ -33,6 +33,15 @@ stream of their own, overlapping the GEMMs in between; ``"main"`` (the default) 
 order on the compute stream.  Measured on MI355X (28 layers, M = 2048) the in-order form is
 1.3 ms per step faster: each GEMM holds all of a CU's registers at two workgroups per CU, so a
 concurrent dequant only takes workgroup slots from it.
+
+``ahead="carried"`` (the default) keeps two whole-layer slots (layer i in slot i % 2) and has the GEMM launches
+of layer i carry the dequant of the next layer in step order into the other slot
+(k_nf4.side_dequant): each launch in ``CARRY`` takes its share of the next layer's second-level
+blocks on extra workgroups, which the hardware dispatches after the tiles, onto the CUs the
+GEMM's last round leaves idle.  A layer no launch carries is dequantised by a launch of its own
+right before its first GEMM.  The dequant count per step is the reference's: every layer is
+dequantised once in the forward (layer 0 excepted, resident from the previous backward) and once
+in the backward (the last layer excepted, resident from the forward).
 """
 
 import torch
@@ -79,9 +88,16 @@ class NF4LinearStack:
     and synthetic activations, all resident on `device`."""
 
     KINDS = ("qkv", "o", "gu", "d")
+    # ahead="carried": the share of the next layer's dequant (fraction of its second-level blocks)
+    # that each GEMM launch carries, in step order; the launches that leave CUs idle (a last round
+    # of 128 x 128 tiles, split-K grids short of the CU count, 128 x 128 grids short of a round).
+    # Backward only: measured on MI355X, the forward's idle windows are too short and the carried
+    # stream slows the forward GEMMs' operand traffic by more than the launch it saves.
+    CARRY = {"fwd": (),
+             "bwd": (("d", 0.45), ("gu", 0.15), ("o", 0.15), ("qkv", 0.25))}
 
     def __init__(self, n_layers=28, m=2048, seed=0, device="cuda", p_drop=0.05, lora_scale=2.0,
-                 save_gu=True, ahead="layer", dq_stream="main"):
+                 save_gu=True, ahead="carried", dq_stream="main"):
         self.n_layers, self.m, self.device = n_layers, m, torch.device(device)
         self.s = float(lora_scale)
         self.keep_scale = 1.0 / float(torch.tensor(1.0 - p_drop, dtype=torch.float32))
@@ -132,7 +148,31 @@ class NF4LinearStack:
 
     def _setup_schedule(self, ahead, dq_stream):
         """The fp16 slots of the dequant-ahead schedule (see the module docstring)."""
-        self.whole_layer = ahead == "layer"
+        self.carried = ahead == "carried"
+        self.whole_layer = ahead in ("layer", "carried")
+        if self.carried:
+            self.ahead = self.KINDS
+            pk = self.layers[0]["packed"]
+            first = {"qkv": "q_proj", "o": "o_proj", "gu": "gate_proj", "d": "down_proj"}
+            self.views = {k: (pk.segments[first[k]][0], self.layers[0][k].rows * self.layers[0][k].cols)
+                          for k in self.KINDS}
+            self.slots = [torch.empty(pk.numel, dtype=torch.float16, device=self.device)
+                          for _ in range(2)]
+            self.slot_layer = [None, None]    # (layer, pass that dequantised it) per slot
+            self._pass = 0
+            self.dq = None
+            n_sb = self.n_sb = pk.n_qblocks // 256
+            self.carry = {}
+            for way, shares in self.CARRY.items():
+                acc, bounds = 0.0, {}
+                for kind, frac in shares:
+                    lo = round(acc * n_sb)
+                    acc += frac
+                    bounds[kind] = (lo, round(min(acc, 1.0) * n_sb))
+                if shares:
+                    bounds[shares[-1][0]] = (bounds[shares[-1][0]][0], n_sb)
+                self.carry[way] = bounds
+            return
         if self.whole_layer:
             self.ahead = self.KINDS
             pk = self.layers[0]["packed"]
@@ -157,6 +197,19 @@ class NF4LinearStack:
         """Layer i's fp16 weight of `kind` from its slot, or None for an NF4 read."""
         if kind not in self.ahead:
             return None
+        if self.carried:
+            # a layer's weights are dequantised in this pass (carried in by the previous layer's
+            # launches, else by a launch of their own here), except the pass's first layer, which
+            # may still hold them from the other pass (the reference's reuse at the turn and
+            # between steps)
+            slot = i % 2
+            held = self.slot_layer[slot]
+            first = 0 if self._forward else self.n_layers - 1
+            if held != (i, self._pass) and not (i == first and held is not None and held[0] == i):
+                k_nf4.dequant_layer(self.layers[i]["packed"], self.code2, self.nf4, self.slots[slot])
+                self.slot_layer[slot] = (i, self._pass)
+            start, n = self.views[kind]
+            return self.slots[slot][start:start + n]
         if self.whole_layer:
             self.dq.issue("layer", i, _WholeLayer(self, i))     # no-op when already resident
             start, n = self.views[kind]
@@ -165,10 +218,25 @@ class NF4LinearStack:
         self.dq.issue(kind, key, self.layers[i][kind])     # no-op when already resident
         return self.dq.take(kind, key)
 
+    def _side(self, kind, nxt):
+        """ahead="carried": the share of layer `nxt`'s dequant that this launch of `kind` carries
+        into slot nxt % 2, or None."""
+        if not self.carried or not 0 <= nxt < self.n_layers:
+            return None
+        bounds = self.carry["fwd" if self._forward else "bwd"]
+        if kind not in bounds:
+            return None
+        sb0, sb1 = bounds[kind]
+        slot = nxt % 2
+        if sb1 == self.n_sb:    # the layer's last share: from here on the slot holds layer nxt
+            self.slot_layer[slot] = (nxt, self._pass)
+        return k_nf4.side_dequant(self.layers[nxt]["packed"], self.code2, self.nf4,
+                                  self.slots[slot], sb0, sb1, -1)
+
     def _done(self, kind, nxt):
         """The slot of `kind` has had its last reader; dequantise layer `nxt`'s weight into it
         (whole-layer slot: after the last weight of the layer in step order)."""
-        if kind not in self.ahead:
+        if kind not in self.ahead or self.carried:
             return
         if self.whole_layer:
             if kind != ("d" if self._forward else "qkv"):    # the layer's last weight
@@ -186,36 +254,42 @@ class NF4LinearStack:
         return ("h16" if kind in self.ahead else "w4") + base
 
     def forward_layer(self, i):
+        if i == 0 or not getattr(self, "_forward", False):
+            self._pass = getattr(self, "_pass", 0) + 1
         self._forward = True
         L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
-        op, nm, w16, done = self._op, self.op_name, self._w16, self._done
+        op, nm, w16, done, side = self._op, self.op_name, self._w16, self._done, self._side
         op("lora_down q+v", lora_down_multi, x,
            [(lo["Aq"], lo["mq"], self.keep_scale), (lo["Av"], lo["mv"], self.keep_scale)],
            outs=[z["q"], z["v"]])
         op(nm("qkv", "_linear_fwd qkv+lora"), linear_forward_lora, x, L["qkv"], lo["bias"],
-           self.qkv_terms(i), out=o["qkv"], w16=w16("qkv", i))
+           self.qkv_terms(i), out=o["qkv"], w16=w16("qkv", i), side=side("qkv", i + 1))
         done("qkv", i + 1)
-        op(nm("o", "_linear_fwd o"), linear_forward, x, L["o"], out=o["o"], w16=w16("o", i))
+        op(nm("o", "_linear_fwd o"), linear_forward, x, L["o"], out=o["o"], w16=w16("o", i),
+           side=side("o", i + 1))
         done("o", i + 1)
         op(nm("gu", "_gateup_swiglu_fwd"), gateup_swiglu_forward, x, L["gu"], act=self.act,
-           gu=self.gu[i], w16=w16("gu", i))
+           gu=self.gu[i], w16=w16("gu", i), side=side("gu", i + 1))
         done("gu", i + 1)
         op(nm("d", "_linear_fwd down"), linear_forward, self.act, L["d"], out=o["y"],
-           w16=w16("d", i))
+           w16=w16("d", i), side=side("d", i + 1))
         done("d", i + 1)
 
     def backward_layer(self, i):
+        if i == self.n_layers - 1 or getattr(self, "_forward", True):
+            self._pass = getattr(self, "_pass", 0) + 1
         self._forward = False
         L, lo, z, x, dy = self.layers[i], self.lora[i], self.z[i], self.x, self.dy
         gu = self.gu[i]
-        op, nm, w16, done = self._op, self.op_name, self._w16, self._done
-        op(nm("d", "_down_swiglu_bwd"), down_swiglu_backward, dy["d"], L["d"], gu, w16=w16("d", i))
+        op, nm, w16, done, side = self._op, self.op_name, self._w16, self._done, self._side
+        op(nm("d", "_down_swiglu_bwd"), down_swiglu_backward, dy["d"], L["d"], gu, w16=w16("d", i),
+           side=side("d", i - 1))
         done("d", i - 1)
         op(nm("gu", "_linear_bwd_dx gate|up"), linear_backward_dx, gu, L["gu"], out=self.dx_mlp,
-           w16=w16("gu", i))
+           w16=w16("gu", i), side=side("gu", i - 1))
         done("gu", i - 1)
         op(nm("o", "_linear_bwd_dx o"), linear_backward_dx, dy["o"], L["o"], out=self.dx_o,
-           w16=w16("o", i))
+           w16=w16("o", i), side=side("o", i - 1))
         done("o", i - 1)
         dqkv = dy["qkv"]
         (daq, dbq, dzq), (dav, dbv, dzv) = op(
@@ -224,7 +298,7 @@ class NF4LinearStack:
              (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, lo["mv"], self.keep_scale)])
         op(nm("qkv", "_linear_bwd_dx qkv+lora"), linear_backward_dx_lora, dqkv, L["qkv"],
            [(dzq, lo["Aq"], lo["mq"], self.keep_scale), (dzv, lo["Av"], lo["mv"], self.keep_scale)],
-           out=self.dx_qkv, w16=w16("qkv", i))
+           out=self.dx_qkv, w16=w16("qkv", i), side=side("qkv", i - 1))
         done("qkv", i - 1)
         self.grads[i] = (daq, dbq, dav, dbv)
 

@@ -118,6 +118,15 @@ def _check_w16(w16, w):
         raise ValueError(f"w16 has {w16.numel()} elements, the weight {w.rows} x {w.cols}")
 
 
+def _side(side):
+    """Pointer argument for a carried dequant (k_nf4.side_dequant) or None."""
+    if side is None:
+        return None
+    if not isinstance(side, _lib.SideDequantC):
+        raise ValueError("side must come from k_nf4.side_dequant")
+    return ctypes.byref(side)
+
+
 def _check16(t, name, shape=None):
     if t.dtype != torch.float16 or not t.is_cuda:
         raise ValueError(f"{name} must be a CUDA fp16 tensor, got {t.dtype} on {t.device}")
@@ -183,14 +192,18 @@ def lora_down_multi(x, terms, outs=None):
     return zs
 
 
-def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None, w16=None):
+def linear_forward(x, w, bias=None, z=None, lora_B=None, lora_scale=2.0, out=None, w16=None,
+                   side=None):
     """y = fp16(fp32(fp16(x W^T + bias)) + s * fp32(fp16(z B^T)))  (LoRA part optional).
-    x [M, in] fp16, w a W4 [out, in], z [M, r], lora_B [out, r]; w16 as in linear_forward_lora."""
+    x [M, in] fp16, w a W4 [out, in], z [M, r], lora_B [out, r]; w16, side as in
+    linear_forward_lora."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     if w16 is not None:
         if (z is None) != (lora_B is None):
             raise ValueError("z and lora_B go together")
         terms = [(z, lora_B, 0, w.rows, lora_scale)] if z is not None else []
-        return linear_forward_lora(x, w, bias, terms, out, w16=w16)
+        return linear_forward_lora(x, w, bias, terms, out, w16=w16, side=side)
     _check16(x, "x")
     m = x.shape[0]
     if x.shape[1] != w.cols:
@@ -246,12 +259,15 @@ def _lora_terms(terms, m, backward, n_cols):
     return arr, len(terms), rank, keep
 
 
-def linear_forward_lora(x, w, bias=None, terms=(), out=None, w16=None):
+def linear_forward_lora(x, w, bias=None, terms=(), out=None, w16=None, side=None):
     """The fused linear forward with up to two LoRA terms on disjoint output-column ranges:
     terms = [(z [M, r], lora_B [c1 - c0, r], col_begin c0, col_end c1, scale s), ...].  The fused
     QKV projection passes the q term on columns [0, NQ*HD) and the v term on the last NKV*HD
     columns (solution/fast_qwen.py:943-949).  w16: the weight already dequantised to fp16 (the
-    reference's workspace view), or None to read the NF4 sections."""
+    reference's workspace view), or None to read the NF4 sections.  side (w16 only): dequant
+    work the launch carries, from k_nf4.side_dequant, or None."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     _check16(x, "x")
     m = x.shape[0]
     if x.shape[1] != w.cols:
@@ -268,7 +284,7 @@ def linear_forward_lora(x, w, bias=None, terms=(), out=None, w16=None):
         ws, nbytes = _h16_workspace(m, w.rows, w.cols, _lib.DK_OP_LINEAR_FWD, x.device)
         rc = _lib.lib().dk_h16_linear_fwd_lora(_lib.ptr(x), x.stride(0), m, _lib.ptr(w16), w.rows,
                                                w.cols, _lib.ptr(bias), arr, n, rank, _lib.ptr(out),
-                                               out.stride(0), _lib.ptr(ws), nbytes,
+                                               out.stride(0), _lib.ptr(ws), nbytes, _side(side),
                                                _lib.stream_handle(x.device))
         _lib.check(rc, "dk_h16_linear_fwd_lora")
         return out
@@ -299,11 +315,13 @@ def _dx_out(out, m, w, out_dtype, accumulate, device):
 
 
 def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, accumulate=False,
-                            w16=None):
+                            w16=None, side=None):
     """dX = fp32(fp16(dy W)) + sum over terms of (mask ? fp32(fp16(dz A)) * keep_scale : 0),
     terms = [(dz [M, r], lora_A [r, in], mask [M, in] or None, keep_scale), ...] added in order
     (the QKV backward: dy1 = mm(dqkv, W_qkv) plus the lq and lv terms of rms_backward,
-    solution/fast_qwen.py:1364, 1376-1380)."""
+    solution/fast_qwen.py:1364, 1376-1380).  w16, side as in linear_forward_lora."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     _check16(dy, "dy")
     m = dy.shape[0]
     if dy.shape[1] != w.rows:
@@ -317,7 +335,7 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
         rc = _lib.lib().dk_h16_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, _lib.ptr(w16),
                                                   w.rows, w.cols, arr, n, rank, _lib.ptr(out),
                                                   out.stride(0), mode, _lib.ptr(ws), nbytes,
-                                                  _lib.stream_handle(dy.device))
+                                                  _side(side), _lib.stream_handle(dy.device))
         _lib.check(rc, "dk_h16_linear_bwd_dx_lora")
         return out
     ws, nbytes = _workspace(w, m, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
@@ -329,16 +347,19 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
 
 
 def linear_backward_dx(dy, w, dz=None, lora_A=None, mask=None, keep_scale=1.0, out=None,
-                       out_dtype=torch.float32, accumulate=False, w16=None):
+                       out_dtype=torch.float32, accumulate=False, w16=None, side=None):
     """dX = fp32(fp16(dy W)) + (mask ? fp32(fp16(dz A)) * keep_scale : 0).
     dy [M, out] fp16, w a W4 [out, in], dz [M, r], lora_A [r, in], mask [M, in].
     out_dtype float16 rounds dX to fp16; accumulate=True adds into an fp32 `out`; w16 as in
     linear_forward_lora."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     if w16 is not None:
         if (dz is None) != (lora_A is None):
             raise ValueError("dz and lora_A go together")
         terms = [(dz, lora_A, mask, keep_scale)] if dz is not None else []
-        return linear_backward_dx_lora(dy, w, terms, out, out_dtype, accumulate, w16=w16)
+        return linear_backward_dx_lora(dy, w, terms, out, out_dtype, accumulate, w16=w16,
+                                       side=side)
     _check16(dy, "dy")
     m = dy.shape[0]
     if dy.shape[1] != w.rows:
@@ -436,9 +457,11 @@ def lora_grads_multi(x, terms):
     return res
 
 
-def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None):
+def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None, side=None):
     """gate|up as one NF4 GEMM with the gated-SiLU epilogue.  w_gu is [2I, in] (gate rows then up
-    rows).  Returns (act [M, I], gu [M, 2I] or None)."""
+    rows).  Returns (act [M, I], gu [M, 2I] or None).  w16, side as in linear_forward_lora."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     _check16(x, "x")
     m = x.shape[0]
     inter = w_gu.rows // 2
@@ -460,7 +483,7 @@ def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None):
         _check_w16(w16, w_gu)
         rc = _lib.lib().dk_h16_gateup_swiglu_fwd(_lib.ptr(x), x.stride(0), m, _lib.ptr(w16),
                                                  w_gu.rows, w_gu.cols, _lib.ptr(act), _lib.ptr(gu),
-                                                 None, 0, _lib.stream_handle(dev))
+                                                 None, 0, _side(side), _lib.stream_handle(dev))
         _lib.check(rc, "dk_h16_gateup_swiglu_fwd")
         return act, gu
     ws, nbytes = _workspace(w_gu, m, _lib.DK_OP_GATEUP_SWIGLU_FWD, dev)
@@ -471,8 +494,11 @@ def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None):
     return act, gu
 
 
-def down_swiglu_backward(dh, w_down, gu, w16=None):
-    """dact = fp16(dh W_down), then gu <- [dgate | dup] in place.  Returns gu."""
+def down_swiglu_backward(dh, w_down, gu, w16=None, side=None):
+    """dact = fp16(dh W_down), then gu <- [dgate | dup] in place.  Returns gu.  w16, side as in
+    linear_forward_lora."""
+    if side is not None and w16 is None:
+        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
     _check16(dh, "dh")
     _check16(gu, "gu", (dh.shape[0], 2 * w_down.cols))
     if dh.shape[1] != w_down.rows or not gu.is_contiguous():
@@ -481,7 +507,7 @@ def down_swiglu_backward(dh, w_down, gu, w16=None):
         _check_w16(w16, w_down)
         rc = _lib.lib().dk_h16_down_swiglu_bwd(_lib.ptr(dh), dh.stride(0), dh.shape[0], _lib.ptr(w16),
                                                w_down.rows, w_down.cols, _lib.ptr(gu), None, 0,
-                                               _lib.stream_handle(dh.device))
+                                               _side(side), _lib.stream_handle(dh.device))
         _lib.check(rc, "dk_h16_down_swiglu_bwd")
         return gu
     ws, nbytes = _workspace(w_down, dh.shape[0], _lib.DK_OP_DOWN_SWIGLU_BWD, dh.device)

@@ -245,26 +245,53 @@ int dk_w4_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const dk_nf4_
  * The same GEMMs and epilogues on a weight already dequantised to fp16 (w16 [rows][cols], stored
  * like the NF4 weight: [out, in], in contiguous, 16-byte aligned).  These are the reference's
  * GEMMs on its dequantised workspace (torch.mm/addmm on views filled by k_nf4.dequant_range on a
- * side stream ahead of use, solution/fast_qwen.py:694-756, 943-947, 1093-1112, 1310-1364): a
- * caller dequantises the next weight with dk_nf4_dequant on a second stream while the current
- * GEMM runs, and orders the two streams with events.  Arguments, rounding and rules as the dk_w4_*
- * entry point of the same name; workspace (split-K partials only) sized by dk_h16_workspace, or
- * NULL. */
+ * side stream ahead of use, solution/fast_qwen.py:694-756, 943-947, 1093-1112, 1310-1364).
+ * Arguments, rounding and rules as the dk_w4_* entry point of the same name; workspace (split-K
+ * partials only) sized by dk_h16_workspace, or NULL.
+ *
+ * `side` (or NULL) is dequant work the launch carries: the reference's ahead-of-use dequant
+ * (k_nf4.dequant_range on dq_stream, solution/fast_qwen.py:729-731) done inside the GEMM launch
+ * by `wgs` extra workgroups, which run on the CUs the GEMM's tiles leave idle, instead of on a
+ * second stream.  It dequantises second-level blocks [sb0, sb1) of one repacked layer: the four
+ * section pointers are the layer's (as dk_nf4_dequant takes them), and weight e of the layer goes
+ * to out[e] (fp16, 16-byte aligned), so out is the base of a whole-layer fp16 buffer.  The work is
+ * complete when the GEMM is (stream order); out must not overlap anything the GEMM reads or
+ * writes.  Bit-identical to dk_nf4_dequant over the same blocks.  wgs = 0 or sb0 = sb1: none.
+ * GEMMs that the 256 x 256-tile kernel does not take run the work as a dequant launch of its own
+ * after the GEMM. */
+typedef struct dk_side_dequant {
+  const uint8_t* packed;
+  const uint8_t* qabs;
+  const float* scale2;
+  const float* offset2;
+  const float* code2;
+  const float* nf4;
+  void* out;
+  int64_t sb0, sb1;   /* second-level blocks (16384 weights each) */
+  int32_t wgs;        /* 1 .. 1024, or DK_SIDE_WGS_AUTO: as many as the CUs the launch's last
+                         round of tiles leaves idle (at least 16) */
+} dk_side_dequant;
+#define DK_SIDE_WGS_AUTO (-1)
+
 int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op);
 int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
                            int64_t cols, const void* bias, const dk_lora_term* terms, int n_terms,
                            int64_t rank, void* y, int64_t ldy, void* workspace,
-                           int64_t workspace_bytes, hipStream_t stream);
+                           int64_t workspace_bytes, const dk_side_dequant* side,
+                           hipStream_t stream);
 int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
                               int64_t rows, int64_t cols, const dk_lora_term* terms, int n_terms,
                               int64_t rank, void* dx, int64_t lddx, int out_mode, void* workspace,
-                              int64_t workspace_bytes, hipStream_t stream);
+                              int64_t workspace_bytes, const dk_side_dequant* side,
+                              hipStream_t stream);
 int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
                              int64_t cols, void* act, void* gu_out, void* workspace,
-                             int64_t workspace_bytes, hipStream_t stream);
+                             int64_t workspace_bytes, const dk_side_dequant* side,
+                             hipStream_t stream);
 int dk_h16_down_swiglu_bwd(const void* dh, int64_t lddh, int64_t m, const void* w16,
                            int64_t rows, int64_t cols, void* gu, void* workspace,
-                           int64_t workspace_bytes, hipStream_t stream);
+                           int64_t workspace_bytes, const dk_side_dequant* side,
+                           hipStream_t stream);
 
 #ifdef __cplusplus
 }

@@ -57,19 +57,37 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_h16_workspace(0, 1536, 1536, _lib.DK_OP_LINEAR_FWD) == 0
     p16 = ctypes.c_void_p(16)
     assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, None, 1536, 1536, None, None, 0, 0, p16, 1536,
-                                      None, 0, None) == _lib.DK_ERR_INVALID     # no weight
+                                      None, 0, None, None) == _lib.DK_ERR_INVALID     # no weight
     assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, ctypes.c_void_p(8), 1536, 1536, None, None, 0,
-                                      0, p16, 1536, None, 0, None) == _lib.DK_ERR_ALIGN
+                                      0, p16, 1536, None, 0, None, None) == _lib.DK_ERR_ALIGN
     assert lib.dk_h16_linear_fwd_lora(p16, 1536, 8, p16, 1000, 1536, None, None, 0, 0, p16, 1536,
-                                      None, 0, None) == _lib.DK_ERR_INVALID     # rows % 64
+                                      None, 0, None, None) == _lib.DK_ERR_INVALID     # rows % 64
     assert lib.dk_h16_linear_bwd_dx_lora(p16, 1536, 8, p16, 1536, 1536, None, 0, 0, p16, 1536, 9,
-                                         None, 0, None) == _lib.DK_ERR_INVALID  # output mode
+                                         None, 0, None, None) == _lib.DK_ERR_INVALID  # output mode
     assert lib.dk_h16_gateup_swiglu_fwd(p16, 1536, 8, p16, 17920 + 64, 1536, p16, None, None, 0,
-                                        None) == _lib.DK_ERR_INVALID            # rows % 128
+                                        None, None) == _lib.DK_ERR_INVALID            # rows % 128
     assert lib.dk_h16_down_swiglu_bwd(p16, 1536, 8, p16, 1536, 8960, None, None, 0,
-                                      None) == _lib.DK_ERR_INVALID              # no gu
+                                      None, None) == _lib.DK_ERR_INVALID              # no gu
     assert lib.dk_h16_linear_fwd_lora(p16, 1536, 0, p16, 1536, 1536, None, None, 0, 0, p16, 1536,
-                                      None, 0, None) == 0                       # zero rows
+                                      None, 0, None, None) == 0                       # zero rows
+    # carried dequant: rejected before any launch when malformed
+    good = dict(packed=16, qabs=16, scale2=16, offset2=16, code2=16, nf4=16, out=16, sb0=0, sb1=4,
+                wgs=-1)
+    for bad, err in ((dict(wgs=-2), _lib.DK_ERR_INVALID), (dict(wgs=1025), _lib.DK_ERR_INVALID),
+                     (dict(sb0=5), _lib.DK_ERR_INVALID), (dict(sb0=-1), _lib.DK_ERR_INVALID),
+                     (dict(packed=None), _lib.DK_ERR_INVALID), (dict(nf4=None), _lib.DK_ERR_INVALID),
+                     (dict(out=8), _lib.DK_ERR_ALIGN), (dict(packed=4), _lib.DK_ERR_ALIGN)):
+        side = _lib.SideDequantC(**{**good, **bad})
+        for call in (
+                lambda: lib.dk_h16_linear_fwd_lora(p16, 1536, 8, p16, 1536, 1536, None, None, 0, 0,
+                                                   p16, 1536, None, 0, ctypes.byref(side), None),
+                lambda: lib.dk_h16_linear_bwd_dx_lora(p16, 1536, 8, p16, 1536, 1536, None, 0, 0, p16,
+                                                      1536, 0, None, 0, ctypes.byref(side), None),
+                lambda: lib.dk_h16_gateup_swiglu_fwd(p16, 1536, 8, p16, 17920, 1536, p16, None,
+                                                     None, 0, ctypes.byref(side), None),
+                lambda: lib.dk_h16_down_swiglu_bwd(p16, 1536, 8, p16, 1536, 8960, p16, None, 0,
+                                                   ctypes.byref(side), None)):
+            assert call() == err, bad
     # LoRA gradient partial sums: 16 row chunks x (n_out + k) columns x rank fp32, per term
     assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * (1536 + 1536) * 16 * 4
     n_outs = (ctypes.c_int64 * 2)(1536, 256)

@@ -1,17 +1,17 @@
 """CPU check of the dequant-ahead schedule (decentrik_prime_amd/schedule.py, stack.py), the
 counterpart of the reference's schedule check (dev/test_ws_schedule.py:102-235): the stack's real
 step() runs against a model of HIP streams and events in which every launch is a node and a
-stream's launches depend on its previous launch and on the events it waited for.  For several
-steps of forward + backward, in every schedule (whole layer or per weight kind, in order or on a
-side stream) it checks that
+stream's launches depend on its previous launch and on the events it waited for.  A launch reads
+and writes fp16 slot memory in units of one second-level block (16384 weights).  For several
+steps of forward + backward, in every schedule (per weight kind or whole layer, in order or on a
+side stream, or carried by the GEMM launches into two alternating slots) it checks that
 
-  * every GEMM reads slot contents dequantised from the layer and weight it multiplies, by the
-    last dequant into that slot ordered before it, with no dequant into that slot unordered
-    against it (no stale or racing read);
-  * every dequant into a slot is ordered after every read of the slot's previous contents (no
-    overwrite while in use);
-  * the dequant count per step: 2 per layer, less the two layers still resident at the
-    forward/backward turn and between steps (54 of 56 for 28 layers).
+  * every GEMM reads, in each unit of its weight, what the last write ordered before it put
+    there, and that write dequantised the layer the GEMM multiplies, with no write of that unit
+    unordered against the read (no stale or racing read);
+  * no write of a unit is unordered against a read of the unit (no overwrite while in use);
+  * the dequant work per step: every layer twice, less the two layers still resident at the
+    forward/backward turn and between steps (54 of 56 for 28 layers), in every schedule.
 """
 
 import types
@@ -23,10 +23,12 @@ from decentrik_prime_amd import k_nf4, stack as stack_mod
 from decentrik_prime_amd.schedule import DequantAhead
 from decentrik_prime_amd.stack import NF4LinearStack
 
+UNIT = 16384   # weights per second-level block
+
 
 class _Node:
-    def __init__(self, what, deps):
-        self.what, self.deps = what, deps
+    def __init__(self, acts, deps):
+        self.acts, self.deps = acts, deps
 
 
 class _Streams:
@@ -50,13 +52,16 @@ class _Streams:
                     todo.append(d)
         return False
 
+    def acts(self, kind):
+        return [(n, a) for n in self.nodes for a in n.acts if a[0] == kind]
+
 
 class _Stream:
     def __init__(self, g, name):
         self.g, self.name, self.last, self.waits = g, name, None, []
 
-    def launch(self, what):
-        node = _Node(what, ([self.last] if self.last else []) + self.waits)
+    def launch(self, *acts):
+        node = _Node(list(acts), ([self.last] if self.last else []) + self.waits)
         self.waits = []
         self.last = node
         self.g.nodes.append(node)
@@ -86,28 +91,34 @@ class _StreamCtx:
         self.g.cur = self.prev
 
 
+def _units(t, lo=0, n=None):
+    """(storage, frozenset of units) of elements [lo, lo + n) of the flat tensor t."""
+    n = t.numel() if n is None else n
+    first = t.storage_offset() + lo
+    assert first % UNIT == 0 and n % UNIT == 0
+    return t.untyped_storage().data_ptr(), frozenset(range(first // UNIT, (first + n) // UNIT))
+
+
 class _W4:
     def __init__(self, g, layer, kind, n):
         self.g, self.layer, self.kind = g, layer, kind
         self.rows, self.cols = n, 1
 
     def dequantize(self, out):
-        self.g.cur.launch(("write", _slot(out), (self.layer, self.kind)))
+        self.g.cur.launch(("write",) + _units(out) + ((self.layer, self.kind),))
         return out
 
 
 class _Packed:
     def __init__(self, layer, segments, numel):
         self.layer, self.segments, self.numel = layer, segments, numel
+        self.n_qblocks = numel // 64
 
 
-def _slot(t):
-    return t.untyped_storage().data_ptr()
-
-
-# a layer of 72 weights: q|k|v 16 at 0, o 8 at 16, gate|up 32 at 24, down 16 at 56
-_SIZES = {"qkv": (0, 16), "o": (16, 8), "gu": (24, 32), "d": (56, 16)}
+# a layer of 8 units: q|k|v 2 at 0, o 1 at 2, gate|up 3 at 3, down 2 at 6
+_SIZES = {"qkv": (0, 2 * UNIT), "o": (2 * UNIT, UNIT), "gu": (3 * UNIT, 3 * UNIT), "d": (6 * UNIT, 2 * UNIT)}
 _FIRST = {"q_proj": "qkv", "o_proj": "o", "gate_proj": "gu", "down_proj": "d"}
+_LAYER_UNITS = 8
 
 
 def _fake_stack(g, n_layers, ahead, where):
@@ -116,7 +127,7 @@ def _fake_stack(g, n_layers, ahead, where):
     st.s, st.keep_scale, st.probe = 2.0, 1.0, None
     st.code2 = st.nf4 = None
     segments = {name: (_SIZES[k][0], _SIZES[k][1], 1) for name, k in _FIRST.items()}
-    st.layers = [dict(packed=_Packed(i, segments, 72),
+    st.layers = [dict(packed=_Packed(i, segments, _LAYER_UNITS * UNIT),
                       **{k: _W4(g, i, k, n) for k, (_, n) in _SIZES.items()})
                  for i in range(n_layers)]
     st.lora = [dict(Aq=0, Av=0, Bq=0, Bv=0, mq=0, mv=0, bias=0) for _ in range(n_layers)]
@@ -131,12 +142,24 @@ def _fake_stack(g, n_layers, ahead, where):
     return st
 
 
+class _Side:
+    """What k_nf4.side_dequant describes: blocks [sb0, sb1) of a layer into a whole-layer slot."""
+
+    def __init__(self, layer, code2, nf4, out, sb0, sb1, wgs):
+        assert wgs == -1 or wgs > 0
+        self.act = ("write",) + _units(out, sb0 * UNIT, (sb1 - sb0) * UNIT) + ((layer.layer, "layer"),)
+
+
 def _gemm(g):
     def run(*args, **kwargs):
         w = next(a for a in args if isinstance(a, _W4))
         w16 = kwargs.get("w16")
         assert w16 is not None, "every GEMM reads a dequantised slot in these schedules"
-        g.cur.launch(("read", _slot(w16), (w.layer, w.kind), w16.storage_offset()))
+        side = kwargs.get("side")
+        acts = [("read",) + _units(w16) + ((w.layer, w.kind), w16.storage_offset())]
+        if side is not None:
+            acts.append(side.act)
+        g.cur.launch(*acts)
     return run
 
 
@@ -154,53 +177,75 @@ def model(monkeypatch):
     monkeypatch.setattr(stack_mod, "lora_grads_multi", lambda *a, **k: [(0, 0, 0), (0, 0, 0)])
 
     def dequant_layer(layer, code2, nf4, out):
-        g.cur.launch(("write", _slot(out), (layer.layer, "layer")))
+        g.cur.launch(("write",) + _units(out) + ((layer.layer, "layer"),))
     monkeypatch.setattr(k_nf4, "dequant_layer", dequant_layer)
+    monkeypatch.setattr(k_nf4, "side_dequant", _Side)
     return g
 
 
 def _check(g, n_layers, steps, whole_layer):
-    reads = [n for n in g.nodes if n.what[0] == "read"]
-    writes = [n for n in g.nodes if n.what[0] == "write"]
+    reads = g.acts("read")
+    writes = g.acts("write")
     assert len(reads) == steps * n_layers * 8
-    for r in reads:
-        _, slot, (layer, kind), offset = r.what
-        mine = [w for w in writes if w.what[1] == slot]
-        ordered = [w for w in mine if g.before(w, r)]
-        assert all(g.before(w, r) or g.before(r, w) for w in mine), f"dequant races a read of {kind}"
-        last = [w for w in ordered if not any(g.before(w, x) for x in ordered if x is not w)]
-        assert len(last) == 1
-        wl, wk = last[0].what[2]
-        assert wl == layer and wk == ("layer" if whole_layer else kind), \
-            f"layer {layer} {kind} read slot contents of layer {wl} {wk}"
+    for rn, (_, ptr, units, (layer, kind), offset) in reads:
+        for u in units:
+            mine = [(wn, w) for wn, w in writes if w[1] == ptr and u in w[2]]
+            assert all(wn is not rn for wn, _ in mine), f"a launch writes the unit its GEMM reads"
+            assert all(g.before(wn, rn) or g.before(rn, wn) for wn, _ in mine), \
+                f"a dequant races the read of layer {layer} {kind}"
+            ordered = [(wn, w) for wn, w in mine if g.before(wn, rn)]
+            last = [(wn, w) for wn, w in ordered
+                    if not any(g.before(wn, xn) for xn, _ in ordered if xn is not wn)]
+            assert len(last) == 1
+            wl, wk = last[0][1][3]
+            assert wl == layer and wk == ("layer" if whole_layer else kind), \
+                f"layer {layer} {kind} read unit {u} holding layer {wl} {wk}"
         if whole_layer:
-            assert offset == _SIZES[kind][0]
-    # no overwrite while in use: a write is ordered after every read of the previous contents
-    for w in writes:
-        for r in reads:
-            if r.what[1] == w.what[1] and not g.before(w, r) and \
-                    (r.what[2][0], "layer" if whole_layer else r.what[2][1]) != w.what[2]:
-                assert g.before(r, w), "a dequant overwrites a slot another GEMM still reads"
+            assert offset % (_LAYER_UNITS * UNIT) == _SIZES[kind][0]
 
 
-@pytest.mark.parametrize("ahead", ["layer", ("qkv", "o", "gu", "d")])
-@pytest.mark.parametrize("where", ["main", "side"])
+def _units_written(g):
+    return sum(len(w[2]) for _, w in g.acts("write"))
+
+
+@pytest.mark.parametrize("ahead,where", [("layer", "main"), ("layer", "side"),
+                                         (("qkv", "o", "gu", "d"), "main"),
+                                         (("qkv", "o", "gu", "d"), "side"),
+                                         ("carried", "main")])
 def test_dequant_ahead_schedule(model, ahead, where):
     n_layers, steps = 5, 3
     st = _fake_stack(model, n_layers, ahead, where)
     per_step = []
     for _ in range(steps):
-        before = sum(1 for n in model.nodes if n.what[0] == "write")
+        before = _units_written(model)
         st.step()
-        per_step.append(sum(1 for n in model.nodes if n.what[0] == "write") - before)
-    _check(model, n_layers, steps, ahead == "layer")
-    kinds = 1 if ahead == "layer" else 4
+        per_step.append((_units_written(model) - before) / _LAYER_UNITS)
+    _check(model, n_layers, steps, ahead in ("layer", "carried"))
     # the first step dequantises layer 0 on first use; every later step reuses the resident
     # last layer at the turn and layer 0 from the previous backward
-    assert per_step[0] == kinds * (2 * n_layers - 1)
-    assert per_step[1:] == [kinds * (2 * n_layers - 2)] * (steps - 1)
+    assert per_step[0] == 2 * n_layers - 1
+    assert per_step[1:] == [2 * n_layers - 2] * (steps - 1)
     if where == "side":
-        assert any(n.deps and any(d is not None for d in n.deps) for n in model.nodes)
+        assert any(len(n.deps) > 1 for n in model.nodes)
+
+
+def test_carried_dequant_rides_on_the_gemm_launches(model):
+    """ahead="carried": every launch in the carry table writes the other slot's blocks of the next
+    layer in step order; after the first step, the only dequant launches of their own are those of
+    the layers no launch carries (the forward's, with an empty forward table)."""
+    st = _fake_stack(model, 4, "carried", "main")
+    st.step()
+    first = len(model.nodes)
+    st.step()
+    later = model.nodes[first:]
+    alone = [n for n in later if not any(a[0] == "read" for a in n.acts)]
+    assert len(alone) == (0 if NF4LinearStack.CARRY["fwd"] else 3)
+    carriers = [n for n in later if len(n.acts) == 2]
+    n_fwd, n_bwd = len(NF4LinearStack.CARRY["fwd"]), len(NF4LinearStack.CARRY["bwd"])
+    assert len(carriers) == 3 * n_fwd + 3 * n_bwd    # layers 0-2 forward, 3-1 backward
+    for n in carriers:
+        (_, rptr, _, (layer, _), _), (_, wptr, _, (wl, _)) = n.acts
+        assert rptr != wptr and abs(wl - layer) == 1
 
 
 def test_model_catches_a_missing_wait(model, monkeypatch):
@@ -209,6 +254,16 @@ def test_model_catches_a_missing_wait(model, monkeypatch):
     monkeypatch.setattr(DequantAhead, "take",
                         lambda self, kind, key: self.buf[kind][:self.numel[kind]])
     st = _fake_stack(model, 3, "layer", "side")
+    st.step()
+    with pytest.raises(AssertionError):
+        _check(model, 3, 1, True)
+
+
+def test_model_catches_a_carry_into_the_slot_in_use(model, monkeypatch):
+    """A planted mistake: carrying the next layer into the slot being read (one slot instead of
+    two alternating ones) is caught."""
+    st = _fake_stack(model, 3, "carried", "main")
+    st.slots[1] = st.slots[0]
     st.step()
     with pytest.raises(AssertionError):
         _check(model, 3, 1, True)
