@@ -18,10 +18,10 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
     const float* __restrict__ scale2, const float* __restrict__ offset2,
     const float* __restrict__ code2, const float* __restrict__ nf4, u32x4* __restrict__ out,
     int64_t n_quads) {
-  __shared__ f32x2 pairs[256];
+  __shared__ float lut[16];
   // per wave: 64 lanes x 4 chunks of 16 bytes, one pad chunk per 64 against bank conflicts
   __shared__ u32x4 stage[kDqThreads / 64][64 * 4 + 4];
-  dk_fill_pairs(pairs, nf4, threadIdx.x);
+  dk_fill_lut(lut, nf4, threadIdx.x);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t first = (int64_t)blockIdx.x * kDqQuadsPerBlock;
   const int64_t sb = first >> 9;                    // 512 quads per second-level block
@@ -30,11 +30,11 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
   const int64_t tc = t < n_quads ? t : n_quads - 1;   // clamped: its result is not stored
   const u32x4 w = __builtin_nontemporal_load(packed + tc);
   const float amax = dk_absmax(code2[qabs[tc >> 1]], s2, o2);
-  __syncthreads();   // pairs
+  __syncthreads();   // lut
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = lane * 4 + j;
-    stage[wave][idx + (idx >> 6)] = dk_dequant_word(w[j], amax, pairs);
+    stage[wave][idx + (idx >> 6)] = dk_dequant_word(w[j], amax, lut);
   }
   __syncthreads();
   const int64_t chunk0 = (first + wave * 64) * 4;     // first 8-weight chunk of this wave
