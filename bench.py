@@ -129,6 +129,65 @@ def kernel_table(torch, st, reps, only=None):
     return out
 
 
+def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None):
+    """The kernels on either side of the LoRA'd q/v linear (RMSNorm + dropout forward, its
+    backward with the LoRA input grads, the QKV epilogue forward and backward), each in isolation
+    at config 4's shapes (M tokens, hidden 1536, 12 query / 2 KV heads of 128), with their
+    algorithmic HBM bytes.  They are not part of the linear stack's step."""
+    from decentrik_prime_amd import k_norm, k_rope
+    dev = "cuda"
+    g = torch.Generator(device=dev)
+    g.manual_seed(7)
+    f16, f32 = torch.float16, torch.float32
+    x = torch.randn(m, d, device=dev, generator=g)
+    delta = torch.randn(m, d, device=dev, generator=g).half()
+    w = torch.rand(d, device=dev, generator=g) + 0.5
+    mq = (torch.rand(m, d, device=dev, generator=g) >= 0.05).to(torch.uint8)
+    mv = (torch.rand(m, d, device=dev, generator=g) >= 0.05).to(torch.uint8)
+    y, xq, xv = (torch.empty(m, d, dtype=f16, device=dev) for _ in range(3))
+    xout, out = torch.empty(m, d, device=dev), torch.empty(m, d, device=dev)
+    rstd = torch.empty(m, device=dev)
+    dy16, lq, lv = (torch.randn(m, d, device=dev, generator=g).half() for _ in range(3))
+    out16 = torch.empty(m, d, dtype=f16, device=dev)
+    gs = torch.ones(1, device=dev)
+    row = (nq + 2 * nkv) * hd
+    qkv = torch.randn(m, row, device=dev, generator=g).half()
+    lqq = torch.randn(m, nq * hd, device=dev, generator=g).half()
+    lvv = torch.randn(m, nkv * hd, device=dev, generator=g).half()
+    pos = torch.randint(0, 4096, (m,), device=dev, dtype=torch.int32, generator=g)
+    ang = torch.arange(4096, device=dev, dtype=f32)[:, None] * (
+        1.0 / (1e6 ** (torch.arange(0, hd, 2, device=dev, dtype=f32) / hd)))[None, :]
+    cos, sin = torch.cat((ang, ang), 1).cos().contiguous(), torch.cat((ang, ang), 1).sin().contiguous()
+    gin = nq // nkv
+    dq = torch.randn(m, nq * hd, device=dev, generator=g)
+    dk, dv = (torch.randn(m, nkv * gin * hd, device=dev, generator=g) for _ in range(2))
+    qkv_out = torch.empty(m, row, dtype=f16, device=dev)
+    e = m * d
+    rows = [
+        ("rms_fwd norm+dropout", lambda: k_norm.rms_forward(
+            x, w, y, rstd, 1e-6, delta=delta, xout=xout, xq=xq, xv=xv, mq=mq, mv=mv,
+            keep_scale=1 / 0.95), e * (4 + 2 + 1 + 1 + 4 + 2 + 2 + 2) + m * 4),
+        ("rms_bwd norm+lora grads", lambda: k_norm.rms_backward(
+            dy16, gs, x, w, rstd, out, dres=out, lq=lq, lv=lv, mq=mq, mv=mv, keep_scale=1 / 0.95,
+            out16=out16, delta=delta), e * (2 + 4 + 2 + 2 + 2 + 1 + 1 + 4 + 4 + 2) + m * 4),
+        ("qkv_epilogue_fwd lora+rope", lambda: k_rope.qkv_epilogue_forward(
+            qkv, lqq, lvv, pos, cos, sin, 2.0, nq, nkv, hd),
+         m * (row * 2 * 2 + (nq + nkv) * hd * 2 + hd * 4)),
+        ("qkv_epilogue_bwd rope^T+gqa", lambda: k_rope.qkv_epilogue_backward(
+            dq, dk, dv, pos, cos, sin, qkv_out, nq, nkv, hd, gin),
+         m * (nq * hd * 4 + 2 * nkv * gin * hd * 4 + row * 2 + hd * 4)),
+    ]
+    res = []
+    for name, fn, nbytes in rows:
+        if only is not None and name not in only:
+            continue
+        ms = time_op(torch, fn, reps)
+        gbps = nbytes / (ms * 1e-3) / 1e9
+        res.append({"kernel": name, "avg_us": round(ms * 1e3, 2), "bytes": int(nbytes),
+                    "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)})
+    return res
+
+
 def dequant_bandwidth(torch, st, reps):
     """NF4 dequant of every layer into its own fp16 output (the working set, 3.30 GB of
     algorithmic traffic for 28 layers, does not fit the 256 MB Infinity Cache)."""
@@ -390,7 +449,8 @@ def main():
     torch.cuda.synchronize()
     if args.kernels_only:
         only = set(args.op.split(",")) if args.op else None
-        res = {"kernels": kernel_table(torch, st, args.reps, only)}
+        res = {"kernels": kernel_table(torch, st, args.reps, only),
+               "neighbours": neighbour_table(torch, args.reps, args.m, only=only)}
         if only is None or "dequant" in only:
             res["dequant"] = dequant_bandwidth(torch, st, args.reps)
         res["copy"] = copy_calibration(torch, args.reps)
@@ -461,6 +521,9 @@ def main():
                                                 "frac": dq["frac_hbm_peak"],
                                                 "traffic": dq_traffic["bytes"] if dq_traffic else None}}
         result["kernels"] = kernels
+        result["neighbours"] = neighbour_table(torch, args.reps, args.m)
+        print("[bench] " + ", ".join(f"{r['kernel']} {r['avg_us']} us {r['gbps']} GB/s"
+                                     for r in result["neighbours"]), file=sys.stderr, flush=True)
     if not args.no_cpu:
         print(f"[bench] CPU baseline (oracle, {args.cpu_layers} layers)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_layers, args.m)

@@ -78,6 +78,50 @@ int dk_swiglu_bwd(const void* grad, const void* gate, const void* up, void* dgat
                   int64_t n, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
+ * The producer and the consumer around the LoRA'd q/v linear.
+ *
+ * Fused residual add + RMSNorm + the two LoRA dropout inputs, one token row of d (4 <= d <= 4096,
+ * d % 4 == 0) per wave.  Replaces rms_fwd_kernel / rms_forward (solution/k_norm.py:29-58,
+ * 114-131): h = x [+ fp32(delta)] (xout = h if given), rstd = rsqrt(mean(h^2) + eps),
+ * y = w * (h * rstd), y16 = fp16(y) (if y), xq/xv = fp16(keep ? y * keep_scale : 0) (if xq and
+ * xv, which need the uint8 keep-masks mq/mv).  x, xout, w fp32 (16-byte aligned); delta, y, xq,
+ * xv fp16 [n_rows, d] (8-byte aligned); rstd fp32 [n_rows]; NULL leaves an output unwritten. */
+int dk_rms_fwd(const float* x, const void* delta, float* xout, const float* w, void* y,
+               float* rstd, void* xq, void* xv, const uint8_t* mq, const uint8_t* mv,
+               int64_t n_rows, int64_t d, float eps, float keep_scale, hipStream_t stream);
+
+/* RMSNorm backward with the LoRA-A input gradients.  Replaces rms_bwd_kernel / rms_backward
+ * (solution/k_norm.py:61-88, 134-150): dy = fp32(dy16) * gscale[0]
+ * [+ (mq ? fp32(lq) * keep_scale : 0) + (mv ? fp32(lv) * keep_scale : 0)], h = x [+ delta],
+ * xh = h * rstd, g = dy * w, dx = (g - xh * mean(g * xh)) * rstd [+ dres]; out fp32 (may alias
+ * dres), out16 = fp16(dx) if given.  gscale is a device pointer to one fp32. */
+int dk_rms_bwd(const void* dy16, const float* gscale, const float* x, const void* delta,
+               const float* w, const float* rstd, const float* dres, float* out, const void* lq,
+               const void* lv, void* out16, const uint8_t* mq, const uint8_t* mv, int64_t n_rows,
+               int64_t d, float keep_scale, hipStream_t stream);
+
+/* QKV epilogue, forward, in place on the fused [n_rows, (nq + 2 nkv) hd] fp16 QKV buffer.
+ * Replaces qkv_epilogue_fwd_kernel / qkv_epilogue_forward (solution/k_rope.py:23-61, 107-111):
+ * q += lora_scale * lq, v += lora_scale * lv (fp32), then q and k heads rotated by
+ * [x1 c - x2 s | x2 c + x1 s] with c, s = cos/sin_table[pos[row] * hd + j], j < hd / 2; every
+ * product and sum rounded to fp32 on its own, the result once to fp16.  lq [n_rows, nq hd], lv
+ * [n_rows, nkv hd] fp16; pos int32 [n_rows]; tables fp32 [positions, hd] (16-byte aligned);
+ * hd % 8 == 0. */
+int dk_qkv_epilogue_fwd(void* qkv, const void* lq, const void* lv, const int32_t* pos,
+                        const float* cos_table, const float* sin_table, int64_t n_rows,
+                        float lora_scale, int nq, int nkv, int hd, hipStream_t stream);
+
+/* QKV epilogue, backward.  Replaces qkv_epilogue_bwd_kernel / qkv_epilogue_backward
+ * (solution/k_rope.py:64-104, 114-119): out [n_rows, (nq + 2 nkv) hd] fp16 = [rot^T(dq) |
+ * rot^T(sum of the gin partials of each KV head of dk) | sum of the gin partials of dv], with
+ * rot^T: [d1 c + d2 s | d2 c - d1 s].  dq [n_rows, nq hd], dk/dv [n_rows, nkv gin hd], fp32
+ * (grads_f32 != 0, 16-byte aligned) or fp16. */
+int dk_qkv_epilogue_bwd(const void* dq, const void* dk, const void* dv, int grads_f32,
+                        const int32_t* pos, const float* cos_table, const float* sin_table,
+                        void* out, int64_t n_rows, int nq, int nkv, int hd, int gin,
+                        hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
  * LoRA down projection with the dropout of its input.  Replaces the norm kernel's dropout lines
  * and the lora_A GEMM (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944):
  *   Xd = fp16(mask ? fp32(x) * keep_scale : 0),   z = fp16(Xd A^T)

@@ -108,6 +108,57 @@ def test_argument_errors_come_back_before_launch():
         _lib.check(_lib.DK_ERR_INVALID, "probe")
 
 
+def test_norm_and_rope_argument_errors_come_back_before_launch():
+    lib = _lib.lib()
+    p16, p8, p4 = ctypes.c_void_p(16), ctypes.c_void_p(8), ctypes.c_void_p(4)
+    # RMSNorm: d range and multiple of 4, required pointers, masks with the dropout outputs
+    assert lib.dk_rms_fwd(p16, None, None, p16, p16, p16, None, None, None, None, 4, 1538, 1e-6, 1.0,
+                          None) == _lib.DK_ERR_INVALID
+    assert lib.dk_rms_fwd(p16, None, None, p16, p16, p16, None, None, None, None, 4, 8192, 1e-6, 1.0,
+                          None) == _lib.DK_ERR_INVALID
+    assert lib.dk_rms_fwd(None, None, None, p16, p16, p16, None, None, None, None, 4, 1536, 1e-6, 1.0,
+                          None) == _lib.DK_ERR_INVALID
+    assert lib.dk_rms_fwd(p16, None, None, p16, p16, p16, p16, p16, None, None, 4, 1536, 1e-6, 1.0,
+                          None) == _lib.DK_ERR_INVALID                 # dropout without masks
+    assert lib.dk_rms_fwd(p8, None, None, p16, p16, p16, None, None, None, None, 4, 1536, 1e-6, 1.0,
+                          None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_rms_bwd(p16, None, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
+                          1536, 1.0, None) == _lib.DK_ERR_INVALID        # no gscale
+    assert lib.dk_rms_bwd(p16, p16, p16, None, p16, p16, None, p16, p16, None, None, p16, p16, 4, 1536,
+                          1.0, None) == _lib.DK_ERR_INVALID              # lq without lv
+    assert lib.dk_rms_bwd(p4, p16, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
+                          1536, 1.0, None) == _lib.DK_ERR_ALIGN          # dy16 needs 8 bytes
+    assert lib.dk_rms_fwd(p16, None, None, p16, p16, p16, None, None, None, None, 0, 1536, 1e-6, 1.0,
+                          None) == 0                                     # zero rows
+    # QKV epilogue: head size, GQA partial count, tables aligned
+    assert lib.dk_qkv_epilogue_fwd(p16, p16, p16, p16, p16, p16, 4, 2.0, 12, 2, 100,
+                                   None) == _lib.DK_ERR_INVALID         # hd % 8
+    assert lib.dk_qkv_epilogue_fwd(p16, p16, p16, p16, p8, p16, 4, 2.0, 12, 2, 128,
+                                   None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_qkv_epilogue_bwd(p16, p16, p16, 1, p16, p16, p16, p16, 4, 12, 2, 128, 0,
+                                   None) == _lib.DK_ERR_INVALID         # gin >= 1
+    assert lib.dk_qkv_epilogue_bwd(p8, p16, p16, 1, p16, p16, p16, p16, 4, 12, 2, 128, 6,
+                                   None) == _lib.DK_ERR_ALIGN           # fp32 grads: 16 bytes
+    assert lib.dk_qkv_epilogue_bwd(p8, p8, p8, 0, p16, p16, p16, p16, 0, 12, 2, 128, 1, None) == 0
+
+
+def test_norm_and_rope_mirrors_check_arguments():
+    from decentrik_prime_amd import k_norm, k_rope
+    x = torch.zeros(4, 1536)
+    w = torch.zeros(1536)
+    with pytest.raises(ValueError):
+        k_norm.rms_forward(x, w, None, torch.zeros(4), 1e-6, xq=torch.zeros(4, 1536).half())
+    with pytest.raises(ValueError):
+        k_norm.rms_forward(x, w, None, torch.zeros(4), 1e-6)     # CPU tensors
+    with pytest.raises(ValueError):
+        k_norm.rms_backward(x.half(), torch.ones(1), x, w, torch.zeros(4), x, lq=x.half())
+    with pytest.raises(ValueError):
+        k_rope.qkv_epilogue_forward(torch.zeros(4, 2048).half(), torch.zeros(4, 1536).half(),
+                                    torch.zeros(4, 256).half(), torch.zeros(4, dtype=torch.int32),
+                                    torch.zeros(8, 128), torch.zeros(8, 128), 2.0, 12, 2, 128)
+    assert k_norm.warmup_specs(1536) == [] and k_rope.warmup_specs(12, 2, 128, 6, None) == []
+
+
 def test_zero_rows_is_a_no_op():
     lib = _lib.lib()
     assert lib.dk_gated_silu_fwd(ctypes.c_void_p(16), ctypes.c_void_p(16), 0, 64, None) == 0
