@@ -4,16 +4,19 @@
 // partial sums).  Replace solution/k_norm.py:29-88 and solution/k_rope.py:23-104.
 //
 // Both are HBM-bound row kernels: one wave per token row, 64 lanes over the row in 16-byte
-// vectors, four rows per 256-thread workgroup.  Every product and sum is rounded to fp32 on its
-// own (-ffp-contract=off), as the reference's kernels (compiled with fp fusion off for the QKV
-// epilogue) round; the row sums are a lane-order sum followed by a butterfly across the wave, a
-// different order from the reference's tree, within the reference tests' tolerances.
+// vectors, four rows per 256-thread workgroup; all of a row's loads are issued before its first
+// use.  Every product and sum is rounded to fp32 on its own (-ffp-contract=off), as the
+// reference's kernels (compiled with fp fusion off for the QKV epilogue) round; the row sums are
+// a lane-order sum followed by a butterfly across the wave, a different order from the
+// reference's tree, within the reference tests' tolerances.
 #include "dk_common.h"
 
 namespace {
 
 constexpr int kRowThreads = 256;
 constexpr int kRowsPerBlock = kRowThreads / 64;
+constexpr int kBatch = 4;     // QKV epilogue tasks per lane whose loads are in flight together
+constexpr int kGinBatch = 6;  // GQA partials per KV head whose loads are in flight together
 
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll
@@ -49,13 +52,20 @@ __global__ __launch_bounds__(kRowThreads) void rms_fwd_kernel(
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= n_rows) return;
   const int64_t off = row * d;
-  f32x4 h[KMAX];
+  // every load of the row is issued before the reduction, so the row costs one memory latency
+  f32x4 h[KMAX], wv[KMAX];
+  uint32_t kq[KMAX], kv[KMAX];
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int e = 256 * k + 4 * lane;
     if (e < d) {
       h[k] = *reinterpret_cast<const f32x4*>(x + off + e);
+      wv[k] = *reinterpret_cast<const f32x4*>(w + e);
+      if (xq) {
+        kq[k] = load_mask4(mq + off + e);
+        kv[k] = load_mask4(mv + off + e);
+      }
       if (delta) {
         const f32x4 dl = load_h4(delta + off + e);
 #pragma unroll
@@ -73,19 +83,17 @@ __global__ __launch_bounds__(kRowThreads) void rms_fwd_kernel(
   for (int k = 0; k < KMAX; ++k) {
     const int e = 256 * k + 4 * lane;
     if (e >= d) continue;
-    const f32x4 wv = *reinterpret_cast<const f32x4*>(w + e);
     f32x4 yv;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) yv[i] = __fmul_rn(wv[i], __fmul_rn(h[k][i], r));
+    for (int i = 0; i < 4; ++i) yv[i] = __fmul_rn(wv[k][i], __fmul_rn(h[k][i], r));
     if (y) store_h4(y + off + e, yv);
     if (xq) {
-      const uint32_t kq = load_mask4(mq + off + e), kv = load_mask4(mv + off + e);
       f32x4 a, b;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
         const float ys = __fmul_rn(yv[i], keep_scale);
-        a[i] = kept(kq, i) ? ys : 0.0f;
-        b[i] = kept(kv, i) ? ys : 0.0f;
+        a[i] = kept(kq[k], i) ? ys : 0.0f;
+        b[i] = kept(kv[k], i) ? ys : 0.0f;
       }
       store_h4(xq + off + e, a);
       store_h4(xv + off + e, b);
@@ -108,7 +116,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
   const int64_t off = row * d;
   const float gs = *gscale;
   const float r = rstd[row];
-  f32x4 g[KMAX], xh[KMAX];
+  f32x4 g[KMAX], xh[KMAX], rv[KMAX];
   float cs = 0.0f;
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
@@ -133,6 +141,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
       for (int i = 0; i < 4; ++i) xv[i] = __fadd_rn(xv[i], dl[i]);
     }
     const f32x4 wv = *reinterpret_cast<const f32x4*>(w + e);
+    if (dres) rv[k] = *reinterpret_cast<const f32x4*>(dres + off + e);   // before the reduction
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       xh[k][i] = __fmul_rn(xv[i], r);
@@ -149,9 +158,8 @@ __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
 #pragma unroll
     for (int i = 0; i < 4; ++i) dx[i] = __fmul_rn(__fsub_rn(g[k][i], __fmul_rn(xh[k][i], c)), r);
     if (dres) {
-      const f32x4 rv = *reinterpret_cast<const f32x4*>(dres + off + e);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) dx[i] = __fadd_rn(dx[i], rv[i]);
+      for (int i = 0; i < 4; ++i) dx[i] = __fadd_rn(dx[i], rv[k][i]);
     }
     *reinterpret_cast<f32x4*>(out + off + e) = dx;
     if (out16) store_h4(out16 + off + e, dx);
@@ -176,38 +184,69 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_fwd_kernel(
   f16* base = qkv + row * (int64_t)(nq + 2 * nkv) * hd;
   const f16* lqr = lq + row * (int64_t)nq * hd;
   const f16* lvr = lv + row * (int64_t)nkv * hd;
-  // query heads (LoRA add, rotate) and key heads (rotate)
-  for (int t = lane; t < (nq + nkv) * quads; t += 64) {
-    const int head = t / quads, j = 4 * (t % quads);
-    f16* h1 = base + head * hd + j;
-    f32x4 x1 = load_h4(h1), x2 = load_h4(h1 + half);
-    if (head < nq) {
-      const f32x4 a = load_h4(lqr + head * hd + j), b = load_h4(lqr + head * hd + j + half);
+  // query heads (LoRA add, rotate) and key heads (rotate): a lane's tasks t = lane + 64 i in
+  // batches of kBatch, all loads of a batch issued before the first is used
+  const int tasks = (nq + nkv) * quads;
+  for (int t0 = 0; t0 < tasks; t0 += 64 * kBatch) {
+    f32x4 x1[kBatch], x2[kBatch], a[kBatch], b[kBatch], c[kBatch], s[kBatch];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        x1[i] = __fadd_rn(x1[i], __fmul_rn(a[i], scale));
-        x2[i] = __fadd_rn(x2[i], __fmul_rn(b[i], scale));
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= tasks) continue;
+      const int head = t / quads, j = 4 * (t % quads);
+      const f16* h1 = base + head * hd + j;
+      x1[u] = load_h4(h1);
+      x2[u] = load_h4(h1 + half);
+      c[u] = *reinterpret_cast<const f32x4*>(cr + j);
+      s[u] = *reinterpret_cast<const f32x4*>(sr + j);
+      if (head < nq) {
+        a[u] = load_h4(lqr + head * hd + j);
+        b[u] = load_h4(lqr + head * hd + j + half);
       }
     }
-    const f32x4 c = *reinterpret_cast<const f32x4*>(cr + j);
-    const f32x4 s = *reinterpret_cast<const f32x4*>(sr + j);
-    f32x4 o1, o2;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      o1[i] = __fsub_rn(__fmul_rn(x1[i], c[i]), __fmul_rn(x2[i], s[i]));
-      o2[i] = __fadd_rn(__fmul_rn(x2[i], c[i]), __fmul_rn(x1[i], s[i]));
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= tasks) continue;
+      const int head = t / quads, j = 4 * (t % quads);
+      if (head < nq) {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          x1[u][i] = __fadd_rn(x1[u][i], __fmul_rn(a[u][i], scale));
+          x2[u][i] = __fadd_rn(x2[u][i], __fmul_rn(b[u][i], scale));
+        }
+      }
+      f32x4 o1, o2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o1[i] = __fsub_rn(__fmul_rn(x1[u][i], c[u][i]), __fmul_rn(x2[u][i], s[u][i]));
+        o2[i] = __fadd_rn(__fmul_rn(x2[u][i], c[u][i]), __fmul_rn(x1[u][i], s[u][i]));
+      }
+      f16* h1 = base + head * hd + j;
+      store_h4(h1, o1);
+      store_h4(h1 + half, o2);
     }
-    store_h4(h1, o1);
-    store_h4(h1 + half, o2);
   }
   // value heads: LoRA add
   f16* vb = base + (int64_t)(nq + nkv) * hd;
-  for (int t = lane; t < nkv * hd / 4; t += 64) {
-    f32x4 v = load_h4(vb + 4 * t);
-    const f32x4 a = load_h4(lvr + 4 * t);
+  const int vtasks = nkv * hd / 4;
+  for (int t0 = 0; t0 < vtasks; t0 += 64 * kBatch) {
+    f32x4 v[kBatch], a[kBatch];
 #pragma unroll
-    for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], __fmul_rn(a[i], scale));
-    store_h4(vb + 4 * t, v);
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= vtasks) continue;
+      v[u] = load_h4(vb + 4 * t);
+      a[u] = load_h4(lvr + 4 * t);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= vtasks) continue;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[u][i] = __fadd_rn(v[u][i], __fmul_rn(a[u][i], scale));
+      store_h4(vb + 4 * t, v[u]);
+    }
   }
 }
 
@@ -238,45 +277,86 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_bwd_kernel(
   const T* dqr = dq + row * (int64_t)nq * hd;
   const T* dkr = dk + row * (int64_t)nkv * gin * hd;
   const T* dvr = dv + row * (int64_t)nkv * gin * hd;
-  for (int t = lane; t < (nq + nkv) * quads; t += 64) {
-    const int head = t / quads, j = 4 * (t % quads);
-    f32x4 d1, d2;
-    if (head < nq) {
-      d1 = load4(dqr + head * hd + j);
-      d2 = load4(dqr + head * hd + j + half);
-    } else {
-      const int hk = head - nq;
-      d1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-      d2 = d1;
-      for (int gi = 0; gi < gin; ++gi) {
-        const T* part = dkr + (int64_t)(hk * gin + gi) * hd + j;
-        const f32x4 a = load4(part), b = load4(part + half);
+  // query heads: batches of kBatch tasks, all loads first
+  const int qtasks = nq * quads;
+  for (int t0 = 0; t0 < qtasks; t0 += 64 * kBatch) {
+    f32x4 d1[kBatch], d2[kBatch], c[kBatch], s[kBatch];
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= qtasks) continue;
+      const int head = t / quads, j = 4 * (t % quads);
+      d1[u] = load4(dqr + head * hd + j);
+      d2[u] = load4(dqr + head * hd + j + half);
+      c[u] = *reinterpret_cast<const f32x4*>(cr + j);
+      s[u] = *reinterpret_cast<const f32x4*>(sr + j);
+    }
+#pragma unroll
+    for (int u = 0; u < kBatch; ++u) {
+      const int t = t0 + 64 * u + lane;
+      if (t >= qtasks) continue;
+      const int head = t / quads, j = 4 * (t % quads);
+      f32x4 o1, o2;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) {
+        o1[i] = __fadd_rn(__fmul_rn(d1[u][i], c[u][i]), __fmul_rn(d2[u][i], s[u][i]));
+        o2[i] = __fsub_rn(__fmul_rn(d2[u][i], c[u][i]), __fmul_rn(d1[u][i], s[u][i]));
+      }
+      store_h4(dst + head * hd + j, o1);
+      store_h4(dst + head * hd + j + half, o2);
+    }
+  }
+  // key heads: the gin partials summed in order (up to kGinBatch partials' loads in flight), then
+  // the transposed rotation; value heads: the partials summed
+  const int ktasks = nkv * quads;
+  for (int t = lane; t < ktasks; t += 64) {
+    const int hk = t / quads, j = 4 * (t % quads);
+    const f32x4 c = *reinterpret_cast<const f32x4*>(cr + j);
+    const f32x4 s = *reinterpret_cast<const f32x4*>(sr + j);
+    f32x4 d1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, d2 = d1;
+    for (int g0 = 0; g0 < gin; g0 += kGinBatch) {
+      f32x4 pa[kGinBatch], pb[kGinBatch];
+#pragma unroll
+      for (int u = 0; u < kGinBatch; ++u) {
+        if (g0 + u >= gin) continue;
+        const T* part = dkr + (int64_t)(hk * gin + g0 + u) * hd + j;
+        pa[u] = load4(part);
+        pb[u] = load4(part + half);
+      }
+#pragma unroll
+      for (int u = 0; u < kGinBatch; ++u) {
+        if (g0 + u >= gin) continue;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          d1[i] = __fadd_rn(d1[i], a[i]);
-          d2[i] = __fadd_rn(d2[i], b[i]);
+          d1[i] = __fadd_rn(d1[i], pa[u][i]);
+          d2[i] = __fadd_rn(d2[i], pb[u][i]);
         }
       }
     }
-    const f32x4 c = *reinterpret_cast<const f32x4*>(cr + j);
-    const f32x4 s = *reinterpret_cast<const f32x4*>(sr + j);
     f32x4 o1, o2;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       o1[i] = __fadd_rn(__fmul_rn(d1[i], c[i]), __fmul_rn(d2[i], s[i]));
       o2[i] = __fsub_rn(__fmul_rn(d2[i], c[i]), __fmul_rn(d1[i], s[i]));
     }
-    store_h4(dst + head * hd + j, o1);
-    store_h4(dst + head * hd + j + half, o2);
+    store_h4(dst + (nq + hk) * hd + j, o1);
+    store_h4(dst + (nq + hk) * hd + j + half, o2);
   }
   f16* vdst = dst + (int64_t)(nq + nkv) * hd;
   for (int t = lane; t < nkv * hd / 4; t += 64) {
     const int hk = (4 * t) / hd, e = (4 * t) % hd;
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    for (int gi = 0; gi < gin; ++gi) {
-      const f32x4 a = load4(dvr + (int64_t)(hk * gin + gi) * hd + e);
+    for (int g0 = 0; g0 < gin; g0 += kGinBatch) {
+      f32x4 pa[kGinBatch];
 #pragma unroll
-      for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], a[i]);
+      for (int u = 0; u < kGinBatch; ++u)
+        if (g0 + u < gin) pa[u] = load4(dvr + (int64_t)(hk * gin + g0 + u) * hd + e);
+#pragma unroll
+      for (int u = 0; u < kGinBatch; ++u) {
+        if (g0 + u >= gin) continue;
+#pragma unroll
+        for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], pa[u][i]);
+      }
     }
     store_h4(vdst + 4 * t, acc);
   }
