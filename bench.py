@@ -82,7 +82,17 @@ def kernel_table(torch, st, reps, only=None):
             dy["qkv"], L["qkv"], [(dzq, lo["Aq"], lo["mq"], ks), (dzv, lo["Av"], lo["mv"], ks)],
             out=st.dx_qkv, w16=w16), g(m, D, QKV) + 2 * g(m, D, r)),
     ]
-    rows = []
+    # the fused QKV projection with the rotary epilogue (the QKV epilogue's forward folded in; not
+    # part of the linear stack's step): compare with h16_linear_fwd qkv+lora + qkv_epilogue_fwd
+    rot = torch.arange(4096, device=x.device, dtype=torch.float32)[:, None] * (
+        1.0 / (1e6 ** (torch.arange(0, 128, 2, device=x.device, dtype=torch.float32) / 128)))[None, :]
+    rcos = torch.cat((rot, rot), 1).cos().contiguous()
+    rsin = torch.cat((rot, rot), 1).sin().contiguous()
+    rpos = (torch.arange(m, device=x.device, dtype=torch.int32) % 4096).contiguous()
+    rope_row = ("h16_linear_fwd qkv+lora+rope", lambda: W.linear_forward_rope(
+        x, L["qkv"], lo["bias"], st.qkv_terms(0), rpos, rcos, rsin, D + KV, out=o["qkv"],
+        w16=h["qkv"]), g(m, QKV, D) + g(m, D, r) + g(m, KV, r), None, 0)
+    rows = [rope_row]
     for kind, suffix, fn, flops in gemms:
         # both forms; the one the step runs counts once per layer, the other is reported only
         used = "h16" if kind in st.ahead else "w4"

@@ -62,6 +62,12 @@ class SideDequantC(ctypes.Structure):
 
 _S = ctypes.POINTER(SideDequantC)
 
+
+class RopeC(ctypes.Structure):
+    """struct dk_rope."""
+    _fields_ = [("pos", _c_p), ("cos_table", _c_p), ("sin_table", _c_p), ("hd", ctypes.c_int32),
+                ("cols", _i64)]
+
 # name -> (restype, argtypes)
 SIGNATURES = {
     "dk_error_string": (ctypes.c_char_p, [_int]),
@@ -85,6 +91,8 @@ SIGNATURES = {
     "dk_h16_workspace": (_i64, [_i64, _i64, _i64, _int]),
     "dk_h16_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
                                       _c_p, _i64, _c_p, _i64, _S, _c_p]),
+    "dk_h16_linear_fwd_rope": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
+                                      ctypes.POINTER(RopeC), _c_p, _i64, _S, _c_p]),
     "dk_h16_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64, _c_p,
                                          _i64, _int, _c_p, _i64, _S, _c_p]),
     "dk_h16_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64,

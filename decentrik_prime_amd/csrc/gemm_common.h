@@ -43,6 +43,13 @@ struct GemmParams {
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
   SideDequant side;     // dequant work carried by the launch's last side.wgs workgroups
+  // LINEAR NT only: rotary embedding of output columns [0, rope_cols) (the q and k heads of a
+  // fused QKV projection) in the epilogue, before the single fp16 rounding; null: none
+  const int32_t* rope_pos;   // [M] token positions
+  const float* rope_cos;     // [positions][rope_hd]
+  const float* rope_sin;
+  int rope_hd;               // head size: two 64-column wave blocks
+  int64_t rope_cols;
 };
 
 // Runs the GEMM of `p` (fp16 weight p.w16) on the 256 x 256-tile kernel when the shape suits it:

@@ -95,7 +95,8 @@ __device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
 // global traffic (and the gate/up reads of the SwiGLU backward) moves in whole 16-byte pieces.
 template <bool TRANS, int EPI, int TM, int TN>
 __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
-                                              int64_t mw0, int64_t nw0, uint8_t* escr) {
+                                              int64_t mw0, int64_t nw0, uint8_t* escr,
+                                              const uint8_t* pscr) {
   constexpr int COLS = 32 * TN;          // columns of a strip
   constexpr int SLD = COLS + 8;          // floats per staged row: the two half-waves' rows
                                          // (4 apart) land 32 banks apart
@@ -120,11 +121,12 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
 #pragma unroll
     for (int v = 0; v < 16; ++v) stage[(8 * (v >> 2) + rsub + (v & 3)) * SLD + 32 * j + lrow] = r[v];
   };
-  auto staged8 = [&](int row, int col) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(stage + row * SLD + col);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(stage + row * SLD + col + 4);
+  auto staged8_of = [&](const float* st, int row, int col) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * SLD + col);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(st + row * SLD + col + 4);
     return f32x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   };
+  auto staged8 = [&](int row, int col) { return staged8_of(stage, row, col); };
 
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
@@ -224,7 +226,11 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
           }
         }
       }
-      if (p.out_mode == DK_OUT_F16) {
+      // rotary embedding (solution/k_rope.py:23-61): this wave's 64 columns are one half of a
+      // head, the partner wave (whose scratch is pscr) holds the other half of the same rows;
+      // the pair is rotated in fp32 from the staged values, then rounded once
+      const bool rope = !TRANS && p.rope_pos != nullptr && nw0 < p.rope_cols;
+      if (p.out_mode == DK_OUT_F16 && !rope) {
 #pragma unroll
         for (int j = 0; j < TN; ++j)
 #pragma unroll
@@ -234,17 +240,34 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
 #pragma unroll
       for (int j = 0; j < TN; ++j) stage_block(j, res[j]);
       __builtin_amdgcn_wave_barrier();
+      if (!TRANS && p.rope_pos) __syncthreads();   // every wave's strip is staged
 #pragma unroll
       for (int q = 0; q < 32 / ROWS_PER_PASS; ++q) {
         const int row = srow + q * ROWS_PER_PASS;
         const int64_t m = mrow0 + row;
         if (m >= M) continue;
-        const f32x8_t r = staged8(row, 8 * seg);
+        f32x8_t r = staged8(row, 8 * seg);
         const int64_t o = m * p.ldo + nw0 + 8 * seg;
+        if (rope) {
+          const f32x8_t pr = staged8_of(reinterpret_cast<const float*>(pscr), row, 8 * seg);
+          const float* ct = p.rope_cos + (int64_t)p.rope_pos[m] * p.rope_hd + 8 * seg;
+          const float* sn = p.rope_sin + (int64_t)p.rope_pos[m] * p.rope_hd + 8 * seg;
+          const f32x4 c0 = *reinterpret_cast<const f32x4*>(ct), c1 = *reinterpret_cast<const f32x4*>(ct + 4);
+          const f32x4 s0 = *reinterpret_cast<const f32x4*>(sn), s1 = *reinterpret_cast<const f32x4*>(sn + 4);
+          const float c8[8] = {c0[0], c0[1], c0[2], c0[3], c1[0], c1[1], c1[2], c1[3]};
+          const float s8[8] = {s0[0], s0[1], s0[2], s0[3], s1[0], s1[1], s1[2], s1[3]};
+          // first half: x1 c - x2 s (own x1); second half: x2 c + x1 s (own x2)
+          const bool first = (nw0 % p.rope_hd) == 0;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) {
+            const float a = __fmul_rn(r[e], c8[e]), b = __fmul_rn(pr[e], s8[e]);
+            r[e] = first ? __fsub_rn(a, b) : __fadd_rn(a, b);
+          }
+        }
         if (p.out_mode == DK_OUT_F16) {
           f16x8 h;
 #pragma unroll
-          for (int e = 0; e < 8; ++e) h[e] = (f16)r[e];
+          for (int e = 0; e < 8; ++e) h[e] = rope ? dk_h(r[e]) : (f16)r[e];
           *reinterpret_cast<f16x8*>(reinterpret_cast<f16*>(p.out) + o) = h;
         } else {
           float* dst = reinterpret_cast<float*>(p.out) + o;
@@ -263,6 +286,7 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
         }
       }
       __builtin_amdgcn_wave_barrier();
+      if (!TRANS && p.rope_pos) __syncthreads();   // the partner has read this wave's strip
     } else if constexpr (EPI == EPI_SWIGLU_FWD) {
       // block 0: the gate values, block 1: the up values of the same 32 hidden units
       f32x16 g, u;
@@ -528,7 +552,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   }
   // the epilogue scratch: 16 KB per wave, waves 0-3 in the A stages, 4-7 in the W stages
   uint8_t* escr = reinterpret_cast<uint8_t*>(wave < 4 ? As : Bs) + (wave & 3) * kEpiScratch;
-  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN, escr);
+  // the partner wave: the other 64-column half of the same rows (rotary epilogue)
+  const int pw = wave ^ 1;
+  const uint8_t* pscr = reinterpret_cast<const uint8_t*>(pw < 4 ? As : Bs) + (pw & 3) * kEpiScratch;
+  static_assert(WAVES_N % 2 == 0, "partner waves share rows");
+  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN, escr, pscr);
 }
 
 // Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
@@ -605,7 +633,7 @@ __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
 #pragma unroll
         for (int v = 0; v < 16; ++v) acc[0][0][v] = sp + u == 0 ? v_all[u][v] : acc[0][0][v] + v_all[u][v];
   }
-  wave_epilogue<TRANS, EPI, 1, 1>(p, acc, m0, n0, escr);
+  wave_epilogue<TRANS, EPI, 1, 1>(p, acc, m0, n0, escr, escr);   // never rotary: no split-K
 }
 
 int cu_count() {
@@ -627,7 +655,7 @@ struct HPlan {
   int splits;
 };
 
-HPlan hplan(int64_t M, int64_t N, int64_t K, int epi) {
+HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
   HPlan h{false, 0, 0, 0, 0, 1};
   if (M <= 0 || N % kTile || K % kBK || K < kBK) return h;
   const int cus = cu_count();
@@ -650,7 +678,7 @@ HPlan hplan(int64_t M, int64_t N, int64_t K, int epi) {
   // fewer tiles than CUs: split K so that the splits fill the CUs once.  The fp32 partials cost
   // two passes over splits x tiles x 256 KB, which only long K (4096 or more) repays; LINEAR
   // only, at least 4 row tiles
-  if (epi == EPI_LINEAR && h.tiles_m >= 4 && K >= 4096) {
+  if (!no_split && epi == EPI_LINEAR && h.tiles_m >= 4 && K >= 4096) {
     int64_t s = cus / tiles;
     if (s > K / kBK / 8) s = K / kBK / 8;
     if (s >= 2) {
@@ -662,7 +690,7 @@ HPlan hplan(int64_t M, int64_t N, int64_t K, int epi) {
   }
   // otherwise every tile as 128 x 128 quarters, when they fill at least half the CUs
   const int64_t quarters = (M + 127) / 128 * (N / 128);
-  if (quarters * 2 < cus) return h;
+  if (quarters * 2 < cus && !no_split) return h;
   h.main_wgs = 0;
   h.tail_wgs = 4 * tiles;
   h.ok = true;
@@ -690,7 +718,11 @@ static bool vector_outputs_ok(const GemmParams& p, int epi) {
 template <bool TRANS, int EPI>
 int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
   if (!p0.w16 || !vector_outputs_ok(p0, EPI)) return kHgemmDeclined;
-  const HPlan h = hplan(p0.M, p0.N, p0.K, EPI);
+  // the rotary epilogue pairs the two column halves of a head inside one workgroup: no split-K,
+  // and 128-column tiles at any size
+  const bool rope = p0.rope_pos != nullptr;
+  if (rope && (TRANS || EPI != EPI_LINEAR)) return kHgemmDeclined;
+  const HPlan h = hplan(p0.M, p0.N, p0.K, EPI, rope);
   if (!h.ok) return kHgemmDeclined;
   GemmParams p = p0;
   p.tiles_m = (int)h.tiles_m;

@@ -957,6 +957,31 @@ extern "C" int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, con
   return dispatch_h16<false, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream);
 }
 
+extern "C" int dk_h16_linear_fwd_rope(const void* x, int64_t ldx, int64_t m, const void* w16,
+                                      int64_t rows, int64_t cols, const void* bias,
+                                      const dk_lora_term* terms, int n_terms, int64_t rank,
+                                      const dk_rope* rope, void* y, int64_t ldy,
+                                      const dk_side_dequant* side, hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = linear_fwd_params(p, x, ldx, m, rows, cols, bias, terms, n_terms, rank, y, ldy))
+    return e;
+  if (!rope || !rope->pos || !rope->cos_table || !rope->sin_table || !w16) return DK_ERR_INVALID;
+  if (rope->hd != 128 || rope->cols <= 0 || rope->cols % 128 || rope->cols > rows)
+    return DK_ERR_INVALID;
+  if (!dk_aligned(rope->cos_table, 16) || !dk_aligned(rope->sin_table, 16) || !dk_aligned(w16, 16))
+    return DK_ERR_ALIGN;
+  if (int e = set_side(p, side)) return e;
+  p.rope_pos = rope->pos;
+  p.rope_cos = rope->cos_table;
+  p.rope_sin = rope->sin_table;
+  p.rope_hd = rope->hd;
+  p.rope_cols = rope->cols;
+  if (p.M == 0) return side_alone(p.side, stream);
+  p.w16 = (const f16*)w16;
+  const int r = hgemm_launch<false, EPI_LINEAR>(p, nullptr, 0, stream);
+  return r == kHgemmDeclined ? DK_ERR_INVALID : r;   // a shape the fused rotary form does not take
+}
+
 extern "C" int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
                                          int64_t rows, int64_t cols, const dk_lora_term* terms,
                                          int n_terms, int64_t rank, void* dx, int64_t lddx,

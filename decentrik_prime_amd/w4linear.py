@@ -296,6 +296,43 @@ def linear_forward_lora(x, w, bias=None, terms=(), out=None, w16=None, side=None
     return out
 
 
+def linear_forward_rope(x, w, bias, terms, pos, cos, sin, rope_cols, out=None, w16=None,
+                        side=None, hd=128):
+    """linear_forward_lora of the fused QKV projection with the QKV epilogue's rotary embedding
+    (solution/k_rope.py:23-61) folded into the GEMM epilogue: output columns [0, rope_cols) (the q
+    and k heads, head size hd = 128) are rotated by the positions `pos` (int32 [M]) with the fp32
+    tables cos/sin [positions, hd] before the single fp16 rounding, as the reference's epilogue
+    kernel rotates q16 + s lq16.  Needs the fp16 weight (w16) and a shape the 256 x 256-tile
+    kernel takes; side as in linear_forward_lora."""
+    if w16 is None:
+        raise ValueError("the rotary GEMM reads the fp16 weight (w16)")
+    _check16(x, "x")
+    m = x.shape[0]
+    if x.shape[1] != w.cols:
+        raise ValueError(f"x has {x.shape[1]} features, weight expects {w.cols}")
+    if bias is not None:
+        _check16(bias.view(1, -1), "bias", (1, w.rows))
+    if pos.dtype != torch.int32 or not pos.is_cuda or tuple(pos.shape) != (m,):
+        raise ValueError("pos must be a CUDA int32 [M] tensor")
+    for t, nm in ((cos, "cos"), (sin, "sin")):
+        if t.dtype != torch.float32 or not t.is_cuda or not t.is_contiguous() or t.dim() != 2 \
+                or t.shape[1] != hd:
+            raise ValueError(f"{nm} must be a contiguous CUDA fp32 [positions, {hd}] table")
+    arr, n, rank, _keep = _lora_terms([(z, b, None, c0, c1, s) for z, b, c0, c1, s in terms], m,
+                                      False, w.rows)
+    if out is None:
+        out = torch.empty(m, w.rows, dtype=torch.float16, device=x.device)
+    _check16(out, "out", (m, w.rows))
+    _check_w16(w16, w)
+    rope = _lib.RopeC(_lib.ptr(pos), _lib.ptr(cos), _lib.ptr(sin), int(hd), int(rope_cols))
+    rc = _lib.lib().dk_h16_linear_fwd_rope(_lib.ptr(x), x.stride(0), m, _lib.ptr(w16), w.rows,
+                                           w.cols, _lib.ptr(bias), arr, n, rank, ctypes.byref(rope),
+                                           _lib.ptr(out), out.stride(0), _side(side),
+                                           _lib.stream_handle(x.device))
+    _lib.check(rc, "dk_h16_linear_fwd_rope")
+    return out
+
+
 def _dx_out(out, m, w, out_dtype, accumulate, device):
     if out is None:
         if accumulate:

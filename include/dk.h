@@ -323,6 +323,26 @@ int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const void* w1
                            int64_t rank, void* y, int64_t ldy, void* workspace,
                            int64_t workspace_bytes, const dk_side_dequant* side,
                            hipStream_t stream);
+/* The fused QKV projection with the QKV epilogue's forward folded into the GEMM epilogue:
+ * dk_h16_linear_fwd_lora's y, but the output columns [0, rope->cols) (the q and k heads, head size
+ * rope->hd = 128) rotated by [x1 c - x2 s | x2 c + x1 s], c, s = cos/sin_table[pos[row] * hd + j],
+ * j < hd / 2, from the fp32 sum fp32(fp16(x W^T + bias)) + s fp32(fp16(z B^T)) before the single
+ * fp16 rounding — the order of qkv_epilogue_fwd_kernel (solution/k_rope.py:23-61) on the
+ * reference's q16 and lq16 (solution/fast_qwen.py:943-949).  Columns past rope->cols (the v
+ * heads) are dk_h16_linear_fwd_lora's.  Runs on the 256 x 256-tile kernel only (output columns a
+ * multiple of 256, K of 64): DK_ERR_INVALID for other shapes.  pos int32 [m]; tables fp32
+ * [positions, hd], 16-byte aligned. */
+typedef struct dk_rope {
+  const int32_t* pos;
+  const float* cos_table;
+  const float* sin_table;
+  int32_t hd;
+  int64_t cols;
+} dk_rope;
+int dk_h16_linear_fwd_rope(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
+                           int64_t cols, const void* bias, const dk_lora_term* terms, int n_terms,
+                           int64_t rank, const dk_rope* rope, void* y, int64_t ldy,
+                           const dk_side_dequant* side, hipStream_t stream);
 int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const void* w16,
                               int64_t rows, int64_t cols, const dk_lora_term* terms, int n_terms,
                               int64_t rank, void* dx, int64_t lddx, int out_mode, void* workspace,

@@ -140,6 +140,20 @@ def test_norm_and_rope_argument_errors_come_back_before_launch():
     assert lib.dk_qkv_epilogue_bwd(p8, p16, p16, 1, p16, p16, p16, p16, 4, 12, 2, 128, 6,
                                    None) == _lib.DK_ERR_ALIGN           # fp32 grads: 16 bytes
     assert lib.dk_qkv_epilogue_bwd(p8, p8, p8, 0, p16, p16, p16, p16, 0, 12, 2, 128, 1, None) == 0
+    # the QKV GEMM with the rotary epilogue: head size 128, whole heads within the output, tables
+    # aligned, the fp16 weight present
+    def fused(rope, m=4, w16=p16):
+        return lib.dk_h16_linear_fwd_rope(p16, 1536, m, w16, 2048, 1536, None, None, 0, 0,
+                                          None if rope is None else ctypes.byref(rope), p16, 2048,
+                                          None, None)
+    ok = _lib.RopeC(p16, p16, p16, 128, 1792)
+    assert fused(None) == _lib.DK_ERR_INVALID
+    assert fused(ok, w16=None) == _lib.DK_ERR_INVALID
+    assert fused(_lib.RopeC(p16, p16, p16, 64, 1792)) == _lib.DK_ERR_INVALID
+    assert fused(_lib.RopeC(p16, p16, p16, 128, 1700)) == _lib.DK_ERR_INVALID
+    assert fused(_lib.RopeC(p16, p16, p16, 128, 2176)) == _lib.DK_ERR_INVALID   # beyond the output
+    assert fused(_lib.RopeC(p16, p8, p16, 128, 1792)) == _lib.DK_ERR_ALIGN
+    assert fused(ok, m=0) == 0
 
 
 def test_norm_and_rope_mirrors_check_arguments():

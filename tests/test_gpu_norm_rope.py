@@ -152,3 +152,60 @@ def test_qkv_epilogue_forward_backward(torch, n, nq, nkv, hd):
     torch.cuda.synchronize()
     _exact(host(out1), rope.qkv_epilogue_bwd(dq.astype(F16), dk16, dv16, pos, cos, sin, nq, nkv, hd,
                                              1), "qkv backward (fp16, reduced) vs oracle")
+
+
+@pytest.mark.parametrize("m", [2048, 200])
+def test_qkv_gemm_with_rotary_epilogue(torch, m):
+    """The fused QKV projection with the rotary embedding in the GEMM epilogue against the
+    unfused chain (GEMM + bias, LoRA up, then the standalone QKV epilogue kernel, whose order of
+    operations it follows): bit-identical when the chain's lq16 / lv16 are the epilogue's own
+    LoRA products (a GEMM with a zero weight gives fp16(s lo16) = s lo16 exactly); within the
+    GEMM tolerance of the oracle; the v columns equal dk_h16_linear_fwd_lora's."""
+    from decentrik_prime_amd import k_rope, w4linear
+    from oracle import linear, rope
+    from tests.helpers import cuda16, lora_inputs, nf4_weight, to_w4
+    log(f"qkv GEMM + rotary epilogue, M={m}")
+    D, KV, nq, nkv, hd = 1536, 256, 12, 2, 128
+    q = nf4_weight(D + 2 * KV, D, seed=217)
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, seed=31)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, seed=32)
+    rng = np.random.default_rng(33)
+    bias = (rng.standard_normal(D + 2 * KV) * 0.1).astype(F16)
+    cos, sin = rope.rope_tables(4096, hd)
+    pos = rng.integers(0, 4096, m).astype(np.int32)
+    w = to_w4(q)
+    w16 = w.dequantize()
+    ks = linear.keep_scale(0.05)
+    zq = w4linear.lora_down(cuda16(x), cuda16(aq), torch.from_numpy(mq).cuda(), ks)
+    zv = w4linear.lora_down(cuda16(x), cuda16(av), torch.from_numpy(mv).cuda(), ks)
+    terms = [(zq, cuda16(bq), 0, D, 2.0), (zv, cuda16(bv), D + KV, D + 2 * KV, 2.0)]
+    tp = torch.from_numpy(pos).cuda()
+    tc, ts = torch.from_numpy(cos).cuda(), torch.from_numpy(sin).cuda()
+    fused = w4linear.linear_forward_rope(cuda16(x), w, cuda16(bias), terms, tp, tc, ts,
+                                         (nq + nkv) * hd, w16=w16)
+    # unfused: q16/k16/v16 = GEMM + bias; lq16, lv16 = fp16(z B^T); then the epilogue kernel
+    chain = w4linear.linear_forward_lora(cuda16(x), w, cuda16(bias), [], w16=w16)
+    lora2 = w4linear.linear_forward_lora(cuda16(x), w, None, terms, w16=torch.zeros_like(w16))
+    lq16 = (lora2[:, :D] * 0.5).contiguous()
+    lv16 = (lora2[:, D + KV:] * 0.5).contiguous()
+    k_rope.qkv_epilogue_forward(chain, lq16, lv16, tp, tc, ts, 2.0, nq, nkv, hd)
+    plain = w4linear.linear_forward_lora(cuda16(x), w, cuda16(bias), terms, w16=w16)
+    torch.cuda.synchronize()
+    a = host(fused)
+    if m == 2048:   # the chain's GEMMs run the same kernel and tile plan
+        _exact(a, host(chain), "rotary GEMM vs GEMM + LoRA up + QKV epilogue")
+        _exact(a[:, (nq + nkv) * hd:], host(plain)[:, (nq + nkv) * hd:], "v columns")
+    else:           # the chain's plain GEMMs split K on the NF4-form kernel: summation order only
+        b = host(chain).astype(np.float64)
+        tol = 2 * 2.0 ** -10 * np.abs(b) + 2.0 ** -11 * np.abs(b).max()
+        assert not (np.abs(a.astype(np.float64) - b) > tol).any(), "rotary GEMM vs chain"
+    # oracle: fp16 GEMM + bias, LoRA up, rotary (oracle.rope), at the GEMM tolerance
+    base = linear.mm16(x, q["deq"].T)
+    base = (base.astype(np.float32) + bias.astype(np.float32)).astype(F16)
+    lq_o = linear.mm16(host(zq), bq.T)
+    lv_o = linear.mm16(host(zv), bv.T)
+    ref = rope.qkv_epilogue_fwd(base, lq_o, lv_o, pos, cos, sin, 2.0, nq, nkv, hd)
+    _close(a, ref, 1e-2, 2e-2, "rotary qkv vs oracle")
+    with pytest.raises(ValueError):
+        w4linear.linear_forward_rope(cuda16(x), w, cuda16(bias), terms, tp, tc[:, :64].contiguous(),
+                                     ts[:, :64].contiguous(), (nq + nkv) * hd, w16=w16, hd=64)
