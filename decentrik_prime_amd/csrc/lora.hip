@@ -73,9 +73,12 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
   const int64_t cols = J.cols;
   constexpr int RB = R / 16;
   constexpr int NW = kRowThreads / 64;
-  constexpr int kBatch = 4;
-  constexpr int KC = 768;        // rows of B staged per pass (MODE 1)
+  constexpr int kBatch = 6;      // MODE 0: K steps per wave whose loads are in flight together
+  constexpr int KC = R == 16 ? 1536 : 768;   // rows of B staged per pass (MODE 1)
+  constexpr int KU = KC / 32 / NW;           // MODE 1: dY steps per wave per pass
+  constexpr int BI = KC * (R / 8) / kRowThreads;   // MODE 1: 16-byte B pieces per thread per pass
   constexpr int BLD = R + 8;     // halves per staged B row
+  static_assert(KU * 32 * NW == KC && BI * kRowThreads == KC * (R / 8), "MODE 1 pass shape");
   __shared__ float red[NW * 16 * R];
   __shared__ __attribute__((aligned(16))) f16 Bs[MODE == 1 ? KC * BLD : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
@@ -110,26 +113,33 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
       }
     }
   } else {
+    // per pass: this wave's dY operands (steps w, w + NW, ...) and this thread's pieces of B are
+    // all loaded before the first is used, then B goes to LDS behind one barrier
     for (int64_t c0 = 0; c0 < cols; c0 += KC) {
       const int kc = (int)(cols - c0 < KC ? cols - c0 : KC);
+      const int steps = kc / 32;
+      f16x8 a[KU], bv[BI];
+#pragma unroll
+      for (int u = 0; u < KU; ++u) {
+        const int s = w + u * NW < steps ? w + u * NW : steps - 1;   // clamped; not accumulated
+        a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
+      }
+#pragma unroll
+      for (int q = 0; q < BI; ++q) {
+        const int i = tid + q * kRowThreads, kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
+        if (kk < kc) bv[q] = *reinterpret_cast<const f16x8*>(wt + (c0 + kk) * R + r8);
+      }
       __syncthreads();  // the previous pass has finished reading Bs
-      for (int i = tid; i < kc * (R / 8); i += kRowThreads) {
-        const int kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
-        *reinterpret_cast<f16x8*>(Bs + kk * BLD + r8) =
-            *reinterpret_cast<const f16x8*>(wt + (c0 + kk) * R + r8);
+#pragma unroll
+      for (int q = 0; q < BI; ++q) {
+        const int i = tid + q * kRowThreads, kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
+        if (kk < kc) *reinterpret_cast<f16x8*>(Bs + kk * BLD + r8) = bv[q];
       }
       __syncthreads();
-      const int steps = kc / 32;
-      for (int s0 = w; s0 < steps; s0 += NW * kBatch) {
-        f16x8 a[kBatch];
+      {
 #pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int s = s0 + u * NW < steps ? s0 + u * NW : steps - 1;
-          a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
-        }
-#pragma unroll
-        for (int u = 0; u < kBatch; ++u) {
-          const int s = s0 + u * NW;
+        for (int u = 0; u < KU; ++u) {
+          const int s = w + u * NW;
           if (s >= steps) break;
 #pragma unroll
           for (int b = 0; b < RB; ++b) {
@@ -168,7 +178,9 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
 // rows addressed by lanes a, a + 4, a + 8, a + 12, so lane l addressing row
 // 8 (l / 16) + 4 h + (l % 16) / 4, column 4 (l % 4) receives rows 8 (l / 16) + 4 h + 0..3 of
 // column l % 16, and two reads (h = 0, 1) give the 8 consecutive rows of the MFMA operand.
-// Jobs as for the row reductions: column blocks [bx0, next job's bx0) of grid.x serve job j.
+// Column blocks [bx0, next job's bx0) of grid.x serve job j; a job with a mask applies the dropout
+// (dA of a masked term), one without reads P as stored (dB, or dA of an unmasked term), so the dB
+// and dA reductions of both terms share one launch.
 struct ColsJob {
   const f16* P;
   int64_t ld;
@@ -179,18 +191,23 @@ struct ColsJob {
   int64_t cols;
   int bx0;
 };
+constexpr int kMaxColsJobs = 2 * kMaxJobs;
 struct ColsJobs {
-  ColsJob j[kMaxJobs];
+  ColsJob j[kMaxColsJobs];
   int n;
 };
 
-template <int R, bool DROP>
+template <int R>
 __global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int64_t rows) {
-  const int jb = (jobs.n > 1 && (int)blockIdx.x >= jobs.j[1].bx0) ? 1 : 0;
+  int jb = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxColsJobs; ++q)
+    if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].bx0) jb = q;
   const ColsJob& J = jobs.j[jb];
   const f16* __restrict__ P = J.P;
   const int64_t ld = J.ld;
   const uint8_t* __restrict__ mask = J.mask;
+  const bool drop = mask != nullptr;
   const float ks = J.ks;
   const f16* __restrict__ Q = J.Q;
   float* __restrict__ part = J.part;
@@ -213,11 +230,11 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int6
     const int64_t m = r0 + row;
     if (m < rows && c0 + 8 * c8 < cols) {
       pv[i] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + 8 * c8);
-      if (DROP) mv[i] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + 8 * c8);
+      if (drop) mv[i] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + 8 * c8);
     } else {
 #pragma unroll
       for (int e = 0; e < 8; ++e) pv[i][e] = (f16)0.0f;
-      if (DROP) mv[i] = u32x2{0u, 0u};
+      mv[i] = u32x2{0u, 0u};
     }
   }
   for (int i = tid; i < kChunkRows * R / 8; i += kThreads) {
@@ -237,7 +254,7 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int6
     const int c = tid + kThreads * i;
     const int row = c / (kColsPerBlock / 8), c8 = c % (kColsPerBlock / 8);
     f16x8 v = pv[i];
-    if (DROP) {
+    if (drop) {
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         const uint32_t keep = (mv[i][e >> 2] >> (8 * (e & 3))) & 0xffu;
@@ -339,7 +356,6 @@ int rows_launch(int64_t R, hipStream_t stream, const RowsJobs& jobs, int n_jobs,
   return 0;
 }
 
-template <bool DROP>
 int cols_launch(int64_t R, hipStream_t stream, ColsJobs jobs, int64_t rows) {
   int bx = 0;
   for (int q = 0; q < jobs.n; ++q) {
@@ -348,10 +364,10 @@ int cols_launch(int64_t R, hipStream_t stream, ColsJobs jobs, int64_t rows) {
   }
   const dim3 grid((unsigned)bx, (unsigned)((rows + kChunkRows - 1) / kChunkRows));
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_cols_kernel<16, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 32: hipLaunchKernelGGL((lora_cols_kernel<32, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 48: hipLaunchKernelGGL((lora_cols_kernel<48, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 64: hipLaunchKernelGGL((lora_cols_kernel<64, DROP>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 16: hipLaunchKernelGGL((lora_cols_kernel<16>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 32: hipLaunchKernelGGL((lora_cols_kernel<32>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 48: hipLaunchKernelGGL((lora_cols_kernel<48>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 64: hipLaunchKernelGGL((lora_cols_kernel<64>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
     default: return DK_ERR_INVALID;
   }
   DK_CHECK_LAUNCH();
@@ -435,7 +451,6 @@ extern "C" int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t 
     return DK_ERR_INVALID;
   if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
   int64_t n_outs[kMaxJobs];
-  int masked = 0;
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_grads_term& u = terms[t];
     if (u.n_out <= 0 || u.n_out % 32 || !u.dy || !u.z || !u.lora_b || !u.da || !u.db || !u.dz ||
@@ -445,7 +460,6 @@ extern "C" int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t 
         (u.mask && !dk_aligned(u.mask, 8)))
       return DK_ERR_ALIGN;
     n_outs[t] = u.n_out;
-    masked += u.mask != nullptr;
   }
   if (m == 0) return 0;
   if (!ws || ws_bytes < dk_lora_grads_multi_workspace(m, k, rank, n_outs, n_terms))
@@ -466,36 +480,18 @@ extern "C" int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t 
   }
   int e = rows_launch<1, false>(rank, stream, rj, n_terms, m);
   if (e) return e;
-  // dB = fp32(fp16(dY^T z)) * s
-  ColsJobs cb = {};
-  cb.n = n_terms;
+  // one launch: dB = fp32(fp16(dY^T z)) * s of every term, then dA = fp32(fp16(dz^T Xd)), Xd the
+  // dropout of x with the term's mask
+  ColsJobs cj = {};
+  cj.n = 2 * n_terms;
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_grads_term& u = terms[t];
-    cb.j[t] = ColsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.z, part_db[t], u.n_out, 0};
+    cj.j[t] = ColsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.z, part_db[t], u.n_out, 0};
+    cj.j[n_terms + t] = ColsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f,
+                                (const f16*)u.dz, part_da[t], k, 0};
   }
-  e = cols_launch<false>(rank, stream, cb, m);
+  e = cols_launch(rank, stream, cj, m);
   if (e) return e;
-  // dA = fp32(fp16(dz^T Xd)), Xd the dropout of x with the term's mask
-  auto da_job = [&](int t) {
-    const dk_lora_grads_term& u = terms[t];
-    return ColsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f, (const f16*)u.dz,
-                   part_da[t], k, 0};
-  };
-  if (masked == 0 || masked == n_terms) {
-    ColsJobs ca = {};
-    ca.n = n_terms;
-    for (int t = 0; t < n_terms; ++t) ca.j[t] = da_job(t);
-    e = masked ? cols_launch<true>(rank, stream, ca, m) : cols_launch<false>(rank, stream, ca, m);
-    if (e) return e;
-  } else {
-    for (int t = 0; t < n_terms; ++t) {
-      ColsJobs ca = {};
-      ca.n = 1;
-      ca.j[0] = da_job(t);
-      e = terms[t].mask ? cols_launch<true>(rank, stream, ca, m) : cols_launch<false>(rank, stream, ca, m);
-      if (e) return e;
-    }
-  }
   FinalJobs fj = {};
   fj.n = 2 * n_terms;
   for (int t = 0; t < n_terms; ++t) {

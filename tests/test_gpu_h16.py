@@ -196,6 +196,46 @@ def test_lora_multi_matches_single(torch, m):
         _scaled_close(host(got), ref[nm], f"{nm}_q vs oracle")
 
 
+@pytest.mark.parametrize("rank", [32, 64])
+def test_lora_ranks_and_mixed_masks(torch, rank):
+    """Ranks above the reference's 16 (the kernels take 16..64) and a masked term beside an
+    unmasked one in the shared launches, ragged M: shared launches bit-identical to one call
+    each, and the oracle's results (an unmasked term is the oracle's all-kept mask with scale 1)."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    m, D, KV = 300, 1536, 256
+    log(f"LoRA rank {rank}, masked q + unmasked v, M={m}")
+    x, aq, bq, mq, dyq = lora_inputs(m, D, D, r=rank, seed=41)
+    _, av, bv, _, dyv = lora_inputs(m, D, KV, r=rank, seed=42)
+    ks = linear.keep_scale(0.05)
+    keep_all = np.ones_like(mq)
+    tx = cuda16(x)
+    t = {k: cuda16(v) for k, v in (("aq", aq), ("av", av), ("bq", bq), ("bv", bv),
+                                   ("gq", dyq), ("gv", dyv))}
+    tmq = cuda(mq)
+    zq, zv = w4linear.lora_down_multi(tx, [(t["aq"], tmq, ks), (t["av"], None, 1.0)])
+    zq1 = w4linear.lora_down(tx, t["aq"], tmq, ks)
+    zv1 = w4linear.lora_down(tx, t["av"], None, 1.0)
+    torch.cuda.synchronize()
+    _same(zq, zq1, "z_q")
+    _same(zv, zv1, "z_v")
+    assert_close(host(zq), linear.lora_down(x, mq, ks, aq), 2e-3, 2e-3, "z_q vs oracle")
+    assert_close(host(zv), linear.lora_down(x, keep_all, 1.0, av), 2e-3, 2e-3, "z_v vs oracle")
+    multi = w4linear.lora_grads_multi(tx, [(t["gq"], zq, t["bq"], 2.0, tmq, ks),
+                                           (t["gv"], zv, t["bv"], 2.0, None, 1.0)])
+    single = [w4linear.lora_grads(t["gq"], zq, tx, t["bq"], 2.0, tmq, ks),
+              w4linear.lora_grads(t["gv"], zv, tx, t["bv"], 2.0, None, 1.0)]
+    torch.cuda.synchronize()
+    for term, (both, one) in zip("qv", zip(multi, single)):
+        for nm, a, b in zip(("dA", "dB", "dz"), both, one):
+            _same(a, b, f"{nm}_{term}")
+    for term, got, (dy, z, mk, kk, a, b, n) in zip(
+            "qv", multi, ((dyq, zq, mq, ks, aq, bq, D), (dyv, zv, keep_all, 1.0, av, bv, KV))):
+        ref = linear.linear_bwd(dy, np.zeros((n, D), F16), host(z), x, mk, kk, a, b, 2.0)
+        for nm, g in zip(("dA", "dB", "dZ"), got):
+            _scaled_close(host(g), ref[nm], f"{nm}_{term} vs oracle (rank {rank})")
+
+
 def test_h16_argument_checks(torch):
     from decentrik_prime_amd import w4linear
     log("h16 argument checks")
