@@ -114,6 +114,9 @@ SIGNATURES = {
                                    _c_p]),
     "dk_qkv_epilogue_bwd": (_int, [_c_p, _c_p, _c_p, _int, _c_p, _c_p, _c_p, _c_p, _i64, _int, _int,
                                    _int, _int, _c_p]),
+    "dk_attn_fwd": (_int, [_c_p, _c_p, _int, _c_p, _int, _i64, _int, _int, _int, _c_p, _c_p, _c_p]),
+    "dk_attn_bwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _int, _c_p, _int, _i64, _int, _int, _int,
+                           _c_p, _c_p, _c_p, _c_p, _c_p]),
     "dk_w4_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_w4_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _i64, _c_p]),
 }

@@ -1,0 +1,486 @@
+// Variable-length causal GQA attention of the packed batch on gfx950: forward (online softmax) and
+// backward (delta, dK/dV per query head, dQ).  Replaces solution/k_attn.py:40-245.
+//
+// Layout (the fused QKV buffer the QKV epilogue writes): row t of qkv [N, (NQ + 2 NKV) HD] fp16
+// holds token t's query heads, then its key heads, then its value heads; query head h reads key /
+// value head h / (NQ / NKV).  cu_seqlens [n_seq + 1] delimits the sequences; a block table of
+// (sequence, first row) pairs names the workgroups, whose rows never straddle two sequences, so
+// the mask is `key <= query` inside a sequence.  Scores are scaled by qk_scale = log2(e) / sqrt(HD)
+// and the softmax runs in the exp2 domain; lse [NQ, N] holds m + log2(l) per (head, token).
+//
+// MFMA orientation: every product is v_mfma_f32_32x32x16_f16, arranged so that the index a
+// softmax statistic belongs to sits on the lane.  Forward and dQ compute S^T = K Q^T (keys x
+// queries: lane l % 32 is the query, the running max, sum and rescale are per lane) and O^T = V^T
+// P^T, taking P^T straight from the score registers: the 32x32 result register v of lane l is row
+// 8 (v / 4) + 4 (l / 32) + v % 4, so registers 8 t' .. 8 t' + 7 of a lane hold keys
+// 16 t' + 8 (j / 4) + 4 (l / 32) + j % 4 (j = 0..7), and the other operand supplies the same keys
+// in the same order from a transposed LDS copy (the k order of a product is free as long as both
+// operands agree).  dK/dV compute S = Q K^T (the key on the lane) and use P and dS the same way.
+#include "dk_common.h"
+
+namespace {
+
+constexpr int kHD = 128;          // head size (Qwen2.5: 128)
+constexpr int kAThreads = 256;    // 4 waves, 32 query rows (or keys) each
+constexpr int kBM = 128;          // queries per forward / dQ workgroup, keys per dK/dV workgroup
+constexpr int kBN = 64;           // keys per forward / dQ tile, queries per dK/dV tile
+constexpr int kPR = kHD + 8;      // halves per row of a row-major LDS tile
+constexpr int kPT = kBN + 8;      // halves per row of a transposed LDS tile
+static_assert(kBM == 32 * (kAThreads / 64), "a wave owns 32 rows");
+
+struct AttnArgs {
+  const f16* qkv;
+  const int32_t* cu;
+  const int32_t* tab;
+  int n_seq;
+  int64_t n_tokens;
+  int nq, nkv;
+  float qk_scale, sm_scale;
+};
+
+__device__ __forceinline__ f32x16 zero16() {
+  f32x16 z;
+#pragma unroll
+  for (int v = 0; v < 16; ++v) z[v] = 0.0f;
+  return z;
+}
+
+__device__ __forceinline__ f16x8 zero8() {
+  f16x8 z;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) z[e] = (f16)0.0f;
+  return z;
+}
+
+__device__ __forceinline__ f32x16 mfma(const f16x8& a, const f16x8& b, const f32x16& c) {
+  return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
+}
+
+// 8 halves of a transposed LDS row: positions p .. p + 3 and p + 8 .. p + 11 (the keys or
+// queries of MFMA k index j = 0..7 for the lane half whose p = 16 t + 4 (l / 32))
+__device__ __forceinline__ f16x8 read_t8(const f16* row, int p) {
+  const f16x4 lo = *reinterpret_cast<const f16x4*>(row + p);
+  const f16x4 hi = *reinterpret_cast<const f16x4*>(row + p + 8);
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
+// The sequence of a block-table entry; false when the entry names no sequence or a sequence that
+// does not lie within the n_tokens rows (then every row and loop of the workgroup stays in bounds
+// whatever the tables hold).
+__device__ __forceinline__ bool block_of(const AttnArgs& a, int blk, int64_t* s0, int* seqlen,
+                                         int* start) {
+  const int seq = a.tab[2 * blk];
+  *start = a.tab[2 * blk + 1];
+  if (seq < 0 || seq >= a.n_seq || *start < 0) return false;
+  *s0 = a.cu[seq];
+  *seqlen = a.cu[seq + 1] - a.cu[seq];
+  return *s0 >= 0 && *seqlen >= 0 && *s0 + *seqlen <= a.n_tokens;
+}
+
+// Rows [r0, r0 + kBN) of one head (column offset col of rows with stride ld) into a row-major LDS
+// tile and, if tr, also into a transposed one (tr[c][r], pairs of rows packed per dword).  Rows
+// at or past `valid` (or past the buffer) read as zero.  All loads are issued before the stores.
+__device__ __forceinline__ void stage_rows(const f16* base, int64_t ld, int64_t s0, int r0,
+                                           int valid, int64_t n_tokens, f16* rm, f16* tr) {
+  const int tid = threadIdx.x;
+  f16x8 v[2][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = r0 + 2 * rp + u;
+      v[q][u] = r < valid && s0 + r < n_tokens
+                    ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
+                    : zero8();
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+#pragma unroll
+    for (int u = 0; u < 2; ++u)
+      *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = v[q][u];
+    if (tr) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(v[q][0][e], v[q][1][e]);
+    }
+  }
+}
+
+// Like stage_rows, but only the transposed tile.
+__device__ __forceinline__ void stage_rows_t(const f16* base, int64_t ld, int64_t s0, int r0,
+                                             int valid, int64_t n_tokens, f16* tr) {
+  const int tid = threadIdx.x;
+  f16x8 v[2][2];
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+#pragma unroll
+    for (int u = 0; u < 2; ++u) {
+      const int r = r0 + 2 * rp + u;
+      v[q][u] = r < valid && s0 + r < n_tokens
+                    ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
+                    : zero8();
+    }
+  }
+#pragma unroll
+  for (int q = 0; q < 2; ++q) {
+    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+#pragma unroll
+    for (int e = 0; e < 8; ++e)
+      *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(v[q][0][e], v[q][1][e]);
+  }
+}
+
+// 8 k-steps of a head row as the B operand of a 32x32x16 product: lane l (row r = this lane's
+// query or key) holds elements 16 s + 8 (l / 32) + [0, 8) in frag[s]; zero for invalid rows.
+__device__ __forceinline__ void row_frags(const f16* row, bool valid, int hl, f16x8* frag) {
+#pragma unroll
+  for (int s = 0; s < kHD / 16; ++s)
+    frag[s] = valid ? *reinterpret_cast<const f16x8*>(row + 16 * s + 8 * hl) : zero8();
+}
+
+// forward (solution/k_attn.py:40-83): one workgroup per (block of kBM queries, query head)
+__global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __restrict__ out,
+                                                             float* __restrict__ lse) {
+  int64_t s0;
+  int seqlen, mstart;
+  if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
+  const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD;
+  const int kvh = h / (a.nq / a.nkv);
+  const int m = mstart + 32 * w + c;
+  const bool mval = m < seqlen && s0 + m < a.n_tokens;
+  __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
+  __shared__ __attribute__((aligned(16))) f16 Vt[kHD * kPT];
+
+  f16x8 qf[kHD / 16];
+  row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
+  f32x16 oacc[kHD / 32];
+#pragma unroll
+  for (int hb = 0; hb < kHD / 32; ++hb) oacc[hb] = zero16();
+  float m_i = -1.0e30f, l_i = 0.0f;
+  const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
+  const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
+  const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
+  for (int n0 = 0; n0 < hi; n0 += kBN) {
+    __syncthreads();   // every wave has finished reading the previous tile
+    stage_rows(kbase, ROW, s0, n0, seqlen, a.n_tokens, Ks, nullptr);
+    stage_rows_t(vbase, ROW, s0, n0, seqlen, a.n_tokens, Vt);
+    __syncthreads();
+    // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
+    f32x16 sacc[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Ks + (kb * 32 + c) * kPR + 16 * s + 8 * hl),
+                        qf[s], sacc[kb]);
+    float mx = -1.0e30f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+        const float sv = n <= m && n < seqlen ? __fmul_rn(sacc[kb][v], a.qk_scale) : -1.0e30f;
+        sacc[kb][v] = sv;
+        mx = fmaxf(mx, sv);
+      }
+    mx = fmaxf(mx, __shfl_xor(mx, 32));
+    const float m_new = fmaxf(m_i, mx);
+    const float alpha = exp2f(__fsub_rn(m_i, m_new));
+    float rs = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = exp2f(__fsub_rn(sacc[kb][v], m_new));
+        sacc[kb][v] = p;
+        rs = __fadd_rn(rs, p);
+      }
+    rs = __fadd_rn(rs, __shfl_xor(rs, 32));
+    l_i = __fadd_rn(__fmul_rn(l_i, alpha), rs);
+    m_i = m_new;
+#pragma unroll
+    for (int hb = 0; hb < kHD / 32; ++hb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) oacc[hb][v] = __fmul_rn(oacc[hb][v], alpha);
+    // O^T += V^T P^T over the tile's 64 keys, 16 per step
+#pragma unroll
+    for (int t = 0; t < kBN / 16; ++t) {
+      const int kb = t >> 1, i0 = 8 * (t & 1);
+      f16x8 pf;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) pf[j] = (f16)sacc[kb][i0 + j];
+#pragma unroll
+      for (int hb = 0; hb < kHD / 32; ++hb)
+        oacc[hb] = mfma(read_t8(Vt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), pf, oacc[hb]);
+    }
+  }
+  if (!mval) return;
+  // result register v of block hb: head column hb * 32 + 8 (v / 4) + 4 (l / 32) + v % 4
+  f16* orow = out + (s0 + m) * (int64_t)(a.nq * kHD) + h * kHD;
+#pragma unroll
+  for (int hb = 0; hb < kHD / 32; ++hb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f16x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = (f16)__fdiv_rn(oacc[hb][4 * g + e], l_i);
+      *reinterpret_cast<f16x4*>(orow + hb * 32 + 8 * g + 4 * hl) = o;
+    }
+  if (hl == 0) lse[(int64_t)h * a.n_tokens + s0 + m] = __fadd_rn(m_i, log2f(l_i));
+}
+
+// delta[h][t] = sum_d O[t][h][d] dO[t][h][d] (solution/k_attn.py:84-94): 16 lanes per (token, head)
+__global__ __launch_bounds__(kAThreads) void attn_delta_kernel(const f16* __restrict__ o,
+                                                               const f16* __restrict__ dout,
+                                                               float* __restrict__ delta,
+                                                               int64_t n_tokens, int nq) {
+  const int64_t pair = (int64_t)blockIdx.x * (kAThreads / 16) + (threadIdx.x >> 4);
+  if (pair >= n_tokens * nq) return;
+  const int64_t t = pair / nq;
+  const int hh = (int)(pair % nq), e = (threadIdx.x & 15) * 8;
+  const int64_t off = t * nq * kHD + hh * kHD + e;
+  const f16x8 ov = *reinterpret_cast<const f16x8*>(o + off);
+  const f16x8 gv = *reinterpret_cast<const f16x8*>(dout + off);
+  float s = 0.0f;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) s = __fadd_rn(s, __fmul_rn((float)ov[j], (float)gv[j]));
+#pragma unroll
+  for (int x = 1; x < 16; x <<= 1) s = __fadd_rn(s, __shfl_xor(s, x));
+  if ((threadIdx.x & 15) == 0) delta[(int64_t)hh * n_tokens + t] = s;
+}
+
+// dQ (solution/k_attn.py:142-182): one workgroup per (block of kBM queries, query head), key
+// tiles of kBN up to the diagonal
+__global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f16* __restrict__ dout,
+                                                            const float* __restrict__ lse,
+                                                            const float* __restrict__ delta,
+                                                            float* __restrict__ dq) {
+  int64_t s0;
+  int seqlen, mstart;
+  if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
+  const int h = blockIdx.y;
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
+  const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
+  const int kvh = h / (a.nq / a.nkv);
+  const int m = mstart + 32 * w + c;
+  const bool mval = m < seqlen && s0 + m < a.n_tokens;
+  __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
+  __shared__ __attribute__((aligned(16))) f16 Vs[kBN * kPR];
+  __shared__ __attribute__((aligned(16))) f16 Kt[kHD * kPT];
+
+  f16x8 qf[kHD / 16], dof[kHD / 16];
+  row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
+  row_frags(dout + (s0 + m) * OROW + h * kHD, mval, hl, dof);
+  const float lse_m = mval ? lse[(int64_t)h * a.n_tokens + s0 + m] : 0.0f;
+  const float dl_m = mval ? delta[(int64_t)h * a.n_tokens + s0 + m] : 0.0f;
+  f32x16 dqacc[kHD / 32];
+#pragma unroll
+  for (int hb = 0; hb < kHD / 32; ++hb) dqacc[hb] = zero16();
+  const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
+  const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
+  const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
+  for (int n0 = 0; n0 < hi; n0 += kBN) {
+    __syncthreads();
+    stage_rows(kbase, ROW, s0, n0, seqlen, a.n_tokens, Ks, Kt);
+    stage_rows(vbase, ROW, s0, n0, seqlen, a.n_tokens, Vs, nullptr);
+    __syncthreads();
+    f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s)
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        const int o = (kb * 32 + c) * kPR + 16 * s + 8 * hl;
+        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Ks + o), qf[s], sacc[kb]);     // S^T
+        dpacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Vs + o), dof[s], dpacc[kb]);  // dP^T
+      }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
+        const float p = n <= m && n < seqlen && mval
+                            ? exp2f(__fsub_rn(__fmul_rn(sacc[kb][v], a.qk_scale), lse_m))
+                            : 0.0f;
+        sacc[kb][v] = __fmul_rn(p, __fsub_rn(dpacc[kb][v], dl_m));   // dS^T
+      }
+    // dQ^T += K^T dS^T
+#pragma unroll
+    for (int t = 0; t < kBN / 16; ++t) {
+      const int kb = t >> 1, i0 = 8 * (t & 1);
+      f16x8 dsf;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) dsf[j] = (f16)sacc[kb][i0 + j];
+#pragma unroll
+      for (int hb = 0; hb < kHD / 32; ++hb)
+        dqacc[hb] = mfma(read_t8(Kt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dsf, dqacc[hb]);
+    }
+  }
+  if (!mval) return;
+  float* qrow = dq + (s0 + m) * OROW + h * kHD;
+#pragma unroll
+  for (int hb = 0; hb < kHD / 32; ++hb)
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      f32x4 o;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(dqacc[hb][4 * g + e], a.sm_scale);
+      *reinterpret_cast<f32x4*>(qrow + hb * 32 + 8 * g + 4 * hl) = o;
+    }
+}
+
+// dK, dV per query head (solution/k_attn.py:97-139): one workgroup per (block of kBM keys, query
+// head), query tiles of kBN from the block's first key to the end of the sequence; fp32 partials
+// [N, NQ HD] that the QKV epilogue backward sums over each group of NQ / NKV heads.
+__global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const f16* __restrict__ dout,
+                                                              const float* __restrict__ lse,
+                                                              const float* __restrict__ delta,
+                                                              float* __restrict__ dkp,
+                                                              float* __restrict__ dvp) {
+  int64_t s0;
+  int seqlen, nstart;
+  if (!block_of(a, blockIdx.x, &s0, &seqlen, &nstart)) return;
+  const int h = blockIdx.y;
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hl = lane >> 5, c = lane & 31;
+  const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
+  const int kvh = h / (a.nq / a.nkv);
+  const int n = nstart + 32 * w + c;   // this lane's key
+  const bool nval = n < seqlen && s0 + n < a.n_tokens;
+  __shared__ __attribute__((aligned(16))) f16 Qs[kBN * kPR];
+  __shared__ __attribute__((aligned(16))) f16 Ds[kBN * kPR];
+  __shared__ __attribute__((aligned(16))) f16 Qt[kHD * kPT];
+  __shared__ __attribute__((aligned(16))) f16 Dt[kHD * kPT];
+  __shared__ float lse_s[kBN], dl_s[kBN];
+
+  f16x8 kf[kHD / 16], vf[kHD / 16];
+  row_frags(a.qkv + (s0 + n) * ROW + (int64_t)(a.nq + kvh) * kHD, nval, hl, kf);
+  row_frags(a.qkv + (s0 + n) * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD, nval, hl, vf);
+  f32x16 dkacc[kHD / 32], dvacc[kHD / 32];
+#pragma unroll
+  for (int hb = 0; hb < kHD / 32; ++hb) dkacc[hb] = dvacc[hb] = zero16();
+  const f16* qbase = a.qkv + (int64_t)h * kHD;
+  const f16* dbase = dout + (int64_t)h * kHD;
+  for (int m0 = nstart; m0 < seqlen; m0 += kBN) {
+    __syncthreads();
+    stage_rows(qbase, ROW, s0, m0, seqlen, a.n_tokens, Qs, Qt);
+    stage_rows(dbase, OROW, s0, m0, seqlen, a.n_tokens, Ds, Dt);
+    if (tid < 2 * kBN) {
+      const int r = tid & (kBN - 1), q = m0 + r;
+      const bool ok = q < seqlen && s0 + q < a.n_tokens;
+      const float* src = tid < kBN ? lse : delta;
+      const float v = ok ? src[(int64_t)h * a.n_tokens + s0 + q] : 0.0f;
+      if (tid < kBN) lse_s[r] = v; else dl_s[r] = v;
+    }
+    __syncthreads();
+    // S = Q K^T and dP = dO V^T: queries qb * 32 + (row of the result), keys on the lanes
+    f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s)
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb) {
+        const int o = (qb * 32 + c) * kPR + 16 * s + 8 * hl;
+        sacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Qs + o), kf[s], sacc[qb]);
+        dpacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Ds + o), vf[s], dpacc[qb]);
+      }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const int r = qb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3), q = m0 + r;
+        const float p = q >= n && q < seqlen && nval
+                            ? exp2f(__fsub_rn(__fmul_rn(sacc[qb][v], a.qk_scale), lse_s[r]))
+                            : 0.0f;
+        sacc[qb][v] = p;                                              // P
+        dpacc[qb][v] = __fmul_rn(p, __fsub_rn(dpacc[qb][v], dl_s[r]));  // dS
+      }
+    // dV += P^T dO, dK += dS^T Q over the tile's 64 queries, 16 per step
+#pragma unroll
+    for (int t = 0; t < kBN / 16; ++t) {
+      const int qb = t >> 1, i0 = 8 * (t & 1);
+      f16x8 pf, dsf;
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        pf[j] = (f16)sacc[qb][i0 + j];
+        dsf[j] = (f16)dpacc[qb][i0 + j];
+      }
+#pragma unroll
+      for (int hb = 0; hb < kHD / 32; ++hb) {
+        dvacc[hb] = mfma(pf, read_t8(Dt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dvacc[hb]);
+        dkacc[hb] = mfma(dsf, read_t8(Qt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dkacc[hb]);
+      }
+    }
+  }
+  // result register v of block hb: key 32 w + 8 (v / 4) + 4 (l / 32) + v % 4, column hb * 32 + c
+#pragma unroll
+  for (int v = 0; v < 16; ++v) {
+    const int key = nstart + 32 * w + 8 * (v >> 2) + 4 * hl + (v & 3);
+    if (key >= seqlen || s0 + key >= a.n_tokens) continue;
+    const int64_t off = (s0 + key) * OROW + h * kHD + c;
+#pragma unroll
+    for (int hb = 0; hb < kHD / 32; ++hb) {
+      dkp[off + hb * 32] = __fmul_rn(dkacc[hb][v], a.sm_scale);
+      dvp[off + hb * 32] = dvacc[hb][v];
+    }
+  }
+}
+
+int attn_args(AttnArgs& a, const void* qkv, const int32_t* cu, int32_t n_seq, const int32_t* tab,
+              int32_t n_blocks, int64_t n_tokens, int32_t nq, int32_t nkv, int32_t hd) {
+  if (hd != kHD || nq < 1 || nkv < 1 || nq % nkv || nq > 65535 || n_seq < 0 || n_blocks < 0 ||
+      n_tokens < 0)
+    return DK_ERR_INVALID;
+  if (n_blocks > 0 && (!qkv || !cu || !tab || n_seq < 1)) return DK_ERR_INVALID;
+  if (!dk_aligned(qkv, 16) || !dk_aligned(cu, 4) || !dk_aligned(tab, 4)) return DK_ERR_ALIGN;
+  const double log2e = 1.4426950408889634;
+  a = AttnArgs{(const f16*)qkv, cu, tab, n_seq, n_tokens, nq, nkv,
+               (float)(log2e / __builtin_sqrt((double)hd)), (float)(1.0 / __builtin_sqrt((double)hd))};
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int dk_attn_fwd(const void* qkv, const int32_t* cu_seqlens, int32_t n_seq,
+                           const int32_t* block_table, int32_t n_blocks, int64_t n_tokens,
+                           int32_t nq, int32_t nkv, int32_t hd, void* out, float* lse,
+                           hipStream_t stream) {
+  AttnArgs a;
+  if (int e = attn_args(a, qkv, cu_seqlens, n_seq, block_table, n_blocks, n_tokens, nq, nkv, hd))
+    return e;
+  if (n_blocks == 0) return 0;
+  if (!out || !lse) return DK_ERR_INVALID;
+  if (!dk_aligned(out, 16) || !dk_aligned(lse, 4)) return DK_ERR_ALIGN;
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
+                     stream, a, (f16*)out, lse);
+  DK_CHECK_LAUNCH();
+  return 0;
+}
+
+extern "C" int dk_attn_bwd(const void* qkv, const void* out, const float* lse, const void* dout,
+                           const int32_t* cu_seqlens, int32_t n_seq, const int32_t* block_table,
+                           int32_t n_blocks, int64_t n_tokens, int32_t nq, int32_t nkv, int32_t hd,
+                           float* delta, float* dq, float* dkp, float* dvp, hipStream_t stream) {
+  AttnArgs a;
+  if (int e = attn_args(a, qkv, cu_seqlens, n_seq, block_table, n_blocks, n_tokens, nq, nkv, hd))
+    return e;
+  if (n_blocks == 0 || n_tokens == 0) return 0;
+  if (!out || !lse || !dout || !delta || !dq || !dkp || !dvp) return DK_ERR_INVALID;
+  if (!dk_aligned(out, 16) || !dk_aligned(dout, 16) || !dk_aligned(lse, 4) ||
+      !dk_aligned(delta, 4) || !dk_aligned(dq, 16) || !dk_aligned(dkp, 4) || !dk_aligned(dvp, 4))
+    return DK_ERR_ALIGN;
+  const int64_t pairs = n_tokens * nq;
+  hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kAThreads), 0,
+                     stream, (const f16*)out, (const f16*)dout, delta, n_tokens, nq);
+  DK_CHECK_LAUNCH();
+  hipLaunchKernelGGL(attn_dkdv_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
+                     stream, a, (const f16*)dout, lse, delta, dkp, dvp);
+  DK_CHECK_LAUNCH();
+  hipLaunchKernelGGL(attn_dq_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
+                     stream, a, (const f16*)dout, lse, delta, dq);
+  DK_CHECK_LAUNCH();
+  return 0;
+}

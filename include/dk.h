@@ -122,6 +122,25 @@ int dk_qkv_epilogue_bwd(const void* dq, const void* dk, const void* dv, int grad
                         hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
+ * Variable-length causal GQA attention of the packed batch (the consumer of the QKV epilogue).
+ * qkv [n_tokens, (nq + 2 nkv) hd] fp16 as the QKV epilogue writes it; cu_seqlens [n_seq + 1]
+ * int32; block_table: n_blocks (sequence, first row) int32 pairs, blocks of 128 rows that never
+ * straddle two sequences (k_attn.block_table(lens, 128)); hd = 128, nq % nkv == 0.  Scores use
+ * the scale log2(e) / sqrt(hd) in the exp2 domain.
+ * dk_attn_fwd replaces attention_forward (solution/k_attn.py:40-83, 202-212): out
+ * [n_tokens, nq hd] fp16, lse [nq, n_tokens] fp32 = m + log2(l) per (head, token).
+ * dk_attn_bwd replaces attention_backward (solution/k_attn.py:84-182, 215-245): delta
+ * [nq, n_tokens] fp32 scratch, dq [n_tokens, nq hd] fp32, dkp / dvp [n_tokens, nq hd] fp32
+ * per-query-head partials (dk_qkv_epilogue_bwd with gin = nq / nkv sums them). */
+int dk_attn_fwd(const void* qkv, const int32_t* cu_seqlens, int32_t n_seq,
+                const int32_t* block_table, int32_t n_blocks, int64_t n_tokens, int32_t nq,
+                int32_t nkv, int32_t hd, void* out, float* lse, hipStream_t stream);
+int dk_attn_bwd(const void* qkv, const void* out, const float* lse, const void* dout,
+                const int32_t* cu_seqlens, int32_t n_seq, const int32_t* block_table,
+                int32_t n_blocks, int64_t n_tokens, int32_t nq, int32_t nkv, int32_t hd,
+                float* delta, float* dq, float* dkp, float* dvp, hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
  * LoRA down projection with the dropout of its input.  Replaces the norm kernel's dropout lines
  * and the lora_A GEMM (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944):
  *   Xd = fp16(mask ? fp32(x) * keep_scale : 0),   z = fp16(Xd A^T)

@@ -1,0 +1,81 @@
+"""GPU parity of the packed-batch causal GQA attention (dk_attn_fwd / dk_attn_bwd) with the
+oracle, on the reference test's batches (solution/test_kernels.py:272-305: lens [1, 37, 64, 200]
+and [512, 511, 3, 129], qkv ~ 0.8 N(0, 1), out to 3e-3, gradients to 3e-2 / 2e-2) and a config-like
+batch of four 512-token sequences; the per-query-head dK/dV partials are checked head by head and
+through the QKV epilogue backward that sums them (GIN = 6)."""
+
+import numpy as np
+import pytest
+
+from tests.helpers import host, log
+
+pytestmark = pytest.mark.gpu
+NQ, NKV, HD = 12, 2, 128
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    return t
+
+
+def _close(got, want, rtol, atol, what):
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    bad = np.abs(got - want) > atol + rtol * np.abs(want)
+    assert not bad.any(), f"{what}: {bad.sum()} of {bad.size} beyond tolerance, max err " \
+                          f"{np.abs(got - want).max():.3g}"
+
+
+@pytest.mark.parametrize("lens", [[1, 37, 64, 200], [512, 511, 3, 129], [512, 512, 512, 512]])
+def test_varlen_causal_gqa_attention(torch, lens):
+    from decentrik_prime_amd import k_attn, k_rope
+    from oracle import attn, rope
+    log(f"attention fwd+bwd, lens {lens}")
+    n, g = sum(lens), NQ // NKV
+    rng = np.random.default_rng(sum(lens))
+    qkv = (rng.standard_normal((n, (NQ + 2 * NKV) * HD)) * 0.8).astype(np.float16)
+    dout = rng.standard_normal((n, NQ * HD)).astype(np.float16)
+    meta = k_attn.meta_for(lens, "cuda")
+    tq = torch.from_numpy(qkv).cuda()
+    out, lse = k_attn.attention_forward(tq, meta, NQ, NKV, HD)
+    td = torch.from_numpy(dout).cuda()
+    dq, dkp, dvp = k_attn.attention_backward(tq, out, lse, td, meta, NQ, NKV, HD)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = attn.attention_fwd(qkv, lens, NQ, NKV, HD)
+    _close(host(out), o_ref, 3e-3, 3e-3, "attention out")
+    _close(host(lse), lse_ref, 1e-5, 2e-4, "lse (log2 domain)")
+    dq_ref, dkp_ref, dvp_ref = attn.attention_bwd(qkv, dout, lens, NQ, NKV, HD, out=host(out))
+    _close(host(dq), dq_ref, 3e-2, 2e-2, "dq")
+    _close(host(dkp), dkp_ref, 3e-2, 2e-2, "dk per query head")
+    _close(host(dvp), dvp_ref, 3e-2, 2e-2, "dv per query head")
+    _close(host(dkp).reshape(n, NKV, g, HD).sum(2), dkp_ref.reshape(n, NKV, g, HD).sum(2), 3e-2,
+           2e-2, "dk")
+    _close(host(dvp).reshape(n, NKV, g, HD).sum(2), dvp_ref.reshape(n, NKV, g, HD).sum(2), 3e-2,
+           2e-2, "dv")
+    # the partials through the QKV epilogue backward (transposed rotation + GQA sums)
+    pos = np.concatenate([np.arange(L) for L in lens]).astype(np.int32)
+    cos, sin = rope.rope_tables(max(lens), HD)
+    tqkv_grad = torch.empty(n, (NQ + 2 * NKV) * HD, dtype=torch.float16, device="cuda")
+    k_rope.qkv_epilogue_backward(dq, dkp.view(n, NQ * HD), dvp.view(n, NQ * HD),
+                                 torch.from_numpy(pos).cuda(), torch.from_numpy(cos).cuda(),
+                                 torch.from_numpy(sin).cuda(), tqkv_grad, NQ, NKV, HD, g)
+    torch.cuda.synchronize()
+    want = rope.qkv_epilogue_bwd(dq_ref.astype(np.float32), dkp_ref.astype(np.float32),
+                                 dvp_ref.astype(np.float32), pos, cos, sin, NQ, NKV, HD, g)
+    _close(host(tqkv_grad), want, 3e-2, 3e-2, "dqkv through the QKV epilogue backward")
+
+
+def test_attention_argument_checks(torch):
+    from decentrik_prime_amd import k_attn
+    meta = k_attn.meta_for([5, 7], "cuda")
+    qkv = torch.zeros(12, (NQ + 2 * NKV) * HD, dtype=torch.float16, device="cuda")
+    with pytest.raises(ValueError):
+        k_attn.attention_forward(qkv, meta, NQ, NKV, 64)             # head size
+    with pytest.raises(ValueError):
+        k_attn.attention_forward(qkv, meta, NQ, NKV, HD, block_m=64)  # fixed blocks
+    with pytest.raises(ValueError):
+        k_attn.attention_forward(qkv[:11], meta, NQ, NKV, HD)         # rows != tokens
+    bad = k_attn.AttnMeta(meta.cu, meta.tab_fwd[:1], meta.tab_bwd, 1, meta.n_bwd, 12)
+    with pytest.raises(ValueError):
+        k_attn.attention_forward(qkv, bad, NQ, NKV, HD)               # table length
