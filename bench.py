@@ -141,10 +141,12 @@ def kernel_table(torch, st, reps, only=None):
 
 def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None):
     """The kernels on either side of the LoRA'd q/v linear (RMSNorm + dropout forward, its
-    backward with the LoRA input grads, the QKV epilogue forward and backward), each in isolation
+    backward with the LoRA input grads, the QKV epilogue forward and backward, and the causal GQA
+    attention that consumes the QKV buffer, on four sequences of M / 4 tokens), each in isolation
     at config 4's shapes (M tokens, hidden 1536, 12 query / 2 KV heads of 128), with their
-    algorithmic HBM bytes.  They are not part of the linear stack's step."""
-    from decentrik_prime_amd import k_norm, k_rope
+    algorithmic HBM bytes (or, for the attention, FLOPs).  They are not part of the linear stack's
+    step."""
+    from decentrik_prime_amd import k_attn, k_norm, k_rope
     dev = "cuda"
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -172,6 +174,14 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
     dq = torch.randn(m, nq * hd, device=dev, generator=g)
     dk, dv = (torch.randn(m, nkv * gin * hd, device=dev, generator=g) for _ in range(2))
     qkv_out = torch.empty(m, row, dtype=f16, device=dev)
+    lens = [m // 4] * 4
+    meta = k_attn.meta_for(lens, dev)
+    aqkv = (torch.randn(m, row, device=dev, generator=g) * 0.8).half()
+    aout, alse = k_attn.attention_forward(aqkv, meta, nq, nkv, hd)
+    adout = torch.randn(m, nq * hd, device=dev, generator=g).half()
+    # causal: hd L (L + 1) FLOP per (sequence, head) for each of Q K^T and P V; the backward's
+    # S, dP, dV, dK, dQ are 2.5 times that
+    att_fwd = sum(2 * hd * L * (L + 1) for L in lens) * nq
     e = m * d
     rows = [
         ("rms_fwd norm+dropout", lambda: k_norm.rms_forward(
@@ -186,12 +196,22 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
         ("qkv_epilogue_bwd rope^T+gqa", lambda: k_rope.qkv_epilogue_backward(
             dq, dk, dv, pos, cos, sin, qkv_out, nq, nkv, hd, gin),
          m * (nq * hd * 4 + 2 * nkv * gin * hd * 4 + row * 2 + hd * 4)),
+        ("attention_fwd causal gqa", lambda: k_attn.attention_forward(aqkv, meta, nq, nkv, hd),
+         None, att_fwd),
+        ("attention_bwd causal gqa", lambda: k_attn.attention_backward(
+            aqkv, aout, alse, adout, meta, nq, nkv, hd), None, 2.5 * att_fwd),
     ]
     res = []
-    for name, fn, nbytes in rows:
+    for name, fn, nbytes, *flops in rows:
         if only is not None and name not in only:
             continue
         ms = time_op(torch, fn, reps)
+        if nbytes is None:
+            tf = flops[0] / (ms * 1e-3) / 1e12
+            res.append({"kernel": name, "avg_us": round(ms * 1e3, 2),
+                        "gflop": round(flops[0] / 1e9, 3), "tflops": round(tf, 1),
+                        "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)})
+            continue
         gbps = nbytes / (ms * 1e-3) / 1e9
         res.append({"kernel": name, "avg_us": round(ms * 1e3, 2), "bytes": int(nbytes),
                     "gbps": round(gbps, 1), "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)})

@@ -64,6 +64,10 @@ __device__ __forceinline__ f16x8 read_t8(const f16* row, int p) {
   return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// 2^x on the hardware exponential (v_exp_f32); arguments here are <= 0 (scores minus their row
+// maximum or log-sum-exp), results below the normal range flush to zero.
+__device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
+
 // The sequence of a block-table entry; false when the entry names no sequence or a sequence that
 // does not lie within the n_tokens rows (then every row and loop of the workgroup stays in bounds
 // whatever the tables hold).
@@ -77,60 +81,44 @@ __device__ __forceinline__ bool block_of(const AttnArgs& a, int blk, int64_t* s0
   return *s0 >= 0 && *seqlen >= 0 && *s0 + *seqlen <= a.n_tokens;
 }
 
-// Rows [r0, r0 + kBN) of one head (column offset col of rows with stride ld) into a row-major LDS
-// tile and, if tr, also into a transposed one (tr[c][r], pairs of rows packed per dword).  Rows
-// at or past `valid` (or past the buffer) read as zero.  All loads are issued before the stores.
-__device__ __forceinline__ void stage_rows(const f16* base, int64_t ld, int64_t s0, int r0,
-                                           int valid, int64_t n_tokens, f16* rm, f16* tr) {
-  const int tid = threadIdx.x;
+// Rows [r0, r0 + kBN) of one head (column offset folded into base, row stride ld), 8 halves per
+// 16-byte piece, two rows per item and two items per thread, read into registers (rows at or past
+// `valid`, or past the buffer, read as zero); the next tile's rows are read this way while the
+// current tile is computed on.
+struct RowTile {
   f16x8 v[2][2];
+};
+
+__device__ __forceinline__ void load_rows(RowTile& t, const f16* base, int64_t ld, int64_t s0,
+                                          int r0, int valid, int64_t n_tokens) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+    const int it = threadIdx.x + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       const int r = r0 + 2 * rp + u;
-      v[q][u] = r < valid && s0 + r < n_tokens
-                    ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
-                    : zero8();
-    }
-  }
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
-#pragma unroll
-    for (int u = 0; u < 2; ++u)
-      *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = v[q][u];
-    if (tr) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(v[q][0][e], v[q][1][e]);
+      t.v[q][u] = r < valid && s0 + r < n_tokens
+                      ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
+                      : zero8();
     }
   }
 }
 
-// Like stage_rows, but only the transposed tile.
-__device__ __forceinline__ void stage_rows_t(const f16* base, int64_t ld, int64_t s0, int r0,
-                                             int valid, int64_t n_tokens, f16* tr) {
-  const int tid = threadIdx.x;
-  f16x8 v[2][2];
+// The rows into a row-major LDS tile rm[r][c] (if rm) and a transposed one tr[c][r] (if tr; the
+// two rows of an item packed per dword).
+__device__ __forceinline__ void store_rows(const RowTile& t, f16* rm, f16* tr) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
-    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+    const int it = threadIdx.x + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
+    if (rm) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int r = r0 + 2 * rp + u;
-      v[q][u] = r < valid && s0 + r < n_tokens
-                    ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
-                    : zero8();
+      for (int u = 0; u < 2; ++u) *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = t.v[q][u];
     }
-  }
+    if (tr) {
 #pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int it = tid + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
-#pragma unroll
-    for (int e = 0; e < 8; ++e)
-      *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(v[q][0][e], v[q][1][e]);
+      for (int e = 0; e < 8; ++e)
+        *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(t.v[q][0][e], t.v[q][1][e]);
+    }
   }
 }
 
@@ -167,9 +155,14 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
   const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
   const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
   for (int n0 = 0; n0 < hi; n0 += kBN) {
+    // (measured: prefetching the next tile into registers here, as the backward kernels do, made
+    // this kernel slower, not faster)
+    RowTile kt, vt;
+    load_rows(kt, kbase, ROW, s0, n0, seqlen, a.n_tokens);
+    load_rows(vt, vbase, ROW, s0, n0, seqlen, a.n_tokens);
     __syncthreads();   // every wave has finished reading the previous tile
-    stage_rows(kbase, ROW, s0, n0, seqlen, a.n_tokens, Ks, nullptr);
-    stage_rows_t(vbase, ROW, s0, n0, seqlen, a.n_tokens, Vt);
+    store_rows(kt, Ks, nullptr);
+    store_rows(vt, nullptr, Vt);
     __syncthreads();
     // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
     f32x16 sacc[2] = {zero16(), zero16()};
@@ -285,11 +278,18 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
   const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
   const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
   const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
+  RowTile kt, vt;
+  load_rows(kt, kbase, ROW, s0, 0, seqlen, a.n_tokens);
+  load_rows(vt, vbase, ROW, s0, 0, seqlen, a.n_tokens);
   for (int n0 = 0; n0 < hi; n0 += kBN) {
     __syncthreads();
-    stage_rows(kbase, ROW, s0, n0, seqlen, a.n_tokens, Ks, Kt);
-    stage_rows(vbase, ROW, s0, n0, seqlen, a.n_tokens, Vs, nullptr);
+    store_rows(kt, Ks, Kt);
+    store_rows(vt, Vs, nullptr);
     __syncthreads();
+    if (n0 + kBN < hi) {
+      load_rows(kt, kbase, ROW, s0, n0 + kBN, seqlen, a.n_tokens);
+      load_rows(vt, vbase, ROW, s0, n0 + kBN, seqlen, a.n_tokens);
+    }
     f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s)
@@ -299,13 +299,14 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
         sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Ks + o), qf[s], sacc[kb]);     // S^T
         dpacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Vs + o), dof[s], dpacc[kb]);  // dP^T
       }
+    const bool full = n0 + kBN - 1 <= mstart + 32 * w && n0 + kBN <= seqlen;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-        const float p = n <= m && n < seqlen && mval
-                            ? exp2f(__fsub_rn(__fmul_rn(sacc[kb][v], a.qk_scale), lse_m))
+        const float p = mval && (full || (n <= m && n < seqlen))
+                            ? ex2(__fsub_rn(__fmul_rn(sacc[kb][v], a.qk_scale), lse_m))
                             : 0.0f;
         sacc[kb][v] = __fmul_rn(p, __fsub_rn(dpacc[kb][v], dl_m));   // dS^T
       }
@@ -365,18 +366,28 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
   for (int hb = 0; hb < kHD / 32; ++hb) dkacc[hb] = dvacc[hb] = zero16();
   const f16* qbase = a.qkv + (int64_t)h * kHD;
   const f16* dbase = dout + (int64_t)h * kHD;
+  // lse (threads [0, kBN)) or delta (threads [kBN, 2 kBN)) of query m0 + (tid % kBN)
+  auto load_stat = [&](int m0) {
+    const int q = m0 + (tid & (kBN - 1));
+    const bool ok = tid < 2 * kBN && q < seqlen && s0 + q < a.n_tokens;
+    return ok ? (tid < kBN ? lse : delta)[(int64_t)h * a.n_tokens + s0 + q] : 0.0f;
+  };
+  RowTile qt, dt;
+  load_rows(qt, qbase, ROW, s0, nstart, seqlen, a.n_tokens);
+  load_rows(dt, dbase, OROW, s0, nstart, seqlen, a.n_tokens);
+  float stat = load_stat(nstart);
   for (int m0 = nstart; m0 < seqlen; m0 += kBN) {
     __syncthreads();
-    stage_rows(qbase, ROW, s0, m0, seqlen, a.n_tokens, Qs, Qt);
-    stage_rows(dbase, OROW, s0, m0, seqlen, a.n_tokens, Ds, Dt);
-    if (tid < 2 * kBN) {
-      const int r = tid & (kBN - 1), q = m0 + r;
-      const bool ok = q < seqlen && s0 + q < a.n_tokens;
-      const float* src = tid < kBN ? lse : delta;
-      const float v = ok ? src[(int64_t)h * a.n_tokens + s0 + q] : 0.0f;
-      if (tid < kBN) lse_s[r] = v; else dl_s[r] = v;
-    }
+    store_rows(qt, Qs, Qt);
+    store_rows(dt, Ds, Dt);
+    if (tid < kBN) lse_s[tid] = stat;
+    else if (tid < 2 * kBN) dl_s[tid - kBN] = stat;
     __syncthreads();
+    if (m0 + kBN < seqlen) {
+      load_rows(qt, qbase, ROW, s0, m0 + kBN, seqlen, a.n_tokens);
+      load_rows(dt, dbase, OROW, s0, m0 + kBN, seqlen, a.n_tokens);
+      stat = load_stat(m0 + kBN);
+    }
     // S = Q K^T and dP = dO V^T: queries qb * 32 + (row of the result), keys on the lanes
     f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
 #pragma unroll
@@ -387,13 +398,15 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
         sacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Qs + o), kf[s], sacc[qb]);
         dpacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Ds + o), vf[s], dpacc[qb]);
       }
+    // every query of the tile at or after every key of this wave, all inside the sequence
+    const bool full = m0 >= nstart + 32 * w + 31 && m0 + kBN <= seqlen;
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = qb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3), q = m0 + r;
-        const float p = q >= n && q < seqlen && nval
-                            ? exp2f(__fsub_rn(__fmul_rn(sacc[qb][v], a.qk_scale), lse_s[r]))
+        const float p = nval && (full || (q >= n && q < seqlen))
+                            ? ex2(__fsub_rn(__fmul_rn(sacc[qb][v], a.qk_scale), lse_s[r]))
                             : 0.0f;
         sacc[qb][v] = p;                                              // P
         dpacc[qb][v] = __fmul_rn(p, __fsub_rn(dpacc[qb][v], dl_s[r]));  // dS

@@ -146,6 +146,18 @@ def test_norm_and_rope_argument_errors_come_back_before_launch():
         return lib.dk_h16_linear_fwd_rope(p16, 1536, m, w16, 2048, 1536, None, None, 0, 0,
                                           None if rope is None else ctypes.byref(rope), p16, 2048,
                                           None, None)
+    # attention: head size 128, nq a multiple of nkv, pointers and alignment; no blocks = no launch
+    assert lib.dk_attn_fwd(p16, p16, 1, p16, 4, 100, 12, 2, 64, p16, p16, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_attn_fwd(p16, p16, 1, p16, 4, 100, 12, 5, 128, p16, p16, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_attn_fwd(p16, p16, 1, p16, 4, 100, 12, 2, 128, None, p16, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_attn_fwd(p8, p16, 1, p16, 4, 100, 12, 2, 128, p16, p16, None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_attn_fwd(p16, p16, 1, p16, 0, 100, 12, 2, 128, None, None, None) == 0
+    assert lib.dk_attn_bwd(p16, p16, p16, p16, p16, 1, p16, 4, 100, 12, 2, 128, p16, p16, p16, None,
+                           None) == _lib.DK_ERR_INVALID                  # no dv
+    assert lib.dk_attn_bwd(p16, p16, p16, p8, p16, 1, p16, 4, 100, 12, 2, 128, p16, p16, p16, p16,
+                           None) == _lib.DK_ERR_ALIGN                    # dout
+    assert lib.dk_attn_bwd(p16, p16, p16, p16, p16, 1, p16, 4, 0, 12, 2, 128, None, None, None, None,
+                           None) == 0                                    # no tokens
     ok = _lib.RopeC(p16, p16, p16, 128, 1792)
     assert fused(None) == _lib.DK_ERR_INVALID
     assert fused(ok, w16=None) == _lib.DK_ERR_INVALID
