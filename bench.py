@@ -552,8 +552,10 @@ def main():
                                                 "traffic": dq_traffic["bytes"] if dq_traffic else None}}
         result["kernels"] = kernels
         result["neighbours"] = neighbour_table(torch, args.reps, args.m)
-        print("[bench] " + ", ".join(f"{r['kernel']} {r['avg_us']} us {r['gbps']} GB/s"
-                                     for r in result["neighbours"]), file=sys.stderr, flush=True)
+        print("[bench] " + ", ".join(
+            f"{r['kernel']} {r['avg_us']} us " + (f"{r['gbps']} GB/s" if "gbps" in r
+                                                  else f"{r['tflops']} TFLOP/s")
+            for r in result["neighbours"]), file=sys.stderr, flush=True)
     if not args.no_cpu:
         print(f"[bench] CPU baseline (oracle, {args.cpu_layers} layers)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_layers, args.m)
