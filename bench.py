@@ -146,7 +146,7 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
     at config 4's shapes (M tokens, hidden 1536, 12 query / 2 KV heads of 128), with their
     algorithmic HBM bytes (or, for the attention, FLOPs).  They are not part of the linear stack's
     step."""
-    from decentrik_prime_amd import k_attn, k_norm, k_rope
+    from decentrik_prime_amd import k_attn, k_head, k_norm, k_rope
     dev = "cuda"
     g = torch.Generator(device=dev)
     g.manual_seed(7)
@@ -182,6 +182,16 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
     # causal: hd L (L + 1) FLOP per (sequence, head) for each of Q K^T and P V; the backward's
     # S, dP, dV, dK, dQ are 2.5 times that
     att_fwd = sum(2 * hd * L * (L + 1) for L in lens) * nq
+    # LM head over Qwen2.5's 151,936-token vocabulary, every row with a target: the logits GEMM
+    # and the P E accumulation, 2 M V D FLOP each
+    vocab = 151936
+    emb = (torch.randn(vocab, d, device=dev, generator=g) * 0.02).half()
+    yh = torch.randn(m, d, device=dev, generator=g).half()
+    tg = torch.randint(0, vocab, (m,), device=dev, dtype=torch.int32, generator=g)
+    ident = torch.arange(m, device=dev, dtype=torch.int32)
+    et = emb.index_select(0, tg.long()).contiguous()
+    src = k_head.ResidentEmbedding(emb)
+    head_flops = 2 * 2 * m * vocab * d
     e = m * d
     rows = [
         ("rms_fwd norm+dropout", lambda: k_norm.rms_forward(
@@ -200,6 +210,8 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
          None, att_fwd),
         ("attention_bwd causal gqa", lambda: k_attn.attention_backward(
             aqkv, aout, alse, adout, meta, nq, nkv, hd), None, 2.5 * att_fwd),
+        ("lm_head streamed loss+grad", lambda: k_head.streamed_head(
+            yh, src, tg, ident, m, et, 1.0), None, head_flops),
     ]
     res = []
     for name, fn, nbytes, *flops in rows:

@@ -117,6 +117,9 @@ SIGNATURES = {
     "dk_attn_fwd": (_int, [_c_p, _c_p, _int, _c_p, _int, _i64, _int, _int, _int, _c_p, _c_p, _c_p]),
     "dk_attn_bwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _int, _c_p, _int, _i64, _int, _int, _int,
                            _c_p, _c_p, _c_p, _c_p, _c_p]),
+    "dk_head_chunk": (_int, [_c_p, _c_p, _c_p, _c_p, _i64, _i64, _i64, _i64, _f32, _i64, _c_p]),
+    "dk_head_finalize": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64, _f32, _f32,
+                                _i64, _c_p]),
     "dk_w4_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_w4_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _W, _c_p, _c_p, _i64, _c_p]),
 }

@@ -141,6 +141,26 @@ int dk_attn_bwd(const void* qkv, const void* out, const float* lse, const void* 
                 float* delta, float* dq, float* dkp, float* dvp, hipStream_t stream);
 
 /* ------------------------------------------------------------------------------------------
+ * LM head over vocabulary chunks (the consumer of the final norm): the row kernels between the
+ * two GEMMs of each chunk (logits_c = Y E_c^T by dk_h16_linear_fwd_lora, acc += P E_c by
+ * dk_h16_linear_bwd_dx_lora with DK_OUT_F32_ACCUM).  Rows are in sorted order (rows with a target
+ * first, n_lab of them); state [n_rows, 8] fp32 = (m, s, t, argmax, x_target, pad), m = -inf and
+ * the rest 0 before the first chunk; acc [n_lab, d] fp32 starts at 0.
+ * dk_head_chunk replaces head_chunk_kernel (solution/k_head.py:50-123): logits [n_rows, vc] fp16
+ * of chunk [v0, v0 + vc) (vc % 8 == 0), merged into the state; rows r < n_lab get
+ * P = p_scale e^(x - m) in place (0 in the target's column) and their acc rows rescaled.
+ * dk_head_finalize replaces head_finalize_kernel (solution/k_head.py:126-161): stats [n_rows, 4]
+ * = (loss, entropy, hit, lse), and dy [n_rows, d] fp16 row perm[r] = out_scale (acc / (p_scale s)
+ * + (p_target - 1) e_target[r]) for r < n_lab, 0 otherwise (inv_p_scale = 1 / p_scale). */
+int dk_head_chunk(void* logits, const int32_t* tgt_sorted, float* state, float* acc,
+                  int64_t n_rows, int64_t n_lab, int64_t vc, int64_t v0, float p_scale, int64_t d,
+                  hipStream_t stream);
+int dk_head_finalize(const float* state, const int32_t* tgt_sorted, const int32_t* perm,
+                     const float* acc, const void* e_target, float* stats, void* dy,
+                     int64_t n_rows, int64_t n_lab, float out_scale, float inv_p_scale, int64_t d,
+                     hipStream_t stream);
+
+/* ------------------------------------------------------------------------------------------
  * LoRA down projection with the dropout of its input.  Replaces the norm kernel's dropout lines
  * and the lora_A GEMM (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944):
  *   Xd = fp16(mask ? fp32(x) * keep_scale : 0),   z = fp16(Xd A^T)

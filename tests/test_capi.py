@@ -158,6 +158,16 @@ def test_norm_and_rope_argument_errors_come_back_before_launch():
                            None) == _lib.DK_ERR_ALIGN                    # dout
     assert lib.dk_attn_bwd(p16, p16, p16, p16, p16, 1, p16, 4, 0, 12, 2, 128, None, None, None, None,
                            None) == 0                                    # no tokens
+    # LM head row kernels: chunk width a multiple of 8, n_lab within the rows, hidden a multiple of 4
+    assert lib.dk_head_chunk(p16, p16, p16, p16, 8, 4, 100, 0, 1.0, 1536, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_head_chunk(p16, p16, p16, p16, 8, 9, 128, 0, 1.0, 1536, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_head_chunk(p16, p16, p16, None, 8, 4, 128, 0, 1.0, 1536, None) == _lib.DK_ERR_INVALID
+    assert lib.dk_head_chunk(p8, p16, p16, p16, 8, 4, 128, 0, 1.0, 1536, None) == _lib.DK_ERR_ALIGN
+    assert lib.dk_head_chunk(p16, p16, p16, None, 0, 0, 128, 0, 1.0, 1536, None) == 0
+    assert lib.dk_head_finalize(p16, p16, p16, p16, None, p16, p16, 8, 4, 1.0, 1.0, 1536,
+                                None) == _lib.DK_ERR_INVALID            # targets without E_t rows
+    assert lib.dk_head_finalize(p16, p16, p16, p16, p16, p16, p4, 8, 4, 1.0, 1.0, 1536,
+                                None) == _lib.DK_ERR_ALIGN
     ok = _lib.RopeC(p16, p16, p16, 128, 1792)
     assert fused(None) == _lib.DK_ERR_INVALID
     assert fused(ok, w16=None) == _lib.DK_ERR_INVALID
