@@ -108,8 +108,8 @@ SIGNATURES = {
                              _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_rms_fwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64,
                           _f32, _f32, _c_p]),
-    "dk_rms_bwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
-                          _c_p, _i64, _i64, _f32, _c_p]),
+    "dk_rms_bwd": (_int, [_c_p, _int, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p,
+                          _c_p, _c_p, _i64, _i64, _f32, _c_p]),
     "dk_qkv_epilogue_fwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _f32, _int, _int, _int,
                                    _c_p]),
     "dk_qkv_epilogue_bwd": (_int, [_c_p, _c_p, _c_p, _int, _c_p, _c_p, _c_p, _c_p, _i64, _int, _int,

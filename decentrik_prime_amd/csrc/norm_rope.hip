@@ -103,9 +103,9 @@ __global__ __launch_bounds__(kRowThreads) void rms_fwd_kernel(
 
 // RMSNorm backward (solution/k_norm.py:61-88): dy = fp16 grad * gscale + the masked LoRA input
 // grads, dx = rstd (w dy - xhat mean(w dy xhat)) [+ dres]; out may alias dres.
-template <int KMAX>
+template <int KMAX, bool DY32>
 __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
-    const f16* __restrict__ dy16, const float* __restrict__ gscale, const float* __restrict__ x,
+    const void* __restrict__ dyp, const float* __restrict__ gscale, const float* __restrict__ x,
     const f16* __restrict__ delta, const float* __restrict__ w, const float* __restrict__ rstd,
     const float* dres, float* out, const f16* __restrict__ lq, const f16* __restrict__ lv,
     f16* __restrict__ out16, const uint8_t* __restrict__ mq, const uint8_t* __restrict__ mv,
@@ -122,7 +122,8 @@ __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
   for (int k = 0; k < KMAX; ++k) {
     const int e = 256 * k + 4 * lane;
     if (e >= d) continue;
-    f32x4 dy = load_h4(dy16 + off + e);
+    f32x4 dy = DY32 ? *reinterpret_cast<const f32x4*>(static_cast<const float*>(dyp) + off + e)
+                    : load_h4(static_cast<const f16*>(dyp) + off + e);
 #pragma unroll
     for (int i = 0; i < 4; ++i) dy[i] = __fmul_rn(dy[i], gs);
     if (lq) {
@@ -391,16 +392,18 @@ extern "C" int dk_rms_fwd(const float* x, const void* delta, float* xout, const 
   return 0;
 }
 
-extern "C" int dk_rms_bwd(const void* dy16, const float* gscale, const float* x, const void* delta,
+extern "C" int dk_rms_bwd(const void* dy, int dy_f32, const float* gscale, const float* x,
+                          const void* delta,
                           const float* w, const float* rstd, const float* dres, float* out,
                           const void* lq, const void* lv, void* out16, const uint8_t* mq,
                           const uint8_t* mv, int64_t n_rows, int64_t d, float keep_scale,
                           hipStream_t stream) {
   if (n_rows < 0 || d < 4 || d > 4096 || d % 4) return DK_ERR_INVALID;
   if (n_rows == 0) return 0;
-  if (!dy16 || !gscale || !x || !w || !rstd || !out) return DK_ERR_INVALID;
+  if (!dy || !gscale || !x || !w || !rstd || !out) return DK_ERR_INVALID;
   if ((lq == nullptr) != (lv == nullptr) || (lq && (!mq || !mv))) return DK_ERR_INVALID;
-  if (!dk_aligned(x, 16) || !dk_aligned(w, 16) || !dk_aligned(out, 16) || !dk_aligned(dy16, 8) ||
+  if (!dk_aligned(x, 16) || !dk_aligned(w, 16) || !dk_aligned(out, 16) ||
+      !dk_aligned(dy, dy_f32 ? 16 : 8) ||
       (dres && !dk_aligned(dres, 16)) || (delta && !dk_aligned(delta, 8)) ||
       (out16 && !dk_aligned(out16, 8)) ||
       (lq && (!dk_aligned(lq, 8) || !dk_aligned(lv, 8) || !dk_aligned(mq, 4) || !dk_aligned(mv, 4))))
@@ -408,13 +411,19 @@ extern "C" int dk_rms_bwd(const void* dy16, const float* gscale, const float* x,
   if (n_rows / kRowsPerBlock >= 0x7fffffff) return DK_ERR_INVALID;
   const dim3 grid(grid_rows(n_rows)), block(kRowThreads);
   auto args = [&](auto kern) {
-    hipLaunchKernelGGL(kern, grid, block, 0, stream, (const f16*)dy16, gscale, x, (const f16*)delta,
+    hipLaunchKernelGGL(kern, grid, block, 0, stream, dy, gscale, x, (const f16*)delta,
                        w, rstd, dres, out, (const f16*)lq, (const f16*)lv, (f16*)out16, mq, mv,
                        n_rows, (int)d, keep_scale);
   };
-  if (d <= 1024) args(rms_bwd_kernel<4>);
-  else if (d <= 2048) args(rms_bwd_kernel<8>);
-  else args(rms_bwd_kernel<16>);
+  if (dy_f32) {
+    if (d <= 1024) args(rms_bwd_kernel<4, true>);
+    else if (d <= 2048) args(rms_bwd_kernel<8, true>);
+    else args(rms_bwd_kernel<16, true>);
+  } else {
+    if (d <= 1024) args(rms_bwd_kernel<4, false>);
+    else if (d <= 2048) args(rms_bwd_kernel<8, false>);
+    else args(rms_bwd_kernel<16, false>);
+  }
   DK_CHECK_LAUNCH();
   return 0;
 }

@@ -67,7 +67,8 @@ def rms_backward(dy16, gscale, x, w, rstd, out, *, dres=None, lq=None, lv=None, 
                  keep_scale=1.0, out16=None, delta=None, dummy16=None, dummy32=None):
     """delta: the norm's input is x + delta (fp16), added in registers as in the forward, so the
     backward needs no recomputed copy of it.  lq/lv (LoRA-A input grads) need the keep-masks.
-    gscale: a CUDA fp32 tensor whose first element scales dy16."""
+    gscale: a CUDA fp32 tensor whose first element scales dy16.  dy16 may also be fp32 (the fused
+    q|k|v dX GEMM's output, which already holds the masked LoRA input gradients)."""
     if x.dim() != 2:
         raise ValueError("x must be [n, d]")
     n, d = x.shape
@@ -80,13 +81,16 @@ def rms_backward(dy16, gscale, x, w, rstd, out, *, dres=None, lq=None, lv=None, 
     _t(out, torch.float32, (n, d), "out")
     if gscale.dtype != torch.float32 or not gscale.is_cuda or gscale.numel() < 1:
         raise ValueError("gscale must be a CUDA fp32 tensor")
-    for t, dt, nm in ((dy16, torch.float16, "dy16"), (delta, torch.float16, "delta"),
+    dy32 = dy16.dtype == torch.float32
+    for t, dt, nm in ((dy16, dy16.dtype if dy32 else torch.float16, "dy16"),
+                      (delta, torch.float16, "delta"),
                       (dres, torch.float32, "dres"), (lq, torch.float16, "lq"),
                       (lv, torch.float16, "lv"), (out16, torch.float16, "out16")):
         _t(t, dt, (n, d), nm)
     mq = _mask(mq, (n, d), "mq") if use_lora else None
     mv = _mask(mv, (n, d), "mv") if use_lora else None
-    rc = _lib.lib().dk_rms_bwd(_lib.ptr(dy16), _lib.ptr(gscale), _lib.ptr(x), _lib.ptr(delta),
+    rc = _lib.lib().dk_rms_bwd(_lib.ptr(dy16), int(dy32), _lib.ptr(gscale), _lib.ptr(x),
+                               _lib.ptr(delta),
                                _lib.ptr(w), _lib.ptr(rstd), _lib.ptr(dres), _lib.ptr(out),
                                _lib.ptr(lq), _lib.ptr(lv), _lib.ptr(out16), _lib.ptr(mq),
                                _lib.ptr(mv), n, d, float(keep_scale), _lib.stream_handle(x.device))

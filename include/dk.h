@@ -91,12 +91,13 @@ int dk_rms_fwd(const float* x, const void* delta, float* xout, const float* w, v
                int64_t n_rows, int64_t d, float eps, float keep_scale, hipStream_t stream);
 
 /* RMSNorm backward with the LoRA-A input gradients.  Replaces rms_bwd_kernel / rms_backward
- * (solution/k_norm.py:61-88, 134-150): dy = fp32(dy16) * gscale[0]
+ * (solution/k_norm.py:61-88, 134-150): dy = fp32(dy) * gscale[0] (dy fp16, or fp32 when dy_f32:
+ * the q|k|v dX GEMM's fp32 output that already holds the masked LoRA terms)
  * [+ (mq ? fp32(lq) * keep_scale : 0) + (mv ? fp32(lv) * keep_scale : 0)], h = x [+ delta],
  * xh = h * rstd, g = dy * w, dx = (g - xh * mean(g * xh)) * rstd [+ dres]; out fp32 (may alias
  * dres), out16 = fp16(dx) if given.  gscale is a device pointer to one fp32. */
-int dk_rms_bwd(const void* dy16, const float* gscale, const float* x, const void* delta,
-               const float* w, const float* rstd, const float* dres, float* out, const void* lq,
+int dk_rms_bwd(const void* dy, int dy_f32, const float* gscale, const float* x,
+               const void* delta, const float* w, const float* rstd, const float* dres, float* out, const void* lq,
                const void* lv, void* out16, const uint8_t* mq, const uint8_t* mv, int64_t n_rows,
                int64_t d, float keep_scale, hipStream_t stream);
 

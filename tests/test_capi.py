@@ -122,11 +122,11 @@ def test_norm_and_rope_argument_errors_come_back_before_launch():
                           None) == _lib.DK_ERR_INVALID                 # dropout without masks
     assert lib.dk_rms_fwd(p8, None, None, p16, p16, p16, None, None, None, None, 4, 1536, 1e-6, 1.0,
                           None) == _lib.DK_ERR_ALIGN
-    assert lib.dk_rms_bwd(p16, None, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
+    assert lib.dk_rms_bwd(p16, 0, None, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
                           1536, 1.0, None) == _lib.DK_ERR_INVALID        # no gscale
-    assert lib.dk_rms_bwd(p16, p16, p16, None, p16, p16, None, p16, p16, None, None, p16, p16, 4, 1536,
+    assert lib.dk_rms_bwd(p16, 0, p16, p16, None, p16, p16, None, p16, p16, None, None, p16, p16, 4, 1536,
                           1.0, None) == _lib.DK_ERR_INVALID              # lq without lv
-    assert lib.dk_rms_bwd(p4, p16, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
+    assert lib.dk_rms_bwd(p4, 0, p16, p16, None, p16, p16, None, p16, None, None, None, None, None, 4,
                           1536, 1.0, None) == _lib.DK_ERR_ALIGN          # dy16 needs 8 bytes
     assert lib.dk_rms_fwd(p16, None, None, p16, p16, p16, None, None, None, None, 0, 1536, 1e-6, 1.0,
                           None) == 0                                     # zero rows

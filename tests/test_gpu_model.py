@@ -1,0 +1,55 @@
+"""End-to-end parity of the whole QLoRA step (decentrik_prime_amd.model: norms, the rotary q|k|v
+GEMM with the LoRA terms, attention, o, SwiGLU MLP, the LM head, and the backward through all of
+it) with the float64 torch reference (oracle/model.py) on the same weights: two layers, three
+ragged sequences, a 4096-token vocabulary in four chunks.  The weights the reference uses are the
+GPU's own NF4 dequant (bit-exact to the oracle, pinned in tests/test_gpu_nf4.py)."""
+
+import numpy as np
+import pytest
+
+from tests.helpers import host, log
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.fixture(scope="module")
+def torch():
+    import torch as t
+    return t
+
+
+def test_qlora_step_matches_float64_reference(torch):
+    from decentrik_prime_amd import k_nf4, model
+    from oracle import model as ref
+    lens = [37, 100, 64]
+    log(f"whole QLoRA step, 2 layers, lens {lens}")
+    st = model.QwenQLoRAStep(lens, n_layers=2, vocab=4096, seed=5, head_chunk=1024)
+    loss = st.step()
+    loss2 = st.step()             # a second step over the same batch: the schedule's steady state
+    torch.cuda.synchronize()
+    assert float(loss) == float(loss2), "the step is deterministic"
+    layers = []
+    for i in range(2):
+        pk = st.layers[i]["packed"]
+        buf = torch.empty(pk.numel, dtype=torch.float16, device="cuda")
+        k_nf4.dequant_layer(pk, st.code2, st.nf4, buf)
+
+        def w(kind):
+            start, n = st.views[kind]
+            W = st.layers[i][kind]
+            return buf[start:start + n].view(W.rows, W.cols).cpu()
+        lo = st.lora[i]
+        layers.append(dict(wqkv=w("qkv"), wo=w("o"), wgu=w("gu"), wd=w("d"), bias=lo["bias"].cpu(),
+                           w_in=st.w_in[i].cpu(), w_post=st.w_post[i].cpu(),
+                           **{k: lo[k].cpu() for k in ("Aq", "Bq", "Av", "Bv", "mq", "mv")}))
+    p = dict(x0=st.x0.cpu(), emb=st.emb.cpu(), tgt=st.tgt.cpu(), pos=st.pos.cpu(), cos=st.cos.cpu(),
+             sin=st.sin.cpu(), w_final=st.w_final.cpu(), eps=st.eps, ks=st.keep_scale, s=st.s,
+             layers=layers)
+    ref_loss, ref_grads = ref.qwen_step(p, lens)
+    assert abs(float(loss) - ref_loss) <= 2e-3 * abs(ref_loss), (float(loss), ref_loss)
+    for i in range(2):
+        for nm, got, want in zip(("dA_q", "dB_q", "dA_v", "dB_v"), st.grads[i], ref_grads[i]):
+            g, r = host(got).astype(np.float64), want.numpy()
+            scale = float(np.abs(r).max())
+            err = float(np.abs(g - r).max()) / scale
+            assert err <= 5e-2, f"layer {i} {nm}: max error {err:.3g} of the gradient's max {scale:.3g}"
