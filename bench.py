@@ -230,6 +230,35 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
     return res
 
 
+def model_step(torch, layers, m, steps, warmup):
+    """The whole Qwen2.5 QLoRA step around the linear stack (decentrik_prime_amd.model: norms,
+    rotary q|k|v GEMM, causal GQA attention, SwiGLU MLP, the LM head over the 151,936-token
+    vocabulary, and the backward to the LoRA gradients) on four sequences of m / 4 tokens: time
+    per step, tokens per second, and algorithmic TFLOP/s (linear layers, attention, LM head)."""
+    from decentrik_prime_amd.model import QwenQLoRAStep
+    lens = [m // 4] * 4
+    st = QwenQLoRAStep(lens, n_layers=layers, seed=0)
+    for _ in range(warmup):
+        st.step()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(steps):
+        st.step()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / steps
+    tf = st.flops_per_step / (ms * 1e-3) / 1e12
+    res = {"workload": "Qwen2.5-1.5B QLoRA training step (embedding rows, 28 decoder layers, "
+                       "final norm, LM head + cross-entropy, backward to the LoRA gradients)",
+           "layers": layers, "lens": lens, "ms_per_step": round(ms, 3),
+           "tokens_per_s": round(m / (ms * 1e-3), 1), "flop_per_step": st.flops_per_step,
+           "tflops": round(tf, 1), "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+    del st
+    torch.cuda.empty_cache()
+    return res
+
+
 def dequant_bandwidth(torch, st, reps):
     """NF4 dequant of every layer into its own fp16 output (the working set, 3.30 GB of
     algorithmic traffic for 28 layers, does not fit the 256 MB Infinity Cache)."""
@@ -447,6 +476,8 @@ def main():
     ap.add_argument("--cpu-layers", type=int, default=6,
                     help="layers of the CPU-oracle sample (about 10-30 s of CPU work)")
     ap.add_argument("--no-kernels", action="store_true")
+    ap.add_argument("--no-model", action="store_true",
+                    help="skip the whole-model step (norms, attention, LM head around the stack)")
     ap.add_argument("--reps", type=int, default=20)
     ap.add_argument("--kernels-only", action="store_true",
                     help="skip the step timing: per-kernel table, dequant and a copy of known size "
@@ -568,6 +599,13 @@ def main():
             f"{r['kernel']} {r['avg_us']} us " + (f"{r['gbps']} GB/s" if "gbps" in r
                                                   else f"{r['tflops']} TFLOP/s")
             for r in result["neighbours"]), file=sys.stderr, flush=True)
+    if not args.no_model:
+        del st
+        torch.cuda.empty_cache()
+        result["model_step"] = model_step(torch, args.layers, args.m, args.steps, args.warmup)
+        ms = result["model_step"]
+        print(f"[bench] whole QLoRA step {ms['ms_per_step']} ms, {ms['tokens_per_s']} tokens/s, "
+              f"{ms['tflops']} TFLOP/s", file=sys.stderr, flush=True)
     if not args.no_cpu:
         print(f"[bench] CPU baseline (oracle, {args.cpu_layers} layers)", file=sys.stderr, flush=True)
         result["cpu_baseline"] = cpu_baseline(args.cpu_layers, args.m)
