@@ -14,8 +14,8 @@
 // P^T, taking P^T straight from the score registers: the 32x32 result register v of lane l is row
 // 8 (v / 4) + 4 (l / 32) + v % 4, so registers 8 t' .. 8 t' + 7 of a lane hold keys
 // 16 t' + 8 (j / 4) + 4 (l / 32) + j % 4 (j = 0..7), and the other operand supplies the same keys
-// in the same order from a transposed LDS copy (the k order of a product is free as long as both
-// operands agree).  dK/dV compute S = Q K^T (the key on the lane) and use P and dS the same way.
+// in the same order, read as columns of the row-major LDS tile by ds_read_b64_tr_b16 (the k order
+// of a product is free as long as both operands agree).  dK/dV compute S = Q K^T (the key on the lane) and use P and dS the same way.
 #include "dk_common.h"
 
 namespace {
@@ -25,7 +25,6 @@ constexpr int kAThreads = 256;    // 4 waves, 32 query rows (or keys) each
 constexpr int kBM = 128;          // queries per forward / dQ workgroup, keys per dK/dV workgroup
 constexpr int kBN = 64;           // keys per forward / dQ tile, queries per dK/dV tile
 constexpr int kPR = kHD + 8;      // halves per row of a row-major LDS tile
-constexpr int kPT = kBN + 8;      // halves per row of a transposed LDS tile
 static_assert(kBM == 32 * (kAThreads / 64), "a wave owns 32 rows");
 
 struct AttnArgs {
@@ -56,11 +55,21 @@ __device__ __forceinline__ f32x16 mfma(const f16x8& a, const f16x8& b, const f32
   return __builtin_amdgcn_mfma_f32_32x32x16_f16(a, b, c, 0, 0, 0);
 }
 
-// 8 halves of a transposed LDS row: positions p .. p + 3 and p + 8 .. p + 11 (the keys or
-// queries of MFMA k index j = 0..7 for the lane half whose p = 16 t + 4 (l / 32))
-__device__ __forceinline__ f16x8 read_t8(const f16* row, int p) {
-  const f16x4 lo = *reinterpret_cast<const f16x4*>(row + p);
-  const f16x4 hi = *reinterpret_cast<const f16x4*>(row + p + 8);
+__device__ __forceinline__ f16x4 read_tr(const f16* q) {
+  return __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+      (__attribute__((address_space(3))) i16x4*)(q)));
+}
+
+// Column (col + l % 32) of rows p .. p + 3 and p + 8 .. p + 11 of a row-major LDS tile (row
+// stride kPR), the 8 values of MFMA k index j = 0..7 for a lane half whose p = 16 t + 4 (l / 32).
+// ds_read_b64_tr_b16: within a 16-lane group, lane 4a + b receives element b of the 4-half
+// pieces addressed by lanes a, a + 4, a + 8, a + 12; lane x addresses row p + x / 4 at columns
+// col + 16 (group) + 4 (x % 4), so lane x' of the group receives column col + 16 (group) + x' of
+// the four rows.  The 16 lanes of a group touch 16 distinct banks.
+__device__ __forceinline__ f16x8 read_col8(const f16* tile, int p, int col) {
+  const int lane = threadIdx.x & 63;
+  const f16* q = tile + (p + ((lane & 15) >> 2)) * kPR + col + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const f16x4 lo = read_tr(q), hi = read_tr(q + 8 * kPR);
   return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
@@ -104,21 +113,13 @@ __device__ __forceinline__ void load_rows(RowTile& t, const f16* base, int64_t l
   }
 }
 
-// The rows into a row-major LDS tile rm[r][c] (if rm) and a transposed one tr[c][r] (if tr; the
-// two rows of an item packed per dword).
-__device__ __forceinline__ void store_rows(const RowTile& t, f16* rm, f16* tr) {
+// The rows into a row-major LDS tile rm[r][c] (16-byte stores, rows padded to kPR halves).
+__device__ __forceinline__ void store_rows(const RowTile& t, f16* rm) {
 #pragma unroll
   for (int q = 0; q < 2; ++q) {
     const int it = threadIdx.x + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
-    if (rm) {
 #pragma unroll
-      for (int u = 0; u < 2; ++u) *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = t.v[q][u];
-    }
-    if (tr) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e)
-        *reinterpret_cast<uint32_t*>(tr + (c8 + e) * kPT + 2 * rp) = dk_pack2(t.v[q][0][e], t.v[q][1][e]);
-    }
+    for (int u = 0; u < 2; ++u) *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = t.v[q][u];
   }
 }
 
@@ -143,7 +144,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
   const int m = mstart + 32 * w + c;
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
   __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Vt[kHD * kPT];
+  __shared__ __attribute__((aligned(16))) f16 Vs[kBN * kPR];
 
   f16x8 qf[kHD / 16];
   row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
@@ -161,8 +162,8 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
     load_rows(kt, kbase, ROW, s0, n0, seqlen, a.n_tokens);
     load_rows(vt, vbase, ROW, s0, n0, seqlen, a.n_tokens);
     __syncthreads();   // every wave has finished reading the previous tile
-    store_rows(kt, Ks, nullptr);
-    store_rows(vt, nullptr, Vt);
+    store_rows(kt, Ks);
+    store_rows(vt, Vs);
     __syncthreads();
     // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
     f32x16 sacc[2] = {zero16(), zero16()};
@@ -210,7 +211,7 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
       for (int j = 0; j < 8; ++j) pf[j] = (f16)sacc[kb][i0 + j];
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb)
-        oacc[hb] = mfma(read_t8(Vt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), pf, oacc[hb]);
+        oacc[hb] = mfma(read_col8(Vs, 16 * t + 4 * hl, hb * 32), pf, oacc[hb]);
     }
   }
   if (!mval) return;
@@ -265,7 +266,6 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
   __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
   __shared__ __attribute__((aligned(16))) f16 Vs[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Kt[kHD * kPT];
 
   f16x8 qf[kHD / 16], dof[kHD / 16];
   row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
@@ -283,8 +283,8 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
   load_rows(vt, vbase, ROW, s0, 0, seqlen, a.n_tokens);
   for (int n0 = 0; n0 < hi; n0 += kBN) {
     __syncthreads();
-    store_rows(kt, Ks, Kt);
-    store_rows(vt, Vs, nullptr);
+    store_rows(kt, Ks);
+    store_rows(vt, Vs);
     __syncthreads();
     if (n0 + kBN < hi) {
       load_rows(kt, kbase, ROW, s0, n0 + kBN, seqlen, a.n_tokens);
@@ -319,7 +319,7 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
       for (int j = 0; j < 8; ++j) dsf[j] = (f16)sacc[kb][i0 + j];
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb)
-        dqacc[hb] = mfma(read_t8(Kt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dsf, dqacc[hb]);
+        dqacc[hb] = mfma(read_col8(Ks, 16 * t + 4 * hl, hb * 32), dsf, dqacc[hb]);
     }
   }
   if (!mval) return;
@@ -354,8 +354,6 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
   const bool nval = n < seqlen && s0 + n < a.n_tokens;
   __shared__ __attribute__((aligned(16))) f16 Qs[kBN * kPR];
   __shared__ __attribute__((aligned(16))) f16 Ds[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Qt[kHD * kPT];
-  __shared__ __attribute__((aligned(16))) f16 Dt[kHD * kPT];
   __shared__ float lse_s[kBN], dl_s[kBN];
 
   f16x8 kf[kHD / 16], vf[kHD / 16];
@@ -378,8 +376,8 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
   float stat = load_stat(nstart);
   for (int m0 = nstart; m0 < seqlen; m0 += kBN) {
     __syncthreads();
-    store_rows(qt, Qs, Qt);
-    store_rows(dt, Ds, Dt);
+    store_rows(qt, Qs);
+    store_rows(dt, Ds);
     if (tid < kBN) lse_s[tid] = stat;
     else if (tid < 2 * kBN) dl_s[tid - kBN] = stat;
     __syncthreads();
@@ -423,8 +421,8 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
       }
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb) {
-        dvacc[hb] = mfma(pf, read_t8(Dt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dvacc[hb]);
-        dkacc[hb] = mfma(dsf, read_t8(Qt + (hb * 32 + c) * kPT, 16 * t + 4 * hl), dkacc[hb]);
+        dvacc[hb] = mfma(pf, read_col8(Ds, 16 * t + 4 * hl, hb * 32), dvacc[hb]);
+        dkacc[hb] = mfma(dsf, read_col8(Qs, 16 * t + 4 * hl, hb * 32), dkacc[hb]);
       }
     }
   }
