@@ -18,7 +18,9 @@ from . import _lib
 from .w4linear import _h16_workspace
 
 STATE_W = 8          # per-row running state: m, s, t, argmax, x_target, (pad)
-CHUNK = 8192         # vocabulary rows per chunk (a multiple of 64)
+CHUNK = 32768        # vocabulary rows per chunk (a multiple of 64): at 2048 tokens a 134 MB
+                     # logits buffer; measured 2.81 / 2.49 / 2.45 ms per full-vocabulary call at
+                     # 8192 / 16384 / 32768 (fewer split-K reduces and launches per call)
 
 
 class ResidentEmbedding:
