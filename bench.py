@@ -19,6 +19,7 @@ forward + backward, on this host's cores.
 
 import argparse
 import json
+import math
 import os
 import sys
 import time
@@ -249,11 +250,16 @@ def model_step(torch, layers, m, steps, warmup):
     torch.cuda.synchronize()
     ms = e0.elapsed_time(e1) / steps
     tf = st.flops_per_step / (ms * 1e-3) / 1e12
+    loss = float(st.step())
+    finite = math.isfinite(loss) and all(bool(torch.isfinite(g).all()) for gs in st.grads for g in gs)
+    if not finite:
+        raise RuntimeError(f"whole QLoRA step: non-finite loss or LoRA gradients (loss {loss})")
     res = {"workload": "Qwen2.5-1.5B QLoRA training step (embedding rows, 28 decoder layers, "
                        "final norm, LM head + cross-entropy, backward to the LoRA gradients)",
            "layers": layers, "lens": lens, "ms_per_step": round(ms, 3),
            "tokens_per_s": round(m / (ms * 1e-3), 1), "flop_per_step": st.flops_per_step,
-           "tflops": round(tf, 1), "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4)}
+           "tflops": round(tf, 1), "frac_fp16_peak": round(tf / FP16_PEAK_TFLOPS, 4),
+           "loss_per_token": round(loss / st.n_lab, 4)}
     del st
     torch.cuda.empty_cache()
     return res
