@@ -1,7 +1,8 @@
 """End-to-end parity of the whole QLoRA step (decentrik_prime_amd.model: norms, the rotary q|k|v
 GEMM with the LoRA terms, attention, o, SwiGLU MLP, the LM head, and the backward through all of
-it) with the float64 torch reference (oracle/model.py) on the same weights: two layers, three
-ragged sequences, a 4096-token vocabulary in four chunks.  The weights the reference uses are the
+it) with the float64 torch reference (oracle/model.py) on the same weights: two layers, a
+4096-token vocabulary in chunks of 1024; three ragged sequences (the small-M GEMM plans) and four
+512-token sequences (M = 2048: the 256-tile GEMM plans of the bench).  The weights the reference uses are the
 GPU's own NF4 dequant (bit-exact to the oracle, pinned in tests/test_gpu_nf4.py)."""
 
 import numpy as np
@@ -18,10 +19,10 @@ def torch():
     return t
 
 
-def test_qlora_step_matches_float64_reference(torch):
+@pytest.mark.parametrize("lens", [[37, 100, 64], [512, 512, 512, 512]])
+def test_qlora_step_matches_float64_reference(torch, lens):
     from decentrik_prime_amd import k_nf4, model
     from oracle import model as ref
-    lens = [37, 100, 64]
     log(f"whole QLoRA step, 2 layers, lens {lens}")
     st = model.QwenQLoRAStep(lens, n_layers=2, vocab=4096, seed=5, head_chunk=1024)
     loss = st.step()
@@ -46,10 +47,15 @@ def test_qlora_step_matches_float64_reference(torch):
              sin=st.sin.cpu(), w_final=st.w_final.cpu(), eps=st.eps, ks=st.keep_scale, s=st.s,
              layers=layers)
     ref_loss, ref_grads = ref.qwen_step(p, lens)
-    assert abs(float(loss) - ref_loss) <= 2e-3 * abs(ref_loss), (float(loss), ref_loss)
+    # measured: loss to ~1e-5 relative, gradients to ~2e-3 of their maximum, at both sizes
+    assert abs(float(loss) - ref_loss) <= 1e-4 * abs(ref_loss), (float(loss), ref_loss)
+    errs = []
     for i in range(2):
         for nm, got, want in zip(("dA_q", "dB_q", "dA_v", "dB_v"), st.grads[i], ref_grads[i]):
             g, r = host(got).astype(np.float64), want.numpy()
             scale = float(np.abs(r).max())
             err = float(np.abs(g - r).max()) / scale
-            assert err <= 5e-2, f"layer {i} {nm}: max error {err:.3g} of the gradient's max {scale:.3g}"
+            errs.append(err)
+            assert err <= 1e-2, f"layer {i} {nm}: max error {err:.3g} of the gradient's max {scale:.3g}"
+    log(f"  loss {float(loss):.6g} vs {ref_loss:.6g}; LoRA gradients max error / max: "
+        f"{max(errs):.3g}")
