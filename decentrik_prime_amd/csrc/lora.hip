@@ -392,14 +392,15 @@ bool rank_ok(int64_t r) { return r >= 16 && r <= 64 && r % 16 == 0; }
 
 extern "C" int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t rank,
                                   const dk_lora_down_term* terms, int n_terms, hipStream_t stream) {
-  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !terms || n_terms < 1 ||
+  // (zero-element tensors have null data pointers: x and z are required only with rows)
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || (m > 0 && !x) || !terms || n_terms < 1 ||
       n_terms > kMaxJobs)
     return DK_ERR_INVALID;
   if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
   int masked = 0;
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_down_term& u = terms[t];
-    if (!u.a || !u.z) return DK_ERR_INVALID;
+    if (m > 0 && (!u.a || !u.z)) return DK_ERR_INVALID;
     if (!dk_aligned(u.a, 16) || (u.mask && !dk_aligned(u.mask, 8))) return DK_ERR_ALIGN;
     masked += u.mask != nullptr;
   }

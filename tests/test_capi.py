@@ -99,6 +99,9 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_INVALID  # no A / z
     down[0] = _lib.LoraDownTermC(None, 1.0, ctypes.c_void_p(8), p16)
     assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_ALIGN
+    # no rows: zero-element tensors have null data pointers, and nothing is read or written
+    down[0] = _lib.LoraDownTermC(None, 1.0, p16, None)
+    assert lib.dk_lora_down_multi(None, 0, 64, 16, down, 1, None) == 0
     grads = (_lib.LoraGradsTermC * 1)()
     assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
     grads[0] = _lib.LoraGradsTermC(p16, 64, 64, p16, p16, 2.0, None, 1.0, p16, p16, p16)
