@@ -170,8 +170,10 @@ __global__ __launch_bounds__(kHThreads) void head_finalize_kernel(
 extern "C" int dk_head_chunk(void* logits, const int32_t* tgt_sorted, float* state, float* acc,
                              int64_t n_rows, int64_t n_lab, int64_t vc, int64_t v0, float p_scale,
                              int64_t d, hipStream_t stream) {
-  if (n_rows < 0 || n_lab < 0 || n_lab > n_rows || vc <= 0 || vc % 8 || vc > INT32_MAX / 2 ||
-      v0 < 0 || d <= 0 || d % 4)
+  // one workgroup per row (the grid's x limit); the argmax index is kept as an fp32 in the state,
+  // exact for every column below 2^24
+  if (n_rows < 0 || n_rows > INT32_MAX || n_lab < 0 || n_lab > n_rows || vc <= 0 || vc % 8 ||
+      vc > INT32_MAX / 2 || v0 < 0 || v0 + vc > (int64_t{1} << 24) || d <= 0 || d % 4)
     return DK_ERR_INVALID;
   if (n_rows == 0) return 0;
   if (!logits || !tgt_sorted || !state || (n_lab > 0 && !acc)) return DK_ERR_INVALID;
@@ -188,7 +190,8 @@ extern "C" int dk_head_finalize(const float* state, const int32_t* tgt_sorted, c
                                 const float* acc, const void* e_target, float* stats, void* dy,
                                 int64_t n_rows, int64_t n_lab, float out_scale, float inv_p_scale,
                                 int64_t d, hipStream_t stream) {
-  if (n_rows < 0 || n_lab < 0 || n_lab > n_rows || d <= 0 || d % 4) return DK_ERR_INVALID;
+  if (n_rows < 0 || n_rows > INT32_MAX || n_lab < 0 || n_lab > n_rows || d <= 0 || d % 4)
+    return DK_ERR_INVALID;
   if (n_rows == 0) return 0;
   if (!state || !tgt_sorted || !perm || !stats || !dy || (n_lab > 0 && (!acc || !e_target)))
     return DK_ERR_INVALID;

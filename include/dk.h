@@ -148,7 +148,8 @@ int dk_attn_bwd(const void* qkv, const void* out, const float* lse, const void* 
  * first, n_lab of them); state [n_rows, 8] fp32 = (m, s, t, argmax, x_target, pad), m = -inf and
  * the rest 0 before the first chunk; acc [n_lab, d] fp32 starts at 0.
  * dk_head_chunk replaces head_chunk_kernel (solution/k_head.py:50-123): logits [n_rows, vc] fp16
- * of chunk [v0, v0 + vc) (vc % 8 == 0), merged into the state; rows r < n_lab get
+ * of chunk [v0, v0 + vc) (vc % 8 == 0, v0 + vc <= 2^24 so that the fp32 argmax is exact,
+ * n_rows <= INT32_MAX), merged into the state; rows r < n_lab get
  * P = p_scale e^(x - m) in place (0 in the target's column) and their acc rows rescaled.
  * dk_head_finalize replaces head_finalize_kernel (solution/k_head.py:126-161): stats [n_rows, 4]
  * = (loss, entropy, hit, lse), and dy [n_rows, d] fp16 row perm[r] = out_scale (acc / (p_scale s)

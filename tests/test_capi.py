@@ -167,6 +167,13 @@ def test_norm_and_rope_argument_errors_come_back_before_launch():
     assert lib.dk_head_chunk(p16, p16, p16, None, 8, 4, 128, 0, 1.0, 1536, None) == _lib.DK_ERR_INVALID
     assert lib.dk_head_chunk(p8, p16, p16, p16, 8, 4, 128, 0, 1.0, 1536, None) == _lib.DK_ERR_ALIGN
     assert lib.dk_head_chunk(p16, p16, p16, None, 0, 0, 128, 0, 1.0, 1536, None) == 0
+    # the argmax (an fp32 in the state) is exact below 2^24 columns; one workgroup per row
+    assert lib.dk_head_chunk(p16, p16, p16, p16, 8, 4, 128, (1 << 24) - 64, 1.0, 1536,
+                             None) == _lib.DK_ERR_INVALID
+    assert lib.dk_head_chunk(p16, p16, p16, p16, 1 << 31, 4, 128, 0, 1.0, 1536,
+                             None) == _lib.DK_ERR_INVALID
+    assert lib.dk_head_finalize(p16, p16, p16, p16, p16, p16, p16, 1 << 31, 4, 1.0, 1.0, 1536,
+                                None) == _lib.DK_ERR_INVALID
     assert lib.dk_head_finalize(p16, p16, p16, p16, None, p16, p16, 8, 4, 1.0, 1.0, 1536,
                                 None) == _lib.DK_ERR_INVALID            # targets without E_t rows
     assert lib.dk_head_finalize(p16, p16, p16, p16, p16, p16, p4, 8, 4, 1.0, 1.0, 1536,
