@@ -563,6 +563,11 @@ def main():
     wall = time.perf_counter() - t0
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value = st.flops_per_step / (ms_per_step * 1e-3) / 1e12
+    # the last step's outputs and every layer's LoRA gradients must be finite
+    checked = [st.out[k] for k in ("qkv", "o", "y")] + [st.dx_qkv, st.dx_o, st.dx_mlp]
+    checked += [g for gs in st.grads for g in gs]
+    if not all(bool(torch.isfinite(t.float()).all()) for t in checked):
+        raise RuntimeError("linear stack: non-finite outputs or LoRA gradients")
     print(f"[bench] {ms_per_step:.3f} ms/step, {value:.1f} TFLOP/s (wall {wall:.2f} s)",
           file=sys.stderr, flush=True)
 

@@ -43,14 +43,14 @@ _T = ctypes.POINTER(LoraTermC)
 
 class LoraDownTermC(ctypes.Structure):
     """struct dk_lora_down_term."""
-    _fields_ = [("mask", _c_p), ("keep_scale", _f32), ("a", _c_p), ("z", _c_p)]
+    _fields_ = [("mask", _c_p), ("keep_scale", _f32), ("a", _c_p), ("z", _c_p), ("x", _c_p)]
 
 
 class LoraGradsTermC(ctypes.Structure):
     """struct dk_lora_grads_term."""
     _fields_ = [("dy", _c_p), ("lddy", _i64), ("n_out", _i64), ("z", _c_p), ("lora_b", _c_p),
                 ("lora_scale", _f32), ("mask", _c_p), ("keep_scale", _f32), ("da", _c_p),
-                ("db", _c_p), ("dz", _c_p)]
+                ("db", _c_p), ("dz", _c_p), ("x", _c_p)]
 
 
 class SideDequantC(ctypes.Structure):

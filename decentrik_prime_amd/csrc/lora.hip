@@ -7,8 +7,8 @@
 //   dz:    dz[m][r] = fp16(fp32(fp16(sum_n dY[m][n] B[n][r])) * s)
 //          (solution/fast_qwen.py:1370, 1373: mm(gq, B).mul_(s) on an fp16 tensor)
 //          B is staged in LDS as stored and read K-contiguous with transposing LDS reads.
-// Column reductions over the token rows, in two deterministic passes (fixed-order partial sums
-// per 128-row chunk into a workspace, MFMA on LDS-staged tiles, then one finalize pass):
+// Column reductions over all token rows in one deterministic pass (a workgroup per 32 columns,
+// MFMA on LDS-staged 32-row chunks, the waves' sums added in a fixed order):
 //   dB[n][r] = fp32(fp16(sum_m dY[m][n] z[m][r])) * s       (solution/fast_qwen.py:1369)
 //   dA[r][k] = fp32(fp16(sum_m dz[m][r] Xd[m][k]))           (solution/fast_qwen.py:1371)
 // Products of two fp16 values are exact in fp32; only the order of the fp32 sums differs from a
@@ -17,12 +17,8 @@
 
 namespace {
 
-constexpr int kThreads = 256;
-constexpr int kWaves = kThreads / 64;
 constexpr int kRowTile = 16;     // rows per workgroup of the row reductions
 constexpr int kRowThreads = 512; // 8 waves split K in the row reductions
-constexpr int kChunkRows = 128;  // rows per partial sum of the column reductions
-constexpr int kColsPerBlock = 128;
 constexpr int kMaxJobs = 2;      // LoRA terms per launch (q and v of the fused QKV projection)
 
 __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, float ks) {
@@ -39,7 +35,7 @@ __device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, fl
 // MODE 0 (down): out[m][r] = fp16(sum_k Xd[m][k] W[r][k]), W = A [R][cols].
 // MODE 1 (dz):   out[m][r] = fp16(fp16(sum_k in[m][k] W[k][r]) * scale), W = B [cols][R], staged
 //                row-major in LDS and read k-contiguous with ds_read_b64_tr_b16 (see
-//                lora_cols_kernel for the lane layout).
+//                lora_colsum_kernel for the lane layout).
 // 16x16x32 MFMA operand layout: lane l holds row/column l % 16 and k = 8 * (l / 16) + [0, 8);
 // the result register v of lane l is row 4 * (l / 16) + v, column l % 16.  The 8 waves split K
 // and issue the loads of kBatch steps before their MFMAs; their sums are added in a fixed order.
@@ -170,101 +166,98 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
   }
 }
 
-// Partial column sums over one kChunkRows-row chunk: part[chunk][c][r] = sum_m P[m][c] Q[m][r]
-// (P = dropout(x) with the keep-mask when DROP).  A workgroup stages its P tile (kChunkRows rows x
-// 128 columns, 16-byte coalesced loads, the dropout applied on the way) and the Q rows in LDS
-// row-major, then v_mfma_f32_16x16x32_f16 runs with both operands read M-contiguous by
-// ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives element b of the 4-element
-// rows addressed by lanes a, a + 4, a + 8, a + 12, so lane l addressing row
-// 8 (l / 16) + 4 h + (l % 16) / 4, column 4 (l % 4) receives rows 8 (l / 16) + 4 h + 0..3 of
-// column l % 16, and two reads (h = 0, 1) give the 8 consecutive rows of the MFMA operand.
-// Column blocks [bx0, next job's bx0) of grid.x serve job j; a job with a mask applies the dropout
-// (dA of a masked term), one without reads P as stored (dB, or dA of an unmasked term), so the dB
-// and dA reductions of both terms share one launch.
-struct ColsJob {
+// Column reductions over every token row, one pass: out[c][r] = sum_m P[m][c] Q[m][r] (P =
+// dropout(x) with the keep-mask when the job has one), then fp32(fp16(sum)) * scale, stored
+// [c][r] or, transposed, [r][c].  A workgroup owns kSumCols columns of one job and all rows; its
+// 8 waves take 32-row chunks in turn (chunk w, w + 8, ...), each with kSumDepth chunks of loads in
+// flight, stage the chunk in a private LDS tile and run v_mfma_f32_16x16x32_f16 with both operands
+// read M-contiguous by ds_read_b64_tr_b16: within each 16-lane group, lane 4a + b receives
+// element b of the 4-element rows addressed by lanes a, a + 4, a + 8, a + 12, so lane l addressing
+// row 8 (l / 16) + 4 h + (l % 16) / 4, column 4 (l % 4) receives rows 8 (l / 16) + 4 h + 0..3 of
+// column l % 16, and two reads (h = 0, 1) give the 8 consecutive rows of the MFMA operand.  The
+// waves' sums are added in wave order through LDS: the order of every sum is fixed, so results
+// are deterministic, and there are no partial sums in memory and no second launch.
+// Column blocks [bx0, next job's bx0) of the grid serve job j: the dB of each term (P = dY, Q = z)
+// and the dA of each term (P = Xd, Q = dz) share one launch.
+constexpr int kSumThreads = 512;
+constexpr int kSumWaves = kSumThreads / 64;
+constexpr int kSumCols = 32;     // columns per workgroup
+constexpr int kSumDepth = 3;     // 32-row chunks of loads in flight per wave
+struct SumJob {
   const f16* P;
   int64_t ld;
-  const uint8_t* mask;
+  const uint8_t* mask;   // [rows][cols] keep-mask or null
   float ks;
-  const f16* Q;
-  float* part;
+  const f16* Q;          // [rows][R]
+  float scale;
+  float* out;
+  int transpose;
   int64_t cols;
   int bx0;
 };
-constexpr int kMaxColsJobs = 2 * kMaxJobs;
-struct ColsJobs {
-  ColsJob j[kMaxColsJobs];
+constexpr int kMaxSumJobs = 2 * kMaxJobs;
+struct SumJobs {
+  SumJob j[kMaxSumJobs];
   int n;
 };
 
 template <int R>
-__global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int64_t rows) {
+__global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, int64_t rows) {
   int jb = 0;
 #pragma unroll
-  for (int q = 1; q < kMaxColsJobs; ++q)
+  for (int q = 1; q < kMaxSumJobs; ++q)
     if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].bx0) jb = q;
-  const ColsJob& J = jobs.j[jb];
+  const SumJob& J = jobs.j[jb];
   const f16* __restrict__ P = J.P;
   const int64_t ld = J.ld;
   const uint8_t* __restrict__ mask = J.mask;
   const bool drop = mask != nullptr;
   const float ks = J.ks;
   const f16* __restrict__ Q = J.Q;
-  float* __restrict__ part = J.part;
   const int64_t cols = J.cols;
-  constexpr int PLD = kColsPerBlock + 16;   // halves per staged P row
-  constexpr int QLD = R + 16;               // halves per staged Q row
-  constexpr int P_CHUNKS = kChunkRows * kColsPerBlock / 8 / kThreads;   // 16-byte chunks per thread
-  __shared__ __attribute__((aligned(16))) f16 Ps[kChunkRows * PLD];
-  __shared__ __attribute__((aligned(16))) f16 Qs[kChunkRows * QLD];
+  constexpr int PLD = kSumCols + 8;   // halves per staged P row
+  constexpr int QLD = R + 8;          // halves per staged Q row
+  constexpr int QL = R / 16;          // 16-byte Q pieces per lane per chunk
+  constexpr int WAVE_LDS = 32 * PLD * 2 + 32 * QLD * 2;
+  constexpr int RED = kSumWaves * kSumCols * 16 * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kSumWaves * WAVE_LDS > RED ? kSumWaves * WAVE_LDS : RED];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t c0 = (int64_t)(blockIdx.x - J.bx0) * kColsPerBlock;
-  const int64_t r0 = (int64_t)blockIdx.y * kChunkRows;
-  // P tile: every load issued before the first store (rows past the end read as zero)
-  f16x8 pv[P_CHUNKS];
-  u32x2 mv[P_CHUNKS];
+  f16* Ps = reinterpret_cast<f16*>(lds + w * WAVE_LDS);
+  f16* Qs = Ps + 32 * PLD;
+  const int64_t c0 = (int64_t)(blockIdx.x - J.bx0) * kSumCols;
+  const int64_t n_chunks = (rows + 31) / 32;
+  const int64_t mine = n_chunks > w ? (n_chunks - w + kSumWaves - 1) / kSumWaves : 0;
+  // this lane's pieces of a chunk: two 16-byte P pieces (rows l / 4 and l / 4 + 16, 8 columns at
+  // 8 (l % 4)) with their mask bytes, and QL 16-byte pieces of the Q rows
+  const int prow = lane >> 2, pc8 = 8 * (lane & 3);
+  f16x8 pv[kSumDepth][2], qv[kSumDepth][QL];
+  u32x2 mv[kSumDepth][2];
+  auto load = [&](int slot, int64_t i) {
+    const int64_t r0 = 32 * (w + kSumWaves * i);
 #pragma unroll
-  for (int i = 0; i < P_CHUNKS; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / (kColsPerBlock / 8), c8 = c % (kColsPerBlock / 8);
-    const int64_t m = r0 + row;
-    if (m < rows && c0 + 8 * c8 < cols) {
-      pv[i] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + 8 * c8);
-      if (drop) mv[i] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + 8 * c8);
-    } else {
+    for (int u = 0; u < 2; ++u) {
+      const int64_t m = r0 + prow + 16 * u;
+      if (m < rows && c0 + pc8 < cols) {
+        pv[slot][u] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + pc8);
+        if (drop) mv[slot][u] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + pc8);
+      } else {
 #pragma unroll
-      for (int e = 0; e < 8; ++e) pv[i][e] = (f16)0.0f;
-      mv[i] = u32x2{0u, 0u};
-    }
-  }
-  for (int i = tid; i < kChunkRows * R / 8; i += kThreads) {
-    const int row = i / (R / 8), r8 = (i % (R / 8)) * 8;
-    const int64_t m = r0 + row;
-    f16x8 q;
-    if (m < rows) {
-      q = *reinterpret_cast<const f16x8*>(Q + m * R + r8);
-    } else {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) q[e] = (f16)0.0f;
-    }
-    *reinterpret_cast<f16x8*>(Qs + row * QLD + r8) = q;
-  }
-#pragma unroll
-  for (int i = 0; i < P_CHUNKS; ++i) {
-    const int c = tid + kThreads * i;
-    const int row = c / (kColsPerBlock / 8), c8 = c % (kColsPerBlock / 8);
-    f16x8 v = pv[i];
-    if (drop) {
-#pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        const uint32_t keep = (mv[i][e >> 2] >> (8 * (e & 3))) & 0xffu;
-        v[e] = keep ? dk_h(__fmul_rn((float)v[e], ks)) : (f16)0.0f;
+        for (int e = 0; e < 8; ++e) pv[slot][u][e] = (f16)0.0f;
+        mv[slot][u] = u32x2{0u, 0u};
       }
     }
-    *reinterpret_cast<f16x8*>(Ps + row * PLD + 8 * c8) = v;
-  }
-  __syncthreads();
-  // wave w: column blocks 2w, 2w + 1 (16 columns each), all R / 16 rank blocks
+#pragma unroll
+    for (int u = 0; u < QL; ++u) {
+      const int idx = lane + 64 * u, row = idx / (R / 8), r8 = (idx % (R / 8)) * 8;
+      const int64_t m = r0 + row;
+      if (m < rows) {
+        qv[slot][u] = *reinterpret_cast<const f16x8*>(Q + m * R + r8);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) qv[slot][u][e] = (f16)0.0f;
+      }
+    }
+  };
   const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
   auto tr8 = [&](const f16* base, int ldh) {
     const f16x4 lo = __builtin_bit_cast(f16x4, __builtin_amdgcn_ds_read_tr16_b64_v4i16(
@@ -273,73 +266,81 @@ __global__ __launch_bounds__(kThreads) void lora_cols_kernel(ColsJobs jobs, int6
         (__attribute__((address_space(3))) i16x4*)(base + 4 * ldh)));
     return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
   };
+  f32x4 acc[kSumCols / 16][R / 16];
 #pragma unroll
-  for (int cb = 0; cb < 2; ++cb) {
-    const int cbase = (2 * w + cb) * 16;
-    f32x4 acc[R / 16];
+  for (int cb = 0; cb < kSumCols / 16; ++cb)
 #pragma unroll
-    for (int rb = 0; rb < R / 16; ++rb) acc[rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int rb = 0; rb < R / 16; ++rb) acc[cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
+  auto consume = [&](int slot) {
+    __builtin_amdgcn_wave_barrier();   // the previous chunk's transposing reads are done
 #pragma unroll
-    for (int kb = 0; kb < kChunkRows / 32; ++kb) {
-      const f16x8 a = tr8(Ps + (32 * kb + trow) * PLD + cbase + tcol, PLD);
+    for (int u = 0; u < 2; ++u) {
+      f16x8 v = pv[slot][u];
+      if (drop) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const uint32_t keep = (mv[slot][u][e >> 2] >> (8 * (e & 3))) & 0xffu;
+          v[e] = keep ? dk_h(__fmul_rn((float)v[e], ks)) : (f16)0.0f;
+        }
+      }
+      *reinterpret_cast<f16x8*>(Ps + (prow + 16 * u) * PLD + pc8) = v;
+    }
+#pragma unroll
+    for (int u = 0; u < QL; ++u) {
+      const int idx = lane + 64 * u, row = idx / (R / 8), r8 = (idx % (R / 8)) * 8;
+      *reinterpret_cast<f16x8*>(Qs + row * QLD + r8) = qv[slot][u];
+    }
+    __builtin_amdgcn_wave_barrier();
+#pragma unroll
+    for (int cb = 0; cb < kSumCols / 16; ++cb) {
+      const f16x8 a = tr8(Ps + trow * PLD + 16 * cb + tcol, PLD);
 #pragma unroll
       for (int rb = 0; rb < R / 16; ++rb) {
-        const f16x8 bq = tr8(Qs + (32 * kb + trow) * QLD + 16 * rb + tcol, QLD);
-        acc[rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, bq, acc[rb], 0, 0, 0);
+        const f16x8 b = tr8(Qs + trow * QLD + 16 * rb + tcol, QLD);
+        acc[cb][rb] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a, b, acc[cb][rb], 0, 0, 0);
       }
     }
-    // result register v of lane l: column cbase + 4 (l / 16) + v, rank 16 rb + l % 16
+  };
+  // kSumDepth chunks in flight: the loads of chunk i + kSumDepth - 1 go out before chunk i is
+  // consumed (slots rotate with the unrolled index)
 #pragma unroll
-    for (int rb = 0; rb < R / 16; ++rb)
+  for (int s = 0; s < kSumDepth - 1; ++s)
+    if (s < mine) load(s, s);
+  for (int64_t i0 = 0; i0 < mine; i0 += kSumDepth) {
 #pragma unroll
-      for (int v = 0; v < 4; ++v) {
-        const int64_t c = c0 + cbase + 4 * (lane >> 4) + v;
-        if (c < cols) part[((int64_t)blockIdx.y * cols + c) * R + 16 * rb + (lane & 15)] = acc[rb][v];
+    for (int s = 0; s < kSumDepth; ++s) {
+      const int64_t i = i0 + s;
+      if (i >= mine) break;
+      if (i + kSumDepth - 1 < mine) load((s + kSumDepth - 1) % kSumDepth, i + kSumDepth - 1);
+      consume(s);
+    }
+  }
+  // the waves' sums in wave order, one rank block at a time; result register v of lane l holds
+  // column 16 cb + 4 (l / 16) + v, rank 16 rb + l % 16
+  __syncthreads();   // every wave is done with its staging tile
+  float* red = reinterpret_cast<float*>(lds);
+#pragma unroll
+  for (int rb = 0; rb < R / 16; ++rb) {
+#pragma unroll
+    for (int cb = 0; cb < kSumCols / 16; ++cb)
+#pragma unroll
+      for (int v = 0; v < 4; ++v)
+        red[(w * kSumCols + 16 * cb + 4 * (lane >> 4) + v) * 16 + (lane & 15)] = acc[cb][rb][v];
+    __syncthreads();
+    for (int t = tid; t < kSumCols * 16; t += kSumThreads) {
+      const int c = t / 16, r = t % 16;
+      float s = 0.0f;
+#pragma unroll
+      for (int ww = 0; ww < kSumWaves; ++ww) s += red[(ww * kSumCols + c) * 16 + r];
+      const float v = __fmul_rn((float)dk_h(s), J.scale);
+      const int64_t col = c0 + c;
+      if (col < cols) {
+        if (J.transpose) J.out[(int64_t)(16 * rb + r) * cols + col] = v;
+        else J.out[col * R + 16 * rb + r] = v;
       }
+    }
+    __syncthreads();
   }
-}
-
-// out = fp32(fp16(sum over chunks of part[chunk][n][r])) * scale, stored [n][r] or, transposed,
-// [r][n].  Up to kMaxFinal jobs per launch; job j owns the threads from its t0 (a multiple of the
-// workgroup size) on.
-constexpr int kMaxFinal = 2 * kMaxJobs;
-struct FinalJob {
-  const float* part;
-  int64_t cols;
-  float scale;
-  float* out;
-  int transpose;
-  int64_t t0;
-};
-struct FinalJobs {
-  FinalJob j[kMaxFinal];
-  int n;
-};
-
-__global__ __launch_bounds__(kThreads) void lora_finalize_kernel(FinalJobs jobs, int64_t n_chunks,
-                                                                 int64_t R) {
-  const int64_t gi = (int64_t)blockIdx.x * kThreads + threadIdx.x;
-  int jb = 0;
-  for (int q = 1; q < jobs.n; ++q)
-    if (gi >= jobs.j[q].t0) jb = q;
-  const FinalJob& J = jobs.j[jb];
-  const int64_t i = gi - J.t0, cols = J.cols;
-  if (i >= cols * R) return;
-  const float* __restrict__ part = J.part;
-  // 8 loads in flight at a time, added in chunk order
-  float s = 0.0f;
-  int64_t c = 0;
-  for (; c + 8 <= n_chunks; c += 8) {
-    float v[8];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) v[u] = part[(c + u) * cols * R + i];
-#pragma unroll
-    for (int u = 0; u < 8; ++u) s += v[u];
-  }
-  for (; c < n_chunks; ++c) s += part[c * cols * R + i];
-  const float v = __fmul_rn((float)dk_h(s), J.scale);
-  const int64_t n = i / R, r = i % R;
-  if (J.transpose) J.out[r * cols + n] = v; else J.out[i] = v;
 }
 
 template <int MODE, bool MASKED>
@@ -356,32 +357,20 @@ int rows_launch(int64_t R, hipStream_t stream, const RowsJobs& jobs, int n_jobs,
   return 0;
 }
 
-int cols_launch(int64_t R, hipStream_t stream, ColsJobs jobs, int64_t rows) {
+int colsum_launch(int64_t R, hipStream_t stream, SumJobs jobs, int64_t rows) {
   int bx = 0;
   for (int q = 0; q < jobs.n; ++q) {
     jobs.j[q].bx0 = bx;
-    bx += (int)((jobs.j[q].cols + kColsPerBlock - 1) / kColsPerBlock);
+    bx += (int)((jobs.j[q].cols + kSumCols - 1) / kSumCols);
   }
-  const dim3 grid((unsigned)bx, (unsigned)((rows + kChunkRows - 1) / kChunkRows));
+  const dim3 grid((unsigned)bx), block(kSumThreads);
   switch (R) {
-    case 16: hipLaunchKernelGGL((lora_cols_kernel<16>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 32: hipLaunchKernelGGL((lora_cols_kernel<32>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 48: hipLaunchKernelGGL((lora_cols_kernel<48>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
-    case 64: hipLaunchKernelGGL((lora_cols_kernel<64>), grid, dim3(kThreads), 0, stream, jobs, rows); break;
+    case 16: hipLaunchKernelGGL((lora_colsum_kernel<16>), grid, block, 0, stream, jobs, rows); break;
+    case 32: hipLaunchKernelGGL((lora_colsum_kernel<32>), grid, block, 0, stream, jobs, rows); break;
+    case 48: hipLaunchKernelGGL((lora_colsum_kernel<48>), grid, block, 0, stream, jobs, rows); break;
+    case 64: hipLaunchKernelGGL((lora_colsum_kernel<64>), grid, block, 0, stream, jobs, rows); break;
     default: return DK_ERR_INVALID;
   }
-  DK_CHECK_LAUNCH();
-  return 0;
-}
-
-int finalize_launch(FinalJobs jobs, int64_t n_chunks, int64_t R, hipStream_t stream) {
-  int64_t t = 0;
-  for (int q = 0; q < jobs.n; ++q) {
-    jobs.j[q].t0 = t;
-    t += (jobs.j[q].cols * R + kThreads - 1) / kThreads * kThreads;
-  }
-  hipLaunchKernelGGL(lora_finalize_kernel, dim3((unsigned)(t / kThreads)), dim3(kThreads), 0, stream,
-                     jobs, n_chunks, R);
   DK_CHECK_LAUNCH();
   return 0;
 }
@@ -392,22 +381,22 @@ bool rank_ok(int64_t r) { return r >= 16 && r <= 64 && r % 16 == 0; }
 
 extern "C" int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t rank,
                                   const dk_lora_down_term* terms, int n_terms, hipStream_t stream) {
-  // (zero-element tensors have null data pointers: x and z are required only with rows)
-  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || (m > 0 && !x) || !terms || n_terms < 1 ||
-      n_terms > kMaxJobs)
+  // (zero-element tensors have null data pointers: the inputs and z are required only with rows)
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !terms || n_terms < 1 || n_terms > kMaxJobs)
     return DK_ERR_INVALID;
   if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
   int masked = 0;
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_down_term& u = terms[t];
-    if (m > 0 && (!u.a || !u.z)) return DK_ERR_INVALID;
-    if (!dk_aligned(u.a, 16) || (u.mask && !dk_aligned(u.mask, 8))) return DK_ERR_ALIGN;
+    if (m > 0 && (!u.a || !u.z || !(u.x ? u.x : x))) return DK_ERR_INVALID;
+    if (!dk_aligned(u.a, 16) || !dk_aligned(u.x, 16) || (u.mask && !dk_aligned(u.mask, 8)))
+      return DK_ERR_ALIGN;
     masked += u.mask != nullptr;
   }
   if (m == 0) return 0;
   auto job = [&](const dk_lora_down_term& u) {
-    return RowsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f, (const f16*)u.a, 1.0f,
-                   (f16*)u.z, k};
+    return RowsJob{(const f16*)(u.x ? u.x : x), k, u.mask, u.mask ? u.keep_scale : 1.0f,
+                   (const f16*)u.a, 1.0f, (f16*)u.z, k};
   };
   if (masked == 0 || masked == n_terms) {
     RowsJobs jobs = {};
@@ -427,80 +416,55 @@ extern "C" int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t r
 
 extern "C" int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const void* a,
                             void* z, int64_t m, int64_t k, int64_t rank, hipStream_t stream) {
-  const dk_lora_down_term t = {mask, keep_scale, a, z};
+  const dk_lora_down_term t = {mask, keep_scale, a, z, nullptr};
   return dk_lora_down_multi(x, m, k, rank, &t, 1, stream);
 }
 
-extern "C" int64_t dk_lora_grads_multi_workspace(int64_t m, int64_t k, int64_t rank,
-                                                 const int64_t* n_outs, int n_terms) {
-  if (m <= 0 || k <= 0 || rank <= 0 || !n_outs || n_terms < 1 || n_terms > kMaxJobs) return 0;
-  const int64_t chunks = (m + kChunkRows - 1) / kChunkRows;
-  int64_t cols = 0;
-  for (int t = 0; t < n_terms; ++t) cols += (n_outs[t] > 0 ? n_outs[t] : 0) + k;
-  return chunks * cols * rank * (int64_t)sizeof(float);
+extern "C" int64_t dk_lora_grads_multi_workspace(int64_t, int64_t, int64_t, const int64_t*, int) {
+  return 0;
 }
 
-extern "C" int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank) {
-  return dk_lora_grads_multi_workspace(m, k, rank, &n_out, 1);
-}
+extern "C" int64_t dk_lora_grads_workspace(int64_t, int64_t, int64_t, int64_t) { return 0; }
 
 extern "C" int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t rank,
-                                   const dk_lora_grads_term* terms, int n_terms, void* ws,
-                                   int64_t ws_bytes, hipStream_t stream) {
-  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !x || !terms || n_terms < 1 ||
-      n_terms > kMaxJobs)
+                                   const dk_lora_grads_term* terms, int n_terms, void*, int64_t,
+                                   hipStream_t stream) {
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !terms || n_terms < 1 || n_terms > kMaxJobs)
     return DK_ERR_INVALID;
   if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
-  int64_t n_outs[kMaxJobs];
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_grads_term& u = terms[t];
-    if (u.n_out <= 0 || u.n_out % 32 || !u.dy || !u.z || !u.lora_b || !u.da || !u.db || !u.dz ||
-        u.lddy < u.n_out)
+    // zero-element tensors have null data pointers: the row operands are required only with rows
+    if (u.n_out <= 0 || u.n_out % 32 || !u.lora_b || !u.da || !u.db || u.lddy < u.n_out ||
+        (m > 0 && (!u.dy || !u.z || !u.dz || !(u.x ? u.x : x))))
       return DK_ERR_INVALID;
-    if (!dk_aligned(u.dy, 16) || u.lddy % 8 || !dk_aligned(u.lora_b, 16) ||
+    if (!dk_aligned(u.dy, 16) || u.lddy % 8 || !dk_aligned(u.lora_b, 16) || !dk_aligned(u.x, 16) ||
         (u.mask && !dk_aligned(u.mask, 8)))
       return DK_ERR_ALIGN;
-    n_outs[t] = u.n_out;
   }
-  if (m == 0) return 0;
-  if (!ws || ws_bytes < dk_lora_grads_multi_workspace(m, k, rank, n_outs, n_terms))
-    return DK_ERR_WORKSPACE;
-  const int64_t chunks = (m + kChunkRows - 1) / kChunkRows;
-  // partial sums: [dB of every term | dA of every term], each chunks x cols x rank fp32
-  float* part_db[kMaxJobs];
-  float* part_da[kMaxJobs];
-  float* next = (float*)ws;
-  for (int t = 0; t < n_terms; ++t) { part_db[t] = next; next += chunks * n_outs[t] * rank; }
-  for (int t = 0; t < n_terms; ++t) { part_da[t] = next; next += chunks * k * rank; }
   // dz = fp16(fp16(dY B) * s)
-  RowsJobs rj = {};
-  for (int t = 0; t < n_terms; ++t) {
-    const dk_lora_grads_term& u = terms[t];
-    rj.j[t] = RowsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.lora_b, u.lora_scale,
-                      (f16*)u.dz, u.n_out};
+  if (m > 0) {
+    RowsJobs rj = {};
+    for (int t = 0; t < n_terms; ++t) {
+      const dk_lora_grads_term& u = terms[t];
+      rj.j[t] = RowsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.lora_b,
+                        u.lora_scale, (f16*)u.dz, u.n_out};
+    }
+    const int e = rows_launch<1, false>(rank, stream, rj, n_terms, m);
+    if (e) return e;
   }
-  int e = rows_launch<1, false>(rank, stream, rj, n_terms, m);
-  if (e) return e;
   // one launch: dB = fp32(fp16(dY^T z)) * s of every term, then dA = fp32(fp16(dz^T Xd)), Xd the
-  // dropout of x with the term's mask
-  ColsJobs cj = {};
-  cj.n = 2 * n_terms;
+  // term's input with its keep-mask (zero rows: both are zero)
+  SumJobs sj = {};
+  sj.n = 2 * n_terms;
   for (int t = 0; t < n_terms; ++t) {
     const dk_lora_grads_term& u = terms[t];
-    cj.j[t] = ColsJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.z, part_db[t], u.n_out, 0};
-    cj.j[n_terms + t] = ColsJob{(const f16*)x, k, u.mask, u.mask ? u.keep_scale : 1.0f,
-                                (const f16*)u.dz, part_da[t], k, 0};
+    sj.j[t] = SumJob{(const f16*)u.dy, u.lddy, nullptr, 1.0f, (const f16*)u.z, u.lora_scale,
+                     u.db, 0, u.n_out, 0};
+    sj.j[n_terms + t] = SumJob{(const f16*)(u.x ? u.x : x), k, u.mask,
+                               u.mask ? u.keep_scale : 1.0f, (const f16*)u.dz, 1.0f, u.da, 1, k, 0};
   }
-  e = cols_launch(rank, stream, cj, m);
-  if (e) return e;
-  FinalJobs fj = {};
-  fj.n = 2 * n_terms;
-  for (int t = 0; t < n_terms; ++t) {
-    const dk_lora_grads_term& u = terms[t];
-    fj.j[t] = FinalJob{part_db[t], u.n_out, u.lora_scale, u.db, 0, 0};
-    fj.j[n_terms + t] = FinalJob{part_da[t], k, 1.0f, u.da, 1, 0};
-  }
-  return finalize_launch(fj, chunks, rank, stream);
+  return colsum_launch(rank, stream, sj, m);
 }
 
 extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x,
@@ -508,6 +472,7 @@ extern "C" int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const 
                              float lora_scale, int64_t m, int64_t n_out, int64_t k, int64_t rank,
                              float* da, float* db, void* dz, void* ws, int64_t ws_bytes,
                              hipStream_t stream) {
-  const dk_lora_grads_term t = {dy, lddy, n_out, z, lora_b, lora_scale, mask, keep_scale, da, db, dz};
+  const dk_lora_grads_term t = {dy, lddy, n_out, z, lora_b, lora_scale, mask, keep_scale, da, db,
+                                dz, nullptr};
   return dk_lora_grads_multi(x, m, k, rank, &t, 1, ws, ws_bytes, stream);
 }

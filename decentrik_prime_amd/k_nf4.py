@@ -16,6 +16,8 @@ of ``w4linear`` read the same sections directly (``PackedLayer.weight``).  Host-
 streaming (the reference's SlotView / WeightPipe) is not part of this build.
 """
 
+import itertools
+
 import torch
 
 from . import _lib
@@ -76,84 +78,99 @@ def section_views(flat, offsets, n_qblocks):
             flat[o_o2:o_o2 + 4 * n2].view(torch.float32))
 
 
+# The format a 4-bit linear must have to be repacked (bitsandbytes NF4 with double quantisation,
+# solution/k_nf4.py:98-114): each rule is (test of (weight, quant_state), what it requires).
+_FORMAT_RULES = (
+    (lambda w, s: getattr(s, "quant_type", None) == "nf4" and int(s.blocksize) == 64,
+     "NF4 codes in first-level blocks of 64"),
+    (lambda w, s: bool(getattr(s, "nested", False)) and s.state2 is not None
+     and int(s.state2.blocksize) == 256,
+     "an absmax double-quantised in second-level blocks of 256"),
+    (lambda w, s: w.data.dtype == torch.uint8, "nibbles stored as uint8"),
+    (lambda w, s: s.dtype == torch.float16, "a float16 dequantised dtype"),
+)
+_ELEMS_PER_SB = 64 * 256     # weights under one (scale2, offset2) entry
+
+
 def _quant_parts(linear):
-    """(packed uint8 data, QuantState) of a 4-bit linear, checked for the nested NF4 format
-    (reference solution/k_nf4.py:98-114)."""
+    """(Params4bit, QuantState) of a 4-bit linear whose format the repacked layer can hold; a
+    ValueError names the first requirement it breaks (the reference's checks,
+    solution/k_nf4.py:98-114)."""
     weight = linear.weight
     state = getattr(weight, "quant_state", None)
-    if state is None:
+    if state is None:          # older bitsandbytes keeps the state on the module
         state = getattr(linear, "quant_state", None)
     if state is None:
-        raise ValueError("4-bit weight without quant_state")
-    if getattr(state, "quant_type", None) != "nf4" or int(state.blocksize) != 64:
-        raise ValueError(f"unsupported 4-bit format {state.quant_type}/{state.blocksize}")
-    if not getattr(state, "nested", False) or state.state2 is None or int(state.state2.blocksize) != 256:
-        raise ValueError("expected double quantisation (nested absmax, blocksize 256)")
-    if weight.data.dtype != torch.uint8:
-        raise ValueError(f"packed storage {weight.data.dtype}, expected uint8")
-    if state.dtype != torch.float16:
-        raise ValueError(f"quant_state dtype {state.dtype}, expected float16")
+        raise ValueError("the 4-bit weight carries no quant_state")
+    for holds, requirement in _FORMAT_RULES:
+        if not holds(weight, state):
+            raise ValueError(f"4-bit weight format not supported: it must have {requirement}")
     return weight, state
 
 
 def layer_numel(linears):
-    """Number of 4-bit weights of a layer (sum over its seven matrices)."""
-    total = 0
-    for name in LAYER_WEIGHTS:
-        _, state = _quant_parts(linears[name])
-        total += int(state.shape[0]) * int(state.shape[1])
-    return total
+    """Number of 4-bit weights of a layer: the element counts of its seven matrices."""
+    return sum(rows * cols for _, _, _, rows, cols in map(_source, LAYER_WEIGHTS,
+                                                          (linears[n] for n in LAYER_WEIGHTS)))
+
+
+def _source(name, linear):
+    """(name, weight, state, rows, cols) of one linear, its section sizes checked against its
+    shape: whole second-level blocks, n/2 packed bytes, n/64 and n/16384 absmax entries."""
+    weight, state = _quant_parts(linear)
+    rows, cols = (int(d) for d in state.shape)
+    n = rows * cols
+    sizes = {"whole second-level blocks": n % _ELEMS_PER_SB == 0,
+             "packed bytes": 2 * weight.data.numel() == n,
+             "first-level absmax entries": 64 * state.absmax.numel() == n,
+             "second-level absmax entries": _ELEMS_PER_SB * state.state2.absmax.numel() == n}
+    wrong = [what for what, ok in sizes.items() if not ok]
+    if wrong:
+        raise ValueError(f"{name}: a [{rows}, {cols}] weight with the wrong {', '.join(wrong)}")
+    return name, weight, state, rows, cols
+
+
+def _layer_buffer(nbytes, device, host, out):
+    if out is None:
+        where = {"pin_memory": True} if host else {"device": device}
+        return torch.empty(nbytes, dtype=torch.uint8, **where)
+    if out.dtype != torch.uint8 or out.numel() != nbytes:
+        raise ValueError(f"the preallocated layer buffer must be {nbytes} uint8 bytes")
+    return out
 
 
 def repack_layer(linears, device, host=False, out=None):
     """Repack the seven 4-bit linears of a layer (dict name -> module) into one PackedLayer and
     re-point their tensors at views of it, so nothing is stored twice (reference
-    solution/k_nf4.py:126-173).  host=True gives a pinned host buffer.  Returns
-    (PackedLayer, code2 fp32)."""
-    parts = [(name, *_quant_parts(linears[name])) for name in LAYER_WEIGHTS]
-    total = 0
-    segments = {}
-    code2 = None
-    for name, weight, state in parts:
-        rows, cols = int(state.shape[0]), int(state.shape[1])
-        n = rows * cols
-        if n % (64 * 256) != 0:
-            raise ValueError(f"{name}: {n} weights do not fill whole absmax blocks")
-        if weight.data.numel() * 2 != n or state.absmax.numel() * 64 != n:
-            raise ValueError(f"{name}: unexpected packed sizes")
-        if state.state2.absmax.numel() * 256 * 64 != n:
-            raise ValueError(f"{name}: unexpected second-level absmax size")
-        if code2 is None:
-            code2 = state.state2.code.to(device)
-        elif not torch.equal(code2, state.state2.code.to(device)):
-            raise ValueError("second-level code tables differ between weights")
-        segments[name] = (total, rows, cols)
-        total += n
-    n_qblocks = total // 64
+    solution/k_nf4.py:126-173).  host=True gives a pinned host buffer; `out` a preallocated one.
+    Returns (PackedLayer, code2 fp32)."""
+    sources = [_source(name, linears[name]) for name in LAYER_WEIGHTS]
+    tables = [src[2].state2.code.to(device) for src in sources]
+    if not all(torch.equal(tables[0], t) for t in tables[1:]):
+        raise ValueError("the weights of a layer must share one second-level code table")
+    starts = list(itertools.accumulate((rows * cols for *_, rows, cols in sources), initial=0))
+    segments = {src[0]: (at, src[3], src[4]) for src, at in zip(sources, starts)}
+    n_qblocks = starts[-1] // 64
     offsets, nbytes = section_layout(n_qblocks)
-    if out is not None:
-        if out.numel() != nbytes or out.dtype != torch.uint8:
-            raise ValueError("preallocated layer buffer has the wrong size")
-        flat = out
-    elif host:
-        flat = torch.empty(nbytes, dtype=torch.uint8, pin_memory=True)
-    else:
-        flat = torch.empty(nbytes, dtype=torch.uint8, device=device)
-    packed, qabs, scale2, offset2 = section_views(flat, offsets, n_qblocks)
-    for name, weight, state in parts:
-        start, rows, cols = segments[name]
+    layer = PackedLayer(_layer_buffer(nbytes, device, host, out), offsets, n_qblocks, segments)
+    home = "cpu" if host else device
+    for (name, weight, state, rows, cols), at in zip(sources, starts):
         n = rows * cols
-        b0, q0, s0 = start // 2, start // 64, start // (64 * 256)
-        b1, q1, s1 = b0 + n // 2, q0 + n // 64, s0 + n // (64 * 256)
-        packed[b0:b1].copy_(weight.data.reshape(-1))
-        qabs[q0:q1].copy_(state.absmax.reshape(-1))
-        scale2[s0:s1].copy_(state.state2.absmax.reshape(-1).float())
-        offset2[s0:s1].copy_(state.offset.float().reshape(1).expand(s1 - s0))
-        weight.data = packed[b0:b1].view(weight.data.shape)
-        state.absmax = qabs[q0:q1].view(state.absmax.shape)
-        state.state2.absmax = scale2[s0:s1].view(state.state2.absmax.shape)
-        state.offset = state.offset.to("cpu" if host else device)
-    return PackedLayer(flat, offsets, n_qblocks, segments), code2.float().contiguous()
+        # this weight's run of each section: bytes, first-level blocks, second-level blocks
+        nib = layer.packed.narrow(0, at // 2, n // 2)
+        first = layer.qabs.narrow(0, at // 64, n // 64)
+        scale2 = layer.scale2.narrow(0, at // _ELEMS_PER_SB, n // _ELEMS_PER_SB)
+        offset2 = layer.offset2.narrow(0, at // _ELEMS_PER_SB, n // _ELEMS_PER_SB)
+        nib.copy_(weight.data.flatten())
+        first.copy_(state.absmax.flatten())
+        scale2.copy_(state.state2.absmax.flatten())
+        # bitsandbytes keeps one offset per weight; the format has one per second-level block
+        offset2.copy_(torch.broadcast_to(state.offset.float().reshape(()), offset2.shape))
+        weight.data = nib.view(weight.data.shape)
+        state.absmax = first.view(state.absmax.shape)
+        state.state2.absmax = scale2.view(state.state2.absmax.shape)
+        state.offset = state.offset.to(home)
+    return layer, tables[0].float().contiguous()
 
 
 def dequant_tensors(packed, qabs, scale2, offset2, n_qblocks, code2, nf4, out):

@@ -5,7 +5,7 @@ slots and their carried schedule) with everything around it, in the order of the
 FastQwen2.forward / backward (solution/fast_qwen.py:985-1390):
   forward   x_0 = E[ids] (fp32 residual stream)
             per layer: y = RMSNorm(x_i) (+ the previous MLP output added on the way, x_i kept),
-            z_q, z_v = LoRA-down(dropout(y)), qkv = y W_qkv^T + b + LoRA-up, rotated (one GEMM),
+            xq, xv = fp16(dropout(y)) of the fp32 y, z_q, z_v = LoRA-down(xq, xv), qkv = y W_qkv^T + b + LoRA-up, rotated (one GEMM),
             attention, o = out W_o^T, y2 = RMSNorm(x_i + o), act, gu = SwiGLU(y2 W_gu^T),
             d = act W_d^T
             y_f = RMSNorm(x_L + d), LM head over vocabulary chunks: loss, stats, d(y_f)
@@ -79,6 +79,9 @@ class QwenQLoRAStep(NF4LinearStack):
         L = n_layers
         self.xin = [self.x0] + [torch.empty(m, D, dtype=f32, device=dev) for _ in range(L - 1)]
         self.y16 = [torch.empty(m, D, dtype=f16, device=dev) for _ in range(L)]
+        # the LoRA inputs: fp16(dropout(y)) of the fp32 norm output, per adapter
+        self.xq = [torch.empty(m, D, dtype=f16, device=dev) for _ in range(L)]
+        self.xv = [torch.empty(m, D, dtype=f16, device=dev) for _ in range(L)]
         self.qkv_b = [torch.empty(m, (NQ + 2 * NKV) * HD, dtype=f16, device=dev) for _ in range(L)]
         self.att = [None] * L
         self.lse = [None] * L
@@ -114,12 +117,15 @@ class QwenQLoRAStep(NF4LinearStack):
         x, d_prev = self.x0, None
         for i in range(self.n_layers):
             Lw, lo, z = self.layers[i], self.lora[i], self.z[i]
-            # norm 1 with the previous layer's MLP output added on the way (x_i materialised)
+            # norm 1 with the previous layer's MLP output added on the way (x_i materialised), and
+            # the two LoRA inputs dropped out from its fp32 output (solution/k_norm.py:49-53)
             k_norm.rms_forward(x, self.w_in[i], self.y16[i], self.rstd1[i], self.eps, delta=d_prev,
-                               xout=self.xin[i] if d_prev is not None else None)
+                               xout=self.xin[i] if d_prev is not None else None,
+                               xq=self.xq[i], xv=self.xv[i], mq=lo["mq"], mv=lo["mv"],
+                               keep_scale=self.keep_scale)
             y = self.y16[i]
-            lora_down_multi(y, [(lo["Aq"], lo["mq"], self.keep_scale),
-                                (lo["Av"], lo["mv"], self.keep_scale)], outs=[z["q"], z["v"]])
+            lora_down_multi(None, [(lo["Aq"], None, 1.0, self.xq[i]),
+                                   (lo["Av"], None, 1.0, self.xv[i])], outs=[z["q"], z["v"]])
             linear_forward_rope(y, Lw["qkv"], lo["bias"], self.qkv_terms(i), self.pos, self.cos,
                                 self.sin, (NQ + NKV) * HD, out=self.qkv_b[i], w16=w16("qkv", i),
                                 side=side("qkv", i + 1))
@@ -170,8 +176,8 @@ class QwenQLoRAStep(NF4LinearStack):
                                          HD, NQ // NKV)
             del dq, dkp, dvp
             (daq, dbq, dzq), (dav, dbv, dzv) = lora_grads_multi(
-                self.y16[i], [(dqkv[:, :D], z["q"], lo["Bq"], self.s, lo["mq"], ks),
-                              (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, lo["mv"], ks)])
+                None, [(dqkv[:, :D], z["q"], lo["Bq"], self.s, None, 1.0, self.xq[i]),
+                       (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, None, 1.0, self.xv[i])])
             if i > 0:
                 # d(y) = dqkv W_qkv + the masked LoRA input terms, in fp32, into norm 1's backward
                 linear_backward_dx_lora(dqkv, Lw["qkv"], [(dzq, lo["Aq"], lo["mq"], ks),

@@ -164,30 +164,39 @@ def lora_down(x, lora_A, mask=None, keep_scale=1.0, out=None):
 
 
 def lora_down_multi(x, terms, outs=None):
-    """lora_down of one or two adapters on the same x in shared launches (the q and v adapters
-    of the fused QKV projection): terms = [(lora_A [r, K], mask or None, keep_scale), ...].
-    Returns [z, ...], each exactly as lora_down computes it."""
-    _check16(x, "x")
-    m, k = x.shape
-    if not x.is_contiguous():
-        raise ValueError("lora_down_multi: x must be contiguous")
+    """lora_down of one or two adapters in shared launches (the q and v adapters of the fused QKV
+    projection): terms = [(lora_A [r, K], mask or None, keep_scale[, x_term]), ...].  A term's
+    input is x, or its own x_term [M, K] (the reference's xq / xv: the fp32 norm output dropped out
+    per adapter, solution/k_norm.py:49-53, given with mask None); x may be None when every term has
+    one.  Returns [z, ...], each exactly as lora_down computes it."""
     if not 1 <= len(terms) <= 2:
         raise ValueError("lora_down_multi takes one or two terms")
+    ins = [t[3] if len(t) > 3 and t[3] is not None else x for t in terms]
+    if any(u is None for u in ins):
+        raise ValueError("lora_down_multi: a term without its own input needs x")
+    for u in ins:
+        _check16(u, "x")
+        if not u.is_contiguous() or u.shape != ins[0].shape:
+            raise ValueError("lora_down_multi: the inputs must be contiguous [M, K] of one shape")
+    m, k = ins[0].shape
     r = terms[0][0].shape[0]
     arr = (_lib.LoraDownTermC * len(terms))()
     keep, zs = [], []
-    for t, (a, mask, ks) in enumerate(terms):
+    for t, term in enumerate(terms):
+        a, mask, ks = term[:3]
         _check16(a, "lora_A")
         if tuple(a.shape) != (r, k) or not a.is_contiguous():
             raise ValueError("lora_down_multi: every lora_A must be a contiguous [r, K]")
         mask = _mask_ok(mask, (m, k))
-        z = outs[t] if outs is not None else torch.empty(m, r, dtype=torch.float16, device=x.device)
+        z = outs[t] if outs is not None else torch.empty(m, r, dtype=torch.float16, device=a.device)
         _check16(z, "z", (m, r))
-        arr[t] = _lib.LoraDownTermC(_lib.ptr(mask), float(ks), _lib.ptr(a), _lib.ptr(z))
+        own = ins[t] if ins[t] is not x else None
+        arr[t] = _lib.LoraDownTermC(_lib.ptr(mask), float(ks), _lib.ptr(a), _lib.ptr(z),
+                                    _lib.ptr(own))
         keep.append((a, mask))
         zs.append(z)
     rc = _lib.lib().dk_lora_down_multi(_lib.ptr(x), m, k, r, arr, len(terms),
-                                       _lib.stream_handle(x.device))
+                                       _lib.stream_handle(ins[0].device))
     _lib.check(rc, "dk_lora_down_multi")
     return zs
 
@@ -436,37 +445,40 @@ def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
     if z.shape[0] != m or x.shape[0] != m or tuple(lora_B.shape) != (n_out, r):
         raise ValueError("lora_grads: inconsistent shapes")
     mask = _mask_ok(mask, (m, k))
-    L = _lib.lib()
     dev = dy.device
     da = torch.empty(r, k, dtype=torch.float32, device=dev)
     db = torch.empty(n_out, r, dtype=torch.float32, device=dev)
     dz = torch.empty(m, r, dtype=torch.float16, device=dev)
-    nbytes = int(L.dk_lora_grads_workspace(m, n_out, k, r))
-    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev)
-    rc = L.dk_lora_grads(_lib.ptr(dy), dy.stride(0), _lib.ptr(z), _lib.ptr(x), _lib.ptr(mask),
-                         float(keep_scale),
-                         _lib.ptr(lora_B), float(lora_scale), m, n_out, k, r, _lib.ptr(da),
-                         _lib.ptr(db), _lib.ptr(dz), _lib.ptr(ws), nbytes, _lib.stream_handle(dev))
+    rc = _lib.lib().dk_lora_grads(_lib.ptr(dy), dy.stride(0), _lib.ptr(z), _lib.ptr(x),
+                                  _lib.ptr(mask), float(keep_scale), _lib.ptr(lora_B),
+                                  float(lora_scale), m, n_out, k, r, _lib.ptr(da), _lib.ptr(db),
+                                  _lib.ptr(dz), None, 0, _lib.stream_handle(dev))
     _lib.check(rc, "dk_lora_grads")
     return da, db, dz
 
 
-def lora_grads_multi(x, terms):
-    """lora_grads of one or two adapters on the same x in shared launches: terms =
-    [(dy, z, lora_B, lora_scale, mask or None, keep_scale), ...].  Returns [(dA, dB, dz), ...],
+def lora_grads_multi(x, terms, outs=None):
+    """lora_grads of one or two adapters in shared launches: terms =
+    [(dy, z, lora_B, lora_scale, mask or None, keep_scale[, x_term]), ...], x_term the term's own
+    input (the reference's xq / xv, given with mask None) in place of x, which may then be None.
+    outs: [(dA, dB, dz), ...] to write into, or None to allocate.  Returns [(dA, dB, dz), ...],
     each exactly as lora_grads computes it."""
-    _check16(x, "x")
-    if not x.is_contiguous():
-        raise ValueError("x must be contiguous")
     if not 1 <= len(terms) <= 2:
         raise ValueError("lora_grads_multi takes one or two terms")
-    m, k = x.shape
+    ins = [t[6] if len(t) > 6 and t[6] is not None else x for t in terms]
+    if any(u is None for u in ins):
+        raise ValueError("lora_grads_multi: a term without its own input needs x")
+    for u in ins:
+        _check16(u, "x")
+        if not u.is_contiguous() or u.shape != ins[0].shape:
+            raise ValueError("lora_grads_multi: the inputs must be contiguous [M, K] of one shape")
+    m, k = ins[0].shape
     r = terms[0][1].shape[1]
-    dev = x.device
+    dev = ins[0].device
     arr = (_lib.LoraGradsTermC * len(terms))()
-    n_outs = (ctypes.c_int64 * len(terms))()
     keep, res = [], []
-    for t, (dy, z, lora_B, s, mask, ks) in enumerate(terms):
+    for t, term in enumerate(terms):
+        dy, z, lora_B, s, mask, ks = term[:6]
         _check16(dy, "dy")
         for u, nm in ((z, "z"), (lora_B, "lora_B")):
             _check16(u, nm)
@@ -476,20 +488,24 @@ def lora_grads_multi(x, terms):
         if dy.shape[0] != m or tuple(z.shape) != (m, r) or tuple(lora_B.shape) != (n_out, r):
             raise ValueError("lora_grads_multi: inconsistent shapes")
         mask = _mask_ok(mask, (m, k))
-        da = torch.empty(r, k, dtype=torch.float32, device=dev)
-        db = torch.empty(n_out, r, dtype=torch.float32, device=dev)
-        dz = torch.empty(m, r, dtype=torch.float16, device=dev)
+        if outs is not None:
+            da, db, dz = outs[t]
+            for u, shp, dt, nm in ((da, (r, k), torch.float32, "dA"), (db, (n_out, r), torch.float32, "dB"),
+                                   (dz, (m, r), torch.float16, "dz")):
+                if u.dtype != dt or tuple(u.shape) != shp or not u.is_contiguous():
+                    raise ValueError(f"lora_grads_multi: {nm} must be a contiguous {dt} {shp}")
+        else:
+            da = torch.empty(r, k, dtype=torch.float32, device=dev)
+            db = torch.empty(n_out, r, dtype=torch.float32, device=dev)
+            dz = torch.empty(m, r, dtype=torch.float16, device=dev)
+        own = ins[t] if ins[t] is not x else None
         arr[t] = _lib.LoraGradsTermC(_lib.ptr(dy), dy.stride(0), n_out, _lib.ptr(z),
                                      _lib.ptr(lora_B), float(s), _lib.ptr(mask), float(ks),
-                                     _lib.ptr(da), _lib.ptr(db), _lib.ptr(dz))
-        n_outs[t] = n_out
+                                     _lib.ptr(da), _lib.ptr(db), _lib.ptr(dz), _lib.ptr(own))
         keep.append((dy, mask))
         res.append((da, db, dz))
-    L = _lib.lib()
-    nbytes = int(L.dk_lora_grads_multi_workspace(m, k, r, n_outs, len(terms)))
-    ws = torch.empty(max(nbytes, 4) // 4, dtype=torch.float32, device=dev)
-    rc = L.dk_lora_grads_multi(_lib.ptr(x), m, k, r, arr, len(terms), _lib.ptr(ws), nbytes,
-                               _lib.stream_handle(dev))
+    rc = _lib.lib().dk_lora_grads_multi(_lib.ptr(x), m, k, r, arr, len(terms), None, 0,
+                                        _lib.stream_handle(dev))
     _lib.check(rc, "dk_lora_grads_multi")
     return res
 

@@ -167,7 +167,7 @@ int dk_head_finalize(const float* state, const int32_t* tgt_sorted, const int32_
  * and the lora_A GEMM (solution/k_norm.py:49-53; solution/fast_qwen.py:943-944):
  *   Xd = fp16(mask ? fp32(x) * keep_scale : 0),   z = fp16(Xd A^T)
  * x [m, k] fp16, mask [m, k] uint8 (nonzero = keep; NULL = no dropout), a [rank, k] fp16,
- * z [m, rank] fp16.  rank % 16 == 0, rank <= 64, k % 8 == 0. */
+ * z [m, rank] fp16.  rank % 16 == 0, rank <= 64, k % 32 == 0. */
 int dk_lora_down(const void* x, const uint8_t* mask, float keep_scale, const void* a, void* z,
                  int64_t m, int64_t k, int64_t rank, hipStream_t stream);
 
@@ -265,23 +265,27 @@ int dk_w4_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const dk_n
  *   dA = fp32(fp16(dz^T Xd)), Xd as in dk_lora_down   [rank, k] fp32
  * dy [m, n_out] fp16 with row stride lddy (a column slice of dQKV: gq = qkv[:, :NQ*HD]),
  * z [m, rank], x [m, k], mask [m, k] (NULL = no dropout), lora_b [n_out, rank].
- * ws: fp32 scratch of dk_lora_grads_workspace(m, n_out, k, rank) bytes. */
+ * Every column sum runs over all m rows in a fixed order (deterministic); with m == 0, dA and dB
+ * are written as zeros and dy, z, x, dz may be NULL.  ws / ws_bytes are accepted and unused: the
+ * workspace query returns 0. */
 int64_t dk_lora_grads_workspace(int64_t m, int64_t n_out, int64_t k, int64_t rank);
 int dk_lora_grads(const void* dy, int64_t lddy, const void* z, const void* x, const uint8_t* mask,
                   float keep_scale, const void* lora_b, float lora_scale, int64_t m,
                   int64_t n_out, int64_t k, int64_t rank, float* da, float* db, void* dz,
                   void* ws, int64_t ws_bytes, hipStream_t stream);
 
-/* One or two LoRA adapters on the same input x in shared launches: the q and v adapters of the
- * fused QKV projection (solution/fast_qwen.py:943-944 forward, 1364-1380 backward), each term
- * computed exactly as by dk_lora_down / dk_lora_grads (same kernels, same summation order), x
- * read by both terms' workgroups of one launch.  No counterpart in the reference as one call:
- * it batches the per-adapter calls above. */
+/* One or two LoRA adapters in shared launches: the q and v adapters of the fused QKV projection
+ * (solution/fast_qwen.py:943-944 forward, 1364-1380 backward), each term computed exactly as by
+ * dk_lora_down / dk_lora_grads (same kernels, same summation order).  A term's input is the
+ * call's x, or its own x when set: the reference's xq and xv, the norm's fp32 output dropped out
+ * per adapter and rounded once (solution/k_norm.py:49-53), are two inputs with no mask.  No
+ * counterpart in the reference as one call: it batches the per-adapter calls above. */
 typedef struct dk_lora_down_term {
   const uint8_t* mask;  /* [m, k] keep-mask or NULL */
   float keep_scale;
   const void* a;        /* lora_A [rank, k] fp16 */
   void* z;              /* [m, rank] fp16 out */
+  const void* x;        /* [m, k] fp16 input of this term, or NULL for the call's x */
 } dk_lora_down_term;
 int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t rank,
                        const dk_lora_down_term* terms, int n_terms, hipStream_t stream);
@@ -298,9 +302,10 @@ typedef struct dk_lora_grads_term {
   float* da;            /* [rank, k] fp32 out */
   float* db;            /* [n_out, rank] fp32 out */
   void* dz;             /* [m, rank] fp16 out */
+  const void* x;        /* [m, k] fp16 input of this term (dA's operand), or NULL for the call's x */
 } dk_lora_grads_term;
-/* ws: fp32 scratch of dk_lora_grads_multi_workspace(m, k, rank, n_outs, n_terms) bytes, n_outs
- * the terms' n_out in order. */
+/* x may be NULL when every term has its own.  ws / ws_bytes are accepted and unused (the
+ * workspace query returns 0). */
 int64_t dk_lora_grads_multi_workspace(int64_t m, int64_t k, int64_t rank, const int64_t* n_outs,
                                       int n_terms);
 int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t rank,

@@ -88,24 +88,33 @@ def test_argument_errors_come_back_before_launch():
                 lambda: lib.dk_h16_down_swiglu_bwd(p16, 1536, 8, p16, 1536, 8960, p16, None, 0,
                                                    ctypes.byref(side), None)):
             assert call() == err, bad
-    # LoRA gradient partial sums: 16 row chunks x (n_out + k) columns x rank fp32, per term
-    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 16 * (1536 + 1536) * 16 * 4
+    # the LoRA gradients need no workspace (one pass over the rows per column block)
+    assert lib.dk_lora_grads_workspace(2048, 1536, 1536, 16) == 0
     n_outs = (ctypes.c_int64 * 2)(1536, 256)
-    assert lib.dk_lora_grads_multi_workspace(2048, 1536, 16, n_outs, 2) == \
-        16 * (1536 + 256 + 2 * 1536) * 16 * 4
-    assert lib.dk_lora_grads_multi_workspace(2048, 1536, 16, n_outs, 3) == 0
+    assert lib.dk_lora_grads_multi_workspace(2048, 1536, 16, n_outs, 2) == 0
     down = (_lib.LoraDownTermC * 3)()
     assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 3, None) == _lib.DK_ERR_INVALID  # 3 terms
     assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_INVALID  # no A / z
     down[0] = _lib.LoraDownTermC(None, 1.0, ctypes.c_void_p(8), p16)
     assert lib.dk_lora_down_multi(p16, 8, 64, 16, down, 1, None) == _lib.DK_ERR_ALIGN
+    # a term's own input: required when the call has no x, and 16-byte aligned
+    down[0] = _lib.LoraDownTermC(None, 1.0, p16, p16, None)
+    assert lib.dk_lora_down_multi(None, 8, 64, 16, down, 1, None) == _lib.DK_ERR_INVALID
+    down[0] = _lib.LoraDownTermC(None, 1.0, p16, p16, ctypes.c_void_p(8))
+    assert lib.dk_lora_down_multi(None, 8, 64, 16, down, 1, None) == _lib.DK_ERR_ALIGN
     # no rows: zero-element tensors have null data pointers, and nothing is read or written
     down[0] = _lib.LoraDownTermC(None, 1.0, p16, None)
     assert lib.dk_lora_down_multi(None, 0, 64, 16, down, 1, None) == 0
     grads = (_lib.LoraGradsTermC * 1)()
     assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
-    grads[0] = _lib.LoraGradsTermC(p16, 64, 64, p16, p16, 2.0, None, 1.0, p16, p16, p16)
-    assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_WORKSPACE
+    grads[0] = _lib.LoraGradsTermC(p16, 64, 64, p16, ctypes.c_void_p(8), 2.0, None, 1.0, p16, p16, p16)
+    assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_ALIGN
+    grads[0] = _lib.LoraGradsTermC(p16, 32, 64, p16, p16, 2.0, None, 1.0, p16, p16, p16)   # lddy < n_out
+    assert lib.dk_lora_grads_multi(p16, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
+    grads[0] = _lib.LoraGradsTermC(p16, 64, 64, p16, p16, 2.0, None, 1.0, p16, p16, p16, None)
+    assert lib.dk_lora_grads_multi(None, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
+    grads[0] = _lib.LoraGradsTermC(None, 64, 64, None, p16, 2.0, None, 1.0, p16, p16, None, None)
+    assert lib.dk_lora_grads_multi(None, 8, 64, 16, grads, 1, None, 0, None) == _lib.DK_ERR_INVALID
     assert b"misaligned" in lib.dk_error_string(_lib.DK_ERR_ALIGN)
     with pytest.raises(ValueError):
         _lib.check(_lib.DK_ERR_INVALID, "probe")

@@ -236,6 +236,59 @@ def test_lora_ranks_and_mixed_masks(torch, rank):
             _scaled_close(host(g), ref[nm], f"{nm}_{term} vs oracle (rank {rank})")
 
 
+def test_lora_per_term_inputs_and_zero_rows(torch):
+    """Each term with its own input (the whole step's xq / xv, given with no mask) in the shared
+    launches: bit-identical to one call per term on that input, and equal to the masked form on
+    the common input wherever the dropout commutes with the rounding (the oracle's dropout of x is
+    the input).  Zero rows: dA and dB come back as zeros (not left unwritten), z and dz empty."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    m, D, KV = 1024, 1536, 256
+    log(f"LoRA per-term inputs, M={m}; zero rows")
+    x, aq, bq, mq, dyq = lora_inputs(m, D, D, seed=51)
+    _, av, bv, mv, dyv = lora_inputs(m, D, KV, seed=52)
+    ks = linear.keep_scale(0.05)
+    xq, xv = linear.dropout_input(x, mq, ks), linear.dropout_input(x, mv, ks)
+    t = {k: cuda16(v) for k, v in (("xq", xq), ("xv", xv), ("aq", aq), ("av", av), ("bq", bq),
+                                   ("bv", bv), ("gq", dyq), ("gv", dyv))}
+    zq, zv = w4linear.lora_down_multi(None, [(t["aq"], None, 1.0, t["xq"]),
+                                             (t["av"], None, 1.0, t["xv"])])
+    zq1 = w4linear.lora_down(t["xq"], t["aq"])
+    zv1 = w4linear.lora_down(t["xv"], t["av"])
+    multi = w4linear.lora_grads_multi(None, [(t["gq"], zq, t["bq"], 2.0, None, 1.0, t["xq"]),
+                                             (t["gv"], zv, t["bv"], 2.0, None, 1.0, t["xv"])])
+    single = [w4linear.lora_grads(t["gq"], zq, t["xq"], t["bq"], 2.0),
+              w4linear.lora_grads(t["gv"], zv, t["xv"], t["bv"], 2.0)]
+    # the masked form on the common input gives the same Xd, so the same results
+    tx = cuda16(x)
+    masked = w4linear.lora_grads_multi(tx, [(t["gq"], zq, t["bq"], 2.0, cuda(mq), ks),
+                                            (t["gv"], zv, t["bv"], 2.0, cuda(mv), ks)])
+    torch.cuda.synchronize()
+    _same(zq, zq1, "z_q")
+    _same(zv, zv1, "z_v")
+    for term, (both, one, msk) in zip("qv", zip(multi, single, masked)):
+        for nm, a, b, c in zip(("dA", "dB", "dz"), both, one, msk):
+            _same(a, b, f"{nm}_{term} per-term input vs one call")
+            _same(a, c, f"{nm}_{term} per-term input vs masked common input")
+    for term, got, (dy, z, a, b, n) in zip("qv", multi, ((dyq, zq, aq, bq, D), (dyv, zv, av, bv, KV))):
+        ref = linear.linear_bwd(dy, np.zeros((n, D), F16), host(z), x, mq if term == "q" else mv,
+                                ks, a, b, 2.0)
+        for nm, g in zip(("dA", "dB", "dZ"), got):
+            _scaled_close(host(g), ref[nm], f"{nm}_{term} vs oracle")
+    # zero rows: dA, dB written as zeros over garbage, no input needed
+    e16 = torch.empty(0, D, dtype=torch.float16, device="cuda")
+    ez = torch.empty(0, 16, dtype=torch.float16, device="cuda")
+    outs = [(torch.full((16, D), 7.0, device="cuda"), torch.full((n, 16), 7.0, device="cuda"),
+             torch.empty(0, 16, dtype=torch.float16, device="cuda")) for n in (D, KV)]
+    res = w4linear.lora_grads_multi(e16, [(torch.empty(0, D, dtype=torch.float16, device="cuda"), ez,
+                                           t["bq"], 2.0, None, 1.0),
+                                          (torch.empty(0, KV, dtype=torch.float16, device="cuda"), ez,
+                                           t["bv"], 2.0, None, 1.0)], outs=outs)
+    torch.cuda.synchronize()
+    for da, db, dz in res:
+        assert float(da.abs().max()) == 0.0 and float(db.abs().max()) == 0.0 and dz.numel() == 0
+
+
 def test_h16_argument_checks(torch):
     from decentrik_prime_amd import w4linear
     log("h16 argument checks")
