@@ -21,13 +21,13 @@ constexpr int kRowTile = 16;     // rows per workgroup of the row reductions
 constexpr int kRowThreads = 512; // 8 waves split K in the row reductions
 constexpr int kMaxJobs = 2;      // LoRA terms per launch (q and v of the fused QKV projection)
 
-__device__ __forceinline__ f16x8 dropout8(const f16x8 x, const uint8_t* mask, float ks) {
+__device__ __forceinline__ f16x8 dropout8(const f16x8 x, const u32x2 mw, float ks) {
   f16x8 out;
-  const u32x2 mw = *reinterpret_cast<const u32x2*>(mask);
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
     const uint32_t keep = (mw[e >> 2] >> (8 * (e & 3))) & 0xffu;
-    out[e] = keep ? dk_h(__fmul_rn((float)x[e], ks)) : (f16)0.0f;
+    const f16 kept = dk_h(__fmul_rn((float)x[e], ks));   // unconditional, then selected
+    out[e] = keep ? kept : (f16)0.0f;
   }
   return out;
 }
@@ -90,19 +90,26 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
     const int64_t steps = cols / 32;
     for (int64_t s0 = w; s0 < steps; s0 += NW * kBatch) {
       f16x8 a[kBatch], bw[kBatch][RB];
+      u32x2 mw[kBatch];
+      // every load of the batch first (x, keep-mask bytes, A), then the dropout and the MFMAs
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
         const int64_t s = s0 + (int64_t)u * NW;
         const int64_t k = (s < steps ? s : steps - 1) * 32 + lk;   // clamped; not accumulated
         a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + k);
-        if (MASKED) a[u] = dropout8(a[u], mask + m * cols + k, ks);
+        if (MASKED) mw[u] = *reinterpret_cast<const u32x2*>(mask + m * cols + k);
 #pragma unroll
         for (int b = 0; b < RB; ++b)
           bw[u][b] = *reinterpret_cast<const f16x8*>(wt + (int64_t)(16 * b + lr) * cols + k);
       }
+      __builtin_amdgcn_sched_barrier(0);   // the batch's loads stay ahead of their first use
+      // straight-line (a step past the end multiplies zeros), so no load is sunk below a branch
 #pragma unroll
       for (int u = 0; u < kBatch; ++u) {
-        if (s0 + (int64_t)u * NW >= steps) break;
+        if (MASKED) a[u] = dropout8(a[u], mw[u], ks);
+        const bool valid = s0 + (int64_t)u * NW < steps;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) a[u][e] = valid ? a[u][e] : (f16)0.0f;
 #pragma unroll
         for (int b = 0; b < RB; ++b)
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bw[u][b], acc[b], 0, 0, 0);
@@ -115,28 +122,34 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
       const int kc = (int)(cols - c0 < KC ? cols - c0 : KC);
       const int steps = kc / 32;
       f16x8 a[KU], bv[BI];
+      // every load of the pass first, at clamped addresses (straight-line: the compiler keeps
+      // them batched); rows of B past the pass are staged but never read
 #pragma unroll
       for (int u = 0; u < KU; ++u) {
-        const int s = w + u * NW < steps ? w + u * NW : steps - 1;   // clamped; not accumulated
+        const int s = w + u * NW < steps ? w + u * NW : steps - 1;   // clamped; zeroed below
         a[u] = *reinterpret_cast<const f16x8*>(in + m * ld + c0 + s * 32 + lk);
       }
 #pragma unroll
       for (int q = 0; q < BI; ++q) {
         const int i = tid + q * kRowThreads, kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
-        if (kk < kc) bv[q] = *reinterpret_cast<const f16x8*>(wt + (c0 + kk) * R + r8);
+        bv[q] = *reinterpret_cast<const f16x8*>(wt + (c0 + (kk < kc ? kk : kc - 1)) * R + r8);
       }
+      __builtin_amdgcn_sched_barrier(0);   // the pass's loads stay ahead of their first use
       __syncthreads();  // the previous pass has finished reading Bs
 #pragma unroll
       for (int q = 0; q < BI; ++q) {
         const int i = tid + q * kRowThreads, kk = i / (R / 8), r8 = (i % (R / 8)) * 8;
-        if (kk < kc) *reinterpret_cast<f16x8*>(Bs + kk * BLD + r8) = bv[q];
+        *reinterpret_cast<f16x8*>(Bs + kk * BLD + r8) = bv[q];
       }
       __syncthreads();
       {
 #pragma unroll
         for (int u = 0; u < KU; ++u) {
-          const int s = w + u * NW;
-          if (s >= steps) break;
+          const int s0 = w + u * NW;
+          const bool valid = s0 < steps;
+          const int s = valid ? s0 : steps - 1;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) a[u][e] = valid ? a[u][e] : (f16)0.0f;
 #pragma unroll
           for (int b = 0; b < RB; ++b) {
             const f16* base = Bs + (s * 32 + trow) * BLD + 16 * b + tcol;
@@ -201,17 +214,14 @@ struct SumJobs {
   int n;
 };
 
-template <int R>
-__global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, int64_t rows) {
-  int jb = 0;
-#pragma unroll
-  for (int q = 1; q < kMaxSumJobs; ++q)
-    if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].bx0) jb = q;
-  const SumJob& J = jobs.j[jb];
+// One column block of one job (see lora_colsum_kernel).  Every load is unconditional (rows past
+// the end read the last row and are zeroed when staged), so the number of loads in flight is the
+// same at every wait and the compiler's vmcnt waits count only the chunk being consumed.
+template <int R, bool DROP>
+__device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, uint8_t* lds) {
   const f16* __restrict__ P = J.P;
   const int64_t ld = J.ld;
   const uint8_t* __restrict__ mask = J.mask;
-  const bool drop = mask != nullptr;
   const float ks = J.ks;
   const f16* __restrict__ Q = J.Q;
   const int64_t cols = J.cols;
@@ -219,8 +229,7 @@ __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, 
   constexpr int QLD = R + 8;          // halves per staged Q row
   constexpr int QL = R / 16;          // 16-byte Q pieces per lane per chunk
   constexpr int WAVE_LDS = 32 * PLD * 2 + 32 * QLD * 2;
-  constexpr int RED = kSumWaves * kSumCols * 16 * 4;
-  __shared__ __attribute__((aligned(16))) uint8_t lds[kSumWaves * WAVE_LDS > RED ? kSumWaves * WAVE_LDS : RED];
+  constexpr int D = kSumDepth;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   f16* Ps = reinterpret_cast<f16*>(lds + w * WAVE_LDS);
   f16* Qs = Ps + 32 * PLD;
@@ -230,32 +239,24 @@ __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, 
   // this lane's pieces of a chunk: two 16-byte P pieces (rows l / 4 and l / 4 + 16, 8 columns at
   // 8 (l % 4)) with their mask bytes, and QL 16-byte pieces of the Q rows
   const int prow = lane >> 2, pc8 = 8 * (lane & 3);
-  f16x8 pv[kSumDepth][2], qv[kSumDepth][QL];
-  u32x2 mv[kSumDepth][2];
+  f16x8 pv[D][2], qv[D][QL];
+  u32x2 mv[D][2];
+  auto row_of = [&](int64_t i, int r) {   // global row r of this wave's chunk i, clamped
+    const int64_t m = 32 * (w + kSumWaves * i) + r;
+    return m < rows ? m : rows - 1;
+  };
   auto load = [&](int slot, int64_t i) {
-    const int64_t r0 = 32 * (w + kSumWaves * i);
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
-      const int64_t m = r0 + prow + 16 * u;
-      if (m < rows && c0 + pc8 < cols) {
-        pv[slot][u] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + pc8);
-        if (drop) mv[slot][u] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + pc8);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) pv[slot][u][e] = (f16)0.0f;
-        mv[slot][u] = u32x2{0u, 0u};
-      }
+      const int64_t m = row_of(i, prow + 16 * u);
+      pv[slot][u] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + pc8);
+      if (DROP) mv[slot][u] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + pc8);
     }
 #pragma unroll
     for (int u = 0; u < QL; ++u) {
-      const int idx = lane + 64 * u, row = idx / (R / 8), r8 = (idx % (R / 8)) * 8;
-      const int64_t m = r0 + row;
-      if (m < rows) {
-        qv[slot][u] = *reinterpret_cast<const f16x8*>(Q + m * R + r8);
-      } else {
-#pragma unroll
-        for (int e = 0; e < 8; ++e) qv[slot][u][e] = (f16)0.0f;
-      }
+      const int idx = lane + 64 * u;
+      qv[slot][u] = *reinterpret_cast<const f16x8*>(Q + row_of(i, idx / (R / 8)) * R +
+                                                    (idx % (R / 8)) * 8);
     }
   };
   const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
@@ -271,24 +272,32 @@ __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, 
   for (int cb = 0; cb < kSumCols / 16; ++cb)
 #pragma unroll
     for (int rb = 0; rb < R / 16; ++rb) acc[cb][rb] = f32x4{0.f, 0.f, 0.f, 0.f};
-  auto consume = [&](int slot) {
+  auto consume = [&](int slot, int64_t i) {
+    const int64_t r0 = 32 * (w + kSumWaves * i);
     __builtin_amdgcn_wave_barrier();   // the previous chunk's transposing reads are done
 #pragma unroll
     for (int u = 0; u < 2; ++u) {
       f16x8 v = pv[slot][u];
-      if (drop) {
+      const bool ok = r0 + prow + 16 * u < rows;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const uint32_t keep = (mv[slot][u][e >> 2] >> (8 * (e & 3))) & 0xffu;
-          v[e] = keep ? dk_h(__fmul_rn((float)v[e], ks)) : (f16)0.0f;
-        }
+      for (int e = 0; e < 8; ++e) {
+        // the product is formed unconditionally, then selected (no branch per element)
+        bool keep = ok;
+        if (DROP) keep = keep && ((mv[slot][u][e >> 2] >> (8 * (e & 3))) & 0xffu) != 0;
+        const f16 kept = DROP ? dk_h(__fmul_rn((float)v[e], ks)) : v[e];
+        v[e] = keep ? kept : (f16)0.0f;
       }
       *reinterpret_cast<f16x8*>(Ps + (prow + 16 * u) * PLD + pc8) = v;
     }
 #pragma unroll
     for (int u = 0; u < QL; ++u) {
       const int idx = lane + 64 * u, row = idx / (R / 8), r8 = (idx % (R / 8)) * 8;
-      *reinterpret_cast<f16x8*>(Qs + row * QLD + r8) = qv[slot][u];
+      f16x8 q = qv[slot][u];
+      if (r0 + row >= rows) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) q[e] = (f16)0.0f;
+      }
+      *reinterpret_cast<f16x8*>(Qs + row * QLD + r8) = q;
     }
     __builtin_amdgcn_wave_barrier();
 #pragma unroll
@@ -301,18 +310,20 @@ __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, 
       }
     }
   };
-  // kSumDepth chunks in flight: the loads of chunk i + kSumDepth - 1 go out before chunk i is
-  // consumed (slots rotate with the unrolled index)
+  // D chunks in flight: the loads of chunk i + D - 1 (clamped to the wave's last chunk) go out
+  // before chunk i is consumed; slots rotate with the unrolled index
+  if (mine > 0) {
 #pragma unroll
-  for (int s = 0; s < kSumDepth - 1; ++s)
-    if (s < mine) load(s, s);
-  for (int64_t i0 = 0; i0 < mine; i0 += kSumDepth) {
+    for (int s = 0; s < D - 1; ++s) load(s, s < mine ? s : mine - 1);
+    for (int64_t i0 = 0; i0 < mine; i0 += D) {
 #pragma unroll
-    for (int s = 0; s < kSumDepth; ++s) {
-      const int64_t i = i0 + s;
-      if (i >= mine) break;
-      if (i + kSumDepth - 1 < mine) load((s + kSumDepth - 1) % kSumDepth, i + kSumDepth - 1);
-      consume(s);
+      for (int s = 0; s < D; ++s) {
+        const int64_t i = i0 + s;
+        const int64_t nx = i + D - 1 < mine ? i + D - 1 : mine - 1;
+        load((s + D - 1) % D, nx);
+        __builtin_amdgcn_sched_barrier(0);   // the next chunk's loads go out before this one's use
+        if (i < mine) consume(s, i);
+      }
     }
   }
   // the waves' sums in wave order, one rank block at a time; result register v of lane l holds
@@ -341,6 +352,19 @@ __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, 
     }
     __syncthreads();
   }
+}
+
+template <int R>
+__global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, int64_t rows) {
+  int jb = 0;
+#pragma unroll
+  for (int q = 1; q < kMaxSumJobs; ++q)
+    if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].bx0) jb = q;
+  constexpr int WAVE_LDS = 32 * (kSumCols + 8) * 2 + 32 * (R + 8) * 2;
+  constexpr int RED = kSumWaves * kSumCols * 16 * 4;
+  __shared__ __attribute__((aligned(16))) uint8_t lds[kSumWaves * WAVE_LDS > RED ? kSumWaves * WAVE_LDS : RED];
+  if (jobs.j[jb].mask) colsum_block<R, true>(jobs.j[jb], rows, lds);
+  else colsum_block<R, false>(jobs.j[jb], rows, lds);
 }
 
 template <int MODE, bool MASKED>

@@ -77,7 +77,9 @@ def test_streamed_head_full_vocabulary(torch):
     tgt[32:36] = [chunk - 1, chunk, 2 * chunk - 1, last0]   # targets on chunk boundaries
     # (row, first column of an identical pair or None for a single planted maximum, target)
     planted = [(0, chunk - 1, chunk - 1), (1, 2 * chunk - 1, 2 * chunk), (2, v - 2, v - 1),
-               (3, None, last0), (4, last0 - 1, last0 - 1), (5, 3 * chunk + 7, 3 * chunk + 8)]
+               (3, None, last0), (4, 3 * chunk - 1, 3 * chunk - 1), (5, 3 * chunk + 7, 3 * chunk + 8)]
+    cols = [c for _, c, t in planted for c in ((t,) if c is None else (c, c + 1))]
+    assert len(set(cols)) == len(cols), "planted columns overlap"
     for row, c, t in planted:
         e = (y[row].astype(np.float32) * 0.01).astype(np.float16)
         if c is None:
