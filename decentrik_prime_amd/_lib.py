@@ -18,6 +18,7 @@ DK_ERR_INVALID = -1
 DK_ERR_ALIGN = -2
 DK_ERR_WORKSPACE = -3
 DK_OUT_F16, DK_OUT_F32, DK_OUT_F32_ACCUM = 0, 1, 2
+DK_NOALLOC_SCRATCH_BYTES = 64 << 20
 DK_OP_LINEAR_FWD, DK_OP_LINEAR_BWD_DX, DK_OP_GATEUP_SWIGLU_FWD, DK_OP_DOWN_SWIGLU_BWD = 0, 1, 2, 3
 
 _c_p, _i64, _int, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
@@ -95,6 +96,8 @@ SIGNATURES = {
                                       ctypes.POINTER(RopeC), _c_p, _i64, _S, _c_p]),
     "dk_h16_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64, _c_p,
                                          _i64, _int, _c_p, _i64, _S, _c_p]),
+    "dk_h16_linear_bwd_dx_lora_noalloc": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int,
+                                                 _i64, _c_p, _i64, _int, _S, _c_p]),
     "dk_h16_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64,
                                         _S, _c_p]),
     "dk_h16_down_swiglu_bwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _i64, _S,

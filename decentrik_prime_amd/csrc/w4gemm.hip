@@ -30,6 +30,8 @@
 // Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
 // (the REDUCE instance: consumer waves only, no LDS) sums them in split order and runs the
 // epilogue.
+#include <mutex>
+
 #include "gemm_common.h"
 
 using namespace dk;
@@ -992,6 +994,58 @@ extern "C" int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m
                                 out_mode))
     return e;
   return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream);
+}
+
+// ---- the allocation-free dX entry point: split-K partials in a library-owned device array
+
+// One copy per device, allocated with the code object and held until the process ends.  In host
+// code `scratch` names a host-side stand-in, never the device memory: the device address comes
+// from hipGetSymbolAddress, once per device with that device current, and only that address is
+// passed to kernels.
+static __device__ __align__(256) uint8_t scratch[DK_NOALLOC_SCRATCH_BYTES];
+
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::mutex g_scratch_lock;
+void* g_scratch_ptr[kMaxDevices] = {};
+
+// The device address of this device's scratch array (looked up on the first call on a device).
+int scratch_on_current_device(void** out) {
+  int dev = 0;
+  if (hipError_t e = hipGetDevice(&dev)) return (int)e;
+  if (dev < 0 || dev >= kMaxDevices) return DK_ERR_INVALID;
+  std::lock_guard<std::mutex> hold(g_scratch_lock);
+  if (!g_scratch_ptr[dev]) {
+    void* ptr = nullptr;
+    if (hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) return (int)e;
+    if (!ptr) return DK_ERR_INVALID;
+    g_scratch_ptr[dev] = ptr;
+  }
+  *out = g_scratch_ptr[dev];
+  return 0;
+}
+
+}  // namespace
+
+extern "C" int dk_h16_linear_bwd_dx_lora_noalloc(const void* dy, int64_t lddy, int64_t m,
+                                                 const void* w16, int64_t rows, int64_t cols,
+                                                 const dk_lora_term* terms, int n_terms,
+                                                 int64_t rank, void* dx, int64_t lddx,
+                                                 int out_mode, const dk_side_dequant* side,
+                                                 hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = linear_bwd_params(p, dy, lddy, m, rows, cols, terms, n_terms, rank, dx, lddx,
+                                out_mode))
+    return e;
+  // the partials this call's plan needs (0 without split-K), within the array's size
+  const int64_t need = dk_h16_workspace(m, rows, cols, DK_OP_LINEAR_BWD_DX);
+  if (need > DK_NOALLOC_SCRATCH_BYTES) return DK_ERR_WORKSPACE;
+  void* ws = nullptr;
+  if (need > 0) {
+    if (int e = scratch_on_current_device(&ws)) return e;
+  }
+  return dispatch_h16<true, EPI_LINEAR>(p, w16, ws, need, side, stream);
 }
 
 extern "C" int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16,

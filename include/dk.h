@@ -394,6 +394,21 @@ int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const voi
                               int64_t rank, void* dx, int64_t lddx, int out_mode, void* workspace,
                               int64_t workspace_bytes, const dk_side_dequant* side,
                               hipStream_t stream);
+/* dk_h16_linear_bwd_dx_lora without a workspace argument, allocating nothing.  No counterpart in
+ * the reference: it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, serving loops, harnesses that forbid hipMalloc).  The split-K partials go to a
+ * library-owned device array of DK_NOALLOC_SCRATCH_BYTES (64 MiB) per device, held until the
+ * process ends (every split plan on a 256-CU MI355X fits it); a plan that needs more returns
+ * DK_ERR_WORKSPACE before any launch.  Results are bit-identical to dk_h16_linear_bwd_dx_lora
+ * with a workspace of dk_h16_workspace bytes.  Every call on a device shares that device's array:
+ * calls that overlap on one device (two streams, two threads) race and must be serialised by the
+ * caller. */
+#define DK_NOALLOC_SCRATCH_BYTES (64ll << 20)
+int dk_h16_linear_bwd_dx_lora_noalloc(const void* dy, int64_t lddy, int64_t m, const void* w16,
+                                      int64_t rows, int64_t cols, const dk_lora_term* terms,
+                                      int n_terms, int64_t rank, void* dx, int64_t lddx,
+                                      int out_mode, const dk_side_dequant* side,
+                                      hipStream_t stream);
 int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
                              int64_t cols, void* act, void* gu_out, void* workspace,
                              int64_t workspace_bytes, const dk_side_dequant* side,
