@@ -10,11 +10,12 @@ One step = every layer's forward then every layer's backward (dX of all seven pr
 the LoRA gradients).  value = algorithmic TFLOP/s of the step (2 M N K per GEMM; dequant counts
 no FLOPs).
 
-Also measured live with HIP events on the launch stream: each kernel of the step in isolation
-(average launch duration -> TFLOP/s or GB/s), and the NF4 dequant of all 28 layers (3.30 GB of
-algorithmic traffic, far above the 256 MB Infinity Cache) -> GB/s against the 8 TB/s HBM peak.
-The CPU baseline times the CPU oracle (numpy dequant + fp32 torch GEMMs) on one layer's
-forward + backward, on this host's cores.
+Also measured, with HIP events: each operator of the step in isolation and the NF4 dequant of all
+28 layers (3.30 GB of algorithmic traffic, far above the 256 MB Infinity Cache), both as CUDA-graph
+replays so the host's launch overhead is not in the figure; BASELINE configs 0-3 on layer 0 of
+the stack (GPU time and roofline fraction, the CPU oracle's time on this host's cores, and the
+parity of the GPU result with the oracle).  The CPU baseline of the metric times the CPU oracle
+(numpy dequant + fp32 torch GEMMs) on a sample of config 4's layers, on this host's cores.
 """
 
 import argparse
@@ -25,6 +26,7 @@ import sys
 import time
 
 HBM_PEAK_GBS = 8000.0
+EAGER = False   # --eager: time operators by plain back-to-back launches (counter runs count dispatches)
 FP16_PEAK_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense fp16 MFMA)
 
 
@@ -44,6 +46,216 @@ def time_op(torch, fn, reps):
     e1.record()
     torch.cuda.synchronize()
     return e0.elapsed_time(e1) / reps
+
+
+def time_graph(torch, fn, iters=10, reps=3):
+    """Average GPU time (ms) of one call of fn: `iters` calls captured in one CUDA graph and the
+    graph replayed `reps` times, timed with HIP events.  This is the kernels' time plus the GPU-side
+    gaps between them, without the host's launch overhead (which exceeds the kernel time of the
+    small operators when they are launched back to back from Python)."""
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()                       # lazy allocations (workspaces, outputs) outside the capture
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        for _ in range(iters):
+            fn()
+    g.replay()
+    torch.cuda.synchronize()
+    e0, e1 = _events(torch)
+    e0.record()
+    for _ in range(reps):
+        g.replay()
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / (reps * iters)
+    del g
+    return ms
+
+
+def _median_s(fn, reps=5):
+    """Median wall time (s) of fn on the CPU over `reps` runs after one warm-up run."""
+    fn()
+    ts = []
+    for _ in range(reps):
+        t0 = time.perf_counter()
+        fn()
+        ts.append(time.perf_counter() - t0)
+    return sorted(ts)[len(ts) // 2]
+
+
+def _scaled_err(got, want):
+    """max |got - want| / max |want| and whether every element is within rtol 1e-2 / atol 2e-2 of
+    the output's scale (the tolerance BASELINE.json's north_star states for GEMM outputs and LoRA
+    gradients)."""
+    import numpy as np
+    got = np.asarray(got, np.float64)
+    want = np.asarray(want, np.float64)
+    scale = float(np.abs(want).max()) or 1.0
+    err = np.abs(got - want) / scale
+    ok = bool(np.all(err <= 2e-2 + 1e-2 * np.abs(want) / scale))
+    return float(err.max()), ok
+
+
+def config_rows(torch, st, cpu=True):
+    """BASELINE.json configs 0-3 on layer 0 of the bench's stack (its NF4 weights, LoRA factors,
+    keep-masks, X and dY, generated as configs 0-4 prescribe): per config the GPU time of the
+    NF4-reading kernels (CUDA-graph replay), its roofline fraction, the CPU oracle's time on this
+    host's cores (NF4 dequant + fp32 GEMMs, median of 5) and the parity of the GPU result with the
+    oracle (dequant bit-exact; GEMM outputs and LoRA gradients at rtol 1e-2 / atol 2e-2)."""
+    import numpy as np
+    from decentrik_prime_amd import k_nf4
+    from decentrik_prime_amd import w4linear as W
+    from oracle import linear, mlp, nf4
+    torch.set_num_threads(os.cpu_count())
+    m, D, I, KV, r = st.m, 1536, 8960, 256, 16
+    L, lo, x, dev = st.layers[0], st.lora[0], st.x, st.x.device
+    pk = L["packed"]
+    ks, s = st.keep_scale, st.s
+    f16 = torch.float16
+    host = lambda t: t.detach().cpu().numpy()  # noqa: E731
+    ws = {n: pk.weight(n, st.code2, st.nf4) for n in ("q_proj", "v_proj", "gate_proj", "down_proj")}
+    wgu = pk.weights(("gate_proj", "up_proj"), st.code2, st.nf4)
+    c2 = host(st.code2)
+
+    def sections(w):
+        return tuple(host(t) for t in (w.packed, w.qabs, w.scale2, w.offset2))
+
+    def cpu_deq(w):
+        return nf4.dequant(*sections(w), c2).reshape(w.rows, w.cols)
+
+    g = lambda mm, n, k: 2.0 * mm * n * k  # noqa: E731
+    rows = []
+    cores = torch.get_num_threads()
+
+    def row(cfg, what, ms, work, unit, cpu_s, parity, alt=None):
+        if unit == "GB/s":
+            rate = work / (ms * 1e-3) / 1e9
+            gpu = {"us": round(ms * 1e3, 2), "bytes": int(work), "gbps": round(rate, 1),
+                   "frac": round(rate / HBM_PEAK_GBS, 4)}
+        else:
+            rate = work / (ms * 1e-3) / 1e12
+            gpu = {"us": round(ms * 1e3, 2), "gflop": round(work / 1e9, 3), "tflops": round(rate, 1),
+                   "frac": round(rate / FP16_PEAK_TFLOPS, 4)}
+        out = {"config": cfg, "what": what, "gpu": gpu}
+        if alt:
+            out["gpu_fp16_slot_form"] = alt
+        if cpu_s is not None:
+            out["cpu"] = {"s": round(cpu_s, 4), "cores": cores, "kind": "port",
+                          "gpu_speedup": round(cpu_s / (ms * 1e-3), 1)}
+        out["parity"] = parity
+        rows.append(out)
+        print(f"[bench] config {cfg}: {what}: {gpu} cpu {out.get('cpu')} parity {parity}",
+              file=sys.stderr, flush=True)
+
+    def check(label, pairs):
+        worst, ok = 0.0, True
+        for got, want in pairs:
+            e, good = _scaled_err(got, want)
+            worst, ok = max(worst, e), ok and good
+        if not ok:
+            raise RuntimeError(f"{label}: GPU result outside rtol 1e-2 / atol 2e-2 of the oracle")
+        return f"rtol 1e-2 / atol 2e-2 of scale: pass (max |err| / scale {worst:.2e})"
+
+    # config 0: dequant of one q_proj weight [1536, 1536]
+    wq = ws["q_proj"]
+    out0 = torch.empty(D * D, dtype=f16, device=dev)
+    dq0 = lambda: k_nf4.dequant_tensors(wq.packed, wq.qabs, wq.scale2, wq.offset2, D * D // 64,  # noqa: E731
+                                        st.code2, st.nf4, out0)
+    ms0 = time_graph(torch, dq0)
+    dq0()
+    torch.cuda.synchronize()
+    want0 = cpu_deq(wq).reshape(-1)
+    exact = bool(np.array_equal(host(out0).view(np.uint16), want0.view(np.uint16)))
+    if not exact:
+        raise RuntimeError("config 0: GPU dequant not bit-exact with the oracle")
+    row(0, "NF4 dequant of q_proj [1536,1536] (latency-bound at this size; the bandwidth figure is "
+           "the 28-layer dequant)", ms0, D * D * (0.5 + 1 / 64 + 8 / 16384 + 2), "GB/s",
+        _median_s(lambda: cpu_deq(wq)) if cpu else None, "bit-exact")
+
+    # config 1: q_proj forward with the rank-16 LoRA term and dropout (no bias)
+    wq16 = out0.view(D, D)
+    aq, bq, mq = lo["Aq"], lo["Bq"], lo["mq"]
+    y1 = torch.empty(m, D, dtype=f16, device=dev)
+    z1 = torch.empty(m, r, dtype=f16, device=dev)
+
+    def fwd1(w16=None):
+        W.lora_down_multi(x, [(aq, mq, ks)], outs=[z1])
+        return W.linear_forward(x, wq, z=z1, lora_B=bq, lora_scale=s, out=y1, w16=w16)
+    f1 = g(m, D, D) + g(m, r, D) + g(m, D, r)
+    ms1 = time_graph(torch, fwd1)
+    ms1h = time_graph(torch, lambda: (dq0(), fwd1(wq16)))
+    fwd1()
+    torch.cuda.synchronize()
+    xn, aqn, bqn, mqn = host(x), host(aq), host(bq), host(mq)
+    ref1 = {}
+
+    def cpu1():
+        ref1["y"], ref1["z"] = linear.linear_fwd(xn, cpu_deq(wq), None, mqn, ks, aqn, bqn, s)
+    cpu1_s = _median_s(cpu1) if cpu else (cpu1() or None)
+    par1 = check("config 1", [(host(y1), ref1["y"]), (host(z1), ref1["z"])])
+    row(1, "q_proj forward + LoRA r=16 with dropout, M=2048 (lora_down + fused NF4 GEMM)", ms1,
+        f1, "TFLOP/s", cpu1_s, par1,
+        alt={"us": round(ms1h * 1e3, 2), "what": "dequant to fp16 + fp16 GEMM"})
+
+    # config 2: MLP forward, no LoRA (gate|up + SwiGLU, down)
+    act2 = torch.empty(m, I, dtype=f16, device=dev)
+    gu2 = torch.empty(m, 2 * I, dtype=f16, device=dev)
+    y2 = torch.empty(m, D, dtype=f16, device=dev)
+
+    def fwd2():
+        W.gateup_swiglu_forward(x, wgu, act=act2, gu=gu2)
+        W.linear_forward(act2, ws["down_proj"], out=y2)
+    f2 = g(m, 2 * I, D) + g(m, D, I)
+    ms2 = time_graph(torch, fwd2, iters=3)
+    fwd2()
+    torch.cuda.synchronize()
+    ref2 = {}
+
+    def cpu2():
+        ref2["gu"], ref2["h"], ref2["y"] = mlp.mlp_fwd(xn, cpu_deq(wgu), cpu_deq(ws["down_proj"]))
+    cpu2_s = _median_s(cpu2, 3) if cpu else (cpu2() or None)
+    par2 = check("config 2", [(host(act2), ref2["h"]), (host(y2), ref2["y"])])
+    row(2, "MLP forward: gate|up + SwiGLU, down, M=2048 (NF4 weights, dequantised once to fp16 "
+           "then the 256-tile GEMMs)", ms2, f2, "TFLOP/s", cpu2_s, par2)
+
+    # config 3: backward of q_proj and v_proj (dX through the NF4 weight + LoRA dX, dA, dB)
+    wv = ws["v_proj"]
+    av, bv, mv = lo["Av"], lo["Bv"], lo["mv"]
+    zv = W.lora_down_multi(x, [(av, mv, ks)])[0]
+    dyq, dyv = st.dy["qkv"][:, :D], st.dy["qkv"][:, D + KV:]
+    dxq = torch.empty(m, D, dtype=torch.float32, device=dev)
+    dxv = torch.empty(m, D, dtype=torch.float32, device=dev)
+    res3 = {}
+
+    def bwd3():
+        (daq, dbq, dzq), (dav, dbv, dzv) = W.lora_grads_multi(
+            x, [(dyq, z1, bq, s, mq, ks), (dyv, zv, bv, s, mv, ks)])
+        W.linear_backward_dx_lora(dyq, wq, [(dzq, aq, mq, ks)], out=dxq)
+        W.linear_backward_dx_lora(dyv, wv, [(dzv, av, mv, ks)], out=dxv)
+        res3.update(daq=daq, dbq=dbq, dav=dav, dbv=dbv)
+    # q: dX + (dB, dz, dA, dX_lora) = 10.066 GFLOP; v: dX + the same four = 1.845 GFLOP
+    f3 = g(m, D, D) + 4 * g(m, r, D) + g(m, D, KV) + 2 * g(m, KV, r) + 2 * g(m, r, D)
+    ms3 = time_graph(torch, bwd3)
+    bwd3()
+    torch.cuda.synchronize()
+    dyqn, dyvn, zqn, zvn = host(dyq), host(dyv), host(z1), host(zv)
+    avn, bvn, mvn = host(av), host(bv), host(mv)
+    ref3 = {}
+
+    def cpu3():
+        ref3["q"] = linear.linear_bwd(dyqn, cpu_deq(wq), zqn, xn, mqn, ks, aqn, bqn, s)
+        ref3["v"] = linear.linear_bwd(dyvn, cpu_deq(wv), zvn, xn, mvn, ks, avn, bvn, s)
+    cpu3_s = _median_s(cpu3) if cpu else (cpu3() or None)
+    par3 = check("config 3", [(host(dxq), ref3["q"]["dx"]), (host(dxv), ref3["v"]["dx"]),
+                              (host(res3["daq"]), ref3["q"]["dA"]), (host(res3["dbq"]), ref3["q"]["dB"]),
+                              (host(res3["dav"]), ref3["v"]["dA"]), (host(res3["dbv"]), ref3["v"]["dB"])])
+    row(3, "q_proj + v_proj backward: dX through the NF4 weights with the masked LoRA dX, dA, dB, "
+           "M=2048", ms3, f3, "TFLOP/s", cpu3_s, par3)
+    return rows
 
 
 def kernel_table(torch, st, reps, only=None):
@@ -126,7 +338,7 @@ def kernel_table(torch, st, reps, only=None):
     for name, fn, flops, nbytes, per_layer in rows:
         if only is not None and name not in only:
             continue
-        ms = time_op(torch, fn, reps)
+        ms = time_op(torch, fn, reps) if EAGER else time_graph(torch, fn, iters=max(3, reps // 2))
         row = {"kernel": name, "avg_us": round(ms * 1e3, 2), "launches_per_layer": per_layer,
                "gflop": round(flops / 1e9, 3)}
         if flops:
@@ -218,7 +430,7 @@ def neighbour_table(torch, reps, m=2048, d=1536, nq=12, nkv=2, hd=128, only=None
     for name, fn, nbytes, *flops in rows:
         if only is not None and name not in only:
             continue
-        ms = time_op(torch, fn, reps)
+        ms = time_op(torch, fn, reps) if EAGER else time_graph(torch, fn, iters=3, reps=max(2, reps // 4))
         if nbytes is None:
             tf = flops[0] / (ms * 1e-3) / 1e12
             res.append({"kernel": name, "avg_us": round(ms * 1e3, 2),
@@ -274,7 +486,7 @@ def dequant_bandwidth(torch, st, reps):
     def run():
         for L, out in zip(st.layers, outs):
             k_nf4.dequant_layer(L["packed"], st.code2, st.nf4, out)
-    ms = time_op(torch, run, reps)
+    ms = time_op(torch, run, reps) if EAGER else time_graph(torch, run, iters=2, reps=max(2, reps // 2))
     n_weights = st.layers[0]["packed"].numel
     bytes_per_weight = 0.5 + 1 / 64 + 8 / 16384 + 2
     per_launch_bytes = n_weights * bytes_per_weight
@@ -387,9 +599,11 @@ def _short(name):
     return re.sub(r"\s+", " ", name[:cut])[:100]
 
 
-def summarize_trace(db, top=40):
+def summarize_trace(db, top=40, ops=()):
     """Per-kernel dispatch statistics of a kernel trace: calls, average and total duration,
-    grouped by kernel name and grid (a kernel instance launched at several shapes is split)."""
+    grouped by kernel name and grid (a kernel instance launched at several shapes is split).
+    ops: [(operator, kernel-name substring, grid)] for which an 'OPAVG' line is added (what
+    bench.py reads back as the profile's average duration of that operator's kernel)."""
     import collections
     import sqlite3
     cur = sqlite3.connect(db).cursor()
@@ -405,6 +619,12 @@ def summarize_trace(db, top=40):
     for (k, wgs, wx), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
         lines.append(f"{k:78s} {wgs:7d} {wx:4d} {len(v):6d} {sum(v) / len(v) / 1e3:9.2f} "
                      f"{sum(v) / 1e6:9.3f} {100 * sum(v) / total:6.2f}")
+    for op, pattern, grid in ops:
+        sel = [(k, v) for k, v in agg.items() if pattern in k[0] and k[1] == grid]
+        if sel:
+            durs = [d for _, v in sel for d in v]
+            lines.append(f"OPAVG {op} | {sel[0][0][0]} | {grid} | {sum(durs) / len(durs) / 1e3:.2f} | "
+                         f"{len(durs)}")
     return "\n".join(lines)
 
 
@@ -457,6 +677,84 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
     return "\n".join(out)
 
 
+def _counters_by_dispatch(db):
+    """{(dispatch id, kernel, grid in workgroups, workgroup size): {counter: (sum, max, n)}} over
+    the counter's instances (SEs / XCDs) of each dispatch, and each dispatch's duration (ns) when
+    the run also traced kernels."""
+    import sqlite3
+    cur = sqlite3.connect(db).cursor()
+    out = {}
+    for did, name, grid, wg, cname, val in cur.execute(
+            "select dispatch_id, kernel_name, grid_size, workgroup_size, counter_name, value "
+            "from counters_collection"):
+        key = (did, _short(name), grid // max(wg, 1), wg)
+        agg = out.setdefault(key, {})
+        s_, m_, n_ = agg.get(cname, (0.0, float("-inf"), 0))
+        agg[cname] = (s_ + val, max(m_, val), n_ + 1)
+    dur = {}
+    try:
+        for did, start, end in cur.execute("select dispatch_id, start, end from kernels"):
+            dur[did] = end - start
+    except sqlite3.Error:
+        pass
+    return out, dur
+
+
+def summarize_counters(db, groups, simds=1024, xcds=8):
+    """MFMA utilisation per operator from a `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES
+    SQ_INSTS_VALU_MFMA_MOPS_F16 GRBM_GUI_ACTIVE SQ_BUSY_CU_CYCLES --kernel-trace` run:
+    MFMA busy = sum over instances of SQ_VALU_MFMA_BUSY_CYCLES / (max GRBM_GUI_ACTIVE x SIMDs)
+    (rocprofv3's MfmaUtil), the MFMA FLOPs the hardware counted (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512)
+    and the effective clock (GRBM_GUI_ACTIVE / kernel duration).  GRBM_GUI_ACTIVE is stored summed
+    over the XCDs, so it is divided by their count (8 on MI355X) for the per-XCD busy cycles; its
+    window also covers the dispatch's start and drain, which for kernels of ~20 us inflates the
+    clock and deflates the busy fraction (the algorithmic FLOPs over the duration are the figure
+    there).
+    groups: [(operator name, kernel-name substring, grid in workgroups or None, algorithmic FLOP)]."""
+    rows, dur = _counters_by_dispatch(db)
+    lines = [f"{'operator':34s} {'kernel':30s} {'wgs':>5s} {'n':>3s} {'mfma_busy':>9s} "
+             f"{'clock_GHz':>9s} {'mfma_GFLOP':>10s} {'algo_GFLOP':>10s} {'avg_us':>8s}"]
+    for op, pattern, wgs_only, algo in groups:
+        sel = [(k, v) for k, v in rows.items()
+               if pattern in k[1] and (wgs_only is None or k[2] == wgs_only)]
+        if not sel:
+            lines.append(f"{op:34s} (no dispatch of {pattern})")
+            continue
+        busy, clk, flops, us = [], [], [], []
+        for (did, name, wgs, wg), v in sel:
+            gui = v.get("GRBM_GUI_ACTIVE", (0, 0, 0))[0] / xcds
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in v and gui > 0:
+                busy.append(v["SQ_VALU_MFMA_BUSY_CYCLES"][0] / (gui * simds))
+            if "SQ_INSTS_VALU_MFMA_MOPS_F16" in v:
+                flops.append(v["SQ_INSTS_VALU_MFMA_MOPS_F16"][0] * 512)
+            if did in dur and dur[did] > 0:
+                us.append(dur[did] / 1e3)
+                if gui > 0:
+                    clk.append(gui / dur[did])
+        mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")  # noqa: E731
+        name = sel[0][0][1]
+        lines.append(f"{op:34s} {name[:30]:30s} {sel[0][0][2]:5d} {len(sel):3d} "
+                     f"{100 * mean(busy):8.1f}% {mean(clk):9.3f} {mean(flops) / 1e9:10.2f} "
+                     f"{(algo or 0) / 1e9:10.2f} {mean(us):8.2f}")
+        lines.append(f"MFMA {op} | busy {mean(busy):.4f} | clock_ghz {mean(clk):.3f} | "
+                     f"avg_us {mean(us):.2f}")
+    return "\n".join(lines)
+
+
+def committed_kernel_avg(op):
+    """Average duration (us) of operator `op`'s kernel in the committed rocprof kernel-trace summary
+    (an 'OPAVG op | kernel | wgs | avg_us | calls' line) and the summary's path, or None."""
+    import glob
+    here = os.path.dirname(os.path.abspath(__file__))
+    for path in sorted(glob.glob(os.path.join(here, "profiles", "*.txt"))):
+        for line in open(path):
+            if line.startswith("OPAVG ") and line[6:].split(" | ")[0] == op:
+                parts = [x.strip() for x in line[6:].split(" | ")]
+                return {"avg_us": float(parts[3]), "kernel": parts[1], "wgs": int(parts[2]),
+                        "calls": int(parts[4]), "source": os.path.relpath(path, here)}
+    return None
+
+
 def committed_traffic(op):
     """HBM bytes per call of `op` from the TRAFFIC lines of the committed profile summaries."""
     import glob
@@ -485,6 +783,11 @@ def main():
     ap.add_argument("--no-model", action="store_true",
                     help="skip the whole-model step (norms, attention, LM head around the stack)")
     ap.add_argument("--reps", type=int, default=20)
+    ap.add_argument("--eager", action="store_true",
+                    help="time operators by plain back-to-back launches instead of CUDA-graph replays "
+                         "(rocprofv3 counter runs: each operator call is then one dispatch per kernel)")
+    ap.add_argument("--no-configs", action="store_true",
+                    help="skip the BASELINE configs 0-3 rows (GPU, CPU oracle, parity)")
     ap.add_argument("--kernels-only", action="store_true",
                     help="skip the step timing: per-kernel table, dequant and a copy of known size "
                          "(the calibration of rocprofv3 FETCH_SIZE / WRITE_SIZE)")
@@ -495,12 +798,35 @@ def main():
                     help="print the per-kernel table of a rocprofv3 kernel-trace database")
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="print HBM traffic per operator call from FETCH_SIZE / WRITE_SIZE runs")
+    ap.add_argument("--op-avg", action="append", default=[],
+                    help="with --summarize-trace: 'operator=kernel-name substring#grid' for an OPAVG line")
+    ap.add_argument("--summarize-counters", metavar="DB",
+                    help="print MFMA busy, clock and MFMA FLOPs per operator from a PMC run")
     ap.add_argument("--group", action="append", default=[],
                     help="with --summarize-pmc: 'operator=kernel-name substring[#grid]@calls' "
                          "(grid: only dispatches of that many workgroups)")
     args = ap.parse_args()
+    global EAGER
+    EAGER = args.eager
     if args.summarize_trace:
-        print(summarize_trace(args.summarize_trace))
+        ops = []
+        for o in args.op_avg:
+            op, rest = o.split("=", 1)
+            pattern, grid = rest.rsplit("#", 1)
+            ops.append((op, pattern, int(grid)))
+        print(summarize_trace(args.summarize_trace, ops=ops))
+        return
+    if args.summarize_counters:
+        groups = []
+        for g in args.group:   # 'operator=kernel substring[#grid]@GFLOP'
+            op, rest = g.split("=", 1)
+            pattern, gflop = rest.rsplit("@", 1)
+            wgs = None
+            if "#" in pattern:
+                pattern, wgs = pattern.rsplit("#", 1)
+                wgs = int(wgs)
+            groups.append((op, pattern, wgs, float(gflop) * 1e9))
+        print(summarize_counters(args.summarize_counters, groups))
         return
     if args.summarize_pmc:
         groups = []
@@ -587,6 +913,7 @@ def main():
         live_ms = sum(a.elapsed_time(b) for a, b in events) / len(events)
         achieved = dom["gflop"] * 1e9 / (live_ms * 1e-3) / 1e12
         traffic = committed_traffic(name)
+        prof = committed_kernel_avg(name)
         result["roofline"] = {
             "kernel": name, "bound": "mfma", "achieved": round(achieved, 1),
             "peak": FP16_PEAK_TFLOPS, "unit": "TFLOP/s", "frac": round(achieved / FP16_PEAK_TFLOPS, 4),
@@ -597,6 +924,13 @@ def main():
             "traffic_source": (f"{traffic['source']}: FETCH_SIZE {traffic['fetch']} B + WRITE_SIZE "
                                f"{traffic['write']} B per call, scaled by a copy of known size")
                               if traffic else None}
+        if prof:
+            a_prof = dom["gflop"] * 1e9 / (prof["avg_us"] * 1e-6) / 1e12
+            result["roofline"]["frac_rocprof"] = round(a_prof / FP16_PEAK_TFLOPS, 4)
+            result["roofline"]["rocprof"] = (
+                f"{prof['source']}: {prof['kernel']} ({prof['wgs']} workgroups) average "
+                f"{prof['avg_us']} us over {prof['calls']} dispatches of the traced bench run -> "
+                f"{a_prof:.1f} TFLOP/s")
         dq = dequant_bandwidth(torch, st, max(3, args.reps // 4))
         print(f"[bench] dequant {dq['gbps']} GB/s", file=sys.stderr, flush=True)
         dq_traffic = committed_traffic("dequant")
@@ -610,6 +944,8 @@ def main():
             f"{r['kernel']} {r['avg_us']} us " + (f"{r['gbps']} GB/s" if "gbps" in r
                                                   else f"{r['tflops']} TFLOP/s")
             for r in result["neighbours"]), file=sys.stderr, flush=True)
+    if not args.no_configs:
+        result["configs"] = config_rows(torch, st, cpu=not args.no_cpu)
     if not args.no_model:
         del st
         torch.cuda.empty_cache()

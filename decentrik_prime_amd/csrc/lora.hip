@@ -218,7 +218,7 @@ struct SumJobs {
 // the end read the last row and are zeroed when staged), so the number of loads in flight is the
 // same at every wait and the compiler's vmcnt waits count only the chunk being consumed.
 template <int R, bool DROP>
-__device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, uint8_t* lds) {
+__device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, int b, uint8_t* lds) {
   const f16* __restrict__ P = J.P;
   const int64_t ld = J.ld;
   const uint8_t* __restrict__ mask = J.mask;
@@ -233,7 +233,7 @@ __device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, uint
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
   f16* Ps = reinterpret_cast<f16*>(lds + w * WAVE_LDS);
   f16* Qs = Ps + 32 * PLD;
-  const int64_t c0 = (int64_t)(blockIdx.x - J.bx0) * kSumCols;
+  const int64_t c0 = (int64_t)(b - J.bx0) * kSumCols;
   const int64_t n_chunks = (rows + 31) / 32;
   const int64_t mine = n_chunks > w ? (n_chunks - w + kSumWaves - 1) / kSumWaves : 0;
   // this lane's pieces of a chunk: two 16-byte P pieces (rows l / 4 and l / 4 + 16, 8 columns at
@@ -356,15 +356,19 @@ __device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, uint
 
 template <int R>
 __global__ __launch_bounds__(kSumThreads) void lora_colsum_kernel(SumJobs jobs, int64_t rows) {
+  // workgroups are dealt to the 8 XCDs round-robin: give each XCD a contiguous run of column
+  // blocks, so the two 64-byte halves of a row's 128-byte line (neighbouring blocks) share an L2
+  int b = blockIdx.x;
+  if ((gridDim.x & 7) == 0) b = (b & 7) * (gridDim.x >> 3) + (b >> 3);
   int jb = 0;
 #pragma unroll
   for (int q = 1; q < kMaxSumJobs; ++q)
-    if (q < jobs.n && (int)blockIdx.x >= jobs.j[q].bx0) jb = q;
+    if (q < jobs.n && b >= jobs.j[q].bx0) jb = q;
   constexpr int WAVE_LDS = 32 * (kSumCols + 8) * 2 + 32 * (R + 8) * 2;
   constexpr int RED = kSumWaves * kSumCols * 16 * 4;
   __shared__ __attribute__((aligned(16))) uint8_t lds[kSumWaves * WAVE_LDS > RED ? kSumWaves * WAVE_LDS : RED];
-  if (jobs.j[jb].mask) colsum_block<R, true>(jobs.j[jb], rows, lds);
-  else colsum_block<R, false>(jobs.j[jb], rows, lds);
+  if (jobs.j[jb].mask) colsum_block<R, true>(jobs.j[jb], rows, b, lds);
+  else colsum_block<R, false>(jobs.j[jb], rows, b, lds);
 }
 
 template <int MODE, bool MASKED>
