@@ -194,6 +194,8 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
 // and the dA of each term (P = Xd, Q = dz) share one launch.
 constexpr int kSumThreads = 512;
 constexpr int kSumWaves = kSumThreads / 64;
+// Measured on MI355X (q+v gradients at M = 2048, graph replay): 32 columns and 3 chunks in
+// flight 17.5 us; 16 or 64 columns, or 5 chunks in flight, 19.7-24.4 us.
 constexpr int kSumCols = 32;     // columns per workgroup
 constexpr int kSumDepth = 3;     // 32-row chunks of loads in flight per wave
 struct SumJob {
@@ -236,19 +238,21 @@ __device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, int 
   const int64_t c0 = (int64_t)(b - J.bx0) * kSumCols;
   const int64_t n_chunks = (rows + 31) / 32;
   const int64_t mine = n_chunks > w ? (n_chunks - w + kSumWaves - 1) / kSumWaves : 0;
-  // this lane's pieces of a chunk: two 16-byte P pieces (rows l / 4 and l / 4 + 16, 8 columns at
-  // 8 (l % 4)) with their mask bytes, and QL 16-byte pieces of the Q rows
-  const int prow = lane >> 2, pc8 = 8 * (lane & 3);
-  f16x8 pv[D][2], qv[D][QL];
-  u32x2 mv[D][2];
+  // this lane's pieces of a chunk: PL 16-byte P pieces (LPR lanes per row, rows l / LPR + RPL u,
+  // 8 columns at 8 (l % LPR)) with their mask bytes, and QL 16-byte pieces of the Q rows
+  constexpr int LPR = kSumCols / 8, RPL = 64 / LPR, PL = 32 / RPL;
+  static_assert(PL * RPL == 32 && LPR * RPL == 64, "chunk layout");
+  const int prow = lane / LPR, pc8 = 8 * (lane % LPR);
+  f16x8 pv[D][PL], qv[D][QL];
+  u32x2 mv[D][PL];
   auto row_of = [&](int64_t i, int r) {   // global row r of this wave's chunk i, clamped
     const int64_t m = 32 * (w + kSumWaves * i) + r;
     return m < rows ? m : rows - 1;
   };
   auto load = [&](int slot, int64_t i) {
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int64_t m = row_of(i, prow + 16 * u);
+    for (int u = 0; u < PL; ++u) {
+      const int64_t m = row_of(i, prow + RPL * u);
       pv[slot][u] = *reinterpret_cast<const f16x8*>(P + m * ld + c0 + pc8);
       if (DROP) mv[slot][u] = *reinterpret_cast<const u32x2*>(mask + m * cols + c0 + pc8);
     }
@@ -276,9 +280,9 @@ __device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, int 
     const int64_t r0 = 32 * (w + kSumWaves * i);
     __builtin_amdgcn_wave_barrier();   // the previous chunk's transposing reads are done
 #pragma unroll
-    for (int u = 0; u < 2; ++u) {
+    for (int u = 0; u < PL; ++u) {
       f16x8 v = pv[slot][u];
-      const bool ok = r0 + prow + 16 * u < rows;
+      const bool ok = r0 + prow + RPL * u < rows;
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         // the product is formed unconditionally, then selected (no branch per element)
@@ -287,7 +291,7 @@ __device__ __forceinline__ void colsum_block(const SumJob& J, int64_t rows, int 
         const f16 kept = DROP ? dk_h(__fmul_rn((float)v[e], ks)) : v[e];
         v[e] = keep ? kept : (f16)0.0f;
       }
-      *reinterpret_cast<f16x8*>(Ps + (prow + 16 * u) * PLD + pc8) = v;
+      *reinterpret_cast<f16x8*>(Ps + (prow + RPL * u) * PLD + pc8) = v;
     }
 #pragma unroll
     for (int u = 0; u < QL; ++u) {
