@@ -64,17 +64,11 @@ class QwenQLoRAStep(NF4LinearStack):
         # embedding, tokens and next-token targets (sorted: rows with a target first)
         self.emb = (torch.randn(vocab, D, generator=gen, device=dev) * 0.02).half()
         ids = torch.randint(0, vocab, (m,), generator=gen, device=dev)
-        self.x0 = self.emb.index_select(0, ids).float()
-        tgt = torch.cat([ids[1:], ids[:1]]).to(torch.int32)
+        tgt = torch.cat([ids[1:], ids[:1]])
         ends = torch.cumsum(torch.tensor(lens, device=dev), 0) - 1
         tgt[ends] = -1
-        has = tgt >= 0
-        self.perm = torch.cat([torch.nonzero(has)[:, 0], torch.nonzero(~has)[:, 0]]).to(torch.int32)
-        self.tgt_sorted = tgt.index_select(0, self.perm.long()).contiguous()
-        self.n_lab = int(has.sum())
-        self.e_target = self.emb.index_select(0, self.tgt_sorted[:self.n_lab].long()).contiguous()
-        self.tgt = tgt
         self.source = k_head.ResidentEmbedding(self.emb, head_chunk)
+        self.use_tokens(ids, tgt)
         # activations kept for the backward, per layer
         L = n_layers
         self.xin = [self.x0] + [torch.empty(m, D, dtype=f32, device=dev) for _ in range(L - 1)]
@@ -101,6 +95,33 @@ class QwenQLoRAStep(NF4LinearStack):
         self.dout = torch.empty(m, NQ * HD, dtype=f16, device=dev)
         self.dx32 = torch.empty(m, D, dtype=f32, device=dev)
         self.one = torch.ones(1, dtype=f32, device=dev)
+
+    @classmethod
+    def for_batch(cls, batch, **kwargs):
+        """The step on the tokens of a packed batch (trainer.pack): its rows' lengths, token ids
+        and next-token targets; the weights are random-init as for any instance."""
+        st = cls(batch.lens, **kwargs)
+        st.use_tokens(batch.ids, batch.tgt)
+        return st
+
+    def use_tokens(self, ids, tgt):
+        """Token ids [m] and next-token targets [m] (-1: none), in token order: the embedding rows
+        the first layer reads, and the head's targets in sorted order (tokens with a target
+        first, the order trainer.pack's perm gives)."""
+        dev = self.device
+        ids = torch.as_tensor(ids, device=dev).long()
+        tgt = torch.as_tensor(tgt, device=dev).to(torch.int32)
+        if ids.shape != (self.m,) or tgt.shape != (self.m,):
+            raise ValueError(f"ids and targets must be [{self.m}] (the step's token count)")
+        self.x0 = self.emb.index_select(0, ids).float()
+        if hasattr(self, "xin"):
+            self.xin[0] = self.x0
+        has = tgt >= 0
+        self.perm = torch.cat([torch.nonzero(has)[:, 0], torch.nonzero(~has)[:, 0]]).to(torch.int32)
+        self.tgt_sorted = tgt.index_select(0, self.perm.long()).contiguous()
+        self.n_lab = int(has.sum())
+        self.e_target = self.emb.index_select(0, self.tgt_sorted[:self.n_lab].long()).contiguous()
+        self.tgt = tgt
 
     @property
     def flops_per_step(self):

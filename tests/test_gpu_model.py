@@ -94,3 +94,44 @@ def test_lora_inputs_from_the_fp32_norm_output(torch):
             zs = float(np.abs(zr).max())
             err = float(np.abs(host(z).astype(np.float64) - zr).max()) / zs
             assert err <= 2e-3, f"layer {i} z_{t}: max error {err:.3g} of its scale"
+
+
+def test_trainer_metrics_of_a_packed_batch(torch):
+    """A right-padded batch with prompt tokens the loss ignores, packed (trainer.pack) and run
+    through the whole step (two layers, a 4096-token vocabulary): batch_metrics of the head's
+    per-token stats against the padded-batch walk (oracle/trainer.py) over the float64 head oracle
+    (oracle/head.py) on the step's final hidden state, and compute_loss against the mean of the
+    oracle's per-token losses."""
+    from decentrik_prime_amd import model, trainer
+    from oracle import head
+    from oracle import trainer as ref
+    rng = np.random.default_rng(8)
+    B, T, vocab = 3, 320, 4096
+    lens = [300, 150, 62]
+    ids = torch.from_numpy(rng.integers(0, vocab, (B, T)))
+    mask = (torch.arange(T)[None, :] < torch.tensor(lens)[:, None]).to(torch.int64)
+    labels = ids.clone()
+    labels[mask == 0] = -100
+    labels[0, :40] = -100
+    labels[1, :100] = -100
+    log(f"trainer metrics of a packed batch, lens {lens}")
+    batch = trainer.pack(ids, mask, labels, vocab)
+    st = model.QwenQLoRAStep.for_batch(batch, n_layers=2, vocab=vocab, seed=9, head_chunk=1024)
+    loss_sum, stats, _ = st.forward()
+    torch.cuda.synchronize()
+    got = trainer.batch_metrics(batch, stats.cpu())
+    # the oracle's per-token stats on the step's final hidden state, in token order
+    tok, _ = head.head(host(st.yf), host(st.emb), batch.tgt.numpy(), 1.0)
+    start = np.concatenate([[0], np.cumsum(lens)[:-1]])
+    want = ref.padded_metrics(lambda b, t: tok[start[b] + t, :3], lens, labels.numpy())
+    assert got["n_lab"] == want["n_lab"] and got["row_tokens"] == want["row_tokens"]
+    assert abs(got["entropy"] - want["entropy"]) <= 2e-3 * abs(want["entropy"])
+    for g, w in zip(got["row_loss"], want["row_loss"]):
+        assert abs(g - w) <= 2e-3 * abs(w) + 1e-6
+    # accuracy: hits agree except where the top two logits are within a GEMM rounding
+    x = np.sort(head.logits16(host(st.yf), host(st.emb)).astype(np.float64), 1)
+    near = int(((x[:, -1] - x[:, -2]) <= 2e-2).sum())
+    assert abs(got["accuracy"] - want["accuracy"]) <= near / max(want["n_lab"], 1) + 1e-12
+    mean = float(trainer.compute_loss(loss_sum, batch))
+    ref_mean = float(tok[batch.tgt.numpy() >= 0, 0].sum()) / batch.n_lab
+    assert abs(mean - ref_mean) <= 2e-3 * abs(ref_mean)

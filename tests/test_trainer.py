@@ -1,0 +1,102 @@
+"""The trainer integration's tensor part on the CPU (decentrik_prime_amd/trainer.py): packing of a
+right-padded batch (solution/fast_qwen.py:803-871), batch_metrics over per-token stats in the
+packing's sorted order (solution/fast_qwen.py:1551-1565) against a walk of the padded batch
+(oracle/trainer.py), and compute_loss's normalisation (solution/integration.py:657-664)."""
+
+import numpy as np
+import pytest
+import torch
+
+from decentrik_prime_amd import trainer
+from oracle import trainer as ref
+
+
+def _batch(seed=0, lens=(5, 3, 7), T=8, vocab=50):
+    rng = np.random.default_rng(seed)
+    B = len(lens)
+    ids = torch.from_numpy(rng.integers(0, vocab, (B, T)))
+    mask = (torch.arange(T)[None, :] < torch.tensor(lens)[:, None]).to(torch.int64)
+    labels = ids.clone()
+    labels[mask == 0] = -100
+    labels[0, :2] = -100          # a prompt the loss ignores
+    labels[2, 3] = -100
+    return ids, mask, labels
+
+
+def test_pack_tokens_targets_and_order():
+    ids, mask, labels = _batch()
+    b = trainer.pack(ids, mask, labels, vocab=50)
+    assert b.lens == [5, 3, 7] and b.n_real == 15 and b.B == 3 and b.T == 8
+    assert torch.equal(b.ids, torch.cat([ids[0, :5], ids[1, :3], ids[2, :7]]))
+    # target of token (r, t) = labels[r, t + 1] (ignore index and past the end: none)
+    want = []
+    for r, n in enumerate(b.lens):
+        for t in range(n):
+            lab = int(labels[r, t + 1]) if t + 1 < 8 else -100
+            want.append(lab if lab != -100 else -1)
+    assert b.tgt.tolist() == want
+    has = np.array(want) >= 0
+    assert b.n_lab == int(has.sum())
+    # sorted order: tokens with a target first, each group in token order
+    assert b.perm.tolist() == list(np.nonzero(has)[0]) + list(np.nonzero(~has)[0])
+    assert b.valid_sorted.tolist() == [True] * b.n_lab + [False] * (15 - b.n_lab)
+    rows = np.repeat(np.arange(3), b.lens)
+    assert b.row_sorted.tolist() == rows[b.perm.numpy()].tolist()
+    assert b.tgt_sorted.tolist() == np.array(want)[b.perm.numpy()].tolist()
+
+
+@pytest.mark.parametrize("case", ["gap", "empty_row", "id_range", "label_range", "shape"])
+def test_pack_refuses_what_it_cannot_pack(case):
+    ids, mask, labels = _batch()
+    if case == "gap":
+        mask[0, 1] = 0                       # not one run of ones from the start
+    elif case == "empty_row":
+        mask[1] = 0
+    elif case == "id_range":
+        ids[2, 0] = 50
+    elif case == "label_range":
+        labels[1, 1] = 50
+    elif case == "shape":
+        labels = labels[:, :-1]
+    assert trainer.pack(ids, mask, labels, vocab=50) is None
+
+
+def test_batch_metrics_against_the_padded_walk():
+    ids, mask, labels = _batch(seed=3, lens=(8, 1, 6, 4), T=8)
+    b = trainer.pack(ids, mask, labels, vocab=50)
+    rng = np.random.default_rng(4)
+    tok = np.stack([rng.uniform(0, 9, b.n_real), rng.uniform(0, 5, b.n_real),
+                    rng.integers(0, 2, b.n_real), rng.uniform(0, 12, b.n_real)], 1)
+    start = np.concatenate([[0], np.cumsum(b.lens)[:-1]])
+    got = trainer.batch_metrics(b, torch.from_numpy(tok[b.perm.numpy()]))
+    want = ref.padded_metrics(lambda r, t: tok[start[r] + t, :3], b.lens, labels.numpy())
+    assert got["n_lab"] == want["n_lab"] == b.n_lab
+    assert got["row_tokens"] == want["row_tokens"]
+    assert got["entropy"] == pytest.approx(want["entropy"], rel=1e-12)
+    assert got["accuracy"] == pytest.approx(want["accuracy"], rel=1e-12)
+    assert got["row_loss"] == pytest.approx(want["row_loss"], rel=1e-12)
+    # a row whose only token has no target gets loss 0 over 0 tokens
+    assert got["row_tokens"][1] == 0 and got["row_loss"][1] == 0.0
+
+
+def test_batch_metrics_without_targets_and_bad_stats():
+    ids, mask, labels = _batch()
+    labels[:] = -100
+    b = trainer.pack(ids, mask, labels, vocab=50)
+    assert b.n_lab == 0
+    m = trainer.batch_metrics(b, torch.ones(b.n_real, 4))
+    assert m["accuracy"] == 0.0 and m["entropy"] == 1.0 and m["row_tokens"] == [0, 0, 0]
+    with pytest.raises(ValueError):
+        trainer.batch_metrics(b, torch.ones(b.n_real - 1, 4))
+
+
+def test_compute_loss_normalisation():
+    ids, mask, labels = _batch()
+    b = trainer.pack(ids, mask, labels, vocab=50)
+    s = torch.tensor(12.0)
+    assert float(trainer.compute_loss(s, b)) == pytest.approx(12.0 / b.n_lab)
+    assert float(trainer.compute_loss(s, b, num_items_in_batch=4)) == pytest.approx(12.0 / b.n_lab)
+    assert float(trainer.compute_loss(s, b, num_items_in_batch=4,
+                                      model_accepts_loss_kwargs=True)) == pytest.approx(3.0)
+    assert float(trainer.compute_loss(s, b, num_items_in_batch=torch.tensor(6),
+                                      model_accepts_loss_kwargs=True)) == pytest.approx(2.0)
