@@ -161,6 +161,46 @@ def test_h16_mlp(torch, m):
     _scaled_close(host(dx16), dx_ref, "dX mlp vs oracle chain")
 
 
+@pytest.mark.parametrize("m", [2048, 1000])
+def test_split_k(torch, m):
+    """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
+    second launch that runs the epilogue): the down forward (NT, K = 8960) and a K = 8960 dX (NN,
+    fp16, fp32 and fp32-accumulate outputs) against the oracle, and two calls bit-identical.
+    M = 1000 has ragged last rows and 10 splits per tile, M = 2048 has 5."""
+    from decentrik_prime_amd import _lib, w4linear
+    from oracle import linear
+    lib = _lib.lib()
+    I, D = 8960, 1536
+    tiles = (m + 255) // 256 * (D // 256)
+    cus = torch.cuda.get_device_properties(0).multi_processor_count
+    splits = min(cus // tiles, I // 64 // 8)
+    log(f"split-K, M={m}: {tiles} tiles x {splits} splits on {cus} CUs")
+    assert lib.dk_h16_workspace(m, D, I, _lib.DK_OP_LINEAR_FWD) == tiles * splits * 256 * 256 * 4
+    assert lib.dk_h16_workspace(m, I, D, _lib.DK_OP_LINEAR_BWD_DX) == tiles * splits * 256 * 256 * 4
+    qd = nf4_weight(D, I, seed=301)      # down [1536, 8960]: NT, K = 8960
+    qg = nf4_weight(I, D, seed=302)      # [8960, 1536]: dX = dy W, K = 8960
+    wd, wg = to_w4(qd), to_w4(qg)
+    d16, g16 = wd.dequantize(), wg.dequantize()
+    rng = np.random.default_rng(303)
+    x = (rng.standard_normal((m, I)) * 0.5).astype(F16)
+    y1 = w4linear.linear_forward(cuda16(x), wd, w16=d16)
+    y2 = w4linear.linear_forward(cuda16(x), wd, w16=d16)
+    torch.cuda.synchronize()
+    _same(y1, y2, "down forward, two calls")
+    assert_close(host(y1), linear.mm16(x, qd["deq"].T), RTOL, ATOL, "down forward vs oracle")
+    dy = (rng.standard_normal((m, I)) * 0.5).astype(F16)
+    want = linear.mm16(dy, qg["deq"])
+    dx16 = w4linear.linear_backward_dx(cuda16(dy), wg, out_dtype=torch.float16, w16=g16)
+    dx32 = w4linear.linear_backward_dx(cuda16(dy), wg, out_dtype=torch.float32, w16=g16)
+    base = torch.full((m, D), 0.25, dtype=torch.float32, device="cuda")
+    acc = w4linear.linear_backward_dx(cuda16(dy), wg, out=base.clone(), accumulate=True, w16=g16)
+    torch.cuda.synchronize()
+    assert_close(host(dx16), want, RTOL, ATOL, "dX fp16 vs oracle")
+    # fp32 output: fp32(fp16(dy W)), the same fp16 rounding as the fp16 output
+    _same(dx32.half(), dx16, "dX fp32 output, rounded, vs fp16 output")
+    _same(acc, dx32 + 0.25, "dX accumulate vs fp32 output + 0.25")
+
+
 @pytest.mark.parametrize("m", [2048, 200])
 def test_lora_multi_matches_single(torch, m):
     """The q and v adapters in shared launches (dk_lora_down_multi / dk_lora_grads_multi) give
