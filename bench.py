@@ -270,6 +270,8 @@ def kernel_table(torch, st, reps, only=None):
     gu_save = gu.clone()
     dzq = (torch.randn(m, r, device=x.device) * 1e-2).half()
     dzv = (torch.randn(m, r, device=x.device) * 1e-2).half()
+    lora_terms = [(dy["qkv"][:, :D], z["q"], lo["Bq"], s, lo["mq"], ks),
+                  (dy["qkv"][:, D + KV:], z["v"], lo["Bv"], s, lo["mv"], ks)]
     g = lambda mm, n, k: 2.0 * mm * n * k  # noqa: E731
     # fp16 copies of layer 0's weights: the operand of the dk_h16_* entry points, as the
     # side-stream dequant leaves it
@@ -329,11 +331,25 @@ def kernel_table(torch, st, reps, only=None):
         ("lora_down q+v", lambda: W.lora_down_multi(
             x, [(lo["Aq"], lo["mq"], ks), (lo["Av"], lo["mv"], ks)], outs=[z["q"], z["v"]]),
          2 * g(m, r, D), m * D * 2 + 2 * m * D + 2 * r * D * 2 + 2 * m * r * 2, 1),
-        ("lora_grads q+v", lambda: W.lora_grads_multi(
-            x, [(dy["qkv"][:, :D], z["q"], lo["Bq"], s, lo["mq"], ks),
-                (dy["qkv"][:, D + KV:], z["v"], lo["Bv"], s, lo["mv"], ks)]),
+        ("lora_grads q+v", lambda: W.lora_grads_multi(x, lora_terms),
          g(m, r, D) * 3 + g(m, r, KV) * 2 + g(m, r, D), None, 1),
     ]
+    # the step's form when the q|k|v dX reads the fp16 slot: dz alone, then the dX GEMM carrying
+    # the column sums (dB, dA of both adapters) on its idle CUs
+    carried_sums = "qkv" in st.ahead
+    pre = W.lora_dz_multi(x, lora_terms)
+    (_, _, pzq), (_, _, pzv) = pre.grads
+    rows += [
+        ("lora_dz q+v", lambda: W.lora_dz_multi(x, lora_terms), g(m, r, D) + g(m, r, KV), None,
+         int(carried_sums)),
+        ("h16_linear_bwd_dx qkv+lora+sums", lambda: W.linear_backward_dx_lora(
+            dy["qkv"], L["qkv"], [(pzq, lo["Aq"], lo["mq"], ks), (pzv, lo["Av"], lo["mv"], ks)],
+            out=st.dx_qkv, w16=h["qkv"], sums=pre),
+         g(m, D, QKV) + 2 * g(m, D, r) + 3 * g(m, r, D) + g(m, r, KV), None, int(carried_sums)),
+    ]
+    if carried_sums:   # the two launches these replace in the step
+        rows = [(n, f, fl, nb, 0 if n in ("lora_grads q+v", "h16_linear_bwd_dx qkv+lora") else pl)
+                for n, f, fl, nb, pl in rows]
     out = []
     for name, fn, flops, nbytes, per_layer in rows:
         if only is not None and name not in only:

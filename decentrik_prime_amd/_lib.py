@@ -54,6 +54,12 @@ class LoraGradsTermC(ctypes.Structure):
                 ("db", _c_p), ("dz", _c_p), ("x", _c_p)]
 
 
+class SideLoraSumsC(ctypes.Structure):
+    """struct dk_side_lora_sums."""
+    _fields_ = [("x", _c_p), ("m", _i64), ("k", _i64), ("rank", _i64),
+                ("terms", ctypes.POINTER(LoraGradsTermC)), ("n_terms", ctypes.c_int32)]
+
+
 class SideDequantC(ctypes.Structure):
     """struct dk_side_dequant."""
     _fields_ = [("packed", _c_p), ("qabs", _c_p), ("scale2", _c_p), ("offset2", _c_p),
@@ -96,6 +102,9 @@ SIGNATURES = {
                                       ctypes.POINTER(RopeC), _c_p, _i64, _S, _c_p]),
     "dk_h16_linear_bwd_dx_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64, _c_p,
                                          _i64, _int, _c_p, _i64, _S, _c_p]),
+    "dk_h16_linear_bwd_dx_lora_sums": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int, _i64,
+                                              _c_p, _i64, _int, _c_p, _i64, _S,
+                                              ctypes.POINTER(SideLoraSumsC), _c_p]),
     "dk_h16_linear_bwd_dx_lora_noalloc": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _T, _int,
                                                  _i64, _c_p, _i64, _int, _S, _c_p]),
     "dk_h16_gateup_swiglu_fwd": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _c_p, _c_p, _i64,
@@ -107,6 +116,8 @@ SIGNATURES = {
     "dk_lora_grads_multi_workspace": (_i64, [_i64, _i64, _i64, ctypes.POINTER(_i64), _int]),
     "dk_lora_grads_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraGradsTermC), _int,
                                    _c_p, _i64, _c_p]),
+    "dk_lora_dz_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraGradsTermC), _int,
+                                _c_p]),
     "dk_lora_grads": (_int, [_c_p, _i64, _c_p, _c_p, _c_p, _f32, _c_p, _f32, _i64, _i64, _i64,
                              _i64, _c_p, _c_p, _c_p, _c_p, _i64, _c_p]),
     "dk_rms_fwd": (_int, [_c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _c_p, _i64, _i64,

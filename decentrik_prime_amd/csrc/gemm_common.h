@@ -1,6 +1,7 @@
 // Parameters shared by the fused GEMM kernels (w4gemm.hip: NF4 or fp16 weights, warp-specialised
 // 128-row tiles; hgemm.hip: fp16 weights, 256 x 256 tiles fed by LDS-DMA loads).
 #pragma once
+#include "lora_dev.h"
 #include "nf4_dev.h"
 
 namespace dk {
@@ -43,6 +44,7 @@ struct GemmParams {
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
   SideDequant side;     // dequant work carried by the launch's last side.wgs workgroups
+  SideSums sums;        // LoRA column sums carried by the sums.wgs workgroups before those
   // LINEAR NT only: rotary embedding of output columns [0, rope_cols) (the q and k heads of a
   // fused QKV projection) in the epilogue, before the single fp16 rounding; null: none
   const int32_t* rope_pos;   // [M] token positions

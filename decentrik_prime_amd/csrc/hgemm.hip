@@ -562,8 +562,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 // Workgroups [0, main_tiles) run 256 x 256 tiles; the tail_wgs after them run the remaining
 // tiles as 128 x 128 quarters.  With split-K (p.splits > 1, LINEAR only) workgroup b runs split
 // b / tiles of tile b % tiles and stores its fp32 partial tile at p.part[tile][split].  Tiles
-// are numbered M-fastest.  The p.side.wgs workgroups after the tiles run the launch's dequant
-// work; dispatched last, they take the CUs the tiles leave idle.
+// are numbered M-fastest.  The p.sums.wgs workgroups after the tiles (NN LINEAR) run the LoRA
+// column sums the launch carries, the p.side.wgs after those its dequant work; dispatched last,
+// they take the CUs the tiles leave idle.
 template <bool TRANS, int EPI>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
@@ -571,8 +572,20 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   __shared__ __attribute__((aligned(1024))) f16 Bs[kStages * kStageHalves];
   static_assert(side_dequant_lds <= kStages * kStageHalves * 2 && kSideThreads == kThreads,
                 "side dequant in the kernel's LDS");
+  static_assert(colsum_lds_bytes<16>() <= kStages * kStageHalves * 2 && kSumThreads == kThreads,
+                "carried LoRA column sums in the kernel's LDS");
   if ((int)blockIdx.x >= main_tiles + tail_wgs) {
-    side_dequant(p.side, (int)blockIdx.x - main_tiles - tail_wgs, reinterpret_cast<uint8_t*>(As));
+    int j = (int)blockIdx.x - main_tiles - tail_wgs;
+    if constexpr (TRANS && EPI == EPI_LINEAR) {
+      if (j < p.sums.wgs) {
+        colsum_run<16>(p.sums.jobs, p.sums.rows,
+                       colsum_block_of(j, p.sums.wgs, main_tiles + tail_wgs),
+                       reinterpret_cast<uint8_t*>(As));
+        return;
+      }
+      j -= p.sums.wgs;
+    }
+    side_dequant(p.side, j, reinterpret_cast<uint8_t*>(As));
     return;
   }
   const int nk_all = (int)(p.K / kBK);
@@ -745,7 +758,11 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
     }
     p.side.wgs = side;
   }
-  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>), dim3((unsigned)(h.main_wgs + h.tail_wgs + side)),
+  // carried LoRA column sums (NN LINEAR only; the caller sets p.sums.wgs)
+  const int sums = TRANS && EPI == EPI_LINEAR ? p.sums.wgs : 0;
+  p.sums.wgs = sums;
+  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>),
+                     dim3((unsigned)(h.main_wgs + h.tail_wgs + sums + side)),
                      dim3(kThreads), 0, stream, p, (int)h.main_wgs, (int)h.tail_wgs);
   DK_CHECK_LAUNCH();
   if constexpr (EPI == EPI_LINEAR) {   // hplan splits K for the LINEAR epilogue only

@@ -846,16 +846,49 @@ int side_alone(const SideDequant& s, hipStream_t stream) {
 
 // fp16 weight: the 256 x 256-tile kernel where the shape suits it (no workspace), else the plan's
 // split-K (partials in the workspace when one is given), one phase.
+// LoRA column sums a dX GEMM carries (dk_side_lora_sums), or none; blocks: their workgroups.
+struct CarriedSums {
+  SumJobs jobs;
+  int blocks = 0;
+  int64_t rows = 0, rank = 0;
+};
+
+int set_sums(CarriedSums& c, const dk_side_lora_sums* sums) {
+  if (!sums) return 0;
+  c.rows = sums->m;
+  c.rank = sums->rank;
+  return lora_sum_jobs(sums->x, sums->m, sums->k, sums->rank, sums->terms, sums->n_terms, &c.jobs,
+                       &c.blocks);
+}
+
+// fp16 weight: the 256 x 256-tile kernel where the shape suits it (no workspace), else the plan's
+// split-K (partials in the workspace when one is given), one phase.  Carried work (side dequant,
+// LoRA column sums) joins the 256-tile launch, or runs after the GEMM in launches of its own.
 template <bool TRANS, int EPI>
 int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes,
-                 const dk_side_dequant* side, hipStream_t stream) {
+                 const dk_side_dequant* side, hipStream_t stream,
+                 const CarriedSums& sums = CarriedSums{}) {
   if (!w16) return DK_ERR_INVALID;
   if (!dk_aligned(w16, 16)) return DK_ERR_ALIGN;
   if (int e = set_side(p, side)) return e;
-  if (p.M == 0) return side_alone(p.side, stream);
+  auto sums_alone = [&]() {
+    return sums.blocks ? lora_sums_launch(sums.rank, sums.jobs, sums.blocks, sums.rows, stream) : 0;
+  };
+  if (p.M == 0) {
+    if (int e = side_alone(p.side, stream)) return e;
+    return sums_alone();
+  }
   p.w16 = (const f16*)w16;
+  // the 256-tile kernel carries rank-16 column sums of NN LINEAR GEMMs
+  const bool carry = sums.blocks > 0 && sums.rank == 16 && TRANS && EPI == EPI_LINEAR;
+  if (carry) {
+    p.sums.jobs = sums.jobs;
+    p.sums.rows = sums.rows;
+    p.sums.wgs = sums.blocks;
+  }
   const int big = hgemm_launch<TRANS, EPI>(p, ws, ws_bytes, stream);
-  if (big != kHgemmDeclined) return big;
+  if (big != kHgemmDeclined) return big ? big : (carry ? 0 : sums_alone());
+  p.sums = SideSums{};
   Plan pl = plan_for(p.M, p.N, p.K, EPI);
   if (ws == nullptr) {
     pl.splits = 1;
@@ -865,7 +898,8 @@ int dispatch_h16(GemmParams p, const void* w16, void* ws, int64_t ws_bytes,
     p.part = reinterpret_cast<float*>(ws);
   }
   if (int e = launch_plan<TRANS, EPI, true>(pl, p, stream)) return e;
-  return side_alone(p.side, stream);
+  if (int e = side_alone(p.side, stream)) return e;
+  return sums_alone();
 }
 
 template <bool TRANS, int EPI>
@@ -994,6 +1028,22 @@ extern "C" int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m
                                 out_mode))
     return e;
   return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream);
+}
+
+extern "C" int dk_h16_linear_bwd_dx_lora_sums(const void* dy, int64_t lddy, int64_t m,
+                                              const void* w16, int64_t rows, int64_t cols,
+                                              const dk_lora_term* terms, int n_terms, int64_t rank,
+                                              void* dx, int64_t lddx, int out_mode,
+                                              void* workspace, int64_t workspace_bytes,
+                                              const dk_side_dequant* side,
+                                              const dk_side_lora_sums* sums, hipStream_t stream) {
+  GemmParams p = {};
+  if (int e = linear_bwd_params(p, dy, lddy, m, rows, cols, terms, n_terms, rank, dx, lddx,
+                                out_mode))
+    return e;
+  CarriedSums cs;
+  if (int e = set_sums(cs, sums)) return e;
+  return dispatch_h16<true, EPI_LINEAR>(p, w16, workspace, workspace_bytes, side, stream, cs);
 }
 
 // ---- the allocation-free dX entry point: split-K partials in a library-owned device array

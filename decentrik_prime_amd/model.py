@@ -25,7 +25,7 @@ from . import k_attn, k_head, k_norm, k_rope
 from .stack import D, KV, NF4LinearStack, layer_flops
 from .w4linear import (down_swiglu_backward, gateup_swiglu_forward, linear_backward_dx,
                        linear_backward_dx_lora, linear_forward, linear_forward_rope,
-                       lora_down_multi, lora_grads_multi)
+                       lora_down_multi, lora_dz_multi, lora_grads_multi)
 
 NQ, NKV, HD = 12, 2, 128
 VOCAB = 151936
@@ -196,14 +196,22 @@ class QwenQLoRAStep(NF4LinearStack):
             k_rope.qkv_epilogue_backward(dq, dkp, dvp, self.pos, self.cos, self.sin, dqkv, NQ, NKV,
                                          HD, NQ // NKV)
             del dq, dkp, dvp
-            (daq, dbq, dzq), (dav, dbv, dzv) = lora_grads_multi(
-                None, [(dqkv[:, :D], z["q"], lo["Bq"], self.s, None, 1.0, self.xq[i]),
-                       (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, None, 1.0, self.xv[i])])
+            terms = [(dqkv[:, :D], z["q"], lo["Bq"], self.s, None, 1.0, self.xq[i]),
+                     (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, None, 1.0, self.xv[i])]
+            w16q = w16("qkv", i) if i > 0 else None
+            sums = None
+            if w16q is not None:
+                # dz now; the q|k|v dX launch carries the column sums (dA, dB) on its idle CUs
+                sums = lora_dz_multi(None, terms)
+                (daq, dbq, dzq), (dav, dbv, dzv) = sums.grads
+            else:
+                (daq, dbq, dzq), (dav, dbv, dzv) = lora_grads_multi(None, terms)
             if i > 0:
                 # d(y) = dqkv W_qkv + the masked LoRA input terms, in fp32, into norm 1's backward
                 linear_backward_dx_lora(dqkv, Lw["qkv"], [(dzq, lo["Aq"], lo["mq"], ks),
                                                           (dzv, lo["Av"], lo["mv"], ks)],
-                                        out=self.dx32, w16=w16("qkv", i), side=side("qkv", i - 1))
+                                        out=self.dx32, w16=w16q, side=side("qkv", i - 1),
+                                        sums=sums)
                 done("qkv", i - 1)
                 k_norm.rms_backward(self.dx32, self.one, self.xin[i], self.w_in[i], self.rstd1[i],
                                     dh, dres=dh, out16=dh16)

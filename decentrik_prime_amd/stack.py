@@ -50,7 +50,7 @@ from . import k_nf4, quant
 from .schedule import DequantAhead
 from .w4linear import (down_swiglu_backward, gateup_swiglu_forward, linear_backward_dx,
                        linear_backward_dx_lora, linear_forward, linear_forward_lora,
-                       lora_down_multi, lora_grads_multi)
+                       lora_down_multi, lora_dz_multi, lora_grads_multi)
 
 D, I, KV, R = 1536, 8960, 256, 16
 QKV = D + 2 * KV
@@ -92,9 +92,10 @@ class NF4LinearStack:
     # that each GEMM launch carries, in step order; the launches that leave CUs idle (a last round
     # of 128 x 128 tiles, split-K grids short of the CU count, 128 x 128 grids short of a round).
     # Backward only: measured on MI355X, the forward's idle windows are too short and the carried
-    # stream slows the forward GEMMs' operand traffic by more than the launch it saves.
+    # stream slows the forward GEMMs' operand traffic by more than the launch it saves.  The
+    # q|k|v dX launch carries the layer's LoRA column sums instead (lora_dz_multi).
     CARRY = {"fwd": (),
-             "bwd": (("d", 0.45), ("gu", 0.15), ("o", 0.15), ("qkv", 0.25))}
+             "bwd": (("d", 0.60), ("gu", 0.20), ("o", 0.20))}
 
     def __init__(self, n_layers=28, m=2048, seed=0, device="cuda", p_drop=0.05, lora_scale=2.0,
                  save_gu=True, ahead="carried", dq_stream="main"):
@@ -292,13 +293,19 @@ class NF4LinearStack:
            w16=w16("o", i), side=side("o", i - 1))
         done("o", i - 1)
         dqkv = dy["qkv"]
-        (daq, dbq, dzq), (dav, dbv, dzv) = op(
-            "lora_grads q+v", lora_grads_multi, x,
-            [(dqkv[:, :D], z["q"], lo["Bq"], self.s, lo["mq"], self.keep_scale),
-             (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, lo["mv"], self.keep_scale)])
+        terms = [(dqkv[:, :D], z["q"], lo["Bq"], self.s, lo["mq"], self.keep_scale),
+                 (dqkv[:, D + KV:], z["v"], lo["Bv"], self.s, lo["mv"], self.keep_scale)]
+        w16q = w16("qkv", i)
+        sums = None
+        if w16q is not None:
+            # dz now; the q|k|v dX launch carries the column sums (dA, dB) on its idle CUs
+            sums = op("lora_grads q+v", lora_dz_multi, x, terms)
+            (daq, dbq, dzq), (dav, dbv, dzv) = sums.grads
+        else:
+            (daq, dbq, dzq), (dav, dbv, dzv) = op("lora_grads q+v", lora_grads_multi, x, terms)
         op(nm("qkv", "_linear_bwd_dx qkv+lora"), linear_backward_dx_lora, dqkv, L["qkv"],
            [(dzq, lo["Aq"], lo["mq"], self.keep_scale), (dzv, lo["Av"], lo["mv"], self.keep_scale)],
-           out=self.dx_qkv, w16=w16("qkv", i), side=side("qkv", i - 1))
+           out=self.dx_qkv, w16=w16q, side=side("qkv", i - 1), sums=sums)
         done("qkv", i - 1)
         self.grads[i] = (daq, dbq, dav, dbv)
 

@@ -361,13 +361,14 @@ def _dx_out(out, m, w, out_dtype, accumulate, device):
 
 
 def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, accumulate=False,
-                            w16=None, side=None):
+                            w16=None, side=None, sums=None):
     """dX = fp32(fp16(dy W)) + sum over terms of (mask ? fp32(fp16(dz A)) * keep_scale : 0),
     terms = [(dz [M, r], lora_A [r, in], mask [M, in] or None, keep_scale), ...] added in order
     (the QKV backward: dy1 = mm(dqkv, W_qkv) plus the lq and lv terms of rms_backward,
-    solution/fast_qwen.py:1364, 1376-1380).  w16, side as in linear_forward_lora."""
-    if side is not None and w16 is None:
-        raise ValueError("a carried dequant (side) needs the fp16-weight form (w16)")
+    solution/fast_qwen.py:1364, 1376-1380).  w16, side as in linear_forward_lora; sums (w16 form
+    only) the LoraSums of lora_dz_multi, whose dA and dB this launch then computes as well."""
+    if (side is not None or sums is not None) and w16 is None:
+        raise ValueError("carried work (side, sums) needs the fp16-weight form (w16)")
     _check16(dy, "dy")
     m = dy.shape[0]
     if dy.shape[1] != w.rows:
@@ -378,6 +379,13 @@ def linear_backward_dx_lora(dy, w, terms=(), out=None, out_dtype=torch.float32, 
     if w16 is not None:
         _check_w16(w16, w)
         ws, nbytes = _h16_workspace(m, w.rows, w.cols, _lib.DK_OP_LINEAR_BWD_DX, dy.device)
+        if sums is not None:
+            rc = _lib.lib().dk_h16_linear_bwd_dx_lora_sums(
+                _lib.ptr(dy), dy.stride(0), m, _lib.ptr(w16), w.rows, w.cols, arr, n, rank,
+                _lib.ptr(out), out.stride(0), mode, _lib.ptr(ws), nbytes, _side(side),
+                ctypes.byref(sums.c), _lib.stream_handle(dy.device))
+            _lib.check(rc, "dk_h16_linear_bwd_dx_lora_sums")
+            return out
         rc = _lib.lib().dk_h16_linear_bwd_dx_lora(_lib.ptr(dy), dy.stride(0), m, _lib.ptr(w16),
                                                   w.rows, w.cols, arr, n, rank, _lib.ptr(out),
                                                   out.stride(0), mode, _lib.ptr(ws), nbytes,
@@ -457,12 +465,9 @@ def lora_grads(dy, z, x, lora_B, lora_scale=2.0, mask=None, keep_scale=1.0):
     return da, db, dz
 
 
-def lora_grads_multi(x, terms, outs=None):
-    """lora_grads of one or two adapters in shared launches: terms =
-    [(dy, z, lora_B, lora_scale, mask or None, keep_scale[, x_term]), ...], x_term the term's own
-    input (the reference's xq / xv, given with mask None) in place of x, which may then be None.
-    outs: [(dA, dB, dz), ...] to write into, or None to allocate.  Returns [(dA, dB, dz), ...],
-    each exactly as lora_grads computes it."""
+def _lora_grads_args(x, terms, outs):
+    """Checked arguments of lora_grads_multi and lora_dz_multi: (ctypes term array, m, k, rank,
+    device, tensors to keep alive, [(dA, dB, dz), ...])."""
     if not 1 <= len(terms) <= 2:
         raise ValueError("lora_grads_multi takes one or two terms")
     ins = [t[6] if len(t) > 6 and t[6] is not None else x for t in terms]
@@ -476,7 +481,7 @@ def lora_grads_multi(x, terms, outs=None):
     r = terms[0][1].shape[1]
     dev = ins[0].device
     arr = (_lib.LoraGradsTermC * len(terms))()
-    keep, res = [], []
+    keep, res = [x], []
     for t, term in enumerate(terms):
         dy, z, lora_B, s, mask, ks = term[:6]
         _check16(dy, "dy")
@@ -502,12 +507,44 @@ def lora_grads_multi(x, terms, outs=None):
         arr[t] = _lib.LoraGradsTermC(_lib.ptr(dy), dy.stride(0), n_out, _lib.ptr(z),
                                      _lib.ptr(lora_B), float(s), _lib.ptr(mask), float(ks),
                                      _lib.ptr(da), _lib.ptr(db), _lib.ptr(dz), _lib.ptr(own))
-        keep.append((dy, mask))
+        keep += [dy, z, lora_B, mask, own, da, db, dz]
         res.append((da, db, dz))
+    return arr, m, k, r, dev, keep, res
+
+
+def lora_grads_multi(x, terms, outs=None):
+    """lora_grads of one or two adapters in shared launches: terms =
+    [(dy, z, lora_B, lora_scale, mask or None, keep_scale[, x_term]), ...], x_term the term's own
+    input (the reference's xq / xv, given with mask None) in place of x, which may then be None.
+    outs: [(dA, dB, dz), ...] to write into, or None to allocate.  Returns [(dA, dB, dz), ...],
+    each exactly as lora_grads computes it."""
+    arr, m, k, r, dev, _keep, res = _lora_grads_args(x, terms, outs)
     rc = _lib.lib().dk_lora_grads_multi(_lib.ptr(x), m, k, r, arr, len(terms), None, 0,
                                         _lib.stream_handle(dev))
     _lib.check(rc, "dk_lora_grads_multi")
     return res
+
+
+class LoraSums:
+    """The column sums (dA, dB) lora_dz_multi left to do, for linear_backward_dx_lora(sums=...)
+    to carry on its GEMM launch.  .grads is [(dA, dB, dz), ...] as lora_grads_multi returns it;
+    dA and dB hold their values once that GEMM has run."""
+
+    def __init__(self, x, arr, m, k, r, n, keep, res):
+        self.grads = res
+        self._keep = keep
+        self.c = _lib.SideLoraSumsC(_lib.ptr(x), m, k, r, arr, n)
+        self._arr = arr
+
+
+def lora_dz_multi(x, terms, outs=None):
+    """The first half of lora_grads_multi (same arguments): dz of every term now; the column sums
+    are returned as a LoraSums for the q|k|v dX GEMM to carry (linear_backward_dx_lora(...,
+    sums=...)), which makes dA and dB bit-identical to lora_grads_multi's."""
+    arr, m, k, r, dev, keep, res = _lora_grads_args(x, terms, outs)
+    rc = _lib.lib().dk_lora_dz_multi(_lib.ptr(x), m, k, r, arr, len(terms), _lib.stream_handle(dev))
+    _lib.check(rc, "dk_lora_dz_multi")
+    return LoraSums(x, arr, m, k, r, len(terms), keep, res)
 
 
 def gateup_swiglu_forward(x, w_gu, act=None, gu=None, save_gu=True, w16=None, side=None):

@@ -312,6 +312,24 @@ int dk_lora_grads_multi(const void* x, int64_t m, int64_t k, int64_t rank,
                         const dk_lora_grads_term* terms, int n_terms, void* ws, int64_t ws_bytes,
                         hipStream_t stream);
 
+/* The first half of dk_lora_grads_multi, for a caller whose q|k|v dX GEMM carries the second
+ * (dk_h16_linear_bwd_dx_lora_sums): dz of every term only, the row pass
+ * dz = fp16(fp16(dY B) * s) (solution/fast_qwen.py:1370, 1373).  Arguments as
+ * dk_lora_grads_multi; da and db are not written here. */
+int dk_lora_dz_multi(const void* x, int64_t m, int64_t k, int64_t rank,
+                     const dk_lora_grads_term* terms, int n_terms, hipStream_t stream);
+
+/* The second half: the column sums dB = fp32(fp16(dY^T z)) * s and dA = fp32(fp16(dz^T Xd)) of
+ * the terms (solution/fast_qwen.py:1369, 1371), for dk_h16_linear_bwd_dx_lora_sums to carry.  The
+ * same x, m, k, rank and terms as the dk_lora_dz_multi call that computed their dz, which must
+ * come first in stream order.  With it, dA and dB are bit-identical to dk_lora_grads_multi's. */
+typedef struct dk_side_lora_sums {
+  const void* x;
+  int64_t m, k, rank;
+  const dk_lora_grads_term* terms;
+  int32_t n_terms;
+} dk_side_lora_sums;
+
 /* gate|up as one NF4 GEMM with the gated-SiLU epilogue.  Replaces the gate and up GEMMs and
  * gated_silu_forward (solution/fast_qwen.py:1080-1108; solution/k_mlp.py:20-29):
  *   g = fp16(X Wg^T), u = fp16(X Wu^T), act = fp16(silu(g) * u)
@@ -394,6 +412,19 @@ int dk_h16_linear_bwd_dx_lora(const void* dy, int64_t lddy, int64_t m, const voi
                               int64_t rank, void* dx, int64_t lddx, int out_mode, void* workspace,
                               int64_t workspace_bytes, const dk_side_dequant* side,
                               hipStream_t stream);
+/* dk_h16_linear_bwd_dx_lora that also computes the LoRA column sums `sums` (or NULL: none): the
+ * q|k|v backward of a layer after dk_lora_dz_multi (mm(dqkv, W_qkv) with the lq and lv terms,
+ * solution/fast_qwen.py:1364, 1376-1380, and the dA and dB of the same terms, 1369, 1371) with
+ * one launch fewer.  The sums run on extra workgroups of the GEMM launch, which start on the CUs
+ * its tiles leave idle, before `side`'s dequant workgroups; a GEMM that the 256 x 256-tile kernel
+ * does not take, or a rank other than 16, runs them as a launch of their own after the GEMM.
+ * dA and dB must not overlap anything the GEMM reads or writes. */
+int dk_h16_linear_bwd_dx_lora_sums(const void* dy, int64_t lddy, int64_t m, const void* w16,
+                                   int64_t rows, int64_t cols, const dk_lora_term* terms,
+                                   int n_terms, int64_t rank, void* dx, int64_t lddx, int out_mode,
+                                   void* workspace, int64_t workspace_bytes,
+                                   const dk_side_dequant* side, const dk_side_lora_sums* sums,
+                                   hipStream_t stream);
 /* dk_h16_linear_bwd_dx_lora without a workspace argument, allocating nothing.  No counterpart in
  * the reference: it is for callers that cannot allocate device memory (code under HIP graph
  * capture, serving loops, harnesses that forbid hipMalloc).  The split-K partials go to a

@@ -448,6 +448,55 @@ def test_carried_dequant_is_the_standalone_dequant(torch):
                 _same(out[e1:], sentinel[e1:], what + ": after the range")
 
 
+@pytest.mark.parametrize("m,rank", [(2048, 16), (200, 16), (2048, 32)])
+def test_lora_sums_carried_by_the_dx_gemm(torch, m, rank):
+    """lora_dz_multi, then the q|k|v dX GEMM carrying the column sums (dk_lora_dz_multi +
+    dk_h16_linear_bwd_dx_lora_sums), against lora_grads_multi and the dX GEMM without them: dA,
+    dB, dz and dX bit-identical.  M = 2048 carries them on the 256-tile launch (also beside a
+    carried dequant share, which stays bit-identical to dk_nf4_dequant); M = 200 (a shape that
+    kernel declines) and rank 32 run them as a launch of their own after the GEMM."""
+    from decentrik_prime_amd import k_nf4, w4linear
+    log(f"LoRA column sums carried by the q|k|v dX GEMM, M={m}, rank {rank}")
+    st, pk, ref = _layer_and_reference(torch)
+    L = st.layers[0]
+    D, KV = 1536, 256
+    w16 = ref[pk.segments["q_proj"][0]:pk.segments["q_proj"][0] + L["qkv"].rows * L["qkv"].cols]
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, r=rank, seed=51)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, r=rank, seed=52)
+    ks = 1.0 / 0.95
+    dqkv = cuda16((np.random.default_rng(53).standard_normal((m, D + 2 * KV)) * 1e-2).astype(F16))
+    tx = cuda16(x)
+    t = {k: cuda16(v) for k, v in (("aq", aq), ("av", av), ("bq", bq), ("bv", bv))}
+    tmq, tmv = cuda(mq), cuda(mv)
+    zq, zv = w4linear.lora_down_multi(tx, [(t["aq"], tmq, ks), (t["av"], tmv, ks)])
+    terms = [(dqkv[:, :D], zq, t["bq"], 2.0, tmq, ks), (dqkv[:, D + KV:], zv, t["bv"], 2.0, tmv, ks)]
+    want = w4linear.lora_grads_multi(tx, terms)
+
+    def dx_terms(g):
+        return [(g[0][2], t["aq"], tmq, ks), (g[1][2], t["av"], tmv, ks)]
+    dx_want = w4linear.linear_backward_dx_lora(dqkv, L["qkv"], dx_terms(want), w16=w16)
+    n_sb = pk.n_qblocks // 256
+    for side_blocks in ((None, (0, n_sb // 4)) if m == 2048 and rank == 16 else (None,)):
+        side, out = None, None
+        if side_blocks is not None:
+            out = torch.full((pk.numel,), -3.5, dtype=torch.float16, device="cuda")
+            side = k_nf4.side_dequant(pk, st.code2, st.nf4, out, *side_blocks, -1)
+        sums = w4linear.lora_dz_multi(tx, terms)
+        got = sums.grads
+        dx = w4linear.linear_backward_dx_lora(dqkv, L["qkv"], dx_terms(got), w16=w16, side=side,
+                                              sums=sums)
+        torch.cuda.synchronize()
+        what = f"M={m} rank {rank}" + (" with a carried dequant" if side else "")
+        for term, (a, b) in zip("qv", zip(got, want)):
+            for nm, u, v in zip(("dA", "dB", "dz"), a, b):
+                _same(u, v, f"{nm}_{term}, {what}")
+        _same(dx, dx_want, f"dX, {what}")
+        if side is not None:
+            e0, e1 = side_blocks[0] * 16384, side_blocks[1] * 16384
+            _same(out[e0:e1], ref[e0:e1], what + ": carried blocks")
+            assert bool((out[e1:] == -3.5).all()), what + ": past the carried blocks"
+
+
 def test_stack_carried_matches_layer_schedule(torch):
     """Two layers, M = 2048 (the shapes whose launches carry the dequant on idle CUs), two steps:
     the carried schedule gives bit-identical outputs and gradients to whole-layer dequant launches

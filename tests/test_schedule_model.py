@@ -175,6 +175,8 @@ def model(monkeypatch):
         monkeypatch.setattr(stack_mod, name, _gemm(g))
     monkeypatch.setattr(stack_mod, "lora_down_multi", lambda *a, **k: [0, 0])
     monkeypatch.setattr(stack_mod, "lora_grads_multi", lambda *a, **k: [(0, 0, 0), (0, 0, 0)])
+    monkeypatch.setattr(stack_mod, "lora_dz_multi",
+                        lambda *a, **k: types.SimpleNamespace(grads=[(0, 0, 0), (0, 0, 0)]))
 
     def dequant_layer(layer, code2, nf4, out):
         g.cur.launch(("write",) + _units(out) + ((layer.layer, "layer"),))
