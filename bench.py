@@ -28,6 +28,9 @@ import time
 HBM_PEAK_GBS = 8000.0
 EAGER = False   # --eager: time operators by plain back-to-back launches (counter runs count dispatches)
 FP16_PEAK_TFLOPS = 2516.6   # 256 CU x 2.4 GHz x 4096 FLOP/clk (dense fp16 MFMA)
+# the operator whose launches the last timed step times (the largest per-layer share of the step):
+# the gate|up forward, h16_ or w4_ by the schedule
+DOMINANT = "_gateup_swiglu_fwd"
 
 
 def _events(torch):
@@ -337,8 +340,12 @@ def kernel_table(torch, st, reps, only=None):
     # the step's form when the q|k|v dX reads the fp16 slot: dz alone, then the dX GEMM carrying
     # the column sums (dB, dA of both adapters) on its idle CUs
     carried_sums = "qkv" in st.ahead
-    pre = W.lora_dz_multi(x, lora_terms)
-    (_, _, pzq), (_, _, pzv) = pre.grads
+    # the carried sums of dz = (dzq, dzv), set up without a launch of their own
+    arr, mm, kk, rr, _, keep, res = W._lora_grads_args(
+        x, lora_terms, [(torch.empty(r, D, device=x.device), torch.empty(n, r, device=x.device), dz_)
+                        for n, dz_ in ((D, dzq), (KV, dzv))])
+    pre = W.LoraSums(x, arr, mm, kk, rr, 2, keep, res)
+    pzq, pzv = dzq, dzv
     rows += [
         ("lora_dz q+v", lambda: W.lora_dz_multi(x, lora_terms), g(m, r, D) + g(m, r, KV), None,
          int(carried_sums)),
@@ -618,15 +625,18 @@ def _short(name):
 def summarize_trace(db, top=40, ops=()):
     """Per-kernel dispatch statistics of a kernel trace: calls, average and total duration,
     grouped by kernel name and grid (a kernel instance launched at several shapes is split).
-    ops: [(operator, kernel-name substring, grid)] for which an 'OPAVG' line is added (what
-    bench.py reads back as the profile's average duration of that operator's kernel)."""
+    ops: [(operator, kernel-name substring, grid, (first, end) or None)] for which an 'OPAVG' line
+    is added (what bench.py reads back as the profile's average duration of that operator's
+    kernel): the average over that kernel's dispatches at that grid, or over dispatches
+    [first, end) of them in launch order (bench.py's timed steps: warmup x 28 .. (warmup + steps)
+    x 28 for a kernel launched once per layer)."""
     import collections
     import sqlite3
     cur = sqlite3.connect(db).cursor()
     agg = collections.defaultdict(list)
     for name, dur, gx, gy, gz, wx, wy, wz in cur.execute(
             "select name, duration, grid_x, grid_y, grid_z, workgroup_x, workgroup_y, workgroup_z "
-            "from kernels"):
+            "from kernels order by start"):
         wgs = (gx // max(wx, 1)) * (gy // max(wy, 1)) * (gz // max(wz, 1))
         agg[(_short(name), wgs, wx * wy * wz)].append(dur)
     total = sum(sum(v) for v in agg.values())
@@ -635,10 +645,12 @@ def summarize_trace(db, top=40, ops=()):
     for (k, wgs, wx), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
         lines.append(f"{k:78s} {wgs:7d} {wx:4d} {len(v):6d} {sum(v) / len(v) / 1e3:9.2f} "
                      f"{sum(v) / 1e6:9.3f} {100 * sum(v) / total:6.2f}")
-    for op, pattern, grid in ops:
+    for op, pattern, grid, span in ops:
         sel = [(k, v) for k, v in agg.items() if pattern in k[0] and k[1] == grid]
         if sel:
             durs = [d for _, v in sel for d in v]
+            if span is not None:
+                durs = durs[span[0]:span[1]]
             lines.append(f"OPAVG {op} | {sel[0][0][0]} | {grid} | {sum(durs) / len(durs) / 1e3:.2f} | "
                          f"{len(durs)}")
     return "\n".join(lines)
@@ -661,7 +673,7 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
     dispatch), each scaled by what the same counter reads for the calibration copy of
     `copy_bytes` read + `copy_bytes` written (the __amd_rocclr_copyBuffer dispatches within a
     factor of two of the largest one: nothing else in the run copies a quarter as much).
-    groups: [(operator name, kernel-name substring, operator calls in the run, grid size in
+    groups: [(operator name, kernel-name substring, operator calls in the run, set of grid sizes in
     workgroups or None for any)]."""
     out = []
     scaled = {}
@@ -677,7 +689,7 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
                    f"(n={len(kib)}), scale factor {factor:.4f}")
         for op, pattern, calls, wgs_only in groups:
             sel = {k: v for k, v in rows.items()
-                   if pattern in k[1] and (wgs_only is None or k[2] == wgs_only)}
+                   if pattern in k[1] and (wgs_only is None or k[2] in wgs_only)}
             per_kernel = {}
             for k, v in sel.items():
                 per_kernel.setdefault((k[1], k[2]), []).append(v)
@@ -815,21 +827,26 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="print HBM traffic per operator call from FETCH_SIZE / WRITE_SIZE runs")
     ap.add_argument("--op-avg", action="append", default=[],
-                    help="with --summarize-trace: 'operator=kernel-name substring#grid' for an OPAVG line")
+                    help="with --summarize-trace: 'operator=kernel-name substring#grid[first:end]' "
+                         "for an OPAVG line (the dispatch range is optional)")
     ap.add_argument("--summarize-counters", metavar="DB",
                     help="print MFMA busy, clock and MFMA FLOPs per operator from a PMC run")
     ap.add_argument("--group", action="append", default=[],
-                    help="with --summarize-pmc: 'operator=kernel-name substring[#grid]@calls' "
+                    help="with --summarize-pmc: 'operator=kernel-name substring[#grid[,grid]]@calls' "
                          "(grid: only dispatches of that many workgroups)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
     if args.summarize_trace:
         ops = []
-        for o in args.op_avg:
+        for o in args.op_avg:   # 'operator=kernel substring#grid[first:end]'
             op, rest = o.split("=", 1)
             pattern, grid = rest.rsplit("#", 1)
-            ops.append((op, pattern, int(grid)))
+            span = None
+            if "[" in grid:
+                grid, rng = grid.rstrip("]").split("[")
+                span = tuple(int(v) for v in rng.split(":"))
+            ops.append((op, pattern, int(grid), span))
         print(summarize_trace(args.summarize_trace, ops=ops))
         return
     if args.summarize_counters:
@@ -850,9 +867,9 @@ def main():
             op, rest = g.split("=", 1)
             pattern, calls = rest.rsplit("@", 1)
             wgs = None
-            if "#" in pattern:
+            if "#" in pattern:   # one grid, or several: '#240,3072'
                 pattern, wgs = pattern.rsplit("#", 1)
-                wgs = int(wgs)
+                wgs = {int(v) for v in wgs.split(",")}
             groups.append((op, pattern, int(calls), wgs))
         print(summarize_pmc(*args.summarize_pmc, groups))
         return
@@ -882,27 +899,36 @@ def main():
         st.step()
     torch.cuda.synchronize()
     print("[bench] warmup done", file=sys.stderr, flush=True)
-    kernels = None
-    if not args.no_kernels:
-        # each operator in isolation first: the one with the largest share of the step is the
-        # dominant kernel, whose launches are then timed inside the last timed step (timing
-        # events in every step would cost the step about 3%)
-        kernels = kernel_table(torch, st, args.reps)
-        dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
-        probe = (dom["kernel"], [])
-        print(f"[bench] kernel table done; dominant operator {dom['kernel']}", file=sys.stderr,
-              flush=True)
+    # the timed steps right after the warmup, so that in a kernel trace of this run they are
+    # dispatches [warmup x 28, (warmup + steps) x 28) of each once-per-layer kernel.  The
+    # dominant operator's launches are timed inside the last one (events in every step would cost
+    # the step about 3%): the gate|up forward, which the per-operator table run afterwards
+    # confirms (another dominant operator gets a probe step of its own after the timed ones)
+    probe = (st.op_name("gu", DOMINANT), []) if not args.no_kernels else None
     torch.cuda.synchronize()
     e0, e1 = _events(torch)
     t0 = time.perf_counter()
     e0.record()
     for k in range(args.steps):
-        if kernels is not None and k == args.steps - 1:
+        if probe is not None and k == args.steps - 1:
             st.probe = probe
         st.step()
     e1.record()
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
+    st.probe = None
+    kernels = None
+    if not args.no_kernels:
+        kernels = kernel_table(torch, st, args.reps)
+        dom = max(kernels, key=lambda r: r["avg_us"] * r["launches_per_layer"])
+        print(f"[bench] kernel table done; dominant operator {dom['kernel']}", file=sys.stderr,
+              flush=True)
+        if dom["kernel"] != probe[0]:
+            probe = (dom["kernel"], [])
+            st.probe = probe
+            st.step()
+            torch.cuda.synchronize()
+            st.probe = None
     ms_per_step = e0.elapsed_time(e1) / args.steps
     value = st.flops_per_step / (ms_per_step * 1e-3) / 1e12
     # the last step's outputs and every layer's LoRA gradients must be finite
@@ -924,8 +950,7 @@ def main():
                    "flop_per_step": st.flops_per_step},
     }
     if kernels is not None:
-        name, events = st.probe
-        st.probe = None
+        name, events = probe
         live_ms = sum(a.elapsed_time(b) for a, b in events) / len(events)
         achieved = dom["gflop"] * 1e9 / (live_ms * 1e-3) / 1e12
         traffic = committed_traffic(name)

@@ -100,3 +100,26 @@ def test_compute_loss_normalisation():
                                       model_accepts_loss_kwargs=True)) == pytest.approx(3.0)
     assert float(trainer.compute_loss(s, b, num_items_in_batch=torch.tensor(6),
                                       model_accepts_loss_kwargs=True)) == pytest.approx(2.0)
+
+
+def test_padded_walk_known_answer():
+    """The padded-batch walk and the packed metrics on a batch small enough to work by hand.
+    Row 0 has 3 real tokens, row 1 has 2 (T = 4).  A token's target is the next position's label:
+    row 0 -> (none: -100, 7, none: -100), row 1 -> (3, none: -100), so tokens (0, 1) and (1, 0)
+    carry the loss.  Per-token (loss, entropy, hit) = (1, 2, 0), (3, 4, 1), (5, 6, 1) | (7, 8, 1),
+    (9, 10, 0): entropy = (2 + 4 + 6 + 8 + 10) / 5 = 6, accuracy = (1 + 1) / 2 = 1, row losses 3
+    and 7 over one token each."""
+    lens = [3, 2]
+    labels = np.array([[5, -100, 7, -100], [9, 3, -100, -100]])
+    stats = {(0, 0): (1, 2, 0), (0, 1): (3, 4, 1), (0, 2): (5, 6, 1), (1, 0): (7, 8, 1),
+             (1, 1): (9, 10, 0)}
+    want = {"entropy": 6.0, "accuracy": 1.0, "n_lab": 2, "row_loss": [3.0, 7.0],
+            "row_tokens": [1, 1]}
+    assert ref.padded_metrics(lambda b, t: stats[(b, t)], lens, labels) == want
+    ids = torch.tensor([[1, 2, 3, 0], [4, 5, 0, 0]])
+    mask = torch.tensor([[1, 1, 1, 0], [1, 1, 0, 0]])
+    b = trainer.pack(ids, mask, torch.from_numpy(labels), vocab=10)
+    assert b.tgt.tolist() == [-1, 7, -1, 3, -1]
+    tok = [stats[(0, 0)], stats[(0, 1)], stats[(0, 2)], stats[(1, 0)], stats[(1, 1)]]
+    st = torch.tensor([list(tok[i]) + [0.0] for i in b.perm.tolist()], dtype=torch.float64)
+    assert trainer.batch_metrics(b, st) == want
