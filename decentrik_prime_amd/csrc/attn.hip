@@ -73,6 +73,55 @@ __device__ __forceinline__ f16x8 read_col8(const f16* tile, int p, int col) {
   return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
 }
 
+// K / V tiles of the forward in a ring of LDS stages filled by LDS DMA (global_load_lds_dwordx4:
+// no registers, the next tiles' loads in flight while this one is computed on).  A tile is kBN
+// rows of 256 bytes with no padding; the 16-byte chunks of row r are permuted by swz16(r), so
+// that both reads of the tile are free of bank conflicts: the S^T operand (16 consecutive rows,
+// one chunk each) and the transposing V reads (4 rows x 2 adjacent chunks per 16-lane group).
+constexpr int kFwdStages = 3;                 // tiles in flight: this one and the next two
+constexpr int kTileHalves = kBN * kHD;        // one operand of one stage: 16 KB
+
+__device__ __forceinline__ int swz16(int r) {
+  return ((r & 3) << 1) | ((r >> 2) & 1) | (((r >> 3) & 1) << 3);
+}
+// offset (halves) of column c of row r in a swizzled tile
+__device__ __forceinline__ int sw_off(int r, int c) {
+  return r * kHD + ((((c >> 3) ^ swz16(r))) << 3) + (c & 7);
+}
+
+__device__ __forceinline__ unsigned lds_addr(const void* p) {
+  return (unsigned)(size_t)(__attribute__((address_space(3))) const void*)p;
+}
+
+// 16 bytes per lane from global memory into LDS at lds + 16 * lane (inline assembly, so that the
+// compiler does not put a wait for it before every LDS read: the kernel counts these loads with
+// its own vmcnt waits; M0, the LDS address, is saved and restored around it).
+__device__ __forceinline__ void dma16(const void* src, unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dwordx4 %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+
+template <int N>
+__device__ __forceinline__ void wait_vmem() {
+  asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
+}
+
+// Column (col + l % 32) of rows p .. p + 3 and p + 8 .. p + 11 of a swizzled tile: read_col8 for
+// the forward's K / V ring.
+__device__ __forceinline__ f16x8 read_col8_sw(const f16* tile, int p, int col) {
+  const int lane = threadIdx.x & 63;
+  const int r = p + ((lane & 15) >> 2), c = col + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
+  const f16x4 lo = read_tr(tile + sw_off(r, c)), hi = read_tr(tile + sw_off(r + 8, c));
+  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+}
+
 // 2^x on the hardware exponential (v_exp_f32); arguments here are <= 0 (scores minus their row
 // maximum or log-sum-exp), results below the normal range flush to zero.
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
@@ -139,39 +188,71 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
   if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD;
   const int kvh = h / (a.nq / a.nkv);
   const int m = mstart + 32 * w + c;
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
-  __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Vs[kBN * kPR];
+  __shared__ __attribute__((aligned(1024))) f16 Ks[kFwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(1024))) f16 Vs[kFwdStages * kTileHalves];
 
-  f16x8 qf[kHD / 16];
-  row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
   f32x16 oacc[kHD / 32];
 #pragma unroll
   for (int hb = 0; hb < kHD / 32; ++hb) oacc[hb] = zero16();
   float m_i = -1.0e30f, l_i = 0.0f;
   const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
-  const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
-  const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
-  for (int n0 = 0; n0 < hi; n0 += kBN) {
-    // (measured: prefetching the next tile into registers here, as the backward kernels do, made
-    // this kernel slower, not faster)
-    RowTile kt, vt;
-    load_rows(kt, kbase, ROW, s0, n0, seqlen, a.n_tokens);
-    load_rows(vt, vbase, ROW, s0, n0, seqlen, a.n_tokens);
-    __syncthreads();   // every wave has finished reading the previous tile
-    store_rows(kt, Ks);
-    store_rows(vt, Vs);
+  const int n_tiles = (hi + kBN - 1) / kBN;
+  const f16* kbase = a.qkv + s0 * ROW + (int64_t)(a.nq + kvh) * kHD;
+  const f16* vbase = a.qkv + s0 * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD;
+  // tile t into stage st: instruction i of wave w fills the stage's chunks (4 i + w) 64 + lane,
+  // row q / 16 (rows past the sequence read its last row: finite, and masked to p = 0)
+  constexpr int kLoads = kTileHalves / 8 / kAThreads;   // per operand per lane: 4
+  auto issue = [&](int t, int st) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int q = (4 * i + wave) * 64 + lane, r = q >> 4;
+      const int row = t * kBN + r < seqlen ? t * kBN + r : seqlen - 1;
+      const int64_t src = (int64_t)row * ROW + (((q & 15) ^ swz16(r)) << 3);
+      const int dst = st * kTileHalves + (4 * i + wave) * 512;
+      dma16(kbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ks + dst)));
+      dma16(vbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Vs + dst)));
+    }
+  };
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+  // this lane's query row as the B operand (rows past the sequence: zeros).  Loaded at a clamped
+  // row unconditionally and selected at once, so the compiler's wait for these loads stands here
+  // (it then also covers the two tiles issued above) and not inside the loop, where it would
+  // wait for the tiles in flight every iteration.
+  f16x8 qf[kHD / 16];
+  {
+    const f16* qrow = a.qkv + (s0 + (mval ? m : mstart)) * ROW + h * kHD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) qf[s] = *reinterpret_cast<const f16x8*>(qrow + 16 * s);
+    // (the empty asm needs the loaded values: the compiler can neither predicate the loads on
+    // mval nor defer their wait into the loop)
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) asm volatile("" : "+v"(qf[s]));
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) qf[s] = mval ? qf[s] : zero8();
+  }
+  for (int t = 0; t < n_tiles; ++t) {
+    // this wave's loads of tile t are done (those of tile t + 1 may still be in flight), then
+    // every wave's, and every wave has finished reading stage (t + 2) % 3 (tile t - 1)
+    if (t + 1 < n_tiles) wait_vmem<2 * kLoads>();
+    else wait_vmem<0>();
     __syncthreads();
+    if (t + 2 < n_tiles) issue(t + 2, (t + 2) % kFwdStages);
+    const f16* Kt = Ks + (t % kFwdStages) * kTileHalves;
+    const f16* Vt = Vs + (t % kFwdStages) * kTileHalves;
+    const int n0 = t * kBN;
     // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
     f32x16 sacc[2] = {zero16(), zero16()};
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Ks + (kb * 32 + c) * kPR + 16 * s + 8 * hl),
+        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + sw_off(kb * 32 + c, 16 * s + 8 * hl)),
                         qf[s], sacc[kb]);
     float mx = -1.0e30f;
 #pragma unroll
@@ -204,14 +285,14 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
       for (int v = 0; v < 16; ++v) oacc[hb][v] = __fmul_rn(oacc[hb][v], alpha);
     // O^T += V^T P^T over the tile's 64 keys, 16 per step
 #pragma unroll
-    for (int t = 0; t < kBN / 16; ++t) {
-      const int kb = t >> 1, i0 = 8 * (t & 1);
+    for (int tt = 0; tt < kBN / 16; ++tt) {
+      const int kb = tt >> 1, i0 = 8 * (tt & 1);
       f16x8 pf;
 #pragma unroll
       for (int j = 0; j < 8; ++j) pf[j] = (f16)sacc[kb][i0 + j];
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb)
-        oacc[hb] = mfma(read_col8(Vs, 16 * t + 4 * hl, hb * 32), pf, oacc[hb]);
+        oacc[hb] = mfma(read_col8_sw(Vt, 16 * tt + 4 * hl, hb * 32), pf, oacc[hb]);
     }
   }
   if (!mval) return;
