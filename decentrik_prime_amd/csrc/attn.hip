@@ -78,7 +78,7 @@ __device__ __forceinline__ f16x8 read_col8(const f16* tile, int p, int col) {
 // rows of 256 bytes with no padding; the 16-byte chunks of row r are permuted by swz16(r), so
 // that both reads of the tile are free of bank conflicts: the S^T operand (16 consecutive rows,
 // one chunk each) and the transposing V reads (4 rows x 2 adjacent chunks per 16-lane group).
-constexpr int kFwdStages = 3;                 // tiles in flight: this one and the next two
+constexpr int kFwdStages = 4;                 // tiles t, t + 1 in use, t + 2, t + 3 in flight
 constexpr int kTileHalves = kBN * kHD;        // one operand of one stage: 16 KB
 
 __device__ __forceinline__ int swz16(int r) {
@@ -220,10 +220,11 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
   };
   issue(0, 0);
   if (n_tiles > 1) issue(1, 1);
+  if (n_tiles > 2) issue(2, 2);
   // this lane's query row as the B operand (rows past the sequence: zeros).  Loaded at a clamped
   // row unconditionally and selected at once, so the compiler's wait for these loads stands here
-  // (it then also covers the two tiles issued above) and not inside the loop, where it would
-  // wait for the tiles in flight every iteration.
+  // (it then also covers the tiles issued above) and not inside the loop, where it would wait for
+  // the tiles in flight every iteration.
   f16x8 qf[kHD / 16];
   {
     const f16* qrow = a.qkv + (s0 + (mval ? m : mstart)) * ROW + h * kHD + 8 * hl;
@@ -236,44 +237,56 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s) qf[s] = mval ? qf[s] : zero8();
   }
-  for (int t = 0; t < n_tiles; ++t) {
-    // this wave's loads of tile t are done (those of tile t + 1 may still be in flight), then
-    // every wave's, and every wave has finished reading stage (t + 2) % 3 (tile t - 1)
-    if (t + 1 < n_tiles) wait_vmem<2 * kLoads>();
-    else wait_vmem<0>();
-    __syncthreads();
-    if (t + 2 < n_tiles) issue(t + 2, (t + 2) % kFwdStages);
-    const f16* Kt = Ks + (t % kFwdStages) * kTileHalves;
-    const f16* Vt = Vs + (t % kFwdStages) * kTileHalves;
-    const int n0 = t * kBN;
-    // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
-    f32x16 sacc[2] = {zero16(), zero16()};
+  // S^T = K Q^T of the tile in stage st: keys kb * 32 + (row of the result), queries on the lanes
+  auto scores = [&](f32x16 (&acc)[2], int st) {
+    const f16* Kt = Ks + st * kTileHalves;
+    acc[0] = acc[1] = zero16();
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
-        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + sw_off(kb * 32 + c, 16 * s + 8 * hl)),
-                        qf[s], sacc[kb]);
+        acc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + sw_off(kb * 32 + c, 16 * s + 8 * hl)),
+                       qf[s], acc[kb]);
+  };
+  // software pipeline: iteration t runs the score MFMAs of tile t + 1 beside the softmax of tile
+  // t (its VALU work), then O += V_t P_t.  Tiles t and t + 1 are in LDS at its start.
+  if (n_tiles > 2) wait_vmem<2 * kLoads>();
+  else wait_vmem<0>();
+  __syncthreads();
+  f32x16 sc[2];
+  scores(sc, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    // stage (t + 3) % 4 held tile t - 1, whose last reader (O += V P of iteration t - 1) every wave
+    // finished before the barrier that ended that iteration
+    if (t + 3 < n_tiles) issue(t + 3, (t + 3) % kFwdStages);
+    const f16* Vt = Vs + (t % kFwdStages) * kTileHalves;
+    const int n0 = t * kBN;
+    // tile t + 1's scores (past the last tile: a stale stage, never used)
+    f32x16 sn[2];
+    scores(sn, (t + 1) % kFwdStages);
+    // softmax of tile t in the exp2 domain: the row maximum of the raw scores, scaled once (the
+    // scaling is monotonic, so this is the maximum of the scaled scores), and
+    // p = 2^(s * qk_scale - m) with one rounding
     float mx = -1.0e30f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-        const float sv = n <= m && n < seqlen ? __fmul_rn(sacc[kb][v], a.qk_scale) : -1.0e30f;
-        sacc[kb][v] = sv;
+        const float sv = n <= m && n < seqlen ? sc[kb][v] : -1.0e30f;
+        sc[kb][v] = sv;
         mx = fmaxf(mx, sv);
       }
     mx = fmaxf(mx, __shfl_xor(mx, 32));
-    const float m_new = fmaxf(m_i, mx);
-    const float alpha = exp2f(__fsub_rn(m_i, m_new));
+    const float m_new = fmaxf(m_i, __fmul_rn(mx, a.qk_scale));
+    const float alpha = ex2(__fsub_rn(m_i, m_new));
     float rs = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = exp2f(__fsub_rn(sacc[kb][v], m_new));
-        sacc[kb][v] = p;
+        const float p = ex2(__builtin_fmaf(sc[kb][v], a.qk_scale, -m_new));
+        sc[kb][v] = p;
         rs = __fadd_rn(rs, p);
       }
     rs = __fadd_rn(rs, __shfl_xor(rs, 32));
@@ -283,17 +296,31 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
     for (int hb = 0; hb < kHD / 32; ++hb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) oacc[hb][v] = __fmul_rn(oacc[hb][v], alpha);
+    // the 16 score MFMAs of tile t + 1 spread among the softmax's VALU work
+#pragma unroll
+    for (int i = 0; i < 16; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // VALU
+    }
     // O^T += V^T P^T over the tile's 64 keys, 16 per step
 #pragma unroll
     for (int tt = 0; tt < kBN / 16; ++tt) {
       const int kb = tt >> 1, i0 = 8 * (tt & 1);
       f16x8 pf;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = (f16)sacc[kb][i0 + j];
+      for (int j = 0; j < 8; ++j) pf[j] = (f16)sc[kb][i0 + j];
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb)
         oacc[hb] = mfma(read_col8_sw(Vt, 16 * tt + 4 * hl, hb * 32), pf, oacc[hb]);
     }
+    // tile t + 2 landed (tile t + 3 may still be in flight) and visible to every wave, and every
+    // wave is done with stage t % 4
+    if (t + 3 < n_tiles) wait_vmem<2 * kLoads>();
+    else wait_vmem<0>();
+    __syncthreads();
+    sc[0] = sn[0];
+    sc[1] = sn[1];
   }
   if (!mval) return;
   // result register v of block hb: head column hb * 32 + 8 (v / 4) + 4 (l / 32) + v % 4
