@@ -19,9 +19,14 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
     const float* __restrict__ code2, const float* __restrict__ nf4, u32x4* __restrict__ out,
     int64_t n_quads) {
   __shared__ float lut[16];
+  // the 256-entry second-level code table, loaded beside the packed bytes and the first-level
+  // codes, so that the absmax needs no global load that waits for another
+  __shared__ float c2[256];
   // per wave: 64 lanes x 4 chunks of 16 bytes, one pad chunk per 64 against bank conflicts
   __shared__ u32x4 stage[kDqThreads / 64][64 * 4 + 4];
+  static_assert(kDqThreads == 256, "one code2 entry per thread");
   dk_fill_lut(lut, nf4, threadIdx.x);
+  c2[threadIdx.x] = code2[threadIdx.x];
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int64_t first = (int64_t)blockIdx.x * kDqQuadsPerBlock;
   const int64_t sb = first >> 9;                    // 512 quads per second-level block
@@ -29,8 +34,9 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
   const int64_t t = first + threadIdx.x;
   const int64_t tc = t < n_quads ? t : n_quads - 1;   // clamped: its result is not stored
   const u32x4 w = __builtin_nontemporal_load(packed + tc);
-  const float amax = dk_absmax(code2[qabs[tc >> 1]], s2, o2);
-  __syncthreads();   // lut
+  const uint8_t qa = qabs[tc >> 1];
+  __syncthreads();   // lut, c2
+  const float amax = dk_absmax(c2[qa], s2, o2);
 #pragma unroll
   for (int j = 0; j < 4; ++j) {
     const int idx = lane * 4 + j;
