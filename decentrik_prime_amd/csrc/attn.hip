@@ -24,7 +24,6 @@ constexpr int kHD = 128;          // head size (Qwen2.5: 128)
 constexpr int kAThreads = 256;    // 4 waves, 32 query rows (or keys) each
 constexpr int kBM = 128;          // queries per forward / dQ workgroup, keys per dK/dV workgroup
 constexpr int kBN = 64;           // keys per forward / dQ tile, queries per dK/dV tile
-constexpr int kPR = kHD + 8;      // halves per row of a row-major LDS tile
 static_assert(kBM == 32 * (kAThreads / 64), "a wave owns 32 rows");
 
 struct AttnArgs {
@@ -60,20 +59,7 @@ __device__ __forceinline__ f16x4 read_tr(const f16* q) {
       (__attribute__((address_space(3))) i16x4*)(q)));
 }
 
-// Column (col + l % 32) of rows p .. p + 3 and p + 8 .. p + 11 of a row-major LDS tile (row
-// stride kPR), the 8 values of MFMA k index j = 0..7 for a lane half whose p = 16 t + 4 (l / 32).
-// ds_read_b64_tr_b16: within a 16-lane group, lane 4a + b receives element b of the 4-half
-// pieces addressed by lanes a, a + 4, a + 8, a + 12; lane x addresses row p + x / 4 at columns
-// col + 16 (group) + 4 (x % 4), so lane x' of the group receives column col + 16 (group) + x' of
-// the four rows.  The 16 lanes of a group touch 16 distinct banks.
-__device__ __forceinline__ f16x8 read_col8(const f16* tile, int p, int col) {
-  const int lane = threadIdx.x & 63;
-  const f16* q = tile + (p + ((lane & 15) >> 2)) * kPR + col + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-  const f16x4 lo = read_tr(q), hi = read_tr(q + 8 * kPR);
-  return f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-}
-
-// K / V tiles of the forward in a ring of LDS stages filled by LDS DMA (global_load_lds_dwordx4:
+// K / V (or Q / dO) tiles in a ring of LDS stages filled by LDS DMA (global_load_lds_dwordx4:
 // no registers, the next tiles' loads in flight while this one is computed on).  A tile is kBN
 // rows of 256 bytes with no padding; the 16-byte chunks of row r are permuted by swz16(r), so
 // that both reads of the tile are free of bank conflicts: the S^T operand (16 consecutive rows,
@@ -113,8 +99,11 @@ __device__ __forceinline__ void wait_vmem() {
   asm volatile("s_waitcnt vmcnt(%0)" ::"n"(N) : "memory");
 }
 
-// Column (col + l % 32) of rows p .. p + 3 and p + 8 .. p + 11 of a swizzled tile: read_col8 for
-// the forward's K / V ring.
+// Column (col + l % 32) of rows p .. p + 3 and p + 8 .. p + 11 of a swizzled tile, the 8 values of
+// MFMA k index j = 0..7 for a lane half whose p = 16 t + 4 (l / 32).  ds_read_b64_tr_b16: within
+// a 16-lane group, lane 4a + b receives element b of the 4-half pieces addressed by lanes a,
+// a + 4, a + 8, a + 12; lane x addresses row p + x / 4 at columns col + 16 (group) + 4 (x % 4),
+// so lane x' of the group receives column col + 16 (group) + x' of the four rows.
 __device__ __forceinline__ f16x8 read_col8_sw(const f16* tile, int p, int col) {
   const int lane = threadIdx.x & 63;
   const int r = p + ((lane & 15) >> 2), c = col + 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
@@ -137,47 +126,6 @@ __device__ __forceinline__ bool block_of(const AttnArgs& a, int blk, int64_t* s0
   *s0 = a.cu[seq];
   *seqlen = a.cu[seq + 1] - a.cu[seq];
   return *s0 >= 0 && *seqlen >= 0 && *s0 + *seqlen <= a.n_tokens;
-}
-
-// Rows [r0, r0 + kBN) of one head (column offset folded into base, row stride ld), 8 halves per
-// 16-byte piece, two rows per item and two items per thread, read into registers (rows at or past
-// `valid`, or past the buffer, read as zero); the next tile's rows are read this way while the
-// current tile is computed on.
-struct RowTile {
-  f16x8 v[2][2];
-};
-
-__device__ __forceinline__ void load_rows(RowTile& t, const f16* base, int64_t ld, int64_t s0,
-                                          int r0, int valid, int64_t n_tokens) {
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int it = threadIdx.x + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) {
-      const int r = r0 + 2 * rp + u;
-      t.v[q][u] = r < valid && s0 + r < n_tokens
-                      ? *reinterpret_cast<const f16x8*>(base + (s0 + r) * ld + c8)
-                      : zero8();
-    }
-  }
-}
-
-// The rows into a row-major LDS tile rm[r][c] (16-byte stores, rows padded to kPR halves).
-__device__ __forceinline__ void store_rows(const RowTile& t, f16* rm) {
-#pragma unroll
-  for (int q = 0; q < 2; ++q) {
-    const int it = threadIdx.x + q * kAThreads, rp = it >> 4, c8 = (it & 15) * 8;
-#pragma unroll
-    for (int u = 0; u < 2; ++u) *reinterpret_cast<f16x8*>(rm + (2 * rp + u) * kPR + c8) = t.v[q][u];
-  }
-}
-
-// 8 k-steps of a head row as the B operand of a 32x32x16 product: lane l (row r = this lane's
-// query or key) holds elements 16 s + 8 (l / 32) + [0, 8) in frag[s]; zero for invalid rows.
-__device__ __forceinline__ void row_frags(const f16* row, bool valid, int hl, f16x8* frag) {
-#pragma unroll
-  for (int s = 0; s < kHD / 16; ++s)
-    frag[s] = valid ? *reinterpret_cast<const f16x8*>(row + 16 * s + 8 * hl) : zero8();
 }
 
 // forward (solution/k_attn.py:40-83): one workgroup per (block of kBM queries, query head)
@@ -358,7 +306,8 @@ __global__ __launch_bounds__(kAThreads) void attn_delta_kernel(const f16* __rest
 }
 
 // dQ (solution/k_attn.py:142-182): one workgroup per (block of kBM queries, query head), key
-// tiles of kBN up to the diagonal
+// tiles of kBN up to the diagonal, in the forward's four-stage K/V ring; the S^T and dP^T MFMAs of
+// tile t + 1 run beside the dS work of tile t
 __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f16* __restrict__ dout,
                                                             const float* __restrict__ lse,
                                                             const float* __restrict__ delta,
@@ -368,67 +317,123 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
   if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
   const int h = blockIdx.y;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
   const int kvh = h / (a.nq / a.nkv);
   const int m = mstart + 32 * w + c;
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
-  __shared__ __attribute__((aligned(16))) f16 Ks[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Vs[kBN * kPR];
+  __shared__ __attribute__((aligned(1024))) f16 Ks[kFwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(1024))) f16 Vs[kFwdStages * kTileHalves];
 
+  const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
+  const int n_tiles = (hi + kBN - 1) / kBN;
+  const f16* kbase = a.qkv + s0 * ROW + (int64_t)(a.nq + kvh) * kHD;
+  const f16* vbase = a.qkv + s0 * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD;
+  constexpr int kLoads = kTileHalves / 8 / kAThreads;
+  auto issue = [&](int t, int st) {
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int q = (4 * i + wave) * 64 + lane, r = q >> 4;
+      const int row = t * kBN + r < seqlen ? t * kBN + r : seqlen - 1;
+      const int64_t src = (int64_t)row * ROW + (((q & 15) ^ swz16(r)) << 3);
+      const int dst = st * kTileHalves + (4 * i + wave) * 512;
+      dma16(kbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ks + dst)));
+      dma16(vbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Vs + dst)));
+    }
+  };
+  issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+  if (n_tiles > 2) issue(2, 2);
+  // this lane's query and dO rows and statistics, loaded at a clamped row and selected at once
+  // (the compiler's wait for them stands here, not in the loop)
   f16x8 qf[kHD / 16], dof[kHD / 16];
-  row_frags(a.qkv + (s0 + m) * ROW + h * kHD, mval, hl, qf);
-  row_frags(dout + (s0 + m) * OROW + h * kHD, mval, hl, dof);
-  const float lse_m = mval ? lse[(int64_t)h * a.n_tokens + s0 + m] : 0.0f;
-  const float dl_m = mval ? delta[(int64_t)h * a.n_tokens + s0 + m] : 0.0f;
+  float lse_m, dl_m;
+  {
+    const int64_t rr = s0 + (mval ? m : mstart);
+    const f16* qrow = a.qkv + rr * ROW + h * kHD + 8 * hl;
+    const f16* drow = dout + rr * OROW + h * kHD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) {
+      qf[s] = *reinterpret_cast<const f16x8*>(qrow + 16 * s);
+      dof[s] = *reinterpret_cast<const f16x8*>(drow + 16 * s);
+    }
+    lse_m = lse[(int64_t)h * a.n_tokens + rr];
+    dl_m = delta[(int64_t)h * a.n_tokens + rr];
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) asm volatile("" : "+v"(qf[s]), "+v"(dof[s]));
+    asm volatile("" : "+v"(lse_m), "+v"(dl_m));
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) {
+      qf[s] = mval ? qf[s] : zero8();
+      dof[s] = mval ? dof[s] : zero8();
+    }
+    lse_m = mval ? lse_m : 0.0f;
+    dl_m = mval ? dl_m : 0.0f;
+  }
   f32x16 dqacc[kHD / 32];
 #pragma unroll
   for (int hb = 0; hb < kHD / 32; ++hb) dqacc[hb] = zero16();
-  const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
-  const f16* kbase = a.qkv + (int64_t)(a.nq + kvh) * kHD;
-  const f16* vbase = a.qkv + (int64_t)(a.nq + a.nkv + kvh) * kHD;
-  RowTile kt, vt;
-  load_rows(kt, kbase, ROW, s0, 0, seqlen, a.n_tokens);
-  load_rows(vt, vbase, ROW, s0, 0, seqlen, a.n_tokens);
-  for (int n0 = 0; n0 < hi; n0 += kBN) {
-    __syncthreads();
-    store_rows(kt, Ks);
-    store_rows(vt, Vs);
-    __syncthreads();
-    if (n0 + kBN < hi) {
-      load_rows(kt, kbase, ROW, s0, n0 + kBN, seqlen, a.n_tokens);
-      load_rows(vt, vbase, ROW, s0, n0 + kBN, seqlen, a.n_tokens);
-    }
-    f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
+  // S^T = K Q^T and dP^T = V dO^T of the tile in stage st: keys kb * 32 + (row), queries on lanes
+  auto products = [&](f32x16 (&sacc)[2], f32x16 (&dpacc)[2], int st) {
+    const f16* Kt = Ks + st * kTileHalves;
+    const f16* Vt = Vs + st * kTileHalves;
+    sacc[0] = sacc[1] = dpacc[0] = dpacc[1] = zero16();
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s)
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb) {
-        const int o = (kb * 32 + c) * kPR + 16 * s + 8 * hl;
-        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Ks + o), qf[s], sacc[kb]);     // S^T
-        dpacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Vs + o), dof[s], dpacc[kb]);  // dP^T
+        const int o = sw_off(kb * 32 + c, 16 * s + 8 * hl);
+        sacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + o), qf[s], sacc[kb]);
+        dpacc[kb] = mfma(*reinterpret_cast<const f16x8*>(Vt + o), dof[s], dpacc[kb]);
       }
+  };
+  if (n_tiles > 2) wait_vmem<2 * kLoads>();
+  else wait_vmem<0>();
+  __syncthreads();
+  f32x16 sc[2], dc[2];
+  products(sc, dc, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    if (t + 3 < n_tiles) issue(t + 3, (t + 3) % kFwdStages);
+    const f16* Kt = Ks + (t % kFwdStages) * kTileHalves;
+    const int n0 = t * kBN;
+    f32x16 sn[2], dn[2];
+    products(sn, dn, (t + 1) % kFwdStages);
     const bool full = n0 + kBN - 1 <= mstart + 32 * w && n0 + kBN <= seqlen;
+    // computed for every score and then selected (a conditional exponential becomes a branch)
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-        const float p = mval && (full || (n <= m && n < seqlen))
-                            ? ex2(__fsub_rn(__fmul_rn(sacc[kb][v], a.qk_scale), lse_m))
-                            : 0.0f;
-        sacc[kb][v] = __fmul_rn(p, __fsub_rn(dpacc[kb][v], dl_m));   // dS^T
+        const float e = ex2(__fsub_rn(__fmul_rn(sc[kb][v], a.qk_scale), lse_m));
+        const bool keep = mval & (full | ((n <= m) & (n < seqlen)));   // no short-circuit
+        const float p = keep ? e : 0.0f;
+        sc[kb][v] = __fmul_rn(p, __fsub_rn(dc[kb][v], dl_m));   // dS^T
       }
+#pragma unroll
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 3, 0);   // VALU
+    }
     // dQ^T += K^T dS^T
 #pragma unroll
-    for (int t = 0; t < kBN / 16; ++t) {
-      const int kb = t >> 1, i0 = 8 * (t & 1);
+    for (int tt = 0; tt < kBN / 16; ++tt) {
+      const int kb = tt >> 1, i0 = 8 * (tt & 1);
       f16x8 dsf;
 #pragma unroll
-      for (int j = 0; j < 8; ++j) dsf[j] = (f16)sacc[kb][i0 + j];
+      for (int j = 0; j < 8; ++j) dsf[j] = (f16)sc[kb][i0 + j];
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb)
-        dqacc[hb] = mfma(read_col8(Ks, 16 * t + 4 * hl, hb * 32), dsf, dqacc[hb]);
+        dqacc[hb] = mfma(read_col8_sw(Kt, 16 * tt + 4 * hl, hb * 32), dsf, dqacc[hb]);
     }
+    if (t + 3 < n_tiles) wait_vmem<2 * kLoads>();
+    else wait_vmem<0>();
+    __syncthreads();
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+    dc[0] = dn[0];
+    dc[1] = dn[1];
   }
   if (!mval) return;
   float* qrow = dq + (s0 + m) * OROW + h * kHD;
@@ -443,9 +448,27 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
     }
 }
 
+// 4 bytes per lane from global memory into LDS at lds + 4 * lane (the dword form of dma16).
+__device__ __forceinline__ void dma4(const void* src, unsigned lds) {
+  unsigned saved;
+  asm volatile(
+      "s_mov_b32 %0, m0\n\t"
+      "s_mov_b32 m0, %1\n\t"
+      "global_load_lds_dword %2, off\n\t"
+      "s_mov_b32 m0, %0"
+      : "=&s"(saved)
+      : "s"(lds), "v"(src)
+      : "memory");
+}
+
 // dK, dV per query head (solution/k_attn.py:97-139): one workgroup per (block of kBM keys, query
 // head), query tiles of kBN from the block's first key to the end of the sequence; fp32 partials
-// [N, NQ HD] that the QKV epilogue backward sums over each group of NQ / NKV heads.
+// [N, NQ HD] that the QKV epilogue backward sums over each group of NQ / NKV heads.  The Q and dO
+// tiles and the tiles' lse and delta rows come through a four-stage LDS ring filled by LDS DMA
+// (swizzled rows as in the forward; the statistics by dword DMA, one lane per query, waves 0
+// and 1), and the S and dP MFMAs of tile t + 1 run beside the P / dS work of tile t.
+constexpr int kBwdStages = 4;
+
 __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const f16* __restrict__ dout,
                                                               const float* __restrict__ lse,
                                                               const float* __restrict__ delta,
@@ -456,83 +479,164 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
   if (!block_of(a, blockIdx.x, &s0, &seqlen, &nstart)) return;
   const int h = blockIdx.y;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hl = lane >> 5, c = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(w);
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
   const int kvh = h / (a.nq / a.nkv);
   const int n = nstart + 32 * w + c;   // this lane's key
   const bool nval = n < seqlen && s0 + n < a.n_tokens;
-  __shared__ __attribute__((aligned(16))) f16 Qs[kBN * kPR];
-  __shared__ __attribute__((aligned(16))) f16 Ds[kBN * kPR];
-  __shared__ float lse_s[kBN], dl_s[kBN];
+  __shared__ __attribute__((aligned(1024))) f16 Qs[kBwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(1024))) f16 Ds[kBwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(16))) float lse_s[kBwdStages][kBN], dl_s[kBwdStages][kBN];
 
+  const int n_tiles = nstart < seqlen ? (seqlen - nstart + kBN - 1) / kBN : 0;
+  const f16* qbase = a.qkv + s0 * ROW + (int64_t)h * kHD;
+  const f16* dbase = dout + s0 * OROW + (int64_t)h * kHD;
+  constexpr int kLoads = kTileHalves / 8 / kAThreads;   // per operand per lane: 4
+  // query tile t (queries nstart + 64 t ...) into stage st; rows past the sequence read its last
+  // row (finite, masked to p = 0); wave 0 also fetches the tile's lse, wave 1 its delta
+  auto issue = [&](int t, int st) {
+    const int m0 = nstart + t * kBN;
+#pragma unroll
+    for (int i = 0; i < kLoads; ++i) {
+      const int q = (4 * i + wave) * 64 + lane, r = q >> 4;
+      const int row = m0 + r < seqlen ? m0 + r : seqlen - 1;
+      const int off = ((q & 15) ^ swz16(r)) << 3;
+      const int dst = st * kTileHalves + (4 * i + wave) * 512;
+      dma16(qbase + (int64_t)row * ROW + off, __builtin_amdgcn_readfirstlane(lds_addr(Qs + dst)));
+      dma16(dbase + (int64_t)row * OROW + off, __builtin_amdgcn_readfirstlane(lds_addr(Ds + dst)));
+    }
+    if (wave < 2) {
+      const int qq = m0 + lane < seqlen ? m0 + lane : seqlen - 1;
+      const float* src = (wave == 0 ? lse : delta) + (int64_t)h * a.n_tokens + s0 + qq;
+      dma4(src, __builtin_amdgcn_readfirstlane(lds_addr(wave == 0 ? lse_s[st] : dl_s[st])));
+    }
+  };
+  // wait until at most `tiles` tiles of this wave's loads are in flight (waves 0 and 1 issue one
+  // more load per tile)
+  auto wait_tiles = [&](int tiles) {
+    if (wave < 2) {
+      if (tiles >= 2) wait_vmem<2 * (2 * kLoads + 1)>();
+      else if (tiles == 1) wait_vmem<2 * kLoads + 1>();
+      else wait_vmem<0>();
+    } else {
+      if (tiles >= 2) wait_vmem<2 * 2 * kLoads>();
+      else if (tiles == 1) wait_vmem<2 * kLoads>();
+      else wait_vmem<0>();
+    }
+  };
+  if (n_tiles > 0) issue(0, 0);
+  if (n_tiles > 1) issue(1, 1);
+  if (n_tiles > 2) issue(2, 2);
+
+  // this lane's key and value rows as B operands, loaded at a clamped row and selected at once
+  // (the compiler's wait for them stands here, not in the loop)
   f16x8 kf[kHD / 16], vf[kHD / 16];
-  row_frags(a.qkv + (s0 + n) * ROW + (int64_t)(a.nq + kvh) * kHD, nval, hl, kf);
-  row_frags(a.qkv + (s0 + n) * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD, nval, hl, vf);
+  {
+    const int64_t rr = s0 + (nval ? n : nstart);
+    const f16* krow = a.qkv + rr * ROW + (int64_t)(a.nq + kvh) * kHD + 8 * hl;
+    const f16* vrow = a.qkv + rr * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD + 8 * hl;
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) {
+      kf[s] = *reinterpret_cast<const f16x8*>(krow + 16 * s);
+      vf[s] = *reinterpret_cast<const f16x8*>(vrow + 16 * s);
+    }
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) asm volatile("" : "+v"(kf[s]), "+v"(vf[s]));
+#pragma unroll
+    for (int s = 0; s < kHD / 16; ++s) {
+      kf[s] = nval ? kf[s] : zero8();
+      vf[s] = nval ? vf[s] : zero8();
+    }
+  }
   f32x16 dkacc[kHD / 32], dvacc[kHD / 32];
 #pragma unroll
   for (int hb = 0; hb < kHD / 32; ++hb) dkacc[hb] = dvacc[hb] = zero16();
-  const f16* qbase = a.qkv + (int64_t)h * kHD;
-  const f16* dbase = dout + (int64_t)h * kHD;
-  // lse (threads [0, kBN)) or delta (threads [kBN, 2 kBN)) of query m0 + (tid % kBN)
-  auto load_stat = [&](int m0) {
-    const int q = m0 + (tid & (kBN - 1));
-    const bool ok = tid < 2 * kBN && q < seqlen && s0 + q < a.n_tokens;
-    return ok ? (tid < kBN ? lse : delta)[(int64_t)h * a.n_tokens + s0 + q] : 0.0f;
-  };
-  RowTile qt, dt;
-  load_rows(qt, qbase, ROW, s0, nstart, seqlen, a.n_tokens);
-  load_rows(dt, dbase, OROW, s0, nstart, seqlen, a.n_tokens);
-  float stat = load_stat(nstart);
-  for (int m0 = nstart; m0 < seqlen; m0 += kBN) {
-    __syncthreads();
-    store_rows(qt, Qs);
-    store_rows(dt, Ds);
-    if (tid < kBN) lse_s[tid] = stat;
-    else if (tid < 2 * kBN) dl_s[tid - kBN] = stat;
-    __syncthreads();
-    if (m0 + kBN < seqlen) {
-      load_rows(qt, qbase, ROW, s0, m0 + kBN, seqlen, a.n_tokens);
-      load_rows(dt, dbase, OROW, s0, m0 + kBN, seqlen, a.n_tokens);
-      stat = load_stat(m0 + kBN);
-    }
-    // S = Q K^T and dP = dO V^T: queries qb * 32 + (row of the result), keys on the lanes
-    f32x16 sacc[2] = {zero16(), zero16()}, dpacc[2] = {zero16(), zero16()};
+  // S = Q K^T and dP = dO V^T of the tile in stage st: queries qb * 32 + (row of the result),
+  // keys on the lanes
+  auto products = [&](f32x16 (&sacc)[2], f32x16 (&dpacc)[2], int st) {
+    const f16* Qt = Qs + st * kTileHalves;
+    const f16* Dt = Ds + st * kTileHalves;
+    sacc[0] = sacc[1] = dpacc[0] = dpacc[1] = zero16();
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s)
 #pragma unroll
       for (int qb = 0; qb < 2; ++qb) {
-        const int o = (qb * 32 + c) * kPR + 16 * s + 8 * hl;
-        sacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Qs + o), kf[s], sacc[qb]);
-        dpacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Ds + o), vf[s], dpacc[qb]);
+        const int o = sw_off(qb * 32 + c, 16 * s + 8 * hl);
+        sacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Qt + o), kf[s], sacc[qb]);
+        dpacc[qb] = mfma(*reinterpret_cast<const f16x8*>(Dt + o), vf[s], dpacc[qb]);
       }
+  };
+  if (n_tiles > 0) {
+    wait_tiles(n_tiles > 2 ? 1 : 0);   // tiles 0 and 1 landed
+    __syncthreads();
+  }
+  f32x16 sc[2], dc[2];
+  if (n_tiles > 0) products(sc, dc, 0);
+  for (int t = 0; t < n_tiles; ++t) {
+    // stage (t + 3) % 4 held tile t - 1, whose last reader every wave finished before the
+    // barrier that ended iteration t - 1
+    if (t + 3 < n_tiles) issue(t + 3, (t + 3) % kBwdStages);
+    const int st = t % kBwdStages;
+    const int m0 = nstart + t * kBN;
+    // tile t + 1's products (past the last tile: a stale stage, never used)
+    f32x16 sn[2], dn[2];
+    products(sn, dn, (t + 1) % kBwdStages);
     // every query of the tile at or after every key of this wave, all inside the sequence
     const bool full = m0 >= nstart + 32 * w + 31 && m0 + kBN <= seqlen;
+    // the statistics of this lane's 32 queries of the tile: rows qb * 32 + 8 g + 4 (l / 32) + 0..3
+    f32x4 ls[2][4], ds[2][4];
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        ls[qb][g] = *reinterpret_cast<const f32x4*>(&lse_s[st][qb * 32 + 8 * g + 4 * hl]);
+        ds[qb][g] = *reinterpret_cast<const f32x4*>(&dl_s[st][qb * 32 + 8 * g + 4 * hl]);
+      }
+    // computed for every score and then selected: a conditional exponential becomes a branch per
+    // score
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
         const int r = qb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3), q = m0 + r;
-        const float p = nval && (full || (q >= n && q < seqlen))
-                            ? ex2(__fsub_rn(__fmul_rn(sacc[qb][v], a.qk_scale), lse_s[r]))
-                            : 0.0f;
-        sacc[qb][v] = p;                                              // P
-        dpacc[qb][v] = __fmul_rn(p, __fsub_rn(dpacc[qb][v], dl_s[r]));  // dS
+        const float e = ex2(__fsub_rn(__fmul_rn(sc[qb][v], a.qk_scale), ls[qb][v >> 2][v & 3]));
+        const bool keep = nval & (full | ((q >= n) & (q < seqlen)));   // no short-circuit
+        const float p = keep ? e : 0.0f;
+        sc[qb][v] = p;                                                           // P
+        dc[qb][v] = __fmul_rn(p, __fsub_rn(dc[qb][v], ds[qb][v >> 2][v & 3]));    // dS
       }
-    // dV += P^T dO, dK += dS^T Q over the tile's 64 queries, 16 per step
+    // the 32 products of tile t + 1 spread among this work
 #pragma unroll
-    for (int t = 0; t < kBN / 16; ++t) {
-      const int qb = t >> 1, i0 = 8 * (t & 1);
+    for (int i = 0; i < 32; ++i) {
+      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
+      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
+      __builtin_amdgcn_sched_group_barrier(0x002, 4, 0);   // VALU
+    }
+    // dV += P^T dO, dK += dS^T Q over the tile's 64 queries, 16 per step
+    const f16* Qt = Qs + st * kTileHalves;
+    const f16* Dt = Ds + st * kTileHalves;
+#pragma unroll
+    for (int tt = 0; tt < kBN / 16; ++tt) {
+      const int qb = tt >> 1, i0 = 8 * (tt & 1);
       f16x8 pf, dsf;
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
-        pf[j] = (f16)sacc[qb][i0 + j];
-        dsf[j] = (f16)dpacc[qb][i0 + j];
+        pf[j] = (f16)sc[qb][i0 + j];
+        dsf[j] = (f16)dc[qb][i0 + j];
       }
 #pragma unroll
       for (int hb = 0; hb < kHD / 32; ++hb) {
-        dvacc[hb] = mfma(pf, read_col8(Ds, 16 * t + 4 * hl, hb * 32), dvacc[hb]);
-        dkacc[hb] = mfma(dsf, read_col8(Qs, 16 * t + 4 * hl, hb * 32), dkacc[hb]);
+        dvacc[hb] = mfma(pf, read_col8_sw(Dt, 16 * tt + 4 * hl, hb * 32), dvacc[hb]);
+        dkacc[hb] = mfma(dsf, read_col8_sw(Qt, 16 * tt + 4 * hl, hb * 32), dkacc[hb]);
       }
     }
+    // tile t + 2 landed and visible to every wave, every wave done with stage t % 4
+    wait_tiles(t + 3 < n_tiles ? 1 : 0);
+    __syncthreads();
+    sc[0] = sn[0];
+    sc[1] = sn[1];
+    dc[0] = dn[0];
+    dc[1] = dn[1];
   }
   // result register v of block hb: key 32 w + 8 (v / 4) + 4 (l / 32) + v % 4, column hb * 32 + c
 #pragma unroll
