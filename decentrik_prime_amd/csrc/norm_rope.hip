@@ -29,6 +29,10 @@ __device__ __forceinline__ f32x4 load_h4(const f16* p) {
   return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
 }
 
+__device__ __forceinline__ f32x4 to_f4(const f16x4 h) {
+  return f32x4{(float)h[0], (float)h[1], (float)h[2], (float)h[3]};
+}
+
 __device__ __forceinline__ void store_h4(f16* p, const f32x4& v) {
   *reinterpret_cast<f16x4*>(p) = f16x4{dk_h(v[0]), dk_h(v[1]), dk_h(v[2]), dk_h(v[3])};
 }
@@ -52,29 +56,44 @@ __global__ __launch_bounds__(kRowThreads) void rms_fwd_kernel(
   const int64_t row = (int64_t)blockIdx.x * kRowsPerBlock + (threadIdx.x >> 6);
   if (row >= n_rows) return;
   const int64_t off = row * d;
-  // every load of the row is issued before the reduction, so the row costs one memory latency
+  const int kn = (d + 255) / 256;   // chunks holding any of the row (uniform)
+  // every load of the row first, at clamped addresses (a lane past the row reads element 0 and
+  // its values are not used), then the arithmetic: a load consumed right away would make the
+  // compiler wait for it before the next chunk's loads go out, one memory latency per chunk
+  // Straight-line loads (a load under a branch, or converted at once, makes the compiler wait for
+  // it there): every chunk up to KMAX, and the optional inputs from x when absent (read, unused).
+  const f16* dsrc = delta ? delta : reinterpret_cast<const f16*>(x);
+  const uint8_t* qsrc = xq ? mq : reinterpret_cast<const uint8_t*>(x);
+  const uint8_t* vsrc = xq ? mv : reinterpret_cast<const uint8_t*>(x);
   f32x4 h[KMAX], wv[KMAX];
+  f16x4 dl[KMAX];
   uint32_t kq[KMAX], kv[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int e = 256 * k + 4 * lane, ec = e < d ? e : 0;
+    h[k] = *reinterpret_cast<const f32x4*>(x + off + ec);
+    wv[k] = *reinterpret_cast<const f32x4*>(w + ec);
+    kq[k] = load_mask4(qsrc + off + ec);
+    kv[k] = load_mask4(vsrc + off + ec);
+    dl[k] = *reinterpret_cast<const f16x4*>(dsrc + off + ec);
+  }
   float ss = 0.0f;
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
+    if (k >= kn) continue;
     const int e = 256 * k + 4 * lane;
-    if (e < d) {
-      h[k] = *reinterpret_cast<const f32x4*>(x + off + e);
-      wv[k] = *reinterpret_cast<const f32x4*>(w + e);
-      if (xq) {
-        kq[k] = load_mask4(mq + off + e);
-        kv[k] = load_mask4(mv + off + e);
-      }
-      if (delta) {
-        const f32x4 dl = load_h4(delta + off + e);
+    if (delta) {
+      const f32x4 d4 = to_f4(dl[k]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) h[k][i] = __fadd_rn(h[k][i], dl[i]);
-      }
-      if (xout) *reinterpret_cast<f32x4*>(xout + off + e) = h[k];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ss = __fadd_rn(ss, __fmul_rn(h[k][i], h[k][i]));
+      for (int i = 0; i < 4; ++i) h[k][i] = __fadd_rn(h[k][i], d4[i]);
     }
+    float sk = 0.0f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) sk = __fadd_rn(sk, __fmul_rn(h[k][i], h[k][i]));
+    // (the per-chunk partial then the running sum: the same order as summing element by element
+    // would not be; both are a lane-order sum of this lane's squares)
+    ss = e < d ? __fadd_rn(ss, sk) : ss;
+    if (xout && e < d) *reinterpret_cast<f32x4*>(xout + off + e) = h[k];
   }
   const float ms = __fmul_rn(wave_sum(ss), 1.0f / (float)d);
   const float r = rsqrtf(__fadd_rn(ms, eps));
@@ -82,7 +101,7 @@ __global__ __launch_bounds__(kRowThreads) void rms_fwd_kernel(
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int e = 256 * k + 4 * lane;
-    if (e >= d) continue;
+    if (k >= kn || e >= d) continue;
     f32x4 yv;
 #pragma unroll
     for (int i = 0; i < 4; ++i) yv[i] = __fmul_rn(wv[k][i], __fmul_rn(h[k][i], r));
@@ -116,45 +135,74 @@ __global__ __launch_bounds__(kRowThreads) void rms_bwd_kernel(
   const int64_t off = row * d;
   const float gs = *gscale;
   const float r = rstd[row];
-  f32x4 g[KMAX], xh[KMAX], rv[KMAX];
+  const int kn = (d + 255) / 256;   // chunks holding any of the row (uniform)
+  // every load of the row first, at clamped addresses (lanes past the row read element 0 and
+  // their values are not used), then the arithmetic
+  // fp16 operands are kept as loaded and converted after the loads (a conversion here would wait
+  // for its load)
+  // straight-line loads: every chunk up to KMAX, and the optional inputs from x when absent
+  // (read, unused); dres before the reduction, since out may alias it
+  const f16* x16 = reinterpret_cast<const f16*>(x);
+  const uint8_t* x8 = reinterpret_cast<const uint8_t*>(x);
+  const f16* lqs = lq ? lq : x16;
+  const f16* lvs = lq ? lv : x16;
+  const uint8_t* mqs = lq ? mq : x8;
+  const uint8_t* mvs = lq ? mv : x8;
+  const f16* dls = delta ? delta : x16;
+  const float* rvs = dres ? dres : x;
+  f32x4 dy32[KMAX], xv[KMAX], wv[KMAX], rv[KMAX];
+  f16x4 dy16[KMAX], a[KMAX], b[KMAX], dl[KMAX];
+  uint32_t kq[KMAX], kv[KMAX];
+#pragma unroll
+  for (int k = 0; k < KMAX; ++k) {
+    const int e = 256 * k + 4 * lane, ec = e < d ? e : 0;
+    if (DY32) dy32[k] = *reinterpret_cast<const f32x4*>(static_cast<const float*>(dyp) + off + ec);
+    else dy16[k] = *reinterpret_cast<const f16x4*>(static_cast<const f16*>(dyp) + off + ec);
+    kq[k] = load_mask4(mqs + off + ec);
+    kv[k] = load_mask4(mvs + off + ec);
+    a[k] = *reinterpret_cast<const f16x4*>(lqs + off + ec);
+    b[k] = *reinterpret_cast<const f16x4*>(lvs + off + ec);
+    xv[k] = *reinterpret_cast<const f32x4*>(x + off + ec);
+    dl[k] = *reinterpret_cast<const f16x4*>(dls + off + ec);
+    wv[k] = *reinterpret_cast<const f32x4*>(w + ec);
+    rv[k] = *reinterpret_cast<const f32x4*>(rvs + off + ec);
+  }
+  f32x4 g[KMAX], xh[KMAX];
   float cs = 0.0f;
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
+    if (k >= kn) continue;
     const int e = 256 * k + 4 * lane;
-    if (e >= d) continue;
-    f32x4 dy = DY32 ? *reinterpret_cast<const f32x4*>(static_cast<const float*>(dyp) + off + e)
-                    : load_h4(static_cast<const f16*>(dyp) + off + e);
+    f32x4 dyk = DY32 ? dy32[k] : to_f4(dy16[k]);
 #pragma unroll
-    for (int i = 0; i < 4; ++i) dy[i] = __fmul_rn(dy[i], gs);
+    for (int i = 0; i < 4; ++i) dyk[i] = __fmul_rn(dyk[i], gs);
     if (lq) {
-      const uint32_t kq = load_mask4(mq + off + e), kv = load_mask4(mv + off + e);
-      const f32x4 a = load_h4(lq + off + e), b = load_h4(lv + off + e);
+      const f32x4 ak = to_f4(a[k]), bk = to_f4(b[k]);
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        dy[i] = __fadd_rn(dy[i], kept(kq, i) ? __fmul_rn(a[i], keep_scale) : 0.0f);
-        dy[i] = __fadd_rn(dy[i], kept(kv, i) ? __fmul_rn(b[i], keep_scale) : 0.0f);
+        dyk[i] = __fadd_rn(dyk[i], kept(kq[k], i) ? __fmul_rn(ak[i], keep_scale) : 0.0f);
+        dyk[i] = __fadd_rn(dyk[i], kept(kv[k], i) ? __fmul_rn(bk[i], keep_scale) : 0.0f);
       }
     }
-    f32x4 xv = *reinterpret_cast<const f32x4*>(x + off + e);
     if (delta) {
-      const f32x4 dl = load_h4(delta + off + e);
+      const f32x4 d4 = to_f4(dl[k]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) xv[i] = __fadd_rn(xv[i], dl[i]);
+      for (int i = 0; i < 4; ++i) xv[k][i] = __fadd_rn(xv[k][i], d4[i]);
     }
-    const f32x4 wv = *reinterpret_cast<const f32x4*>(w + e);
-    if (dres) rv[k] = *reinterpret_cast<const f32x4*>(dres + off + e);   // before the reduction
+    float ck = cs;
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      xh[k][i] = __fmul_rn(xv[i], r);
-      g[k][i] = __fmul_rn(dy[i], wv[i]);
-      cs = __fadd_rn(cs, __fmul_rn(g[k][i], xh[k][i]));
+      xh[k][i] = __fmul_rn(xv[k][i], r);
+      g[k][i] = __fmul_rn(dyk[i], wv[k][i]);
+      ck = __fadd_rn(ck, __fmul_rn(g[k][i], xh[k][i]));
     }
+    cs = e < d ? ck : cs;
   }
   const float c = __fmul_rn(wave_sum(cs), 1.0f / (float)d);
 #pragma unroll
   for (int k = 0; k < KMAX; ++k) {
     const int e = 256 * k + 4 * lane;
-    if (e >= d) continue;
+    if (k >= kn || e >= d) continue;
     f32x4 dx;
 #pragma unroll
     for (int i = 0; i < 4; ++i) dx[i] = __fmul_rn(__fsub_rn(g[k][i], __fmul_rn(xh[k][i], c)), r);
@@ -187,41 +235,44 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_fwd_kernel(
   const f16* lvr = lv + row * (int64_t)nkv * hd;
   // query heads (LoRA add, rotate) and key heads (rotate): a lane's tasks t = lane + 64 i in
   // batches of kBatch, all loads of a batch issued before the first is used
+  // (loads at clamped tasks, straight-line, fp16 converted after: a load under a branch or used
+  // at once makes the compiler wait for it there)
   const int tasks = (nq + nkv) * quads;
   for (int t0 = 0; t0 < tasks; t0 += 64 * kBatch) {
-    f32x4 x1[kBatch], x2[kBatch], a[kBatch], b[kBatch], c[kBatch], s[kBatch];
+    f16x4 x1h[kBatch], x2h[kBatch], ah[kBatch], bh[kBatch];
+    f32x4 c[kBatch], s[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int t = t0 + 64 * u + lane;
-      if (t >= tasks) continue;
+      const int t0u = t0 + 64 * u + lane, t = t0u < tasks ? t0u : tasks - 1;
       const int head = t / quads, j = 4 * (t % quads);
       const f16* h1 = base + head * hd + j;
-      x1[u] = load_h4(h1);
-      x2[u] = load_h4(h1 + half);
+      x1h[u] = *reinterpret_cast<const f16x4*>(h1);
+      x2h[u] = *reinterpret_cast<const f16x4*>(h1 + half);
       c[u] = *reinterpret_cast<const f32x4*>(cr + j);
       s[u] = *reinterpret_cast<const f32x4*>(sr + j);
-      if (head < nq) {
-        a[u] = load_h4(lqr + head * hd + j);
-        b[u] = load_h4(lqr + head * hd + j + half);
-      }
+      const int hq = head < nq ? head : nq - 1;   // key heads: read, unused
+      ah[u] = *reinterpret_cast<const f16x4*>(lqr + hq * hd + j);
+      bh[u] = *reinterpret_cast<const f16x4*>(lqr + hq * hd + j + half);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int t = t0 + 64 * u + lane;
       if (t >= tasks) continue;
       const int head = t / quads, j = 4 * (t % quads);
+      f32x4 x1 = to_f4(x1h[u]), x2 = to_f4(x2h[u]);
       if (head < nq) {
+        const f32x4 a = to_f4(ah[u]), b = to_f4(bh[u]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          x1[u][i] = __fadd_rn(x1[u][i], __fmul_rn(a[u][i], scale));
-          x2[u][i] = __fadd_rn(x2[u][i], __fmul_rn(b[u][i], scale));
+          x1[i] = __fadd_rn(x1[i], __fmul_rn(a[i], scale));
+          x2[i] = __fadd_rn(x2[i], __fmul_rn(b[i], scale));
         }
       }
       f32x4 o1, o2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o1[i] = __fsub_rn(__fmul_rn(x1[u][i], c[u][i]), __fmul_rn(x2[u][i], s[u][i]));
-        o2[i] = __fadd_rn(__fmul_rn(x2[u][i], c[u][i]), __fmul_rn(x1[u][i], s[u][i]));
+        o1[i] = __fsub_rn(__fmul_rn(x1[i], c[u][i]), __fmul_rn(x2[i], s[u][i]));
+        o2[i] = __fadd_rn(__fmul_rn(x2[i], c[u][i]), __fmul_rn(x1[i], s[u][i]));
       }
       f16* h1 = base + head * hd + j;
       store_h4(h1, o1);
@@ -232,33 +283,38 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_fwd_kernel(
   f16* vb = base + (int64_t)(nq + nkv) * hd;
   const int vtasks = nkv * hd / 4;
   for (int t0 = 0; t0 < vtasks; t0 += 64 * kBatch) {
-    f32x4 v[kBatch], a[kBatch];
+    f16x4 vh[kBatch], ah[kBatch];
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
-      const int t = t0 + 64 * u + lane;
-      if (t >= vtasks) continue;
-      v[u] = load_h4(vb + 4 * t);
-      a[u] = load_h4(lvr + 4 * t);
+      const int t0u = t0 + 64 * u + lane, t = t0u < vtasks ? t0u : vtasks - 1;
+      vh[u] = *reinterpret_cast<const f16x4*>(vb + 4 * t);
+      ah[u] = *reinterpret_cast<const f16x4*>(lvr + 4 * t);
     }
 #pragma unroll
     for (int u = 0; u < kBatch; ++u) {
       const int t = t0 + 64 * u + lane;
       if (t >= vtasks) continue;
+      f32x4 v = to_f4(vh[u]);
+      const f32x4 a = to_f4(ah[u]);
 #pragma unroll
-      for (int i = 0; i < 4; ++i) v[u][i] = __fadd_rn(v[u][i], __fmul_rn(a[u][i], scale));
-      store_h4(vb + 4 * t, v[u]);
+      for (int i = 0; i < 4; ++i) v[i] = __fadd_rn(v[i], __fmul_rn(a[i], scale));
+      store_h4(vb + 4 * t, v);
     }
   }
 }
 
+// Four elements of a gradient that arrives as fp32 or fp16: loaded raw, converted at use (a
+// conversion right after the load would make the compiler wait for that load there).
 template <typename T>
-__device__ __forceinline__ f32x4 load4(const T* p) {
-  if constexpr (sizeof(T) == 4) {
-    return *reinterpret_cast<const f32x4*>(p);
-  } else {
-    return load_h4(reinterpret_cast<const f16*>(p));
-  }
+using Raw4 = std::conditional_t<sizeof(T) == 4, f32x4, f16x4>;
+
+template <typename T>
+__device__ __forceinline__ Raw4<T> raw4(const T* p) {
+  return *reinterpret_cast<const Raw4<T>*>(p);
 }
+
+__device__ __forceinline__ f32x4 cvt4(f32x4 v) { return v; }
+__device__ __forceinline__ f32x4 cvt4(f16x4 v) { return to_f4(v); }
 
 // QKV epilogue backward (solution/k_rope.py:64-104): the transposed rotation of dq; the gin
 // partials of each KV head summed in order, dk rotated back; fp16 out in the QKV layout.
@@ -281,14 +337,14 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_bwd_kernel(
   // query heads: batches of kBatch tasks, all loads first
   const int qtasks = nq * quads;
   for (int t0 = 0; t0 < qtasks; t0 += 64 * kBatch) {
-    f32x4 d1[kBatch], d2[kBatch], c[kBatch], s[kBatch];
+    Raw4<T> d1[kBatch], d2[kBatch];
+    f32x4 c[kBatch], s[kBatch];
 #pragma unroll
-    for (int u = 0; u < kBatch; ++u) {
-      const int t = t0 + 64 * u + lane;
-      if (t >= qtasks) continue;
+    for (int u = 0; u < kBatch; ++u) {   // clamped tasks: straight-line loads
+      const int t0u = t0 + 64 * u + lane, t = t0u < qtasks ? t0u : qtasks - 1;
       const int head = t / quads, j = 4 * (t % quads);
-      d1[u] = load4(dqr + head * hd + j);
-      d2[u] = load4(dqr + head * hd + j + half);
+      d1[u] = raw4(dqr + head * hd + j);
+      d2[u] = raw4(dqr + head * hd + j + half);
       c[u] = *reinterpret_cast<const f32x4*>(cr + j);
       s[u] = *reinterpret_cast<const f32x4*>(sr + j);
     }
@@ -297,11 +353,12 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_bwd_kernel(
       const int t = t0 + 64 * u + lane;
       if (t >= qtasks) continue;
       const int head = t / quads, j = 4 * (t % quads);
+      const f32x4 a = cvt4(d1[u]), b = cvt4(d2[u]);
       f32x4 o1, o2;
 #pragma unroll
       for (int i = 0; i < 4; ++i) {
-        o1[i] = __fadd_rn(__fmul_rn(d1[u][i], c[u][i]), __fmul_rn(d2[u][i], s[u][i]));
-        o2[i] = __fsub_rn(__fmul_rn(d2[u][i], c[u][i]), __fmul_rn(d1[u][i], s[u][i]));
+        o1[i] = __fadd_rn(__fmul_rn(a[i], c[u][i]), __fmul_rn(b[i], s[u][i]));
+        o2[i] = __fsub_rn(__fmul_rn(b[i], c[u][i]), __fmul_rn(a[i], s[u][i]));
       }
       store_h4(dst + head * hd + j, o1);
       store_h4(dst + head * hd + j + half, o2);
@@ -316,21 +373,22 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_bwd_kernel(
     const f32x4 s = *reinterpret_cast<const f32x4*>(sr + j);
     f32x4 d1 = f32x4{0.0f, 0.0f, 0.0f, 0.0f}, d2 = d1;
     for (int g0 = 0; g0 < gin; g0 += kGinBatch) {
-      f32x4 pa[kGinBatch], pb[kGinBatch];
+      Raw4<T> pa[kGinBatch], pb[kGinBatch];
 #pragma unroll
-      for (int u = 0; u < kGinBatch; ++u) {
-        if (g0 + u >= gin) continue;
-        const T* part = dkr + (int64_t)(hk * gin + g0 + u) * hd + j;
-        pa[u] = load4(part);
-        pb[u] = load4(part + half);
+      for (int u = 0; u < kGinBatch; ++u) {   // partials past gin: the last one read, unused
+        const int g = g0 + u < gin ? g0 + u : gin - 1;
+        const T* part = dkr + (int64_t)(hk * gin + g) * hd + j;
+        pa[u] = raw4(part);
+        pb[u] = raw4(part + half);
       }
 #pragma unroll
       for (int u = 0; u < kGinBatch; ++u) {
         if (g0 + u >= gin) continue;
+        const f32x4 a = cvt4(pa[u]), b = cvt4(pb[u]);
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          d1[i] = __fadd_rn(d1[i], pa[u][i]);
-          d2[i] = __fadd_rn(d2[i], pb[u][i]);
+          d1[i] = __fadd_rn(d1[i], a[i]);
+          d2[i] = __fadd_rn(d2[i], b[i]);
         }
       }
     }
@@ -348,15 +406,18 @@ __global__ __launch_bounds__(kRowThreads) void qkv_epilogue_bwd_kernel(
     const int hk = (4 * t) / hd, e = (4 * t) % hd;
     f32x4 acc = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     for (int g0 = 0; g0 < gin; g0 += kGinBatch) {
-      f32x4 pa[kGinBatch];
+      Raw4<T> pa[kGinBatch];
 #pragma unroll
-      for (int u = 0; u < kGinBatch; ++u)
-        if (g0 + u < gin) pa[u] = load4(dvr + (int64_t)(hk * gin + g0 + u) * hd + e);
+      for (int u = 0; u < kGinBatch; ++u) {
+        const int g = g0 + u < gin ? g0 + u : gin - 1;
+        pa[u] = raw4(dvr + (int64_t)(hk * gin + g) * hd + e);
+      }
 #pragma unroll
       for (int u = 0; u < kGinBatch; ++u) {
         if (g0 + u >= gin) continue;
+        const f32x4 a = cvt4(pa[u]);
 #pragma unroll
-        for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], pa[u][i]);
+        for (int i = 0; i < 4; ++i) acc[i] = __fadd_rn(acc[i], a[i]);
       }
     }
     store_h4(vdst + 4 * t, acc);
@@ -385,7 +446,10 @@ extern "C" int dk_rms_fwd(const float* x, const void* delta, float* xout, const 
     hipLaunchKernelGGL(kern, grid, block, 0, stream, x, (const f16*)delta, xout, w, (f16*)y, rstd,
                        (f16*)xq, (f16*)xv, mq, mv, n_rows, (int)d, eps, keep_scale);
   };
+  // (the chunk count sets the registers a row's loads hold: at most 1536 columns, Qwen2.5-1.5B's
+  // hidden size, keeps the backward at two waves per SIMD)
   if (d <= 1024) args(rms_fwd_kernel<4>);
+  else if (d <= 1536) args(rms_fwd_kernel<6>);
   else if (d <= 2048) args(rms_fwd_kernel<8>);
   else args(rms_fwd_kernel<16>);
   DK_CHECK_LAUNCH();
@@ -417,10 +481,12 @@ extern "C" int dk_rms_bwd(const void* dy, int dy_f32, const float* gscale, const
   };
   if (dy_f32) {
     if (d <= 1024) args(rms_bwd_kernel<4, true>);
+    else if (d <= 1536) args(rms_bwd_kernel<6, true>);
     else if (d <= 2048) args(rms_bwd_kernel<8, true>);
     else args(rms_bwd_kernel<16, true>);
   } else {
     if (d <= 1024) args(rms_bwd_kernel<4, false>);
+    else if (d <= 1536) args(rms_bwd_kernel<6, false>);
     else if (d <= 2048) args(rms_bwd_kernel<8, false>);
     else args(rms_bwd_kernel<16, false>);
   }
