@@ -29,13 +29,19 @@ FLAGS = [
 ]
 
 
+# per-file additions: the attention forward keeps its MFMA accumulators in VGPRs (in AGPRs, the
+# compiler's default at one wave per SIMD, it copied the output accumulator out and back on every
+# key tile); the backward kernels need more registers than VGPRs hold and keep the default
+EXTRA_FLAGS = {"attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+
+
 def sources():
     return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
 
 
 def _compile(src):
     obj = os.path.join(OBJ, os.path.basename(src)[:-4] + ".o")
-    cmd = [HIPCC, *FLAGS, "-c", src, "-o", obj]
+    cmd = [HIPCC, *FLAGS, *EXTRA_FLAGS.get(os.path.basename(src), []), "-c", src, "-o", obj]
     res = subprocess.run(cmd, capture_output=True, text=True)
     errs = "\n".join(l for l in res.stderr.splitlines()
                      if "packed-fp32-ops' is not a recognized feature" not in l)
