@@ -117,18 +117,28 @@ __global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f1
     const int n0 = t * kBN;
     f32x16 sn[2], dn[2];
     products(sn, dn, (t + 1) % kFwdStages);
-    const bool full = n0 + kBN - 1 <= mstart + 32 * w && n0 + kBN <= seqlen;
-    // computed for every score and then selected (a conditional exponential becomes a branch)
+    // P and dS^T = P (dP^T - delta).  Rows past the sequence have zero q, dO and delta, so their
+    // dS is zero whatever P is; keys past a query or the sequence are masked only on the tiles
+    // that reach this wave's first query (a wave-uniform test): key n = n0 + off + 4 (l / 32) is
+    // kept iff off <= min(m, seqlen - 1) - n0 - 4 (l / 32).  The exponential is computed for
+    // every score and then selected (a conditional exponential becomes a branch).
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int n = n0 + kb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3);
-        const float e = ex2(__fsub_rn(__fmul_rn(sc[kb][v], a.qk_scale), lse_m));
-        const bool keep = mval & (full | ((n <= m) & (n < seqlen)));   // no short-circuit
-        const float p = keep ? e : 0.0f;
-        sc[kb][v] = __fmul_rn(p, __fsub_rn(dc[kb][v], dl_m));   // dS^T
-      }
+      for (int v = 0; v < 16; ++v)
+        sc[kb][v] = ex2(__builtin_fmaf(sc[kb][v], a.qk_scale, -lse_m));
+    if (n0 + kBN - 1 > mstart + 32 * wave || n0 + kBN > seqlen) {
+      const int lim = (m < seqlen - 1 ? m : seqlen - 1) - n0 - 4 * hl;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          sc[kb][v] = kb * 32 + 8 * (v >> 2) + (v & 3) <= lim ? sc[kb][v] : 0.0f;
+    }
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) sc[kb][v] = __fmul_rn(sc[kb][v], __fsub_rn(dc[kb][v], dl_m));
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
       __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
@@ -300,8 +310,6 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
     // tile t + 1's products (past the last tile: a stale stage, never used)
     f32x16 sn[2], dn[2];
     products(sn, dn, (t + 1) % kBwdStages);
-    // every query of the tile at or after every key of this wave, all inside the sequence
-    const bool full = m0 >= nstart + 32 * w + 31 && m0 + kBN <= seqlen;
     // the statistics of this lane's 32 queries of the tile: rows qb * 32 + 8 g + 4 (l / 32) + 0..3
     f32x4 ls[2][4], ds[2][4];
 #pragma unroll
@@ -311,19 +319,30 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
         ls[qb][g] = *reinterpret_cast<const f32x4*>(&lse_s[st][qb * 32 + 8 * g + 4 * hl]);
         ds[qb][g] = *reinterpret_cast<const f32x4*>(&dl_s[st][qb * 32 + 8 * g + 4 * hl]);
       }
-    // computed for every score and then selected: a conditional exponential becomes a branch per
-    // score
+    // P, computed for every score and then selected (a conditional exponential becomes a branch).
+    // Keys past the sequence only reach rows of dK and dV that are not stored; queries before a
+    // key or past the sequence are masked only on the tiles that hold such a query for this wave
+    // (a wave-uniform test): query q = m0 + off + 4 (l / 32) is kept iff lo <= off < hi.
 #pragma unroll
     for (int qb = 0; qb < 2; ++qb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int r = qb * 32 + 8 * (v >> 2) + 4 * hl + (v & 3), q = m0 + r;
-        const float e = ex2(__fsub_rn(__fmul_rn(sc[qb][v], a.qk_scale), ls[qb][v >> 2][v & 3]));
-        const bool keep = nval & (full | ((q >= n) & (q < seqlen)));   // no short-circuit
-        const float p = keep ? e : 0.0f;
-        sc[qb][v] = p;                                                           // P
-        dc[qb][v] = __fmul_rn(p, __fsub_rn(dc[qb][v], ds[qb][v >> 2][v & 3]));    // dS
-      }
+      for (int v = 0; v < 16; ++v)
+        sc[qb][v] = ex2(__builtin_fmaf(sc[qb][v], a.qk_scale, -ls[qb][v >> 2][v & 3]));
+    if (m0 < nstart + 32 * wave + 31 || m0 + kBN > seqlen) {
+      const int lo = n - m0 - 4 * hl, hi = seqlen - m0 - 4 * hl;
+#pragma unroll
+      for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const int off = qb * 32 + 8 * (v >> 2) + (v & 3);
+          sc[qb][v] = ((off >= lo) & (off < hi)) ? sc[qb][v] : 0.0f;
+        }
+    }
+#pragma unroll
+    for (int qb = 0; qb < 2; ++qb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v)   // dS
+        dc[qb][v] = __fmul_rn(sc[qb][v], __fsub_rn(dc[qb][v], ds[qb][v >> 2][v & 3]));
     // the 32 products of tile t + 1 spread among this work
 #pragma unroll
     for (int i = 0; i < 32; ++i) {
