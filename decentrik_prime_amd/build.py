@@ -32,7 +32,7 @@ FLAGS = [
 # per-file additions: the attention forward keeps its MFMA accumulators in VGPRs (in AGPRs, the
 # compiler's default at one wave per SIMD, it copied the output accumulator out and back on every
 # key tile); the backward kernels need more registers than VGPRs hold and keep the default
-EXTRA_FLAGS = {"attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
+EXTRA_FLAGS = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for f in ("attn_fwd.hip", "attn_dq.hip")}
 
 
 def sources():

@@ -27,22 +27,20 @@ __global__ __launch_bounds__(kAThreads) void attn_delta_kernel(const f16* __rest
 // dQ (solution/k_attn.py:142-182): one workgroup per (block of kBM queries, query head), key
 // tiles of kBN up to the diagonal, in the forward's four-stage K/V ring; the S^T and dP^T MFMAs of
 // tile t + 1 run beside the dS work of tile t
-__global__ __launch_bounds__(kAThreads) void attn_dq_kernel(AttnArgs a, const f16* __restrict__ dout,
-                                                            const float* __restrict__ lse,
-                                                            const float* __restrict__ delta,
-                                                            float* __restrict__ dq) {
+__device__ __forceinline__ void dq_block(const AttnArgs& a, int blk, int h,
+                                         const f16* __restrict__ dout,
+                                         const float* __restrict__ lse,
+                                         const float* __restrict__ delta, float* __restrict__ dq,
+                                         f16* Ks, f16* Vs) {
   int64_t s0;
   int seqlen, mstart;
-  if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
-  const int h = blockIdx.y;
+  if (!block_of(a, blk, &s0, &seqlen, &mstart)) return;
   const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(w);
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
   const int kvh = h / (a.nq / a.nkv);
   const int m = mstart + 32 * w + c;
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
-  __shared__ __attribute__((aligned(1024))) f16 Ks[kFwdStages * kTileHalves];
-  __shared__ __attribute__((aligned(1024))) f16 Vs[kFwdStages * kTileHalves];
 
   const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
   const int n_tiles = (hi + kBN - 1) / kBN;
@@ -198,24 +196,22 @@ __device__ __forceinline__ void dma4(const void* src, unsigned lds) {
 // and 1), and the S and dP MFMAs of tile t + 1 run beside the P / dS work of tile t.
 constexpr int kBwdStages = 4;
 
-__global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const f16* __restrict__ dout,
-                                                              const float* __restrict__ lse,
-                                                              const float* __restrict__ delta,
-                                                              float* __restrict__ dkp,
-                                                              float* __restrict__ dvp) {
+__device__ __forceinline__ void dkdv_block(const AttnArgs& a, int blk, int h,
+                                           const f16* __restrict__ dout,
+                                           const float* __restrict__ lse,
+                                           const float* __restrict__ delta,
+                                           float* __restrict__ dkp, float* __restrict__ dvp,
+                                           f16* Qs, f16* Ds, float (*lse_s)[kBN],
+                                           float (*dl_s)[kBN]) {
   int64_t s0;
   int seqlen, nstart;
-  if (!block_of(a, blockIdx.x, &s0, &seqlen, &nstart)) return;
-  const int h = blockIdx.y;
+  if (!block_of(a, blk, &s0, &seqlen, &nstart)) return;
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6, hl = lane >> 5, c = lane & 31;
   const int wave = __builtin_amdgcn_readfirstlane(w);
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD, OROW = (int64_t)a.nq * kHD;
   const int kvh = h / (a.nq / a.nkv);
   const int n = nstart + 32 * w + c;   // this lane's key
   const bool nval = n < seqlen && s0 + n < a.n_tokens;
-  __shared__ __attribute__((aligned(1024))) f16 Qs[kBwdStages * kTileHalves];
-  __shared__ __attribute__((aligned(1024))) f16 Ds[kBwdStages * kTileHalves];
-  __shared__ __attribute__((aligned(16))) float lse_s[kBwdStages][kBN], dl_s[kBwdStages][kBN];
 
   const int n_tiles = nstart < seqlen ? (seqlen - nstart + kBN - 1) / kBN : 0;
   const f16* qbase = a.qkv + s0 * ROW + (int64_t)h * kHD;
@@ -390,6 +386,32 @@ __global__ __launch_bounds__(kAThreads) void attn_dkdv_kernel(AttnArgs a, const 
   }
 }
 
+// dK/dV and dQ in one launch.  Workgroups [0, n_blocks * nq) run the dK/dV blocks in block-table
+// order, the rest the dQ blocks in reverse block-table order, each with every head of a block
+// before the next block.  The hardware deals workgroups to the 8 XCDs round-robin and each XCD
+// starts its own in index order, so with a table whose blocks are ordered by the rows from their
+// start to their sequence's end, longest first (the dK/dV walk; reversed, the dQ walk for sequences
+// of equal length), every XCD gets a balanced share, started longest first: the dQ blocks begin
+// on the CUs the dK/dV blocks leave idle and then on those that short blocks free.  Any table
+// order gives the same results.  Both read delta, which the launch before computes.
+__global__ __launch_bounds__(kAThreads) void attn_bwd_kernel(AttnArgs a, const f16* __restrict__ dout,
+                                                             const float* __restrict__ lse,
+                                                             const float* __restrict__ delta,
+                                                             float* __restrict__ dq,
+                                                             float* __restrict__ dkp,
+                                                             float* __restrict__ dvp, int n_blocks) {
+  static_assert(kBwdStages == kFwdStages, "dK/dV and dQ share the tile ring");
+  __shared__ __attribute__((aligned(1024))) f16 T0[kBwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(1024))) f16 T1[kBwdStages * kTileHalves];
+  __shared__ __attribute__((aligned(16))) float lse_s[kBwdStages][kBN], dl_s[kBwdStages][kBN];
+  const int per = n_blocks * a.nq;
+  const int g = blockIdx.x;
+  if (g < per)
+    dkdv_block(a, g / a.nq, g % a.nq, dout, lse, delta, dkp, dvp, T0, T1, lse_s, dl_s);
+  else
+    dq_block(a, n_blocks - 1 - (g - per) / a.nq, (g - per) % a.nq, dout, lse, delta, dq, T0, T1);
+}
+
 }  // namespace
 
 extern "C" int dk_attn_bwd(const void* qkv, const void* out, const float* lse, const void* dout,
@@ -401,6 +423,7 @@ extern "C" int dk_attn_bwd(const void* qkv, const void* out, const float* lse, c
     return e;
   if (n_blocks == 0 || n_tokens == 0) return 0;
   if (!out || !lse || !dout || !delta || !dq || !dkp || !dvp) return DK_ERR_INVALID;
+  if (2 * (int64_t)n_blocks * nq > INT32_MAX) return DK_ERR_INVALID;   // one workgroup index
   if (!dk_aligned(out, 16) || !dk_aligned(dout, 16) || !dk_aligned(lse, 4) ||
       !dk_aligned(delta, 4) || !dk_aligned(dq, 16) || !dk_aligned(dkp, 4) || !dk_aligned(dvp, 4))
     return DK_ERR_ALIGN;
@@ -408,11 +431,8 @@ extern "C" int dk_attn_bwd(const void* qkv, const void* out, const float* lse, c
   hipLaunchKernelGGL(attn_delta_kernel, dim3((unsigned)((pairs + 15) / 16)), dim3(kAThreads), 0,
                      stream, (const f16*)out, (const f16*)dout, delta, n_tokens, nq);
   DK_CHECK_LAUNCH();
-  hipLaunchKernelGGL(attn_dkdv_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
-                     stream, a, (const f16*)dout, lse, delta, dkp, dvp);
-  DK_CHECK_LAUNCH();
-  hipLaunchKernelGGL(attn_dq_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
-                     stream, a, (const f16*)dout, lse, delta, dq);
+  hipLaunchKernelGGL(attn_bwd_kernel, dim3((unsigned)(2 * n_blocks * nq)), dim3(kAThreads), 0,
+                     stream, a, (const f16*)dout, lse, delta, dq, dkp, dvp, n_blocks);
   DK_CHECK_LAUNCH();
   return 0;
 }

@@ -38,6 +38,17 @@ def block_table(lens, block):
     return tab
 
 
+def bwd_block_table(lens, block):
+    """``block_table``'s blocks ordered by the rows from a block's start to its sequence's end,
+    longest first (stable).  The backward launch runs its dK/dV blocks in table order and its dQ
+    blocks in reverse order, dealt to the XCDs round-robin, so this order starts the longest walks
+    first and gives every XCD a balanced share; any order gives the same results."""
+    tab = block_table(lens, block)
+    pairs = [(tab[i], tab[i + 1]) for i in range(0, len(tab), 2)]
+    pairs.sort(key=lambda p: -(int(lens[p[0]]) - p[1]))
+    return [v for p in pairs for v in p]
+
+
 class AttnMeta:
     """Per-batch tables (device int32 tensors) for the attention kernels
     (solution/k_attn.py:194-199)."""
@@ -53,7 +64,7 @@ def meta_for(lens, device):
     cu = [0]
     for n in lens:
         cu.append(cu[-1] + int(n))
-    tf, tb = block_table(lens, FWD_BLOCK_M), block_table(lens, BWD_BLOCK)
+    tf, tb = block_table(lens, FWD_BLOCK_M), bwd_block_table(lens, BWD_BLOCK)
     i32 = dict(dtype=torch.int32, device=device)
     return AttnMeta(torch.tensor(cu, **i32), torch.tensor(tf, **i32), torch.tensor(tb, **i32),
                     len(tf) // 2, len(tb) // 2, cu[-1])

@@ -86,3 +86,27 @@ def test_oracle_closed_forms():
     dq, dkp, dvp = attn.attention_bwd(qkv, dout, lens, NQ, NKV, HD)
     np.testing.assert_allclose(dvp[0], dout[0], rtol=0, atol=1e-12)   # P = 1 on token 0
     np.testing.assert_allclose(dq[0], 0, atol=1e-12)                   # softmax of one key
+
+
+def test_block_tables():
+    """block_table follows solution/k_attn.py:185-191 (sequence-major, 128-row starts); the
+    backward's table holds the same blocks, ordered by the rows from a block's start to its
+    sequence's end, longest first, ties in block_table order."""
+    from decentrik_prime_amd import k_attn
+    lens = [1, 37, 300, 129, 512, 200]
+    tab = k_attn.block_table(lens, 128)
+    want = [(s, st) for s, n in enumerate(lens) for st in range(0, n, 128)]
+    assert [(tab[i], tab[i + 1]) for i in range(0, len(tab), 2)] == want
+    bt = k_attn.bwd_block_table(lens, 128)
+    got = [(bt[i], bt[i + 1]) for i in range(0, len(bt), 2)]
+    assert sorted(got) == sorted(want)
+    rows = [lens[s] - st for s, st in got]
+    assert rows == sorted(rows, reverse=True)
+    # stable: equal walks keep block_table order
+    for a, b in zip(got, got[1:]):
+        if lens[a[0]] - a[1] == lens[b[0]] - b[1]:
+            assert want.index(a) < want.index(b)
+    # four sequences of 512: every sequence's first block, then every second block, ...
+    bt = k_attn.bwd_block_table([512] * 4, 128)
+    assert [(bt[i], bt[i + 1]) for i in range(0, len(bt), 2)] == \
+        [(s, st) for st in (0, 128, 256, 384) for s in range(4)]
