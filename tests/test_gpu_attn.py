@@ -79,3 +79,47 @@ def test_attention_argument_checks(torch):
     bad = k_attn.AttnMeta(meta.cu, meta.tab_fwd[:1], meta.tab_bwd, 1, meta.n_bwd, 12)
     with pytest.raises(ValueError):
         k_attn.attention_forward(qkv, bad, NQ, NKV, HD)               # table length
+
+
+def test_attention_rescale_and_table_order(torch):
+    """Scores that grow along the keys: every 64-key tile raises a row's maximum by about 16 in
+    log2 units, far past the 2^8 rescale threshold, so the forward rescales its output on every
+    tile, not only the first.  The backward gives the same bits with the sequence-major table as
+    with the longest-first one, and the same bits again when repeated."""
+    from decentrik_prime_amd import k_attn
+    from oracle import attn
+    lens = [300, 77, 512]
+    log(f"attention rescale path and table order, lens {lens}")
+    n = sum(lens)
+    rng = np.random.default_rng(7)
+    qkv = (rng.standard_normal((n, (NQ + 2 * NKV) * HD)) * 0.3).astype(np.float32)
+    pos = np.concatenate([np.arange(L) for L in lens]).astype(np.float32)
+    for kh in range(NKV):
+        qkv[:, (NQ + kh) * HD] = 0.25 * pos        # key component 0 grows with the position
+    for h in range(NQ):
+        qkv[:, h * HD] = 8.0                        # score += 2 * key position
+    qkv = qkv.astype(np.float16)
+    dout = rng.standard_normal((n, NQ * HD)).astype(np.float16)
+    meta = k_attn.meta_for(lens, "cuda")
+    seq_major = k_attn.AttnMeta(meta.cu, meta.tab_fwd,
+                                torch.tensor(k_attn.block_table(lens, k_attn.BWD_BLOCK),
+                                             dtype=torch.int32, device="cuda"),
+                                meta.n_fwd, meta.n_bwd, meta.n_tokens)
+    assert not torch.equal(seq_major.tab_bwd, meta.tab_bwd)
+    tq = torch.from_numpy(qkv).cuda()
+    td = torch.from_numpy(dout).cuda()
+    out, lse = k_attn.attention_forward(tq, meta, NQ, NKV, HD)
+    g1 = k_attn.attention_backward(tq, out, lse, td, meta, NQ, NKV, HD)
+    g2 = k_attn.attention_backward(tq, out, lse, td, seq_major, NQ, NKV, HD)
+    g3 = k_attn.attention_backward(tq, out, lse, td, meta, NQ, NKV, HD)
+    torch.cuda.synchronize()
+    for a, b, c, nm in zip(g1, g2, g3, ("dq", "dk", "dv")):
+        assert torch.equal(a, b), f"{nm}: table order changed the result"
+        assert torch.equal(a, c), f"{nm}: repeat changed the result"
+    o_ref, lse_ref = attn.attention_fwd(qkv, lens, NQ, NKV, HD)
+    _close(host(out), o_ref, 3e-3, 3e-3, "attention out")
+    _close(host(lse), lse_ref, 1e-5, 2e-3, "lse (log2 domain)")
+    dq_ref, dkp_ref, dvp_ref = attn.attention_bwd(qkv, dout, lens, NQ, NKV, HD, out=host(out))
+    _close(host(g1[0]), dq_ref, 3e-2, 2e-2, "dq")
+    _close(host(g1[1]), dkp_ref, 3e-2, 2e-2, "dk per query head")
+    _close(host(g1[2]), dvp_ref, 3e-2, 2e-2, "dv per query head")
