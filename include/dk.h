@@ -132,7 +132,10 @@ int dk_qkv_epilogue_bwd(const void* dq, const void* dk, const void* dv, int grad
  * [n_tokens, nq hd] fp16, lse [nq, n_tokens] fp32 = m + log2(l) per (head, token).
  * dk_attn_bwd replaces attention_backward (solution/k_attn.py:84-182, 215-245): delta
  * [nq, n_tokens] fp32 scratch, dq [n_tokens, nq hd] fp32, dkp / dvp [n_tokens, nq hd] fp32
- * per-query-head partials (dk_qkv_epilogue_bwd with gin = nq / nkv sums them). */
+ * per-query-head partials (dk_qkv_epilogue_bwd with gin = nq / nkv sums them).  Any order of
+ * the block table gives the same results; ordered by the rows from a block's start to its
+ * sequence's end, longest first (k_attn.bwd_block_table), the launch balances best.  Requires
+ * 2 n_blocks nq < 2^31 (DK_ERR_INVALID otherwise). */
 int dk_attn_fwd(const void* qkv, const int32_t* cu_seqlens, int32_t n_seq,
                 const int32_t* block_table, int32_t n_blocks, int64_t n_tokens, int32_t nq,
                 int32_t nkv, int32_t hd, void* out, float* lse, hipStream_t stream);
