@@ -539,15 +539,18 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   // flight: the stages are free for the per-wave epilogue scratch
 
   if (part) {
-    // split-K: this wave's fp32 partial blocks, lane-major (each register store is 256
-    // contiguous bytes); the reduce launch sums the splits and runs the epilogue
-    float* mine = part + (int64_t)wave * TM * TN * 1024 + lane;
+    // split-K: this wave's fp32 partial blocks; in a block, registers 4 q .. 4 q + 3 of lane l
+    // at 256 q + 4 l, so each 16-byte store instruction writes 1 KiB contiguous; the reduce
+    // launch sums the splits and runs the epilogue
+    float* mine = part + (int64_t)wave * TM * TN * 1024 + 4 * lane;
 #pragma unroll
     for (int i = 0; i < TM; ++i)
 #pragma unroll
       for (int j = 0; j < TN; ++j)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) mine[((i * TN + j) * 16 + v) * 64] = acc[i][j][v];
+        for (int q = 0; q < 4; ++q)
+          *reinterpret_cast<f32x4*>(mine + (i * TN + j) * 1024 + 256 * q) =
+              f32x4{acc[i][j][4 * q], acc[i][j][4 * q + 1], acc[i][j][4 * q + 2], acc[i][j][4 * q + 3]};
     return;
   }
   // the epilogue scratch: 16 KB per wave, waves 0-3 in the A stages, 4-7 in the W stages
@@ -630,21 +633,24 @@ __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
   const int64_t n0 = (int64_t)(tile / p.tiles_m) * kTile + (wave % 4) * 64 + 32 * j;
   if (m0 >= p.M) return;
   const float* src = p.part + (int64_t)tile * p.splits * kTile * kTile +
-                     (wave * TM * TN + i * TN + j) * 1024 + lane;
+                     (wave * TM * TN + i * TN + j) * 1024 + 4 * lane;
   f32x16 acc[1][1];
-  float v_all[4][16];
-  // four splits' loads in flight at a time, then their sum in split order
+  f32x4 v_all[4][4];
+  // four splits' loads in flight at a time (clamped, straight-line), then their sum in split order
   for (int sp = 0; sp < p.splits; sp += 4) {
 #pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int s = sp + u < p.splits ? sp + u : p.splits - 1;
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        v_all[u][q] = *reinterpret_cast<const f32x4*>(src + (int64_t)s * kTile * kTile + 256 * q);
+    }
+#pragma unroll
     for (int u = 0; u < 4; ++u)
       if (sp + u < p.splits)
 #pragma unroll
-        for (int v = 0; v < 16; ++v) v_all[u][v] = src[(int64_t)(sp + u) * kTile * kTile + v * 64];
-#pragma unroll
-    for (int u = 0; u < 4; ++u)
-      if (sp + u < p.splits)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) acc[0][0][v] = sp + u == 0 ? v_all[u][v] : acc[0][0][v] + v_all[u][v];
+        for (int v = 0; v < 16; ++v)
+          acc[0][0][v] = sp + u == 0 ? v_all[u][v >> 2][v & 3] : acc[0][0][v] + v_all[u][v >> 2][v & 3];
   }
   wave_epilogue<TRANS, EPI, 1, 1>(p, acc, m0, n0, escr, escr);   // never rotary: no split-K
 }
