@@ -140,91 +140,102 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) res[j][v] = (float)dk_h(__fadd_rn(acc[i][j][v], bias[j]));
-      // LoRA terms, one at a time.  Every global load a term needs in this strip (the z rows, the
-      // B rows or A columns of each block, the keep-mask bytes) is issued before the first is
-      // used, so a term costs one memory round trip rather than one per block and operand.
-      const int64_t zm = mrow0 + lrow;
-      for (int t = 0; t < p.n_lora; ++t) {
-        const LoraTerm& L = p.lora[t];
-        bool on[TN];
+      // LoRA terms (at most two), in batches of TB: both at once for a single strip per wave
+      // (128 x 128 tiles, registers to spare), one at a time otherwise.  Every global load a batch
+      // needs in this strip (the z rows, the B rows or A columns of each block, the keep-mask
+      // bytes) is issued, at rows clamped to M (rows past M are never stored), before the first
+      // is used: one memory round trip per batch and 16 ranks.  The terms are added to the result
+      // in order, as separate roundings.
+      constexpr int TB = TM == 1 ? 2 : 1;
+      const int64_t zm = mrow0 + lrow < M ? mrow0 + lrow : M - 1;
+      for (int t0 = 0; t0 < p.n_lora; t0 += TB) {
+        bool on[TB][TN], masked[TB];
+        f32x16 lo[TB][TN];
+        u32x4 mw[TB][TN];
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          on[j] = TRANS || (nw0 + 32 * j >= L.n_begin && nw0 + 32 * j < L.n_end);
-        f32x16 lo[TN];
+        for (int b = 0; b < TB; ++b) {
+          const LoraTerm& L = p.lora[t0 + b < 2 ? t0 + b : 1];
+          const bool live = t0 + b < p.n_lora;
+          masked[b] = TRANS && live && L.mask;
 #pragma unroll
-        for (int j = 0; j < TN; ++j)
+          for (int j = 0; j < TN; ++j) {
+            on[b][j] = live && (TRANS || (nw0 + 32 * j >= L.n_begin && nw0 + 32 * j < L.n_end));
 #pragma unroll
-          for (int v = 0; v < 16; ++v) lo[j][v] = 0.0f;
-        u32x4 mw[TN];
-        const bool masked = TRANS && L.mask;
-        if (masked) {
-          // the blocks' 32 x 32 keep-mask bytes: one 16-byte load per lane and block
-          const int64_t mr = mrow0 + (lane >> 1);
+            for (int v = 0; v < 16; ++v) lo[b][j][v] = 0.0f;
+          }
+          if (masked[b]) {
+            // the blocks' 32 x 32 keep-mask bytes: one 16-byte load per lane and block
+            const int64_t mr = mrow0 + (lane >> 1) < M ? mrow0 + (lane >> 1) : M - 1;
 #pragma unroll
-          for (int j = 0; j < TN; ++j)
-            mw[j] = mr < M ? *reinterpret_cast<const u32x4*>(L.mask + mr * N + nw0 + 32 * j +
-                                                              16 * (lane & 1))
-                           : u32x4{0u, 0u, 0u, 0u};
+            for (int j = 0; j < TN; ++j)
+              mw[b][j] = *reinterpret_cast<const u32x4*>(L.mask + mr * N + nw0 + 32 * j +
+                                                          16 * (lane & 1));
+          }
         }
         for (int rc = 0; rc < p.rank; rc += 16) {
-          f16x8 zf, rr[TN];
-          if (zm < M) {
-            zf = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
-          } else {
+          f16x8 zf[TB], rr[TB][TN];
 #pragma unroll
-            for (int e = 0; e < 8; ++e) zf[e] = (f16)0.0f;
-          }
+          for (int b = 0; b < TB; ++b) {
+            if (t0 + b >= p.n_lora) continue;
+            const LoraTerm& L = p.lora[t0 + b];
+            zf[b] = *reinterpret_cast<const f16x8*>(L.z + zm * p.rank + rc + lk8);
 #pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            if (!on[j]) continue;
-            if (!TRANS)   // B row of this lane's column, ranks rc + lk8 ..
-              rr[j] = *reinterpret_cast<const f16x8*>(L.r + (nw0 + 32 * j + lrow - L.n_begin) * p.rank +
-                                                     rc + lk8);
-            else          // A[rc + lane / 4][8 columns of the block]
-              rr[j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N + nw0 +
-                                                     32 * j + 8 * (lane & 3));
-          }
-#pragma unroll
-          for (int j = 0; j < TN; ++j) {
-            if (!on[j]) continue;
-            f16x8 rf = rr[j];
-            if (TRANS) {
-              // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
-              // rank-contiguous with transposing reads
-              __builtin_amdgcn_wave_barrier();
-              *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr[j];
-              __builtin_amdgcn_wave_barrier();
-              const f16* base = ascr + tr_k * 48 + tr_n;
-              const f16x4 lo4 = read_tr(base), hi4 = read_tr(base + 4 * 48);
-              rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-              __builtin_amdgcn_wave_barrier();
+            for (int j = 0; j < TN; ++j) {
+              if (!on[b][j]) continue;
+              if (!TRANS)   // B row of this lane's column, ranks rc + lk8 ..
+                rr[b][j] = *reinterpret_cast<const f16x8*>(
+                    L.r + (nw0 + 32 * j + lrow - L.n_begin) * p.rank + rc + lk8);
+              else          // A[rc + lane / 4][8 columns of the block]
+                rr[b][j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N +
+                                                          nw0 + 32 * j + 8 * (lane & 3));
             }
-            lo[j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf, rf, lo[j], 0, 0, 0);
           }
+#pragma unroll
+          for (int b = 0; b < TB; ++b)
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+              if (!on[b][j]) continue;
+              f16x8 rf = rr[b][j];
+              if (TRANS) {
+                // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
+                // rank-contiguous with transposing reads
+                __builtin_amdgcn_wave_barrier();
+                *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr[b][j];
+                __builtin_amdgcn_wave_barrier();
+                const f16* base = ascr + tr_k * 48 + tr_n;
+                const f16x4 lo4 = read_tr(base), hi4 = read_tr(base + 4 * 48);
+                rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
+                __builtin_amdgcn_wave_barrier();
+              }
+              lo[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf[b], rf, lo[b][j], 0, 0, 0);
+            }
         }
 #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          if (!on[j]) continue;
-          if (masked) {
-            // staged in LDS (rows of 48 bytes), then read per element
-            __builtin_amdgcn_wave_barrier();
-            *reinterpret_cast<u32x4*>(mscr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw[j];
-            __builtin_amdgcn_wave_barrier();
+        for (int b = 0; b < TB; ++b)
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const int mloc = 8 * (v >> 2) + rsub + (v & 3);
-              const float lf = (float)dk_h(lo[j][v]);
-              res[j][v] = __fadd_rn(res[j][v], mscr[mloc * 48 + lrow] ? __fmul_rn(lf, L.scale) : 0.0f);
-            }
-            __builtin_amdgcn_wave_barrier();
-          } else {
+          for (int j = 0; j < TN; ++j) {
+            if (!on[b][j]) continue;
+            const float sc = p.lora[t0 + b].scale;
+            if (masked[b]) {
+              // staged in LDS (rows of 48 bytes), then read per element
+              __builtin_amdgcn_wave_barrier();
+              *reinterpret_cast<u32x4*>(mscr + (lane >> 1) * 48 + 16 * (lane & 1)) = mw[b][j];
+              __builtin_amdgcn_wave_barrier();
 #pragma unroll
-            for (int v = 0; v < 16; ++v) {
-              const float lf = (float)dk_h(lo[j][v]);
-              res[j][v] = __fadd_rn(res[j][v], TRANS ? lf : __fmul_rn(L.scale, lf));
+              for (int v = 0; v < 16; ++v) {
+                const int mloc = 8 * (v >> 2) + rsub + (v & 3);
+                const float lf = (float)dk_h(lo[b][j][v]);
+                res[j][v] = __fadd_rn(res[j][v], mscr[mloc * 48 + lrow] ? __fmul_rn(lf, sc) : 0.0f);
+              }
+              __builtin_amdgcn_wave_barrier();
+            } else {
+#pragma unroll
+              for (int v = 0; v < 16; ++v) {
+                const float lf = (float)dk_h(lo[b][j][v]);
+                res[j][v] = __fadd_rn(res[j][v], TRANS ? lf : __fmul_rn(sc, lf));
+              }
             }
           }
-        }
       }
       // rotary embedding (solution/k_rope.py:23-61): this wave's 64 columns are one half of a
       // head, the partner wave (whose scratch is pscr) holds the other half of the same rows;
