@@ -95,6 +95,7 @@ SIGNATURES = {
                                         _c_p, _i64, _c_p]),
     "dk_w4_linear_workspace": (_i64, [_i64, _W, _int]),
     "dk_w4_workspace": (_i64, [_i64, _W, _int]),
+    "dk_set_w4_gemm_mode": (_int, [_int]),
     "dk_h16_workspace": (_i64, [_i64, _i64, _i64, _int]),
     "dk_h16_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
                                       _c_p, _i64, _c_p, _i64, _S, _c_p]),

@@ -61,7 +61,9 @@ struct GemmParams {
 // CUs.  p.side's workgroups (if any) join the launch.  Returns kHgemmDeclined without launching
 // anything otherwise, a HIP error code, or 0.
 constexpr int kHgemmDeclined = -1000;
-template <bool TRANS, int EPI>
+// W4: the weight read as packed NF4 (p.packed, p.qabs, p.scale2, p.offset2, p.code2, p.nf4; no
+// p.w16) and dequantised by each workgroup into LDS, bit-identical to the fp16 form's results.
+template <bool TRANS, int EPI, bool W4 = false>
 int hgemm_launch(const GemmParams& p, void* ws, int64_t ws_bytes, hipStream_t stream);
 int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi);
 

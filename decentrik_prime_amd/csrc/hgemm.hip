@@ -381,9 +381,10 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
 
 // NST: LDS stages of this tile shape in the kernel's 2 x 64 KB (256 x 256: 2, 128 x 128: 4, so
 // the smaller tiles, whose steps are a quarter as long, still load three steps ahead).
-template <bool TRANS, int EPI, int BM, int BN, int WAVES_M, int NST>
+template <bool TRANS, int EPI, int BM, int BN, int WAVES_M, int NST, bool W4>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64_t n0, int kt0,
-                                          int nk, float* part, f16* As, f16* Bs) {
+                                          int nk, float* part, f16* As, f16* Bs,
+                                          const float* w4tab) {
   constexpr int SA = BM * kBK, SB = BN * kBK;   // halves per stage of A and of W
   static_assert(NST * SA <= kStages * kStageHalves && NST * SB <= kStages * kStageHalves &&
                 (NST & (NST - 1)) == 0 && NST >= 2, "LDS stages");
@@ -392,7 +393,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   constexpr int TM = WM / 32, TN = WN / 32;
   constexpr int LA = BM * 8 / kThreads;     // A chunks per lane per stage
   constexpr int LB = BN * 8 / kThreads;     // W chunks per lane per stage
-  constexpr int LOADS = LA + LB;            // DMA instructions per lane per stage
+  constexpr int LOADS = W4 ? LA : LA + LB;  // DMA instructions per lane per stage (W4: A only)
   constexpr int NCH = BN / 8;               // NN: 16-byte chunks per W-tile row
   static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile shape");
   static_assert(EPI != EPI_SWIGLU_FWD || (TN == 2 && !TRANS), "SwiGLU forward needs WN = 64");
@@ -439,6 +440,79 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
           lds_offset(Bs + st * SB + (j * 8 + wave) * 512));
       dma16(b_src[j] + (TRANS ? (int64_t)kt * kBK * N : (int64_t)kt * kBK), dst);
     }
+  };
+
+  // ---- W4: the W tile of every step dequantised from packed NF4 by the workgroup itself (no fp16
+  // weight in memory).  Each thread converts PW consecutive weights of one W row per step: NT,
+  // tile row tid / (64 / PW) at k offset PW (tid % (64 / PW)); NN, tile k-row tid / (BN / PW) at
+  // column offset PW (tid % (BN / PW)).  PW divides a 64-weight first-level block, so one absmax
+  // per piece.  Step j's packed bytes, code and second-level scale/offset are loaded during step
+  // j - NST - 1, converted beside step j - NST's first sub-steps and written to stage j % NST
+  // after step j - NST's barrier, where the A refill of the same stage goes out.
+  constexpr int PW = BN * kBK / kThreads;   // 32 (256-wide tiles) or 16 (128-wide)
+  static_assert(!W4 || PW == 32 || PW == 16, "W4 pieces");
+  constexpr int PWD = PW / 8;               // packed dwords per piece = 16-byte LDS chunks
+  int64_t w4_e0 = 0;                        // the piece's first element at step 0
+  int w4_lds = 0;                           // its LDS offset (halves) in a stage, chunk 0
+  int w4_swz = 0;
+  if constexpr (W4) {
+    if (!TRANS) {
+      constexpr int PPR = kBK / PW;
+      const int row = tid / PPR, pc = tid % PPR;
+      int64_t n = n0 + row;
+      if (EPI == EPI_SWIGLU_FWD) {
+        const int64_t g = n >> 6, w = n & 63;
+        n = w < 32 ? g * 32 + w : p.inter + g * 32 + (w - 32);
+      }
+      w4_e0 = n * K + (int64_t)kt0 * kBK + pc * PW;
+      w4_lds = row * kBK;
+      w4_swz = swz_k(row);
+      w4_lds |= (pc * PWD) << 16;            // first chunk index, kept in the high half
+    } else {
+      constexpr int PPR = BN / PW;
+      const int k = tid / PPR, pc = tid % PPR;
+      w4_e0 = ((int64_t)kt0 * kBK + k) * N + n0 + pc * PW;
+      w4_lds = k * BN;
+      w4_swz = swz_n(k);
+      w4_lds |= (pc * PWD) << 16;
+    }
+  }
+  struct W4Piece {
+    uint32_t w[PWD];
+    uint32_t qa;
+    float s2, o2;
+  };
+  auto w4_load = [&](int kt) {
+    W4Piece r;
+    const int64_t e = w4_e0 + (TRANS ? (int64_t)kt * kBK * N : (int64_t)kt * kBK);
+    if constexpr (PWD == 4) {
+      const u32x4 v = *reinterpret_cast<const u32x4*>(p.packed + (e >> 1));
+#pragma unroll
+      for (int i = 0; i < 4; ++i) r.w[i] = v[i];
+    } else {
+      const u32x2 v = *reinterpret_cast<const u32x2*>(p.packed + (e >> 1));
+#pragma unroll
+      for (int i = 0; i < PWD; ++i) r.w[i] = v[i];
+    }
+    r.qa = p.qabs[e >> 6];
+    r.s2 = p.scale2[e >> 14];
+    r.o2 = p.offset2[e >> 14];
+    return r;
+  };
+  u32x4 w4_out[PWD];   // the converted piece: PWD chunks of 8 fp16
+  auto w4_convert = [&](const W4Piece& r) {
+    const float* lut = w4tab;
+    const float* c2 = w4tab + 16;
+    const float amax = dk_absmax(c2[r.qa & 0xffu], r.s2, r.o2);
+#pragma unroll
+    for (int i = 0; i < PWD; ++i) w4_out[i] = dk_dequant_word(r.w[i], amax, lut);
+  };
+  auto w4_write = [&](int st) {
+    const int c0 = w4_lds >> 16;
+#pragma unroll
+    for (int i = 0; i < PWD; ++i)
+      *reinterpret_cast<u32x4*>(Bs + st * SB + (w4_lds & 0xffff) + (((c0 + i) ^ w4_swz) * 8)) =
+          w4_out[i];
   };
 
   // ---- MFMA operands
@@ -509,33 +583,61 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     else if (later >= 1) wait_vmem<LOADS>();
     else wait_vmem<0>();
   };
+  // W4, before a step's barrier: every A refill issued so far has landed; only the packed loads
+  // of the current step (the 4 newest vector-memory instructions, issued after them) may still
+  // be in flight
+  constexpr int kW4Loads = 4;
 
   // ---- main loop.  Step kt lives in stage kt % NST.  In step kt: each sub-step's MFMAs run
   // beside the operand reads of the next; before the last sub-step, wait for this wave's loads of
   // step kt + 1 and for every wave's last read of stage kt % NST (one barrier), then refill that
   // stage with step kt + NST, spreading the DMA instructions between the last sub-step's MFMAs,
   // which run beside the first reads of step kt + 1.
+  W4Piece w4_next;   // W4: the packed piece of step kt + NST (loaded one step before its use)
+  if constexpr (W4) {
+    // the first NST steps' W tiles converted and written before the loop (their loads waited at
+    // once: a prologue)
+#pragma unroll
+    for (int q = 0; q < NST; ++q)
+      if (q < nk) {
+        w4_convert(w4_load(q));
+        w4_write(q);
+      }
+    w4_next = w4_load(NST < nk ? NST : nk - 1);   // clamped: its result is then never written
+  }
 #pragma unroll
   for (int q = 0; q < NST; ++q)
     if (q < nk)
 #pragma unroll
       for (int d = 0; d < LOADS; ++d) issue(q, q, d);
-  wait_loads((nk < NST ? nk : NST) - 1);
+  if (W4) wait_vmem<0>();
+  else wait_loads((nk < NST ? nk : NST) - 1);
   __syncthreads();
   read_frags(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
     const int st = kt & (NST - 1);
+    W4Piece w4_after;
+    if constexpr (W4) {
+      // step kt + NST + 1's packed piece (clamped at the end: loaded, never written)
+      w4_after = w4_load(kt + NST + 1 < nk ? kt + NST + 1 : nk - 1);
+    }
 #pragma unroll
     for (int j = 0; j < 3; ++j) {
       read_frags(st, j + 1, (j + 1) & 1);
+      if (W4 && j == 0) w4_convert(w4_next);   // step kt + NST's W tile, beside the MFMAs
       mfmas(j & 1);
       interleave();
     }
     // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
-    wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
+    if (W4) wait_vmem<kW4Loads>();
+    else wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
     __syncthreads();
     if (kt + 1 < nk) read_frags((kt + 1) & (NST - 1), 0, 0);
     const bool refill = kt + NST < nk;
+    if constexpr (W4) {
+      if (refill) w4_write(st);
+      w4_next = w4_after;
+    }
 #pragma unroll
     for (int q = 0; q < TM * TN; ++q) {   // sub-step 3 (buffer 1)
       acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
@@ -579,11 +681,13 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 // are numbered M-fastest.  The p.sums.wgs workgroups after the tiles (NN LINEAR) run the LoRA
 // column sums the launch carries, the p.side.wgs after those its dequant work; dispatched last,
 // they take the CUs the tiles leave idle.
-template <bool TRANS, int EPI>
+template <bool TRANS, int EPI, bool W4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   __shared__ __attribute__((aligned(1024))) f16 As[kStages * kStageHalves];
   __shared__ __attribute__((aligned(1024))) f16 Bs[kStages * kStageHalves];
+  // W4: the 16 NF4 values and the 256-entry second-level code table
+  __shared__ float w4tab[W4 ? 16 + 256 : 1];
   static_assert(side_dequant_lds <= kStages * kStageHalves * 2 && kSideThreads == kThreads,
                 "side dequant in the kernel's LDS");
   static_assert(colsum_lds_bytes<16>() <= kStages * kStageHalves * 2 && kSumThreads == kThreads,
@@ -603,6 +707,11 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     return;
   }
   const int nk_all = (int)(p.K / kBK);
+  if constexpr (W4) {
+    if (threadIdx.x < 16) w4tab[threadIdx.x] = p.nf4[threadIdx.x];
+    if (threadIdx.x < 256) w4tab[16 + threadIdx.x] = p.code2[threadIdx.x];
+    __syncthreads();
+  }
   int b = blockIdx.x;
   if (b < main_tiles) {
     // workgroups are dealt to the 8 XCDs round-robin: give each XCD a contiguous run of tiles
@@ -617,7 +726,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     const int nk = (int)((int64_t)nk_all * (split + 1) / p.splits) - kt0;
     float* part =
         p.splits > 1 ? p.part + ((int64_t)tile * p.splits + split) * kTile * kTile : nullptr;
-    gemm_tile<TRANS, EPI, 256, 256, 2, 2>(p, m0, n0, kt0, nk, part, As, Bs);
+    gemm_tile<TRANS, EPI, 256, 256, 2, 2, W4>(p, m0, n0, kt0, nk, part, As, Bs, w4tab);
   } else {
     int t = b - main_tiles;
     if ((tail_wgs & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
@@ -625,7 +734,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     const int64_t m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
     const int64_t n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
     if (m0 >= p.M) return;
-    gemm_tile<TRANS, EPI, 128, 128, 4, 4>(p, m0, n0, 0, nk_all, nullptr, As, Bs);
+    gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk_all, nullptr, As, Bs, w4tab);
   }
 }
 
@@ -745,9 +854,13 @@ static bool vector_outputs_ok(const GemmParams& p, int epi) {
   return dk_aligned(p.gu, 16) && p.inter % 8 == 0;
 }
 
-template <bool TRANS, int EPI>
+template <bool TRANS, int EPI, bool W4>
 int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (!p0.w16 || !vector_outputs_ok(p0, EPI)) return kHgemmDeclined;
+  if (!(W4 ? p0.packed && p0.qabs && p0.scale2 && p0.offset2 && p0.code2 && p0.nf4 &&
+                 dk_aligned(p0.packed, 16)
+           : p0.w16 != nullptr) ||
+      !vector_outputs_ok(p0, EPI))
+    return kHgemmDeclined;
   // the rotary epilogue pairs the two column halves of a head inside one workgroup: no split-K,
   // and 128-column tiles at any size
   const bool rope = p0.rope_pos != nullptr;
@@ -778,7 +891,7 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   // carried LoRA column sums (NN LINEAR only; the caller sets p.sums.wgs)
   const int sums = TRANS && EPI == EPI_LINEAR ? p.sums.wgs : 0;
   p.sums.wgs = sums;
-  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI>),
+  hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI, W4>),
                      dim3((unsigned)(h.main_wgs + h.tail_wgs + sums + side)),
                      dim3(kThreads), 0, stream, p, (int)h.main_wgs, (int)h.tail_wgs);
   DK_CHECK_LAUNCH();
@@ -792,9 +905,13 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   return 0;
 }
 
-template int hgemm_launch<false, EPI_LINEAR>(const GemmParams&, void*, int64_t, hipStream_t);
-template int hgemm_launch<true, EPI_LINEAR>(const GemmParams&, void*, int64_t, hipStream_t);
-template int hgemm_launch<false, EPI_SWIGLU_FWD>(const GemmParams&, void*, int64_t, hipStream_t);
-template int hgemm_launch<true, EPI_SWIGLU_BWD>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<false, EPI_LINEAR, false>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_LINEAR, false>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<false, EPI_SWIGLU_FWD, false>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_SWIGLU_BWD, false>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<false, EPI_LINEAR, true>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_LINEAR, true>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<false, EPI_SWIGLU_FWD, true>(const GemmParams&, void*, int64_t, hipStream_t);
+template int hgemm_launch<true, EPI_SWIGLU_BWD, true>(const GemmParams&, void*, int64_t, hipStream_t);
 
 }  // namespace dk

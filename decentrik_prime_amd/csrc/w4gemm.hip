@@ -30,6 +30,7 @@
 // Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
 // (the REDUCE instance: consumer waves only, no LDS) sums them in split order and runs the
 // epilogue.
+#include <atomic>
 #include <mutex>
 
 #include "gemm_common.h"
@@ -617,11 +618,16 @@ int64_t plan_workspace(const Plan& pl) {
 }
 
 // Workspace of one GEMM: [split-K partial tiles | fp16 weight (two-phase)].
+// Workspace of an NF4-reading GEMM: room for whichever path dispatch takes, the 256-tile kernel's
+// split-K partials (reading NF4 itself), or the 128 x 128 kernel's partials with the fp16 weight
+// after them (two-phase shapes).
 int64_t gemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
   if (M <= 0) return 0;
   const int64_t part = plan_workspace(plan_for(M, N, K, epi));
   const int64_t w16 = two_phase(M, N) ? N * K * (int64_t)sizeof(f16) : 0;
-  return w16 ? round256(part) + w16 : part;
+  const int64_t own = w16 ? round256(part) + w16 : part;
+  const int64_t tile = hgemm_workspace(M, N, K, epi);
+  return own > tile ? own : tile;
 }
 
 template <int BM, int BN, bool TRANS, int EPI, bool F16B>
@@ -663,8 +669,22 @@ int launch_plan(const Plan& pl, GemmParams p, hipStream_t stream) {
 // Runs the plan.  Without a workspace: one phase (W dequantised in LDS), no split-K.  With one
 // (at least gemm_workspace bytes): split-K partials and, on the two-phase shapes, the weight
 // dequantised to fp16 in the workspace first (both launches on `stream`, in order).
+// dk_set_w4_gemm_mode: 0 the fused 256-tile path where it is fastest (split-K plans), 1 wherever
+// its plan takes the shape, 2 never (process-wide)
+std::atomic<int> g_w4_tile_mode{0};
+
 template <bool TRANS, int EPI>
 int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, hipStream_t stream) {
+  if (ws && ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI)) return DK_ERR_WORKSPACE;
+  // the 256-tile kernel with the weight dequantised in LDS (W4) where its plan splits K (few
+  // output tiles, long K): there it beats the separate dequant + fp16 GEMM (gate|up dX at
+  // M = 2048: 179 against 188 us); elsewhere its per-step conversion costs more than the
+  // dequant launch saves (measured on every config-4 shape), and the paths below run
+  const int mode = g_w4_tile_mode.load(std::memory_order_relaxed);
+  if (mode == 1 || (mode == 0 && ws && hgemm_workspace(p.M, p.N, p.K, EPI) > 0)) {
+    const int r = hgemm_launch<TRANS, EPI, true>(p, ws, ws_bytes, stream);
+    if (r != kHgemmDeclined) return r;
+  }
   Plan pl = plan_for(p.M, p.N, p.K, EPI);
   if (ws == nullptr) {
     pl.splits = 1;
@@ -913,6 +933,12 @@ int dispatch_w4(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes
 }
 
 }  // namespace
+
+extern "C" int dk_set_w4_gemm_mode(int mode) {
+  if (mode < 0 || mode > 2) return DK_ERR_INVALID;
+  g_w4_tile_mode.store(mode, std::memory_order_relaxed);
+  return 0;
+}
 
 extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
                                      const dk_nf4_weight* w, const void* bias,

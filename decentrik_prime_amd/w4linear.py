@@ -82,6 +82,12 @@ _WS = {}
 _WS_LOCK = threading.Lock()
 
 
+def set_w4_gemm_mode(mode):
+    """Which kernel the NF4-reading GEMMs run (dk_set_w4_gemm_mode): 0 the 256-tile kernel reading
+    NF4 where its plan splits K (default), 1 wherever its plan takes the shape, 2 never."""
+    _lib.check(_lib.lib().dk_set_w4_gemm_mode(int(mode)), "dk_set_w4_gemm_mode")
+
+
 def _workspace(w, m, op, device):
     """Scratch of a fused NF4 GEMM (split-K partials and the two-phase fp16 weight; None when the
     shape needs none): one buffer per (device, stream), grown on demand.  Kernels on one stream

@@ -8,7 +8,8 @@
  *     dimension is given;
  *   - return 0 on success, a negative DK_ERR_* for an argument error detected before any launch,
  *     or a positive hipError_t from the launch;
- *   - no mutable global state: entry points may be called from any host thread.
+ *   - no mutable global state but the NF4 GEMM mode of dk_set_w4_gemm_mode (an atomic setting
+ *     each call reads once): entry points may be called from any host thread.
  */
 #ifndef DK_H
 #define DK_H
@@ -229,6 +230,15 @@ int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const dk_nf4_we
 #define DK_OP_GATEUP_SWIGLU_FWD 2  /* dk_w4_gateup_swiglu_fwd */
 #define DK_OP_DOWN_SWIGLU_BWD 3    /* dk_w4_down_swiglu_bwd */
 int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op);
+
+/* Which kernel the dk_w4_* GEMMs run (no counterpart in the reference: its GEMMs read a
+ * dequantised workspace).  The 256 x 256-tile kernel can read the packed NF4 weight itself,
+ * each workgroup dequantising its W tiles into LDS (bit-identical to the fp16-weight form), or
+ * the weight is first dequantised into the workspace and read as fp16, or the 128 x 128
+ * warp-specialised kernel dequantises in LDS.  mode 0 (default): the tile kernel reads NF4
+ * where its plan splits K (few output tiles, long K), where that is fastest; 1: wherever its
+ * plan takes the shape; 2: never.  Process-wide; DK_ERR_INVALID for another mode. */
+int dk_set_w4_gemm_mode(int mode);
 
 /* dk_w4_workspace(m, w, backward ? DK_OP_LINEAR_BWD_DX : DK_OP_LINEAR_FWD). */
 int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward);

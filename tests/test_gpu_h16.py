@@ -162,6 +162,65 @@ def test_h16_mlp(torch, m):
 
 
 @pytest.mark.parametrize("m", [2048, 1000])
+def test_w4_tile_kernel_reads_nf4(torch, m):
+    """dk_set_w4_gemm_mode(1): every NF4-reading GEMM whose shape the 256-tile plan takes runs on
+    that kernel with its workgroups dequantising the W tiles into LDS (256 x 256 tiles, the
+    128 x 128 quarters, split K; NT and NN; linear with LoRA terms and bias, the SwiGLU forward
+    and backward), and must give the same bits as the fp16-weight form, which runs the same plan
+    on the GPU-dequantised weight."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    log(f"W4 tile kernel vs fp16 form, M={m}")
+    D, KV, I = 1536, 256, 8960
+    rng = np.random.default_rng(41)
+    w_qkv = to_w4(nf4_weight(D + 2 * KV, D, seed=211))
+    w_o = to_w4(nf4_weight(D, D, seed=212))
+    w_gu = to_w4(nf4_weight(2 * I, D, seed=213))
+    w_d = to_w4(nf4_weight(D, I, seed=214))
+    h = {k: w.dequantize() for k, w in (("qkv", w_qkv), ("o", w_o), ("gu", w_gu), ("d", w_d))}
+    x, aq, bq, mq, _ = lora_inputs(m, D, D, seed=42)
+    _, av, bv, mv, _ = lora_inputs(m, D, KV, seed=43)
+    ks = linear.keep_scale(0.05)
+    bias = cuda16((rng.standard_normal(D + 2 * KV) * 0.1).astype(F16))
+    tx = cuda16(x)
+    tzq = w4linear.lora_down(tx, cuda16(aq), cuda(mq), ks)
+    tzv = w4linear.lora_down(tx, cuda16(av), cuda(mv), ks)
+    fterms = [(tzq, cuda16(bq), 0, D, 2.0), (tzv, cuda16(bv), D + KV, D + 2 * KV, 2.0)]
+    dqkv = cuda16((rng.standard_normal((m, D + 2 * KV)) * 1e-2).astype(F16))
+    dzq = (torch.randn(m, 16, device="cuda") * 1e-2).half()
+    dzv = (torch.randn(m, 16, device="cuda") * 1e-2).half()
+    bterms = [(dzq, cuda16(aq), cuda(mq), ks), (dzv, cuda16(av), cuda(mv), ks)]
+    dy_o = cuda16((rng.standard_normal((m, D)) * 1e-2).astype(F16))
+    dh = cuda16((rng.standard_normal((m, D)) * 1e-2).astype(F16))
+
+    def run(nf4):
+        pick = (lambda k: None) if nf4 else (lambda k: h[k])   # noqa: E731
+        out = {}
+        out["qkv"] = w4linear.linear_forward_lora(tx, w_qkv, bias, fterms, w16=pick("qkv"))
+        out["o"] = w4linear.linear_forward(tx, w_o, w16=pick("o"))
+        out["act"], gu = w4linear.gateup_swiglu_forward(tx, w_gu, w16=pick("gu"))
+        out["gu"] = gu.clone()
+        out["down"] = w4linear.linear_forward(out["act"], w_d, w16=pick("d"))
+        w4linear.down_swiglu_backward(dh, w_d, gu, w16=pick("d"))
+        out["dgu"] = gu
+        out["dx_gu"] = w4linear.linear_backward_dx(gu, w_gu, out_dtype=torch.float16,
+                                                   w16=pick("gu"))
+        out["dx_o"] = w4linear.linear_backward_dx(dy_o, w_o, w16=pick("o"))
+        out["dx_qkv"] = w4linear.linear_backward_dx_lora(dqkv, w_qkv, bterms, w16=pick("qkv"))
+        return out
+
+    want = run(False)
+    w4linear.set_w4_gemm_mode(1)
+    try:
+        got = run(True)
+        torch.cuda.synchronize()
+    finally:
+        w4linear.set_w4_gemm_mode(0)
+    for k in want:
+        _same(got[k], want[k], f"{k}: W4 tile kernel vs fp16 form")
+
+
+@pytest.mark.parametrize("m", [2048, 1000])
 def test_split_k(torch, m):
     """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
     second launch that runs the epilogue): the down forward (NT, K = 8960) and a K = 8960 dX (NN,
