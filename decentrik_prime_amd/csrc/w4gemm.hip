@@ -600,13 +600,15 @@ Plan plan_for(int64_t M, int64_t N, int64_t K, int epi) {
 }
 
 // Two-phase path: with many row tiles, dequantising each W tile once per row tile (in LDS) costs
-// more LDS bandwidth than the MFMAs can hide, so for wide outputs (many W tiles) from
-// kTwoPhaseRows rows on, the weight is first dequantised once into the workspace at HBM rate
-// (nf4_dequant_kernel) and the GEMM reads fp16 W.  Measured on MI355X at M = 2048: gate|up
-// forward (N = 17920) 174 -> 153 us, down backward (N = 8960) 139 -> 132 us; the N = 1536 and
-// 2048 outputs are as fast or faster in one phase.
+// more LDS bandwidth than the MFMAs can hide, so from kTwoPhaseRows rows and kTwoPhaseCols
+// output columns on, the weight is first dequantised once into the workspace at HBM rate
+// (nf4_dequant_kernel) and the GEMM reads fp16 W (on the 256-tile kernel where it takes the
+// shape).  Measured on MI355X at M = 2048 against this file's kernel: gate|up forward
+// (N = 17920) 174 -> 153 us, down backward (N = 8960) 139 -> 132 us, and, with the 256-tile
+// kernel's 128 x 128 quarters, q|k|v forward 33.3 -> 27.9 us, o forward 30.3 -> 24.7, o dX
+// 31.5 -> 24.5, q|k|v dX 42.3 -> 33.4.
 constexpr int64_t kTwoPhaseRows = 512;
-constexpr int64_t kTwoPhaseCols = 4096;
+constexpr int64_t kTwoPhaseCols = 1536;
 
 bool two_phase(int64_t M, int64_t N) { return M >= kTwoPhaseRows && N >= kTwoPhaseCols; }
 

@@ -219,7 +219,7 @@ int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const dk_nf4_we
 
 /* Workspace of the fused NF4 GEMMs.  No counterpart in the reference (cuBLAS manages its own);
  * it stands in for the reference's fp16 dequant workspace (solution/fast_qwen.py:398-418).
- * It holds split-K partial tiles and, from 512 rows on for outputs of at least 4096 columns, the
+ * It holds split-K partial tiles and, from 512 rows on for outputs of at least 1536 columns, the
  * weight dequantised to fp16 once per call (the "two-phase" path: dequant at HBM rate, then the
  * MFMA GEMM on fp16 W), which at many row tiles is faster than dequantising each W tile again for
  * every row tile.  Without a

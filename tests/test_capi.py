@@ -39,10 +39,10 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_set_w4_gemm_mode(-1) == _lib.DK_ERR_INVALID
     assert lib.dk_set_w4_gemm_mode(2) == 0 and lib.dk_set_w4_gemm_mode(0) == 0
     # workspace sizes (no device access): split-K partials, and the fp16 weight of the two-phase
-    # path (from 512 rows on, outputs of 4096 columns or more)
+    # path (from 512 rows on, outputs of 1536 columns or more)
     wq = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 1536, 1536)
     wgu = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 17920, 1536)
-    assert lib.dk_w4_workspace(2048, ctypes.byref(wq), _lib.DK_OP_LINEAR_FWD) == 0
+    assert lib.dk_w4_workspace(2048, ctypes.byref(wq), _lib.DK_OP_LINEAR_FWD) == 1536 * 1536 * 2
     assert lib.dk_w4_workspace(256, ctypes.byref(wq), _lib.DK_OP_LINEAR_FWD) == 48 * 3 * 128 * 64 * 4
     assert lib.dk_w4_workspace(2048, ctypes.byref(wgu), _lib.DK_OP_GATEUP_SWIGLU_FWD) == 17920 * 1536 * 2
     assert lib.dk_w4_workspace(256, ctypes.byref(wgu), _lib.DK_OP_GATEUP_SWIGLU_FWD) == 0
