@@ -25,8 +25,12 @@ def _case(n, v, d, seed, frac_no_target):
     return y, emb, tgt
 
 
+# chunk widths from 1024 to 65,536 columns (the full-vocabulary test below: 32,768 and a last
+# chunk of 20,864), with a ragged last chunk in each case but the second
 @pytest.mark.parametrize("n,v,chunk,frac,gscale", [(300, 9984, 4096, 0.2, 4.0),
-                                                   (64, 4096, 1024, 1.0, 1.0)])
+                                                   (64, 4096, 1024, 1.0, 1.0),
+                                                   (64, 20480, 16384, 0.5, 1.0),
+                                                   (48, 70016, 65536, 0.8, 2.0)])
 def test_streamed_head(torch, n, v, chunk, frac, gscale):
     from decentrik_prime_amd import k_head
     from oracle import head
