@@ -311,6 +311,19 @@ def kernel_table(torch, st, reps, only=None):
         x, L["qkv"], lo["bias"], st.qkv_terms(0), rpos, rcos, rsin, D + KV, out=o["qkv"],
         w16=h["qkv"]), g(m, QKV, D) + g(m, D, r) + g(m, KV, r), None, 0)
     rows = [rope_row]
+    # k_proj alone (the step runs it inside the fused q|k|v GEMM): 2048 x 256 x 1536 does ~200
+    # FLOP per byte of its operands, under the ~315 of the MFMA / HBM ridge, so the row gives both
+    # TFLOP/s and GB/s.  Its NF4 weight is rows [D, D + KV) of the fused one (whole second-level
+    # blocks).
+    wk = W.W4.from_sections(L["qkv"].packed, L["qkv"].qabs, L["qkv"].scale2, L["qkv"].offset2,
+                            D * D, KV, D, st.code2, st.nf4)
+    ok = torch.empty(m, KV, dtype=torch.float16, device=x.device)
+    k_bytes = lambda wb: m * D * 2 + wb + m * KV * 2  # noqa: E731
+    rows.append(("w4_linear_fwd k alone", lambda: W.linear_forward(x, wk, out=ok), g(m, KV, D),
+                 k_bytes(KV * D * (0.5 + 1 / 64 + 8 / 16384)), 0))
+    rows.append(("h16_linear_fwd k alone",
+                 lambda: W.linear_forward(x, wk, out=ok, w16=h["qkv"][D:D + KV]), g(m, KV, D),
+                 k_bytes(KV * D * 2), 0))
     for kind, suffix, fn, flops in gemms:
         # both forms; the one the step runs counts once per layer, the other is reported only
         used = "h16" if kind in st.ahead else "w4"
@@ -369,6 +382,7 @@ def kernel_table(torch, st, reps, only=None):
             row["frac_fp16_peak"] = round(flops / (ms * 1e-3) / 1e12 / FP16_PEAK_TFLOPS, 4)
         if nbytes:
             row["gbps"] = round(nbytes / (ms * 1e-3) / 1e9, 1)
+            row["frac_hbm_peak"] = round(nbytes / (ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)
         out.append(row)
     gu.copy_(gu_save)
     del h, hl
