@@ -717,9 +717,15 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
   }
   int b = blockIdx.x;
   if (b >= tail_wgs) {
-    b -= tail_wgs;
-    // workgroups are dealt to the 8 XCDs round-robin: give each XCD a contiguous run of tiles
-    if ((main_tiles & 7) == 0) b = (b & 7) * (main_tiles >> 3) + (b >> 3);
+    // workgroups are dealt to the 8 XCDs round-robin (workgroup i to XCD i % 8): give each XCD a
+    // contiguous run of tiles.  XCD x's full-tile workgroups are first, first + 8, ... from the
+    // first index at or past tail_wgs that it receives.
+    if ((main_tiles & 7) == 0) {
+      const int x = b & 7, first = tail_wgs + ((x - tail_wgs) & 7);
+      b = x * (main_tiles >> 3) + ((b - first) >> 3);
+    } else {
+      b -= tail_wgs;
+    }
     // split-K: the splits are the slowest index, so an XCD's run covers neighbouring tiles of
     // one K range, which share A and W slices in its L2
     const int tiles = main_tiles / p.splits;
