@@ -638,6 +638,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       if (refill) w4_write(st);
       w4_next = w4_after;
     }
+    // the last sub-step, which issues the refill, at wave priority 1: the wave past the barrier
+    // gets its DMA out ahead of the other wave's operand reads (measured on MI355X: every GEMM of
+    // the step 0.5-6 % faster, the step ~1 %)
+    __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int q = 0; q < TM * TN; ++q) {   // sub-step 3 (buffer 1)
       acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
@@ -647,6 +651,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
         if (refill) issue(kt + NST, st, d);
       __builtin_amdgcn_sched_barrier(0);
     }
+    __builtin_amdgcn_s_setprio(0);
   }
   // every wave is past the last barrier, after which no wave reads a stage and no load is in
   // flight: the stages are free for the per-wave epilogue scratch
