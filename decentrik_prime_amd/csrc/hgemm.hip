@@ -680,13 +680,15 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN, escr, pscr);
 }
 
-// Workgroups [0, tail_wgs) run the tiles past main_tiles as 128 x 128 quarters; the main_tiles
-// after them run 256 x 256 tiles.  Dispatching the quarters first staggers the rounds: the CUs
-// that ran a quarter start their full tiles later than the rest, so the rounds' HBM-bound
-// epilogues do not all fall at once (measured on MI355X: down^T SwiGLU backward 79.7 -> 77.2 us,
-// gate|up forward 114.5 -> 113.9 us).  With split-K (p.splits > 1, LINEAR only) the full-tile
-// workgroup b (counted from tail_wgs) runs split b / tiles of tile b % tiles and stores its fp32
-// partial tile at p.part[tile][split].  Tiles are numbered M-fastest.  The p.sums.wgs workgroups after the tiles (NN LINEAR) run the LoRA
+// main_tiles workgroups run 256 x 256 tiles and tail_wgs run the tiles past main_tiles as
+// 128 x 128 quarters: the full tiles first, except in the SwiGLU backward, whose quarters go
+// first.  There that staggers the rounds: the CUs that ran a quarter start their full tiles
+// later than the rest, so the rounds' epilogues (HBM-bound: they read and rewrite [g|u]) do not
+// all fall at once (measured on MI355X: 79.7 -> 77.2 us at M = 2048).  Elsewhere the stagger
+// leaves the time unchanged but, with the XCDs' tiles no longer in step along K, fetches more
+// (gate|up forward 198 -> 287 MB).  With split-K (p.splits > 1, LINEAR only) full-tile
+// workgroup b (counted from the first) runs split b / tiles of tile b % tiles and stores its
+// fp32 partial tile at p.part[tile][split].  Tiles are numbered M-fastest.  The p.sums.wgs workgroups after the tiles (NN LINEAR) run the LoRA
 // column sums the launch carries, the p.side.wgs after those its dequant work; dispatched last,
 // they take the CUs the tiles leave idle.
 template <bool TRANS, int EPI, bool W4>
@@ -720,16 +722,19 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
     if (threadIdx.x < 256) w4tab[16 + threadIdx.x] = p.code2[threadIdx.x];
     __syncthreads();
   }
+  constexpr bool kQuartersFirst = EPI == EPI_SWIGLU_BWD;
+  const int fbase = kQuartersFirst ? tail_wgs : 0;    // first full-tile workgroup
+  const int qbase = kQuartersFirst ? 0 : main_tiles;  // first quarter workgroup
   int b = blockIdx.x;
-  if (b >= tail_wgs) {
+  if (b >= fbase && b < fbase + main_tiles) {
     // workgroups are dealt to the 8 XCDs round-robin (workgroup i to XCD i % 8): give each XCD a
     // contiguous run of tiles.  XCD x's full-tile workgroups are first, first + 8, ... from the
-    // first index at or past tail_wgs that it receives.
+    // first index at or past fbase that it receives.
     if ((main_tiles & 7) == 0) {
-      const int x = b & 7, first = tail_wgs + ((x - tail_wgs) & 7);
+      const int x = b & 7, first = fbase + ((x - fbase) & 7);
       b = x * (main_tiles >> 3) + ((b - first) >> 3);
     } else {
-      b -= tail_wgs;
+      b -= fbase;
     }
     // split-K: the splits are the slowest index, so an XCD's run covers neighbouring tiles of
     // one K range, which share A and W slices in its L2
@@ -743,8 +748,8 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
         p.splits > 1 ? p.part + ((int64_t)tile * p.splits + split) * kTile * kTile : nullptr;
     gemm_tile<TRANS, EPI, 256, 256, 2, 2, W4>(p, m0, n0, kt0, nk, part, As, Bs, w4tab);
   } else {
-    int t = b;
-    if ((tail_wgs & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
+    int t = b - qbase;
+    if ((tail_wgs & 7) == 0 && (qbase & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
     const int parent = main_tiles + t / 4, quarter = t % 4;
     const int64_t m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
     const int64_t n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
