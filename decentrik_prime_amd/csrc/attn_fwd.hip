@@ -161,11 +161,15 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
     sc[0] = sn[0];
     sc[1] = sn[1];
   }
-  if (!mval) return;
   // result register v of block hb: head column hb * 32 + 8 (v / 4) + 4 (l / 32) + v % 4; one
-  // correctly rounded reciprocal per row, then a product per element
-  f16* orow = out + (s0 + m) * (int64_t)(a.nq * kHD) + h * kHD;
-  const float inv_l = __fdiv_rn(1.0f, l_i);
+  // correctly rounded reciprocal per row, then a product per element.  The wave's 32 x 128 block
+  // of O is staged in its part of the K stages (free after the loop's last barrier) and written
+  // back 16 bytes per lane, four whole 256-byte rows per store instruction: stored from the
+  // registers, each instruction would cover 16 bytes of each of 32 rows' cache lines.
+  constexpr int kOStride = kHD + 8;   // halves per staged row
+  static_assert(kAThreads / 64 * 32 * kOStride <= kFwdStages * kTileHalves, "O staging in Ks");
+  f16* ostage = Ks + w * 32 * kOStride;
+  const float inv_l = __fdiv_rn(1.0f, l_i);   // rows past the sequence: not stored
 #pragma unroll
   for (int hb = 0; hb < kHD / 32; ++hb)
 #pragma unroll
@@ -173,9 +177,18 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
       f16x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = (f16)__fmul_rn(oacc[hb][4 * g + e], inv_l);
-      *reinterpret_cast<f16x4*>(orow + hb * 32 + 8 * g + 4 * hl) = o;
+      *reinterpret_cast<f16x4*>(ostage + c * kOStride + hb * 32 + 8 * g + 4 * hl) = o;
     }
-  if (hl == 0) lse[(int64_t)h * a.n_tokens + s0 + m] = __fadd_rn(m_i, log2f(l_i));
+  if (mval && hl == 0) lse[(int64_t)h * a.n_tokens + s0 + m] = __fadd_rn(m_i, log2f(l_i));
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 8; ++i) {
+    const int r = 4 * i + (lane >> 4), cc = lane & 15;
+    const int row = mstart + 32 * w + r;
+    const f16x8 v = *reinterpret_cast<const f16x8*>(ostage + r * kOStride + 8 * cc);
+    if (row < seqlen && s0 + row < a.n_tokens)
+      *reinterpret_cast<f16x8*>(out + (s0 + row) * (int64_t)(a.nq * kHD) + h * kHD + 8 * cc) = v;
+  }
 }
 
 }  // namespace
