@@ -162,8 +162,13 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int blk, int h,
     dc[0] = dn[0];
     dc[1] = dn[1];
   }
-  if (!mval) return;
-  float* qrow = dq + (s0 + m) * OROW + h * kHD;
+  // the wave's 32 x 128 block of dQ staged in the (now free) tile ring, waves 0-1 in the K stages
+  // and 2-3 in the V stages, then written back 16 bytes per lane, two whole 512-byte rows per
+  // store instruction (stored from the registers, each instruction would cover 32 bytes of each
+  // of 32 rows' cache lines); rows past the sequence are not stored
+  constexpr int kQStride = kHD + 4;   // floats per staged row
+  static_assert(2 * 32 * kQStride * 4 <= kFwdStages * kTileHalves * 2, "dQ staging in the ring");
+  float* qstage = reinterpret_cast<float*>(w < 2 ? Ks : Vs) + (w & 1) * 32 * kQStride;
 #pragma unroll
   for (int hb = 0; hb < kHD / 32; ++hb)
 #pragma unroll
@@ -171,8 +176,16 @@ __device__ __forceinline__ void dq_block(const AttnArgs& a, int blk, int h,
       f32x4 o;
 #pragma unroll
       for (int e = 0; e < 4; ++e) o[e] = __fmul_rn(dqacc[hb][4 * g + e], a.sm_scale);
-      *reinterpret_cast<f32x4*>(qrow + hb * 32 + 8 * g + 4 * hl) = o;
+      *reinterpret_cast<f32x4*>(qstage + c * kQStride + hb * 32 + 8 * g + 4 * hl) = o;
     }
+  __syncthreads();
+#pragma unroll
+  for (int i = 0; i < 16; ++i) {
+    const int r = 2 * i + hl, row = mstart + 32 * w + r;
+    const f32x4 v = *reinterpret_cast<const f32x4*>(qstage + r * kQStride + 4 * c);
+    if (row < seqlen && s0 + row < a.n_tokens)
+      *reinterpret_cast<f32x4*>(dq + (s0 + row) * OROW + h * kHD + 4 * c) = v;
+  }
 }
 
 // 4 bytes per lane from global memory into LDS at lds + 4 * lane (the dword form of dma16).
