@@ -11,9 +11,13 @@
 // (2 x 64 KB): the loads of step k + 2 go out during the last MFMAs of step k, into the stage
 // step k has just finished reading.  Each wave waits only for its own loads (vmcnt), and one
 // barrier per step both publishes the next step's tiles and frees the stage just read.  The MFMA
-// operands of the next 16-wide sub-step are read while the MFMAs of the current one run.
-// (Measured on MI355X: 64-wide steps in two stages run about 8% faster than 32-wide steps in a
-// four-stage ring; the barriers, not the load distance, are what costs.)
+// operands of the next 16-wide sub-step are read while the MFMAs of the current one run; the
+// last sub-step, which issues the refill, runs at wave priority 1 so that its loads go out ahead
+// of the other wave's operand reads.  (Measured on MI355X: 64-wide steps in two stages run about
+// 8% faster than 32-wide steps in a four-stage ring; the barriers, not the load distance, are
+// what costs.)  With W4 = true the workgroup builds each step's W tile itself from the packed NF4
+// weight (dequantised in registers beside the MFMAs and written into the stage), bit-identical
+// to the fp16-weight form.
 //
 // LDS layout: A tiles and NT W tiles are rows of 64 halves (128 bytes) whose eight 16-byte
 // chunks are XOR-swizzled by row (swz_k), so the b128 operand reads of 16 consecutive rows hit
@@ -24,7 +28,8 @@
 //
 // Tiles are dealt M-fastest inside each XCD's contiguous run of workgroups.  When the tile count
 // leaves a last round at most half full, those last tiles run as four 128 x 128 sub-tiles each
-// (8 waves of 32 x 64), so the final round is short instead of mostly idle.
+// (8 waves of 32 x 64), so the final round is short instead of mostly idle; in the SwiGLU
+// backward they are dispatched first, which staggers the rounds' HBM-bound epilogues.
 //
 // Epilogues as in w4gemm.hip (the same per-element rounding): LINEAR with up to two LoRA terms
 // and the three output modes, SWIGLU_FWD (gate/up rows interleaved in groups of 32 so g and u of
