@@ -993,6 +993,15 @@ def main():
                                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                 "frac": dq["frac_hbm_peak"],
                                                 "traffic": dq_traffic["bytes"] if dq_traffic else None}}
+        # beside the graph-replayed figure (which includes the gaps between the 28 launches): the
+        # kernel's own average duration in the committed trace of the round-end command
+        dq_prof = committed_kernel_avg("dequant layer")
+        if dq_prof:
+            g_prof = dq["bytes_per_launch"] / (dq_prof["avg_us"] * 1e-6) / 1e9
+            result["dequant"]["roofline"]["frac_rocprof"] = round(g_prof / HBM_PEAK_GBS, 4)
+            result["dequant"]["roofline"]["rocprof"] = (
+                f"{dq_prof['source']}: {dq_prof['kernel']} ({dq_prof['wgs']} workgroups) average "
+                f"{dq_prof['avg_us']} us over {dq_prof['calls']} dispatches -> {g_prof:.1f} GB/s")
         result["kernels"] = kernels
         result["neighbours"] = neighbour_table(torch, args.reps, args.m)
         print("[bench] " + ", ".join(
