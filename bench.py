@@ -988,7 +988,7 @@ def main():
                 f"{a_prof:.1f} TFLOP/s")
         dq = dequant_bandwidth(torch, st, max(3, args.reps // 4))
         print(f"[bench] dequant {dq['gbps']} GB/s", file=sys.stderr, flush=True)
-        dq_traffic = committed_traffic("dequant")
+        dq_traffic = committed_traffic("dequant layer")
         result["dequant"] = {**dq, "roofline": {"bound": "hbm", "achieved": dq["gbps"],
                                                 "peak": HBM_PEAK_GBS, "unit": "GB/s",
                                                 "frac": dq["frac_hbm_peak"],
