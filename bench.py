@@ -994,7 +994,7 @@ def main():
                                                 "frac": dq["frac_hbm_peak"],
                                                 "traffic": dq_traffic["bytes"] if dq_traffic else None}}
         # beside the graph-replayed figure (which includes the gaps between the 28 launches): the
-        # kernel's own average duration in the committed trace of the round-end command
+        # kernel's own average duration in the committed trace of the default bench command
         dq_prof = committed_kernel_avg("dequant layer")
         if dq_prof:
             g_prof = dq["bytes_per_launch"] / (dq_prof["avg_us"] * 1e-6) / 1e9
