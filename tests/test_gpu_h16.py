@@ -222,6 +222,38 @@ def test_w4_tile_kernel_reads_nf4(torch, m):
         _same(got[k], want[k], f"{k}: W4 tile kernel vs fp16 form")
 
 
+def test_w4_own_kernel_split_k(torch):
+    """dk_set_w4_gemm_mode(2): the split-K shapes at M = 2048 (down forward, K = 8960; gate|up dX,
+    K = 17920), which mode 0 gives to the 256-tile kernel, run on the NF4-form kernel's own split-K
+    plan instead (its REDUCE launch).  Its summation order differs, so it is checked against the
+    fp16 form at the split-K tolerance and against the oracle."""
+    from decentrik_prime_amd import w4linear
+    from oracle import linear
+    m, D, I = 2048, 1536, 8960
+    log(f"NF4-form kernel's own split-K, M={m}")
+    qd, qg = nf4_weight(D, I, seed=231), nf4_weight(2 * I, D, seed=232)
+    wd, wg = to_w4(qd), to_w4(qg)
+    hd, hg = wd.dequantize(), wg.dequantize()
+    rng = np.random.default_rng(233)
+    act = (rng.standard_normal((m, I)) * 0.1).astype(np.float16)
+    gu = (rng.standard_normal((m, 2 * I)) * 1e-2).astype(np.float16)
+    tact, tgu = cuda16(act), cuda16(gu)
+    want_y = w4linear.linear_forward(tact, wd, w16=hd)
+    want_dx = w4linear.linear_backward_dx(tgu, wg, w16=hg)
+    w4linear.set_w4_gemm_mode(2)
+    try:
+        got_y = w4linear.linear_forward(tact, wd)
+        got_dx = w4linear.linear_backward_dx(tgu, wg)
+        torch.cuda.synchronize()
+    finally:
+        w4linear.set_w4_gemm_mode(0)
+    _near(got_y, want_y, "down forward: own split-K vs fp16 form")
+    _near(got_dx, want_dx, "gate|up dX: own split-K vs fp16 form")
+    _scaled_close(host(got_y), linear.mm16(act, qd["deq"].T), "down forward vs oracle")
+    _scaled_close(host(got_dx), gu.astype(np.float32) @ qg["deq"].astype(np.float32),
+                  "gate|up dX vs oracle")
+
+
 @pytest.mark.parametrize("m", [2048, 1000])
 def test_split_k(torch, m):
     """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
