@@ -254,6 +254,44 @@ def test_w4_own_kernel_split_k(torch):
                   "gate|up dX vs oracle")
 
 
+def test_w4_without_workspace(torch):
+    """A NULL workspace: the NF4 GEMMs that would split K (down forward, K = 8960) or dequantise W
+    into the workspace first (q|k|v forward, o dX) run in one phase with the dequant in LDS.
+    Checked against the fp16 form at summation-order tolerance and against the oracle."""
+    from decentrik_prime_amd import _lib, w4linear
+    from oracle import linear
+    lib = _lib.lib()
+    m, D, KV, I = 2048, 1536, 256, 8960
+    log(f"NF4 GEMMs without a workspace, M={m}")
+    qd, qq, qo = nf4_weight(D, I, seed=241), nf4_weight(D + 2 * KV, D, seed=242), nf4_weight(D, D, seed=243)
+    wd, wq, wo = to_w4(qd), to_w4(qq), to_w4(qo)
+    rng = np.random.default_rng(244)
+    act = (rng.standard_normal((m, I)) * 0.1).astype(F16)
+    x = rng.standard_normal((m, D)).astype(F16)
+    dy = (rng.standard_normal((m, D)) * 1e-2).astype(F16)
+    stream = _lib.stream_handle(torch.device("cuda"))
+
+    def fwd(a, w):
+        y = torch.empty(m, w.rows, dtype=torch.float16, device="cuda")
+        assert lib.dk_w4_linear_fwd(_lib.ptr(a), a.stride(0), m, w.c_ref(), None, None, None, 0, 2.0,
+                                    _lib.ptr(y), y.stride(0), None, 0, stream) == 0
+        return y
+
+    ta, tx, tdy = cuda16(act), cuda16(x), cuda16(dy)
+    y_d, y_q = fwd(ta, wd), fwd(tx, wq)
+    dx_o = torch.empty(m, D, dtype=torch.float32, device="cuda")
+    assert lib.dk_w4_linear_bwd_dx(_lib.ptr(tdy), tdy.stride(0), m, wo.c_ref(), None, None, 0, None,
+                                   1.0, _lib.ptr(dx_o), dx_o.stride(0), _lib.DK_OUT_F32, None, 0,
+                                   stream) == 0
+    torch.cuda.synchronize()
+    _near(y_d, w4linear.linear_forward(ta, wd, w16=wd.dequantize()), "down: no workspace vs fp16 form")
+    _near(y_q, w4linear.linear_forward(tx, wq, w16=wq.dequantize()), "qkv: no workspace vs fp16 form")
+    _near(dx_o, w4linear.linear_backward_dx(tdy, wo, w16=wo.dequantize()), "o dX: no workspace vs fp16 form")
+    assert_close(host(y_d), linear.mm16(act, qd["deq"].T), RTOL, ATOL, "down vs oracle")
+    assert_close(host(y_q), linear.mm16(x, qq["deq"].T), RTOL, ATOL, "qkv vs oracle")
+    _scaled_close(host(dx_o), linear.mm16(dy, qo["deq"]).astype(np.float32), "o dX vs oracle")
+
+
 @pytest.mark.parametrize("m", [2048, 1000])
 def test_split_k(torch, m):
     """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
