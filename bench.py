@@ -995,6 +995,10 @@ def main():
                                                 "traffic": dq_traffic["bytes"] if dq_traffic else None}}
         # beside the graph-replayed figure (which includes the gaps between the 28 launches): the
         # kernel's own average duration in the committed trace of the default bench command
+        # the practical ceiling beside it: a plain 512 MiB device copy (read + write) on this box
+        cp = copy_calibration(torch, max(3, args.reps // 4))
+        result["dequant"]["copy_gbps"] = cp["gbps"]
+        result["dequant"]["frac_of_copy"] = round(dq["gbps"] / cp["gbps"], 4)
         dq_prof = committed_kernel_avg("dequant layer")
         if dq_prof:
             g_prof = dq["bytes_per_launch"] / (dq_prof["avg_us"] * 1e-6) / 1e9
