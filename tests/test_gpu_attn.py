@@ -66,6 +66,33 @@ def test_varlen_causal_gqa_attention(torch, lens):
     _close(host(tqkv_grad), want, 3e-2, 3e-2, "dqkv through the QKV epilogue backward")
 
 
+@pytest.mark.parametrize("nq,nkv", [(4, 4), (8, 2), (2, 1)])
+def test_attention_head_configs(torch, nq, nkv):
+    """Other head counts than Qwen2.5-1.5B's 12 / 2: plain multi-head (every query head its own
+    K/V head), a group of 4 and a group of 2, forward and backward against the oracle."""
+    from decentrik_prime_amd import k_attn
+    from oracle import attn
+    lens = [64, 200, 129]
+    log(f"attention fwd+bwd, {nq} query / {nkv} KV heads, lens {lens}")
+    n = sum(lens)
+    rng = np.random.default_rng(7 * nq + nkv)
+    qkv = (rng.standard_normal((n, (nq + 2 * nkv) * HD)) * 0.8).astype(np.float16)
+    dout = rng.standard_normal((n, nq * HD)).astype(np.float16)
+    meta = k_attn.meta_for(lens, "cuda")
+    tq = torch.from_numpy(qkv).cuda()
+    out, lse = k_attn.attention_forward(tq, meta, nq, nkv, HD)
+    dq, dkp, dvp = k_attn.attention_backward(tq, out, lse, torch.from_numpy(dout).cuda(), meta,
+                                             nq, nkv, HD)
+    torch.cuda.synchronize()
+    o_ref, lse_ref = attn.attention_fwd(qkv, lens, nq, nkv, HD)
+    _close(host(out), o_ref, 3e-3, 3e-3, "attention out")
+    _close(host(lse), lse_ref, 1e-5, 2e-4, "lse (log2 domain)")
+    dq_ref, dkp_ref, dvp_ref = attn.attention_bwd(qkv, dout, lens, nq, nkv, HD, out=host(out))
+    _close(host(dq), dq_ref, 3e-2, 2e-2, "dq")
+    _close(host(dkp), dkp_ref, 3e-2, 2e-2, "dk per query head")
+    _close(host(dvp), dvp_ref, 3e-2, 2e-2, "dv per query head")
+
+
 def test_attention_argument_checks(torch):
     from decentrik_prime_amd import k_attn
     meta = k_attn.meta_for([5, 7], "cuda")
