@@ -104,7 +104,9 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
                                               const uint8_t* pscr) {
   constexpr int COLS = 32 * TN;          // columns of a strip
   constexpr int SLD = COLS + 8;          // floats per staged row: the two half-waves' rows
-                                         // (4 apart) land 32 banks apart
+                                         // (4 apart) land 32 banks apart; on odd rows the
+                                         // 16-byte chunks swap in pairs (column bit 2), so the
+                                         // read-back's neighbouring rows hit distinct banks
   constexpr int SEGS = COLS / 8;         // 8-column segments per row
   constexpr int ROWS_PER_PASS = 64 / SEGS;
   static_assert(32 * SLD * 4 + 3072 == epi_scratch_bytes(TN) && epi_scratch_bytes(TN) <= kEpiScratch,
@@ -124,11 +126,15 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   // registers -> staged strip (the values, already rounded where the output is fp16)
   auto stage_block = [&](int j, const f32x16& r) {
 #pragma unroll
-    for (int v = 0; v < 16; ++v) stage[(8 * (v >> 2) + rsub + (v & 3)) * SLD + 32 * j + lrow] = r[v];
+    for (int v = 0; v < 16; ++v) {
+      const int row = 8 * (v >> 2) + rsub + (v & 3);
+      stage[row * SLD + ((32 * j + lrow) ^ ((row & 1) << 2))] = r[v];
+    }
   };
   auto staged8_of = [&](const float* st, int row, int col) {
-    const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * SLD + col);
-    const f32x4 b = *reinterpret_cast<const f32x4*>(st + row * SLD + col + 4);
+    const int sw = (row & 1) << 2;
+    const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * SLD + (col ^ sw));
+    const f32x4 b = *reinterpret_cast<const f32x4*>(st + row * SLD + ((col + 4) ^ sw));
     return f32x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   };
   auto staged8 = [&](int row, int col) { return staged8_of(stage, row, col); };
