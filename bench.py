@@ -90,14 +90,15 @@ def _median_s(fn, reps=5):
     return sorted(ts)[len(ts) // 2]
 
 
-def _scaled_err(got, want):
-    """max |got - want| / max |want| and whether every element is within rtol 1e-2 / atol 2e-2 of
-    the output's scale (the tolerance BASELINE.json's north_star states for GEMM outputs and LoRA
-    gradients)."""
+def _scaled_err(got, want, absolute=False):
+    """Whether every element is within rtol 1e-2 / atol 2e-2 (the tolerance BASELINE.json's
+    north_star states for GEMM outputs and LoRA gradients), and the largest error.  absolute: on
+    the values themselves (forward outputs, of order 1); otherwise relative to the output's scale
+    max |want| (gradients, which dY ~ N(0, 1e-2) makes small), reported as max |err| / scale."""
     import numpy as np
     got = np.asarray(got, np.float64)
     want = np.asarray(want, np.float64)
-    scale = float(np.abs(want).max()) or 1.0
+    scale = 1.0 if absolute else (float(np.abs(want).max()) or 1.0)
     err = np.abs(got - want) / scale
     ok = bool(np.all(err <= 2e-2 + 1e-2 * np.abs(want) / scale))
     return float(err.max()), ok
@@ -154,13 +155,15 @@ def config_rows(torch, st, cpu=True):
         print(f"[bench] config {cfg}: {what}: {gpu} cpu {out.get('cpu')} parity {parity}",
               file=sys.stderr, flush=True)
 
-    def check(label, pairs):
+    def check(label, pairs, absolute):
         worst, ok = 0.0, True
         for got, want in pairs:
-            e, good = _scaled_err(got, want)
+            e, good = _scaled_err(got, want, absolute)
             worst, ok = max(worst, e), ok and good
         if not ok:
             raise RuntimeError(f"{label}: GPU result outside rtol 1e-2 / atol 2e-2 of the oracle")
+        if absolute:
+            return f"rtol 1e-2 / atol 2e-2: pass (max |err| {worst:.2e})"
         return f"rtol 1e-2 / atol 2e-2 of scale: pass (max |err| / scale {worst:.2e})"
 
     # config 0: dequant of one q_proj weight [1536, 1536]
@@ -199,8 +202,10 @@ def config_rows(torch, st, cpu=True):
     def cpu1():
         ref1["y"], ref1["z"] = linear.linear_fwd(xn, cpu_deq(wq), None, mqn, ks, aqn, bqn, s)
     cpu1_s = _median_s(cpu1) if cpu else (cpu1() or None)
-    par1 = check("config 1", [(host(y1), ref1["y"]), (host(z1), ref1["z"])])
-    row(1, "q_proj forward + LoRA r=16 with dropout, M=2048 (lora_down + fused NF4 GEMM)", ms1,
+    par1 = check("config 1", [(host(y1), ref1["y"]), (host(z1), ref1["z"])], True)
+    row(1, "q_proj forward + LoRA r=16 with dropout, M=2048 (lora_down + dk_w4_linear_fwd: the NF4 "
+           "weight dequantised into the workspace, then the 256-tile fp16 GEMM with the LoRA "
+           "epilogue)", ms1,
         f1, "TFLOP/s", cpu1_s, par1,
         alt={"us": round(ms1h * 1e3, 2), "what": "dequant to fp16 + fp16 GEMM"})
 
@@ -221,7 +226,7 @@ def config_rows(torch, st, cpu=True):
     def cpu2():
         ref2["gu"], ref2["h"], ref2["y"] = mlp.mlp_fwd(xn, cpu_deq(wgu), cpu_deq(ws["down_proj"]))
     cpu2_s = _median_s(cpu2, 3) if cpu else (cpu2() or None)
-    par2 = check("config 2", [(host(act2), ref2["h"]), (host(y2), ref2["y"])])
+    par2 = check("config 2", [(host(act2), ref2["h"]), (host(y2), ref2["y"])], True)
     row(2, "MLP forward: gate|up + SwiGLU, down, M=2048 (NF4 weights, dequantised once to fp16 "
            "then the 256-tile GEMMs)", ms2, f2, "TFLOP/s", cpu2_s, par2)
 
@@ -255,7 +260,8 @@ def config_rows(torch, st, cpu=True):
     cpu3_s = _median_s(cpu3) if cpu else (cpu3() or None)
     par3 = check("config 3", [(host(dxq), ref3["q"]["dx"]), (host(dxv), ref3["v"]["dx"]),
                               (host(res3["daq"]), ref3["q"]["dA"]), (host(res3["dbq"]), ref3["q"]["dB"]),
-                              (host(res3["dav"]), ref3["v"]["dA"]), (host(res3["dbv"]), ref3["v"]["dB"])])
+                              (host(res3["dav"]), ref3["v"]["dA"]), (host(res3["dbv"]), ref3["v"]["dB"])],
+                  False)
     row(3, "q_proj + v_proj backward: dX through the NF4 weights with the masked LoRA dX, dA, dB, "
            "M=2048", ms3, f3, "TFLOP/s", cpu3_s, par3)
     return rows
@@ -537,6 +543,19 @@ def dequant_bandwidth(torch, st, reps):
             "frac_hbm_peak": round(gbps / HBM_PEAK_GBS, 4)}
 
 
+def gemm_calibration(torch, m, reps, n=2 * 8960, k=1536):
+    """torch.mm (hipBLASLt) of fp16 [m, k] x [k, n] (the gate|up forward's shape, no dequant, no
+    epilogue), launched back to back (each call is ~140 us, far above the launch overhead; a
+    library call is kept out of graph capture): the box's GEMM rate in this run, beside the
+    step."""
+    a = torch.randn(m, k, device="cuda").half()
+    b = torch.randn(n, k, device="cuda").half()
+    out = torch.empty(m, n, dtype=torch.float16, device="cuda")
+    us = time_op(torch, lambda: torch.mm(a, b.t(), out=out), 10 * reps) * 1e3
+    return {"kernel": f"torch.mm fp16 [{m}, {k}] x [{k}, {n}]", "avg_us": round(us, 2),
+            "tflops": round(2 * m * n * k / (us * 1e-6) / 1e12, 1)}
+
+
 def copy_calibration(torch, reps, nbytes=512 << 20):
     """A plain device copy of known size (read nbytes + write nbytes per launch): the reference
     against which rocprofv3's FETCH_SIZE / WRITE_SIZE counters are scaled."""
@@ -654,7 +673,8 @@ def summarize_trace(db, top=40, ops=()):
         wgs = (gx // max(wx, 1)) * (gy // max(wy, 1)) * (gz // max(wz, 1))
         agg[(_short(name), wgs, wx * wy * wz)].append(dur)
     total = sum(sum(v) for v in agg.values())
-    lines = [f"{'kernel':78s} {'wgs':>7s} {'wg':>4s} {'calls':>6s} {'avg_us':>9s} "
+    lines = [f"SOURCES {source_digest()}",
+             f"{'kernel':78s} {'wgs':>7s} {'wg':>4s} {'calls':>6s} {'avg_us':>9s} "
              f"{'total_ms':>9s} {'pct':>6s}"]
     for (k, wgs, wx), v in sorted(agg.items(), key=lambda kv: -sum(kv[1]))[:top]:
         lines.append(f"{k:78s} {wgs:7d} {wx:4d} {len(v):6d} {sum(v) / len(v) / 1e3:9.2f} "
@@ -742,58 +762,116 @@ def _counters_by_dispatch(db):
     return out, dur
 
 
-def summarize_counters(db, groups, simds=1024, xcds=8):
-    """MFMA utilisation per operator from a `rocprofv3 --pmc SQ_VALU_MFMA_BUSY_CYCLES
-    SQ_INSTS_VALU_MFMA_MOPS_F16 GRBM_GUI_ACTIVE SQ_BUSY_CU_CYCLES --kernel-trace` run:
-    MFMA busy = sum over instances of SQ_VALU_MFMA_BUSY_CYCLES / (max GRBM_GUI_ACTIVE x SIMDs)
-    (rocprofv3's MfmaUtil), the MFMA FLOPs the hardware counted (SQ_INSTS_VALU_MFMA_MOPS_F16 x 512)
-    and the effective clock (GRBM_GUI_ACTIVE / kernel duration).  GRBM_GUI_ACTIVE is stored summed
-    over the XCDs, so it is divided by their count (8 on MI355X) for the per-XCD busy cycles; its
-    window also covers the dispatch's start and drain, which for kernels of ~20 us inflates the
-    clock and deflates the busy fraction (the algorithmic FLOPs over the duration are the figure
-    there).
-    groups: [(operator name, kernel-name substring, grid in workgroups or None, algorithmic FLOP)]."""
+def summarize_counters(db, groups, simds=1024, xcds=8, cus=256):
+    """Counters per operator from one `rocprofv3 --pmc ... --kernel-trace` pass.
+
+    Every counter the pass collected is listed per operator (mean over its dispatches of the sum
+    over the counter's instances), then what follows from them where the pass has the inputs:
+    - mfma_busy = SQ_VALU_MFMA_BUSY_CYCLES / (GRBM_GUI_ACTIVE per XCD x SIMDs) (rocprofv3's
+      MfmaUtil), mfma_GFLOP = SQ_INSTS_VALU_MFMA_MOPS_F16 x 512 (the FLOPs the hardware counted);
+    - clock_GHz = GRBM_GUI_ACTIVE per XCD / kernel duration (GRBM_GUI_ACTIVE is stored summed over
+      the XCDs, 8 on MI355X; its window also covers the dispatch's start and drain, which for
+      kernels of ~20 us inflates the clock and deflates the busy fractions);
+    - lds_read_B_per_clk_cu, lds_write_B_per_clk_cu: bytes moved by LDS instructions
+      (SQ_INSTS_LDS_LOAD_BANDWIDTH / _STORE_BANDWIDTH, units of 64 bytes) per busy clock per CU;
+    - lds_active = SQ_LDS_IDX_ACTIVE / (GRBM_GUI_ACTIVE per XCD x CUs): the fraction of clocks a
+      CU's LDS works on indexed (ds_*) instructions; lds_conflict = SQ_LDS_BANK_CONFLICT over
+      SQ_LDS_IDX_ACTIVE;
+    - lds_wait = SQ_WAIT_INST_LDS / SQ_WAVE_CYCLES (both in quad-cycles per wave), any_wait =
+      SQ_WAIT_INST_ANY / SQ_WAVE_CYCLES: the fraction of a wave's life spent waiting to issue an
+      LDS instruction / any instruction;
+    - ta_busy = TA_TA_BUSY_sum / (GRBM_GUI_ACTIVE per XCD x CUs): the texture-addresser (vector
+      memory, LDS DMA included) busy fraction; dma_waves = TA_FLAT_READ_LDS_WAVEFRONTS_sum, the
+      LDS-DMA load instructions.
+    groups: [(operator name, kernel-name substring, grid in workgroups or None, algorithmic
+    FLOP)]."""
     rows, dur = _counters_by_dispatch(db)
-    lines = [f"{'operator':34s} {'kernel':30s} {'wgs':>5s} {'n':>3s} {'mfma_busy':>9s} "
-             f"{'clock_GHz':>9s} {'mfma_GFLOP':>10s} {'algo_GFLOP':>10s} {'avg_us':>8s}"]
+    lines = []
+    mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")  # noqa: E731
     for op, pattern, wgs_only, algo in groups:
         sel = [(k, v) for k, v in rows.items()
                if pattern in k[1] and (wgs_only is None or k[2] == wgs_only)]
         if not sel:
-            lines.append(f"{op:34s} (no dispatch of {pattern})")
+            lines.append(f"{op}: (no dispatch of {pattern})")
             continue
-        busy, clk, flops, us = [], [], [], []
-        for (did, name, wgs, wg), v in sel:
-            gui = v.get("GRBM_GUI_ACTIVE", (0, 0, 0))[0] / xcds
-            if "SQ_VALU_MFMA_BUSY_CYCLES" in v and gui > 0:
-                busy.append(v["SQ_VALU_MFMA_BUSY_CYCLES"][0] / (gui * simds))
-            if "SQ_INSTS_VALU_MFMA_MOPS_F16" in v:
-                flops.append(v["SQ_INSTS_VALU_MFMA_MOPS_F16"][0] * 512)
-            if did in dur and dur[did] > 0:
-                us.append(dur[did] / 1e3)
-                if gui > 0:
-                    clk.append(gui / dur[did])
-        mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")  # noqa: E731
-        name = sel[0][0][1]
-        lines.append(f"{op:34s} {name[:30]:30s} {sel[0][0][2]:5d} {len(sel):3d} "
-                     f"{100 * mean(busy):8.1f}% {mean(clk):9.3f} {mean(flops) / 1e9:10.2f} "
-                     f"{(algo or 0) / 1e9:10.2f} {mean(us):8.2f}")
-        lines.append(f"MFMA {op} | busy {mean(busy):.4f} | clock_ghz {mean(clk):.3f} | "
-                     f"avg_us {mean(us):.2f}")
+        name, wgs = sel[0][0][1], sel[0][0][2]
+        cnt = {}
+        for _, v in sel:
+            for c, (tot, _, _) in v.items():
+                cnt.setdefault(c, []).append(tot)
+        c = {k: mean(v) for k, v in cnt.items()}
+        us = mean([dur[k[0]] / 1e3 for k, _ in sel if k[0] in dur and dur[k[0]] > 0])
+        gui = c.get("GRBM_GUI_ACTIVE", 0.0) / xcds
+        lines.append(f"{op} | {name} | {wgs} workgroups | {len(sel)} dispatches | "
+                     f"{us:.2f} us | {(algo or 0) / 1e9:.2f} GFLOP algorithmic")
+        for k in sorted(c):
+            lines.append(f"    {k:36s} {c[k]:16.0f}")
+        der = {}
+        if gui > 0:
+            if us == us:
+                der["clock_ghz"] = gui / (us * 1e3)
+            if "SQ_VALU_MFMA_BUSY_CYCLES" in c:
+                der["mfma_busy"] = c["SQ_VALU_MFMA_BUSY_CYCLES"] / (gui * simds)
+            if "SQ_INSTS_LDS_LOAD_BANDWIDTH" in c:
+                der["lds_read_B_per_clk_cu"] = c["SQ_INSTS_LDS_LOAD_BANDWIDTH"] * 64 / (gui * cus)
+            if "SQ_INSTS_LDS_STORE_BANDWIDTH" in c:
+                der["lds_write_B_per_clk_cu"] = c["SQ_INSTS_LDS_STORE_BANDWIDTH"] * 64 / (gui * cus)
+            if "SQ_LDS_IDX_ACTIVE" in c:
+                der["lds_active"] = c["SQ_LDS_IDX_ACTIVE"] / (gui * cus)
+            if "TA_TA_BUSY_sum" in c:
+                der["ta_busy"] = c["TA_TA_BUSY_sum"] / (gui * cus)
+        if c.get("SQ_LDS_IDX_ACTIVE"):
+            der["lds_conflict"] = c.get("SQ_LDS_BANK_CONFLICT", 0.0) / c["SQ_LDS_IDX_ACTIVE"]
+        if c.get("SQ_WAVE_CYCLES"):
+            for cn, dn in (("SQ_WAIT_INST_LDS", "lds_wait"), ("SQ_WAIT_INST_ANY", "any_wait")):
+                if cn in c:
+                    der[dn] = c[cn] / c["SQ_WAVE_CYCLES"]
+        if "SQ_INSTS_VALU_MFMA_MOPS_F16" in c:
+            der["mfma_gflop"] = c["SQ_INSTS_VALU_MFMA_MOPS_F16"] * 512 / 1e9
+        if "TA_FLAT_READ_LDS_WAVEFRONTS_sum" in c:
+            der["dma_waves"] = c["TA_FLAT_READ_LDS_WAVEFRONTS_sum"]
+        if der:
+            lines.append("COUNTERS " + op + " | " + " | ".join(
+                f"{k} {v:.4g}" for k, v in der.items()))
+        if "mfma_busy" in der:   # the line the MFMA summary has always had
+            lines.append(f"MFMA {op} | busy {der['mfma_busy']:.4f} | clock_ghz "
+                         f"{der.get('clock_ghz', float('nan')):.3f} | avg_us {us:.2f}")
     return "\n".join(lines)
+
+
+def source_digest():
+    """Digest of the kernel sources (csrc/*.hip, csrc/*.h, include/dk.h): a profile summary carries
+    the digest of the sources it was taken on, so a figure read back from it is labelled stale
+    once the kernels change."""
+    import glob
+    import hashlib
+    here = os.path.dirname(os.path.abspath(__file__))
+    h = hashlib.sha256()
+    files = sorted(glob.glob(os.path.join(here, "decentrik_prime_amd", "csrc", "*.hip")) +
+                   glob.glob(os.path.join(here, "decentrik_prime_amd", "csrc", "*.h")) +
+                   [os.path.join(here, "include", "dk.h")])
+    for f in files:
+        h.update(os.path.basename(f).encode())
+        h.update(open(f, "rb").read())
+    return h.hexdigest()[:16]
 
 
 def committed_kernel_avg(op):
     """Average duration (us) of operator `op`'s kernel in the committed rocprof kernel-trace summary
-    (an 'OPAVG op | kernel | wgs | avg_us | calls' line) and the summary's path, or None."""
+    (an 'OPAVG op | kernel | wgs | avg_us | calls' line), the summary's path, the source digest it
+    records ('SOURCES <digest>' line) and whether that is the digest of the sources now, or
+    None."""
     import glob
     here = os.path.dirname(os.path.abspath(__file__))
     for path in sorted(glob.glob(os.path.join(here, "profiles", "*.txt"))):
-        for line in open(path):
+        lines = open(path).read().splitlines()
+        digest = next((l.split()[1] for l in lines if l.startswith("SOURCES ")), None)
+        for line in lines:
             if line.startswith("OPAVG ") and line[6:].split(" | ")[0] == op:
                 parts = [x.strip() for x in line[6:].split(" | ")]
                 return {"avg_us": float(parts[3]), "kernel": parts[1], "wgs": int(parts[2]),
-                        "calls": int(parts[4]), "source": os.path.relpath(path, here)}
+                        "calls": int(parts[4]), "source": os.path.relpath(path, here),
+                        "sources_digest": digest, "sources_match": digest == source_digest()}
     return None
 
 
@@ -980,12 +1058,22 @@ def main():
                                f"{traffic['write']} B per call, scaled by a copy of known size")
                               if traffic else None}
         if prof:
+            # the committed trace's figure, labelled with whether it was taken on these sources
             a_prof = dom["gflop"] * 1e9 / (prof["avg_us"] * 1e-6) / 1e12
-            result["roofline"]["frac_rocprof"] = round(a_prof / FP16_PEAK_TFLOPS, 4)
-            result["roofline"]["rocprof"] = (
-                f"{prof['source']}: {prof['kernel']} ({prof['wgs']} workgroups) average "
-                f"{prof['avg_us']} us over {prof['calls']} dispatches of the traced bench run -> "
-                f"{a_prof:.1f} TFLOP/s")
+            result["roofline"]["committed_profile"] = {
+                **prof, "frac": round(a_prof / FP16_PEAK_TFLOPS, 4),
+                "note": f"{prof['kernel']} ({prof['wgs']} workgroups) average {prof['avg_us']} us "
+                        f"over {prof['calls']} dispatches of the traced bench run -> "
+                        f"{a_prof:.1f} TFLOP/s"}
+            if prof["sources_match"]:
+                result["roofline"]["frac_rocprof"] = round(a_prof / FP16_PEAK_TFLOPS, 4)
+        # the box's GEMM clock in this run: hipBLASLt (torch.mm, fp16) at the gate|up shape, so a
+        # step time can be compared across boxes whose power-limited clocks differ
+        mm = gemm_calibration(torch, args.m, max(3, args.reps // 4))
+        mm["step_tflops_over_mm"] = round(value / mm["tflops"], 4)
+        result["gemm_clock"] = mm
+        print(f"[bench] torch.mm gate|up shape {mm['avg_us']} us, {mm['tflops']} TFLOP/s",
+              file=sys.stderr, flush=True)
         dq = dequant_bandwidth(torch, st, max(3, args.reps // 4))
         print(f"[bench] dequant {dq['gbps']} GB/s", file=sys.stderr, flush=True)
         dq_traffic = committed_traffic("dequant layer")
@@ -1002,10 +1090,13 @@ def main():
         dq_prof = committed_kernel_avg("dequant layer")
         if dq_prof:
             g_prof = dq["bytes_per_launch"] / (dq_prof["avg_us"] * 1e-6) / 1e9
-            result["dequant"]["roofline"]["frac_rocprof"] = round(g_prof / HBM_PEAK_GBS, 4)
-            result["dequant"]["roofline"]["rocprof"] = (
-                f"{dq_prof['source']}: {dq_prof['kernel']} ({dq_prof['wgs']} workgroups) average "
-                f"{dq_prof['avg_us']} us over {dq_prof['calls']} dispatches -> {g_prof:.1f} GB/s")
+            result["dequant"]["roofline"]["committed_profile"] = {
+                **dq_prof, "frac": round(g_prof / HBM_PEAK_GBS, 4),
+                "note": f"{dq_prof['kernel']} ({dq_prof['wgs']} workgroups) average "
+                        f"{dq_prof['avg_us']} us over {dq_prof['calls']} dispatches -> "
+                        f"{g_prof:.1f} GB/s"}
+            if dq_prof["sources_match"]:
+                result["dequant"]["roofline"]["frac_rocprof"] = round(g_prof / HBM_PEAK_GBS, 4)
         result["kernels"] = kernels
         result["neighbours"] = neighbour_table(torch, args.reps, args.m)
         print("[bench] " + ", ".join(

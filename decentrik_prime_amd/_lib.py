@@ -17,9 +17,11 @@ HEADER = os.path.join(os.path.dirname(HERE), "include", "dk.h")
 DK_ERR_INVALID = -1
 DK_ERR_ALIGN = -2
 DK_ERR_WORKSPACE = -3
+DK_ERR_CAPTURE = -4
 DK_OUT_F16, DK_OUT_F32, DK_OUT_F32_ACCUM = 0, 1, 2
 DK_NOALLOC_SCRATCH_BYTES = 64 << 20
 DK_OP_LINEAR_FWD, DK_OP_LINEAR_BWD_DX, DK_OP_GATEUP_SWIGLU_FWD, DK_OP_DOWN_SWIGLU_BWD = 0, 1, 2, 3
+DK_W4_KERNEL_AUTO, DK_W4_KERNEL_TILE, DK_W4_KERNEL_STAGED = 0, 1, 2
 
 _c_p, _i64, _int, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c_float
 
@@ -27,7 +29,8 @@ _c_p, _i64, _int, _f32 = ctypes.c_void_p, ctypes.c_int64, ctypes.c_int, ctypes.c
 class NF4WeightC(ctypes.Structure):
     """struct dk_nf4_weight."""
     _fields_ = [("packed", _c_p), ("qabs", _c_p), ("scale2", _c_p), ("offset2", _c_p),
-                ("code2", _c_p), ("nf4", _c_p), ("rows", _i64), ("cols", _i64)]
+                ("code2", _c_p), ("nf4", _c_p), ("rows", _i64), ("cols", _i64),
+                ("kernel", ctypes.c_int32)]
 
 
 _W = ctypes.POINTER(NF4WeightC)
@@ -95,7 +98,6 @@ SIGNATURES = {
                                         _c_p, _i64, _c_p]),
     "dk_w4_linear_workspace": (_i64, [_i64, _W, _int]),
     "dk_w4_workspace": (_i64, [_i64, _W, _int]),
-    "dk_set_w4_gemm_mode": (_int, [_int]),
     "dk_h16_workspace": (_i64, [_i64, _i64, _i64, _int]),
     "dk_h16_linear_fwd_lora": (_int, [_c_p, _i64, _i64, _c_p, _i64, _i64, _c_p, _T, _int, _i64,
                                       _c_p, _i64, _c_p, _i64, _S, _c_p]),

@@ -32,11 +32,15 @@ FLAGS = [
 # per-file additions: the attention forward keeps its MFMA accumulators in VGPRs (in AGPRs, the
 # compiler's default at one wave per SIMD, it copied the output accumulator out and back on every
 # key tile); the backward kernels need more registers than VGPRs hold and keep the default
-EXTRA_FLAGS = {f: ["-mllvm", "-amdgpu-mfma-vgpr-form=1"] for f in ("attn_fwd.hip", "attn_dq.hip")}
+EXTRA_FLAGS = {"attn_fwd.hip": ["-mllvm", "-amdgpu-mfma-vgpr-form=1"]}
 
 
 def sources():
-    return sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    srcs = sorted(os.path.join(CSRC, f) for f in os.listdir(CSRC) if f.endswith(".hip"))
+    missing = set(EXTRA_FLAGS) - {os.path.basename(f) for f in srcs}
+    if missing:
+        raise RuntimeError(f"per-file flags name sources that do not exist: {sorted(missing)}")
+    return srcs
 
 
 def _compile(src):

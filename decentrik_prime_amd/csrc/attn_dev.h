@@ -120,9 +120,10 @@ __device__ __forceinline__ f16x8 read_col8_sw(const f16* tile, int p, int col) {
 // maximum or log-sum-exp), results below the normal range flush to zero.
 __device__ __forceinline__ float ex2(float x) { return __builtin_amdgcn_exp2f(x); }
 
-// The sequence of a block-table entry; false when the entry names no sequence or a sequence that
-// does not lie within the n_tokens rows (then every row and loop of the workgroup stays in bounds
-// whatever the tables hold).
+// The sequence of a block-table entry; false when the entry names no sequence, a sequence that
+// does not lie within the n_tokens rows, or a block start at or past the sequence's end (an empty
+// sequence included).  A workgroup whose entry is refused returns before any load, so every row
+// a kernel reads unconditionally (row start of the sequence) exists whatever the tables hold.
 __device__ __forceinline__ bool block_of(const AttnArgs& a, int blk, int64_t* s0, int* seqlen,
                                          int* start) {
   const int seq = a.tab[2 * blk];
@@ -130,7 +131,7 @@ __device__ __forceinline__ bool block_of(const AttnArgs& a, int blk, int64_t* s0
   if (seq < 0 || seq >= a.n_seq || *start < 0) return false;
   *s0 = a.cu[seq];
   *seqlen = a.cu[seq + 1] - a.cu[seq];
-  return *s0 >= 0 && *seqlen >= 0 && *s0 + *seqlen <= a.n_tokens;
+  return *s0 >= 0 && *seqlen > 0 && *start < *seqlen && *s0 + *seqlen <= a.n_tokens;
 }
 
 // the launch arguments, with the checks every attention entry point shares

@@ -1,54 +1,75 @@
 // NF4 double-quantised weights on gfx950: the HBM-rate dequant and the blockwise quantiser.
 //
-// Dequant (replaces solution/k_nf4.py:40-57).  One thread handles a "quad" of 32 weights: one
-// 16-byte load of packed nibbles (half a first-level block, so one absmax), 64 bytes of fp16 out.
-// A workgroup's 256 quads are 8192 weights, half a second-level block, so scale2/offset2 are
-// uniform (scalar loads).  The 64 output bytes of a lane are staged in LDS and written back
-// lane-contiguous, so every store instruction of a wave writes 1 KiB contiguous.  HBM traffic:
-// 2.516 bytes per weight (0.5 packed + 1/64 code + 8/16384 scale/offset in, 2 out).
+// Dequant (replaces solution/k_nf4.py:40-57).  Each lane converts kDqDwords packed dwords of 8
+// weights, dword j of wave lane l at wave offset 64 j + l: every load instruction of a wave reads
+// 256 contiguous bytes and every store instruction writes the 64 lanes' 16-byte results, 1 KiB
+// contiguous, straight from registers (no LDS staging, no barrier before the stores).  A wave's
+// 64 kDqDwords dwords lie in one second-level block (2048 dwords), so its scale2/offset2 are
+// wave-uniform (scalar loads).  They span 8 kDqDwords first-level blocks: lane k loads the codes
+// of blocks k, k + 64, ... and forms their absmax once, and each dword takes its block's absmax
+// from the owning lane by a cross-lane read.  Every global load of a lane (tables, codes, packed
+// dwords) is issued before the first conversion.  HBM traffic: 2.516 bytes per weight (0.5
+// packed + 1/64 code + 8/16384 scale/offset in, 2 out).
 #include "nf4_dev.h"
 
 namespace {
 
+// 8 dwords per lane in 256-thread workgroups (2856 per Qwen2.5-1.5B layer): measured on MI355X
+// against the former one-quad-per-lane kernel with LDS-staged stores (4.8-5.0 TB/s over 28 layer
+// buffers), 4 dwords per lane (4.8-5.0), 16 per lane (4.7-4.8; with 512 threads 5.1-5.2) and
+// 8 per lane with 512 threads (4.7-4.8): 5.1-5.2 TB/s, the same as this access pattern with the
+// conversion replaced by a plain copy of the packed words (5.2), so the conversion is hidden and
+// the read/write mix of the stream is the bound (writes alone reach 6.9 TB/s)
 constexpr int kDqThreads = 256;
-constexpr int kDqQuadsPerBlock = kDqThreads;   // 8192 weights = half a second-level block
+constexpr int kDqDwords = 8;                                   // packed dwords per lane
+constexpr int kDqOwn = kDqDwords / 8;                          // first-level codes per lane
+constexpr int kDqWgDwords = kDqThreads * kDqDwords;
+static_assert((kDqDwords == 8 || kDqDwords == 16) && kDqThreads >= 256 && kDqThreads % 64 == 0,
+              "a wave within one second-level block; one code2 entry per thread");
 
 __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
-    const u32x4* __restrict__ packed, const uint8_t* __restrict__ qabs,
+    const uint32_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
     const float* __restrict__ scale2, const float* __restrict__ offset2,
     const float* __restrict__ code2, const float* __restrict__ nf4, u32x4* __restrict__ out,
-    int64_t n_quads) {
+    int64_t n_dwords) {
   __shared__ float lut[16];
-  // the 256-entry second-level code table, loaded beside the packed bytes and the first-level
-  // codes, so that the absmax needs no global load that waits for another
   __shared__ float c2[256];
-  // per wave: 64 lanes x 4 chunks of 16 bytes, one pad chunk per 64 against bank conflicts
-  __shared__ u32x4 stage[kDqThreads / 64][64 * 4 + 4];
-  static_assert(kDqThreads == 256, "one code2 entry per thread");
-  dk_fill_lut(lut, nf4, threadIdx.x);
-  c2[threadIdx.x] = code2[threadIdx.x];
-  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-  const int64_t first = (int64_t)blockIdx.x * kDqQuadsPerBlock;
-  const int64_t sb = first >> 9;                    // 512 quads per second-level block
-  const float s2 = scale2[sb], o2 = offset2[sb];
-  const int64_t t = first + threadIdx.x;
-  const int64_t tc = t < n_quads ? t : n_quads - 1;   // clamped: its result is not stored
-  const u32x4 w = __builtin_nontemporal_load(packed + tc);
-  const uint8_t qa = qabs[tc >> 1];
-  __syncthreads();   // lut, c2
-  const float amax = dk_absmax(c2[qa], s2, o2);
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t d_wave = (int64_t)blockIdx.x * kDqWgDwords + wave * 64 * kDqDwords;
+  const int64_t last = n_dwords - 1;
+  // the tables' loads first (the LDS fill waits only for them), then the codes, then the dwords
+  const float c2v = code2[threadIdx.x & 255];
+  const float lutv = nf4[threadIdx.x & 15];
+  const int64_t blk_last = last / 8;
+  uint8_t q[kDqOwn];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = lane * 4 + j;
-    stage[wave][idx + (idx >> 6)] = dk_dequant_word(w[j], amax, lut);
+  for (int o = 0; o < kDqOwn; ++o) {
+    const int64_t blk = d_wave / 8 + 64 * o + lane;
+    q[o] = qabs[blk < blk_last ? blk : blk_last];
   }
-  __syncthreads();
-  const int64_t chunk0 = (first + wave * 64) * 4;     // first 8-weight chunk of this wave
-  const int64_t n_chunks = n_quads * 4;
+  const int64_t sb = (d_wave < last ? d_wave : last) / (DK_ELEMS_PER_SB / 8);   // wave-uniform
+  const float s2 = scale2[sb], o2 = offset2[sb];
+  uint32_t w[kDqDwords];
 #pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const int idx = j * 64 + lane;
-    if (chunk0 + idx < n_chunks) out[chunk0 + idx] = stage[wave][idx + (idx >> 6)];
+  for (int j = 0; j < kDqDwords; ++j) {
+    const int64_t d = d_wave + 64 * j + lane;
+    w[j] = __builtin_nontemporal_load(packed + (d < last ? d : last));   // clamped: not stored
+  }
+  if (threadIdx.x < 256) c2[threadIdx.x] = c2v;
+  if (threadIdx.x < 16) lut[threadIdx.x] = lutv;
+  __syncthreads();
+  // absmax of blocks (wave's first block + 64 o + lane); dword j of lane l is in block 8 j + l / 8
+  // of the wave, owned by lane (8 j + l / 8) % 64, entry (8 j) / 64
+  float amax_own[kDqOwn];
+#pragma unroll
+  for (int o = 0; o < kDqOwn; ++o) amax_own[o] = dk_absmax(c2[q[o]], s2, o2);
+#pragma unroll
+  for (int j = 0; j < kDqDwords; ++j) {
+    const float amax = __shfl(amax_own[j / 8], 8 * (j % 8) + (lane >> 3));
+    const int64_t d = d_wave + 64 * j + lane;
+    const u32x4 o = dk_dequant_word(w[j], amax, lut);
+    if (d <= last) out[d] = o;
   }
 }
 
@@ -163,11 +184,12 @@ extern "C" int dk_nf4_dequant(const uint8_t* packed, const uint8_t* qabs, const 
   if (n_qblocks == 0) return 0;
   if (!packed || !qabs || !scale2 || !offset2 || !code2 || !nf4 || !out_f16) return DK_ERR_INVALID;
   if (!dk_aligned(packed, 16) || !dk_aligned(out_f16, 16)) return DK_ERR_ALIGN;
-  const int64_t n_quads = n_qblocks * 2;
-  const int64_t grid = (n_quads + kDqQuadsPerBlock - 1) / kDqQuadsPerBlock;
+  const int64_t n_dwords = n_qblocks * 8;
+  const int64_t grid = (n_dwords + kDqWgDwords - 1) / kDqWgDwords;
+  if (grid > 0x7fffffff) return DK_ERR_INVALID;
   hipLaunchKernelGGL(nf4_dequant_kernel, dim3((unsigned)grid), dim3(kDqThreads), 0, stream,
-                     reinterpret_cast<const u32x4*>(packed), qabs, scale2, offset2, code2, nf4,
-                     reinterpret_cast<u32x4*>(out_f16), n_quads);
+                     reinterpret_cast<const uint32_t*>(packed), qabs, scale2, offset2, code2, nf4,
+                     reinterpret_cast<u32x4*>(out_f16), n_dwords);
   DK_CHECK_LAUNCH();
   return 0;
 }

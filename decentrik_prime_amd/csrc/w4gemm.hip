@@ -30,7 +30,6 @@
 // Split-K (shapes with too few tiles): a first launch stores fp32 partial tiles, a second launch
 // (the REDUCE instance: consumer waves only, no LDS) sums them in split order and runs the
 // epilogue.
-#include <atomic>
 #include <mutex>
 
 #include "gemm_common.h"
@@ -670,10 +669,9 @@ int launch_plan(const Plan& pl, GemmParams p, hipStream_t stream) {
 
 // Runs the plan.  Without a workspace: one phase (W dequantised in LDS), no split-K.  With one
 // (at least gemm_workspace bytes): split-K partials and, on the two-phase shapes, the weight
-// dequantised to fp16 in the workspace first (both launches on `stream`, in order).
-// dk_set_w4_gemm_mode: 0 the fused 256-tile path where it is fastest (split-K plans), 1 wherever
-// its plan takes the shape, 2 never (process-wide)
-std::atomic<int> g_w4_tile_mode{0};
+// dequantised to fp16 in the workspace first (both launches on `stream`, in order).  The weight's
+// `kernel` field picks the 256-tile kernel reading NF4: where it is fastest (AUTO: split-K
+// plans), wherever its plan takes the shape (TILE), or never (STAGED).
 
 template <bool TRANS, int EPI>
 int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, hipStream_t stream) {
@@ -682,8 +680,9 @@ int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, h
   // output tiles, long K): there it beats the separate dequant + fp16 GEMM (gate|up dX at
   // M = 2048: 179 against 188 us); elsewhere its per-step conversion costs more than the
   // dequant launch saves (measured on every config-4 shape), and the paths below run
-  const int mode = g_w4_tile_mode.load(std::memory_order_relaxed);
-  if (mode == 1 || (mode == 0 && ws && hgemm_workspace(p.M, p.N, p.K, EPI) > 0)) {
+  const int mode = w->kernel;
+  if (mode == DK_W4_KERNEL_TILE ||
+      (mode == DK_W4_KERNEL_AUTO && ws && hgemm_workspace(p.M, p.N, p.K, EPI) > 0)) {
     const int r = hgemm_launch<TRANS, EPI, true>(p, ws, ws_bytes, stream);
     if (r != kHgemmDeclined) return r;
   }
@@ -708,7 +707,8 @@ int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, h
 
 bool weight_ok(const dk_nf4_weight* w) {
   return w && w->packed && w->qabs && w->scale2 && w->offset2 && w->code2 && w->nf4 &&
-         w->rows > 0 && w->cols > 0 && (w->rows * w->cols) % DK_ELEMS_PER_SB == 0;
+         w->rows > 0 && w->cols > 0 && (w->rows * w->cols) % DK_ELEMS_PER_SB == 0 &&
+         w->kernel >= DK_W4_KERNEL_AUTO && w->kernel <= DK_W4_KERNEL_STAGED;
 }
 
 void set_weight(GemmParams& p, const dk_nf4_weight* w) {
@@ -936,12 +936,6 @@ int dispatch_w4(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes
 
 }  // namespace
 
-extern "C" int dk_set_w4_gemm_mode(int mode) {
-  if (mode < 0 || mode > 2) return DK_ERR_INVALID;
-  g_w4_tile_mode.store(mode, std::memory_order_relaxed);
-  return 0;
-}
-
 extern "C" int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m,
                                      const dk_nf4_weight* w, const void* bias,
                                      const dk_lora_term* terms, int n_terms, int64_t rank,
@@ -1088,13 +1082,18 @@ constexpr int kMaxDevices = 64;
 std::mutex g_scratch_lock;
 void* g_scratch_ptr[kMaxDevices] = {};
 
-// The device address of this device's scratch array (looked up on the first call on a device).
-int scratch_on_current_device(void** out) {
+// The device address of this device's scratch array (looked up on the first call on a device,
+// which must not be under stream capture: the lookup may load the code object, which a capture
+// does not allow).
+int scratch_on_current_device(hipStream_t stream, void** out) {
   int dev = 0;
   if (hipError_t e = hipGetDevice(&dev)) return (int)e;
   if (dev < 0 || dev >= kMaxDevices) return DK_ERR_INVALID;
   std::lock_guard<std::mutex> hold(g_scratch_lock);
   if (!g_scratch_ptr[dev]) {
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (hipError_t e = hipStreamIsCapturing(stream, &cap)) return (int)e;
+    if (cap != hipStreamCaptureStatusNone) return DK_ERR_CAPTURE;
     void* ptr = nullptr;
     if (hipError_t e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch))) return (int)e;
     if (!ptr) return DK_ERR_INVALID;
@@ -1116,14 +1115,17 @@ extern "C" int dk_h16_linear_bwd_dx_lora_noalloc(const void* dy, int64_t lddy, i
   if (int e = linear_bwd_params(p, dy, lddy, m, rows, cols, terms, n_terms, rank, dx, lddx,
                                 out_mode))
     return e;
-  // the partials this call's plan needs (0 without split-K), within the array's size
+  // the partials this call's plan needs (0 without split-K), within the array's size; the
+  // dispatch is given the whole array, so a fallback plan (one the 256-tile kernel declines at
+  // launch, e.g. for an unaligned dx) finds room for its own partials too
   const int64_t need = dk_h16_workspace(m, rows, cols, DK_OP_LINEAR_BWD_DX);
   if (need > DK_NOALLOC_SCRATCH_BYTES) return DK_ERR_WORKSPACE;
   void* ws = nullptr;
   if (need > 0) {
-    if (int e = scratch_on_current_device(&ws)) return e;
+    if (int e = scratch_on_current_device(stream, &ws)) return e;
   }
-  return dispatch_h16<true, EPI_LINEAR>(p, w16, ws, need, side, stream);
+  return dispatch_h16<true, EPI_LINEAR>(p, w16, ws, ws ? DK_NOALLOC_SCRATCH_BYTES : 0, side,
+                                        stream);
 }
 
 extern "C" int dk_h16_gateup_swiglu_fwd(const void* x, int64_t ldx, int64_t m, const void* w16,

@@ -47,36 +47,53 @@ class PackedBatch:
     T: int
 
 
+def _row_length(mask_row):
+    """Real tokens of one right-padded row: n when the row's mask is n ones followed by zeros
+    (values other than 0 and 1 do not qualify), else None."""
+    n = int(mask_row.count_nonzero())
+    if bool((mask_row[:n] == 1).all()) and bool((mask_row[n:] == 0).all()):
+        return n
+    return None
+
+
 def pack(input_ids, attention_mask, labels, vocab):
-    """Host-side packing of a right-padded batch (the reference's FastQwen2.pack,
-    solution/fast_qwen.py:803-871): the real tokens of each row concatenated, each token's target
-    the next position's label (-100 and the row's last token: none), tokens with a target sorted
-    first.  Returns None when the batch is not exactly packable (the caller then uses the stock
-    path): a mask that is not one contiguous run of ones from the start of each row, an empty row,
-    or an id or target outside the vocabulary."""
+    """Host-side packing of a right-padded batch (the contract of the reference's
+    FastQwen2.pack, solution/fast_qwen.py:803-871): the real tokens of each row concatenated; the
+    target of a row's token t is the row's label at t + 1 (-1 past the padded length, and every
+    negative label, -100 included, means none); tokens with a target first in the sorted order,
+    each group in token order.  Returns None when the batch is not exactly packable (the caller
+    then uses the stock path): a row whose mask is not a run of ones from its start, an empty row,
+    or an id or target outside the vocabulary.
+
+    Rows are walked one at a time (a batch has a handful): each row's run length is validated,
+    its ids and targets are sliced out, and the sorted order is a stable sort on "has no
+    target"."""
     if input_ids.dim() != 2 or attention_mask.shape != input_ids.shape or labels.shape != input_ids.shape:
         return None
     B, T = input_ids.shape
-    mask = attention_mask.to("cpu", torch.int64)
-    lens = mask.sum(1)
-    if not torch.equal(mask, (torch.arange(T)[None, :] < lens[:, None]).to(torch.int64)):
-        return None
-    if int(lens.min()) < 1:
-        return None
-    keep = mask.bool()
-    ids = input_ids.to("cpu", torch.int64)[keep]
-    shifted = torch.full((B, T), -1, dtype=torch.int64)
-    shifted[:, :-1] = labels.to("cpu", torch.int64)[:, 1:]
-    tgt = shifted[keep]
-    tgt[tgt < 0] = -1
+    ids_rows = input_ids.to("cpu", torch.int64)
+    lab_rows = labels.to("cpu", torch.int64)
+    mask_rows = attention_mask.to("cpu", torch.int64)
+    lens, ids, tgt = [], [], []
+    for b in range(B):
+        n = _row_length(mask_rows[b])
+        if not n:
+            return None
+        lens.append(n)
+        ids.append(ids_rows[b, :n])
+        t = torch.full((n,), -1, dtype=torch.int64)
+        shifted = lab_rows[b, 1:n + 1]          # T - 1 labels at most: the last token may get none
+        t[:shifted.numel()] = shifted
+        tgt.append(t.clamp_(min=-1))
+    ids, tgt = torch.cat(ids), torch.cat(tgt)
     if int(ids.min()) < 0 or int(ids.max()) >= vocab or int(tgt.max()) >= vocab:
         return None
-    rows = torch.arange(B)[:, None].expand(B, T)[keep]
+    rows = torch.repeat_interleave(torch.arange(B, dtype=torch.int64), torch.tensor(lens))
     has = tgt >= 0
-    perm = torch.cat([torch.nonzero(has)[:, 0], torch.nonzero(~has)[:, 0]])
-    return PackedBatch(lens=[int(v) for v in lens], ids=ids, tgt=tgt, perm=perm,
-                       tgt_sorted=tgt[perm], row_sorted=rows[perm], valid_sorted=has[perm],
-                       n_real=int(ids.numel()), n_lab=int(has.sum()), B=B, T=T)
+    perm = torch.sort((~has).to(torch.int8), stable=True).indices
+    return PackedBatch(lens=lens, ids=ids, tgt=tgt, perm=perm, tgt_sorted=tgt[perm],
+                       row_sorted=rows[perm], valid_sorted=has[perm], n_real=int(ids.numel()),
+                       n_lab=int(has.sum()), B=B, T=T)
 
 
 def batch_metrics(batch, stats):

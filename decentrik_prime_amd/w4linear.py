@@ -19,12 +19,21 @@ from .quant import code2_on, nf4_table
 
 
 class W4:
-    """An NF4 weight [rows, cols] on the GPU: views of the four sections plus the two tables."""
+    """An NF4 weight [rows, cols] on the GPU: views of the four sections plus the two tables.
 
-    def __init__(self, packed, qabs, scale2, offset2, code2, nf4, rows, cols):
+    ``kernel`` (``_lib.DK_W4_KERNEL_*``) is the GEMM kernel the ``dk_w4_*`` calls on this weight
+    run: AUTO (the library's choice), TILE (the 256-tile kernel reading NF4 wherever its plan
+    takes the shape) or STAGED (never that kernel).  It travels with every call (the weight
+    struct's ``kernel`` field); ``with_kernel`` gives another view of the same sections."""
+
+    def __init__(self, packed, qabs, scale2, offset2, code2, nf4, rows, cols,
+                 kernel=_lib.DK_W4_KERNEL_AUTO):
         self.packed, self.qabs, self.scale2, self.offset2 = packed, qabs, scale2, offset2
         self.code2, self.nf4 = code2, nf4
         self.rows, self.cols = int(rows), int(cols)
+        if kernel not in (_lib.DK_W4_KERNEL_AUTO, _lib.DK_W4_KERNEL_TILE, _lib.DK_W4_KERNEL_STAGED):
+            raise ValueError(f"unknown W4 kernel choice {kernel}")
+        self.kernel = int(kernel)
         n = self.rows * self.cols
         if n % 16384:
             raise ValueError("an NF4 weight must fill whole second-level blocks (16384 weights)")
@@ -33,7 +42,12 @@ class W4:
             raise ValueError("NF4 section sizes do not match the weight shape")
         self._c = _lib.NF4WeightC(packed.data_ptr(), qabs.data_ptr(), scale2.data_ptr(),
                                   offset2.data_ptr(), code2.data_ptr(), nf4.data_ptr(),
-                                  self.rows, self.cols)
+                                  self.rows, self.cols, self.kernel)
+
+    def with_kernel(self, kernel):
+        """The same weight (the same section tensors) with another ``kernel`` choice."""
+        return W4(self.packed, self.qabs, self.scale2, self.offset2, self.code2, self.nf4,
+                  self.rows, self.cols, kernel)
 
     @property
     def shape(self):
@@ -80,12 +94,6 @@ class W4:
 
 _WS = {}
 _WS_LOCK = threading.Lock()
-
-
-def set_w4_gemm_mode(mode):
-    """Which kernel the NF4-reading GEMMs run (dk_set_w4_gemm_mode): 0 the 256-tile kernel reading
-    NF4 where its plan splits K (default), 1 wherever its plan takes the shape, 2 never."""
-    _lib.check(_lib.lib().dk_set_w4_gemm_mode(int(mode)), "dk_set_w4_gemm_mode")
 
 
 def _workspace(w, m, op, device):

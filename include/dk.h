@@ -8,8 +8,9 @@
  *     dimension is given;
  *   - return 0 on success, a negative DK_ERR_* for an argument error detected before any launch,
  *     or a positive hipError_t from the launch;
- *   - no mutable global state but the NF4 GEMM mode of dk_set_w4_gemm_mode (an atomic setting
- *     each call reads once): entry points may be called from any host thread.
+ *   - no mutable global state (only once-filled per-device caches: the CU count, the address of
+ *     the allocation-free entry point's device array): entry points may be called from any host
+ *     thread; every choice a call makes comes from its own arguments.
  */
 #ifndef DK_H
 #define DK_H
@@ -24,6 +25,8 @@ extern "C" {
 #define DK_ERR_INVALID (-1)   /* a size or a null pointer that the operation cannot accept */
 #define DK_ERR_ALIGN (-2)     /* a pointer or an offset breaks the alignment the kernel needs */
 #define DK_ERR_WORKSPACE (-3) /* the workspace is missing or too small */
+#define DK_ERR_CAPTURE (-4)   /* a one-time set-up that cannot run under stream capture is still
+                                 due: make the same call once outside capture first */
 
 /* An NF4 double-quantised weight [rows, cols] (out_features x in_features), element
  * e = row * cols + col.  The four sections are those of the reference's repacked layer
@@ -39,7 +42,20 @@ typedef struct dk_nf4_weight {
   const float* nf4;       /* [16]  */
   int64_t rows;
   int64_t cols;
+  int32_t kernel;         /* DK_W4_KERNEL_*: which GEMM kernel the dk_w4_* calls on this weight
+                             run (0, the default, lets the library choose) */
 } dk_nf4_weight;
+
+/* Values of dk_nf4_weight.kernel (no counterpart in the reference: its GEMMs read a dequantised
+ * workspace).  The 256 x 256-tile kernel can read the packed NF4 weight itself, each workgroup
+ * dequantising its W tiles into LDS (bit-identical to the fp16-weight form); otherwise the weight
+ * is first dequantised into the workspace and read as fp16, or the 128 x 128 warp-specialised
+ * kernel dequantises in LDS.  AUTO: the tile kernel reads NF4 where that is fastest (its split-K
+ * plans: few output tiles, long K); TILE: wherever its plan takes the shape; STAGED: never.  The
+ * choice travels with each call's weight argument: the library keeps no setting of its own. */
+#define DK_W4_KERNEL_AUTO 0
+#define DK_W4_KERNEL_TILE 1
+#define DK_W4_KERNEL_STAGED 2
 
 /* Human-readable text for a return code (static storage). */
 const char* dk_error_string(int code);
@@ -230,15 +246,6 @@ int dk_w4_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const dk_nf4_we
 #define DK_OP_GATEUP_SWIGLU_FWD 2  /* dk_w4_gateup_swiglu_fwd */
 #define DK_OP_DOWN_SWIGLU_BWD 3    /* dk_w4_down_swiglu_bwd */
 int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op);
-
-/* Which kernel the dk_w4_* GEMMs run (no counterpart in the reference: its GEMMs read a
- * dequantised workspace).  The 256 x 256-tile kernel can read the packed NF4 weight itself,
- * each workgroup dequantising its W tiles into LDS (bit-identical to the fp16-weight form), or
- * the weight is first dequantised into the workspace and read as fp16, or the 128 x 128
- * warp-specialised kernel dequantises in LDS.  mode 0 (default): the tile kernel reads NF4
- * where its plan splits K (few output tiles, long K), where that is fastest; 1: wherever its
- * plan takes the shape; 2: never.  Process-wide; DK_ERR_INVALID for another mode. */
-int dk_set_w4_gemm_mode(int mode);
 
 /* dk_w4_workspace(m, w, backward ? DK_OP_LINEAR_BWD_DX : DK_OP_LINEAR_FWD). */
 int64_t dk_w4_linear_workspace(int64_t m, const dk_nf4_weight* w, int backward);
@@ -446,7 +453,10 @@ int dk_h16_linear_bwd_dx_lora_sums(const void* dy, int64_t lddy, int64_t m, cons
  * DK_ERR_WORKSPACE before any launch.  Results are bit-identical to dk_h16_linear_bwd_dx_lora
  * with a workspace of dk_h16_workspace bytes.  Every call on a device shares that device's array:
  * calls that overlap on one device (two streams, two threads) race and must be serialised by the
- * caller. */
+ * caller.  The array's device address is looked up (hipGetSymbolAddress) by the first call on
+ * each device; under stream capture that first call returns DK_ERR_CAPTURE before doing anything,
+ * so a caller that captures makes one call outside capture first (any later call, captured or
+ * not, uses the address found then). */
 #define DK_NOALLOC_SCRATCH_BYTES (64ll << 20)
 int dk_h16_linear_bwd_dx_lora_noalloc(const void* dy, int64_t lddy, int64_t m, const void* w16,
                                       int64_t rows, int64_t cols, const dk_lora_term* terms,

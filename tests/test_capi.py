@@ -34,10 +34,16 @@ def test_argument_errors_come_back_before_launch():
     assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 100, 8, ctypes.byref(w), None, None, None, 0,
                                 2.0, ctypes.c_void_p(16), 100, None, 0, None) == _lib.DK_ERR_INVALID
     assert lib.dk_w4_linear_workspace(2048, ctypes.byref(w), 0) == 0
-    # the NF4 GEMM mode: 0, 1, 2 only (a host-side setting; 0 restored)
-    assert lib.dk_set_w4_gemm_mode(3) == _lib.DK_ERR_INVALID
-    assert lib.dk_set_w4_gemm_mode(-1) == _lib.DK_ERR_INVALID
-    assert lib.dk_set_w4_gemm_mode(2) == 0 and lib.dk_set_w4_gemm_mode(0) == 0
+    # the per-weight kernel choice: AUTO, TILE or STAGED only, refused before any launch
+    for bad in (3, -1):
+        wk = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 1536, 1536, bad)
+        assert lib.dk_w4_linear_fwd(ctypes.c_void_p(16), 1536, 8, ctypes.byref(wk), None, None, None,
+                                    0, 2.0, ctypes.c_void_p(16), 1536, None, 0,
+                                    None) == _lib.DK_ERR_INVALID
+        assert lib.dk_w4_workspace(2048, ctypes.byref(wk), _lib.DK_OP_LINEAR_FWD) == 0
+    for good in (_lib.DK_W4_KERNEL_AUTO, _lib.DK_W4_KERNEL_TILE, _lib.DK_W4_KERNEL_STAGED):
+        wk = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 1536, 1536, good)
+        assert lib.dk_w4_workspace(2048, ctypes.byref(wk), _lib.DK_OP_LINEAR_FWD) == 1536 * 1536 * 2
     # workspace sizes (no device access): split-K partials, and the fp16 weight of the two-phase
     # path (from 512 rows on, outputs of 1536 columns or more)
     wq = _lib.NF4WeightC(16, 16, 16, 16, 16, 16, 1536, 1536)

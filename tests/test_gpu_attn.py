@@ -150,3 +150,31 @@ def test_attention_rescale_and_table_order(torch):
     _close(host(g1[0]), dq_ref, 3e-2, 2e-2, "dq")
     _close(host(g1[1]), dkp_ref, 3e-2, 2e-2, "dk per query head")
     _close(host(g1[2]), dvp_ref, 3e-2, 2e-2, "dv per query head")
+
+
+def test_table_entries_without_rows_are_skipped(torch):
+    """Block-table entries that name no rows: an empty sequence (cu[s] == cu[s + 1]) and blocks
+    starting at or past their sequence's end.  The kernels skip such workgroups before any load,
+    so the results are bit-identical to the run on the clean tables."""
+    from decentrik_prime_amd import k_attn
+    lens = [37, 0, 200]
+    log(f"attention with table entries that name no rows, lens {lens}")
+    n = sum(lens)
+    rng = np.random.default_rng(99)
+    qkv = torch.from_numpy((rng.standard_normal((n, (NQ + 2 * NKV) * HD)) * 0.8)
+                           .astype(np.float16)).cuda()
+    dout = torch.from_numpy(rng.standard_normal((n, NQ * HD)).astype(np.float16)).cuda()
+    clean = k_attn.meta_for(lens, "cuda")
+    extra = [1, 0, 0, 128, 2, 256, 1, 128]   # empty sequence; starts at or past the end
+    i32 = dict(dtype=torch.int32, device="cuda")
+    tf = torch.cat([clean.tab_fwd, torch.tensor(extra, **i32)])
+    tb = torch.cat([torch.tensor(extra, **i32), clean.tab_bwd])
+    dirty = k_attn.AttnMeta(clean.cu, tf, tb, tf.numel() // 2, tb.numel() // 2, n)
+    results = []
+    for meta in (clean, dirty):
+        out, lse = k_attn.attention_forward(qkv, meta, NQ, NKV, HD)
+        dq, dkp, dvp = k_attn.attention_backward(qkv, out, lse, dout, meta, NQ, NKV, HD)
+        results.append([host(t) for t in (out, lse, dq, dkp, dvp)])
+    torch.cuda.synchronize()
+    for name, a, b in zip(("out", "lse", "dq", "dk", "dv"), *results):
+        assert np.array_equal(a.view(np.uint8), b.view(np.uint8)), f"{name} changed"

@@ -12,6 +12,7 @@ scale for the small-valued gradients)."""
 import numpy as np
 import pytest
 
+from decentrik_prime_amd import _lib
 from tests.helpers import assert_close, cuda, cuda16, host, log, lora_inputs, nf4_weight, to_w4
 
 pytestmark = pytest.mark.gpu
@@ -32,6 +33,11 @@ def _same(a, b, what):
         bad = np.argwhere(a != b)
         raise AssertionError(f"{what}: {len(bad)} of {a.size} differ; first at {bad[0].tolist()}: "
                              f"{a[tuple(bad[0])]} vs {b[tuple(bad[0])]}")
+
+
+def _abs_close(got, want, what):
+    """rtol 1e-2 / atol 2e-2 on the values themselves (the forward outputs, of order 1)."""
+    assert_close(np.asarray(got, np.float64), np.asarray(want, np.float64), RTOL, ATOL, what)
 
 
 def _near(a, b, what):
@@ -165,11 +171,12 @@ def test_h16_mlp(torch, m):
 
 @pytest.mark.parametrize("m", [2048, 1000])
 def test_w4_tile_kernel_reads_nf4(torch, m):
-    """dk_set_w4_gemm_mode(1): every NF4-reading GEMM whose shape the 256-tile plan takes runs on
-    that kernel with its workgroups dequantising the W tiles into LDS (256 x 256 tiles, the
-    128 x 128 quarters, split K; NT and NN; linear with LoRA terms and bias, the SwiGLU forward
-    and backward), and must give the same bits as the fp16-weight form, which runs the same plan
-    on the GPU-dequantised weight."""
+    """Weights marked DK_W4_KERNEL_TILE: every NF4-reading GEMM whose shape the 256-tile plan
+    takes runs on that kernel with its workgroups dequantising the W tiles into LDS (256 x 256
+    tiles, the 128 x 128 quarters, split K; NT and NN; linear with LoRA terms and bias, the SwiGLU
+    forward and backward), and must give the same bits as the fp16-weight form, which runs the
+    same plan on the GPU-dequantised weight.  The gate|up forward and the down forward are also
+    checked against the oracle directly (fp32 GEMMs of the oracle's dequantised weights)."""
     from decentrik_prime_amd import w4linear
     from oracle import linear
     log(f"W4 tile kernel vs fp16 form, M={m}")
@@ -196,36 +203,43 @@ def test_w4_tile_kernel_reads_nf4(torch, m):
     dh = cuda16((rng.standard_normal((m, D)) * 1e-2).astype(F16))
 
     def run(nf4):
+        tile = _lib.DK_W4_KERNEL_TILE
+        wq, wo, wg, wd = (w.with_kernel(tile) for w in (w_qkv, w_o, w_gu, w_d))
         pick = (lambda k: None) if nf4 else (lambda k: h[k])   # noqa: E731
         out = {}
-        out["qkv"] = w4linear.linear_forward_lora(tx, w_qkv, bias, fterms, w16=pick("qkv"))
-        out["o"] = w4linear.linear_forward(tx, w_o, w16=pick("o"))
-        out["act"], gu = w4linear.gateup_swiglu_forward(tx, w_gu, w16=pick("gu"))
+        out["qkv"] = w4linear.linear_forward_lora(tx, wq, bias, fterms, w16=pick("qkv"))
+        out["o"] = w4linear.linear_forward(tx, wo, w16=pick("o"))
+        out["act"], gu = w4linear.gateup_swiglu_forward(tx, wg, w16=pick("gu"))
         out["gu"] = gu.clone()
-        out["down"] = w4linear.linear_forward(out["act"], w_d, w16=pick("d"))
-        w4linear.down_swiglu_backward(dh, w_d, gu, w16=pick("d"))
+        out["down"] = w4linear.linear_forward(out["act"], wd, w16=pick("d"))
+        w4linear.down_swiglu_backward(dh, wd, gu, w16=pick("d"))
         out["dgu"] = gu
-        out["dx_gu"] = w4linear.linear_backward_dx(gu, w_gu, out_dtype=torch.float16,
+        out["dx_gu"] = w4linear.linear_backward_dx(gu, wg, out_dtype=torch.float16,
                                                    w16=pick("gu"))
-        out["dx_o"] = w4linear.linear_backward_dx(dy_o, w_o, w16=pick("o"))
-        out["dx_qkv"] = w4linear.linear_backward_dx_lora(dqkv, w_qkv, bterms, w16=pick("qkv"))
+        out["dx_o"] = w4linear.linear_backward_dx(dy_o, wo, w16=pick("o"))
+        out["dx_qkv"] = w4linear.linear_backward_dx_lora(dqkv, wq, bterms, w16=pick("qkv"))
         return out
 
     want = run(False)
-    w4linear.set_w4_gemm_mode(1)
-    try:
-        got = run(True)
-        torch.cuda.synchronize()
-    finally:
-        w4linear.set_w4_gemm_mode(0)
+    got = run(True)
+    torch.cuda.synchronize()
     for k in want:
         _same(got[k], want[k], f"{k}: W4 tile kernel vs fp16 form")
+    # the oracle: gate|up forward (act and the saved [g | u]) and the down forward on the NF4
+    # tile kernel's own act, at rtol 1e-2 / atol 2e-2
+    from oracle import mlp
+    gu_ref = linear.mm16(x, host(h["gu"]).reshape(2 * I, D).T)
+    act_ref = mlp.gated_silu_fwd(gu_ref)
+    _abs_close(host(got["act"]), act_ref, "act: W4 tile kernel vs oracle")
+    _abs_close(host(got["gu"]), gu_ref, "[g | u]: W4 tile kernel vs oracle")
+    down_ref = linear.mm16(host(got["act"]), host(h["d"]).reshape(D, I).T)
+    _abs_close(host(got["down"]), down_ref, "down forward: W4 tile kernel vs oracle")
 
 
 def test_w4_own_kernel_split_k(torch):
-    """dk_set_w4_gemm_mode(2): the split-K shapes at M = 2048 (down forward, K = 8960; gate|up dX,
-    K = 17920), which mode 0 gives to the 256-tile kernel, run on the NF4-form kernel's own split-K
-    plan instead (its REDUCE launch).  Its summation order differs, so it is checked against the
+    """Weights marked DK_W4_KERNEL_STAGED: the split-K shapes at M = 2048 (down forward,
+    K = 8960; gate|up dX, K = 17920), which AUTO gives to the 256-tile kernel, run on the NF4-form
+    kernel's own split-K plan instead (its REDUCE launch).  Its summation order differs, so it is checked against the
     fp16 form at the split-K tolerance and against the oracle."""
     from decentrik_prime_amd import w4linear
     from oracle import linear
@@ -240,13 +254,10 @@ def test_w4_own_kernel_split_k(torch):
     tact, tgu = cuda16(act), cuda16(gu)
     want_y = w4linear.linear_forward(tact, wd, w16=hd)
     want_dx = w4linear.linear_backward_dx(tgu, wg, w16=hg)
-    w4linear.set_w4_gemm_mode(2)
-    try:
-        got_y = w4linear.linear_forward(tact, wd)
-        got_dx = w4linear.linear_backward_dx(tgu, wg)
-        torch.cuda.synchronize()
-    finally:
-        w4linear.set_w4_gemm_mode(0)
+    staged = _lib.DK_W4_KERNEL_STAGED
+    got_y = w4linear.linear_forward(tact, wd.with_kernel(staged))
+    got_dx = w4linear.linear_backward_dx(tgu, wg.with_kernel(staged))
+    torch.cuda.synchronize()
     _near(got_y, want_y, "down forward: own split-K vs fp16 form")
     _near(got_dx, want_dx, "gate|up dX: own split-K vs fp16 form")
     _scaled_close(host(got_y), linear.mm16(act, qd["deq"].T), "down forward vs oracle")

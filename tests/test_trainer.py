@@ -45,6 +45,37 @@ def test_pack_tokens_targets_and_order():
     assert b.tgt_sorted.tolist() == np.array(want)[b.perm.numpy()].tolist()
 
 
+@pytest.mark.parametrize("seed", range(6))
+def test_pack_against_a_token_walk(seed):
+    """Random batches, full rows included, against a walk over every (row, position): the target
+    of a real token is the row's next label, even when that label sits at a padded position (the
+    collator's -100 there is what makes it none), and -1 past the padded length."""
+    rng = np.random.default_rng(100 + seed)
+    B, T, vocab = int(rng.integers(1, 5)), int(rng.integers(2, 12)), 40
+    lens = [int(v) for v in rng.integers(1, T + 1, B)]
+    ids = torch.from_numpy(rng.integers(0, vocab, (B, T)))
+    mask = (torch.arange(T)[None, :] < torch.tensor(lens)[:, None]).to(torch.int64)
+    labels = torch.from_numpy(np.where(rng.random((B, T)) < 0.3, -100,
+                                       rng.integers(0, vocab, (B, T))))
+    b = trainer.pack(ids, mask, labels, vocab)
+    toks, tg, rows = [], [], []
+    for r in range(B):
+        for t in range(T):
+            if mask[r, t] == 1:
+                toks.append(int(ids[r, t]))
+                nxt = int(labels[r, t + 1]) if t + 1 < T else -100
+                tg.append(nxt if nxt >= 0 else -1)
+                rows.append(r)
+    assert b.lens == lens and b.ids.tolist() == toks and b.tgt.tolist() == tg
+    order = [i for i, v in enumerate(tg) if v >= 0] + [i for i, v in enumerate(tg) if v < 0]
+    assert b.perm.tolist() == order
+    assert b.row_sorted.tolist() == [rows[i] for i in order]
+    assert b.n_lab == sum(v >= 0 for v in tg) and b.n_real == len(toks)
+    # a mask value other than 0 and 1 makes the batch unpackable
+    mask[0, 0] = 2
+    assert trainer.pack(ids, mask, labels, vocab) is None
+
+
 @pytest.mark.parametrize("case", ["gap", "empty_row", "id_range", "label_range", "shape"])
 def test_pack_refuses_what_it_cannot_pack(case):
     ids, mask, labels = _batch()

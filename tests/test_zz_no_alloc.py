@@ -88,3 +88,39 @@ def test_noalloc_dx_matches_workspace_form(torch):
         assert 0 < nbytes <= _lib.DK_NOALLOC_SCRATCH_BYTES, nbytes      # the split-K plan ran
         assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), f"M={m}: differs"
         assert bool(torch.isfinite(got.float()).all())
+
+
+def test_noalloc_dx_under_graph_capture(torch):
+    """The no-alloc entry point captured in a HIP graph (torch.cuda.graph) after one call outside
+    capture: every replay, with eager work and synchronisations between them, gives the bits of
+    the workspace form, and so does an eager call afterwards."""
+    from decentrik_prime_amd import _lib
+    lib = _lib.lib()
+    ks = float(np.float32(1.0) / np.float32(0.95))
+    m, rows, cols = 1024, 8960, 1536
+    log(f"no-alloc dX under graph capture: M={m} K={rows} N={cols}")
+    dy, w16, terms = _case(torch, m, rows, cols, True, seed=7)
+    want, _ = _with_workspace(torch, dy, w16, terms, _lib.DK_OUT_F32, ks)
+    _no_alloc(torch, dy, w16, terms, _lib.DK_OUT_F32, ks)     # outside capture: the set-up call
+    torch.cuda.synchronize()
+    out = torch.empty(m, cols, dtype=torch.float32, device="cuda")
+    arr = _terms_c(terms, ks)
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        rc = lib.dk_h16_linear_bwd_dx_lora_noalloc(dy.data_ptr(), dy.stride(0), m, w16.data_ptr(),
+                                                   rows, cols, arr, len(terms), 16, out.data_ptr(),
+                                                   cols, _lib.DK_OUT_F32, None,
+                                                   _lib.stream_handle())
+    _lib.check(rc, "dk_h16_linear_bwd_dx_lora_noalloc (captured)")
+    for r in range(3):
+        out.fill_(float("nan"))
+        graph.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out.view(torch.uint8), want.view(torch.uint8)), f"replay {r} differs"
+        # eager work on the same array between replays (a smaller plan)
+        small, _, _ = _case(torch, 512, rows, cols, False, seed=r)
+        _no_alloc(torch, small, w16, [], _lib.DK_OUT_F16, ks)
+        torch.cuda.synchronize()
+    got = _no_alloc(torch, dy, w16, terms, _lib.DK_OUT_F32, ks)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.uint8), want.view(torch.uint8)), "eager call after replays"
