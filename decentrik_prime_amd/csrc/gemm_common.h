@@ -41,6 +41,8 @@ struct GemmParams {
   f16* gu;              // SWIGLU_FWD: optional [M][2I] output; SWIGLU_BWD: [M][2I] in/out
   int tiles_m, tiles_n;
   int m_fastest;        // tile order: row tiles fastest (1) or column tiles fastest (0)
+  int xcd_gm;           // 256-tile kernel: the 128 x 128 quarters split into a block per XCD,
+                        // xcd_gm blocks along M by 8 / xcd_gm along N (0: runs of quarters)
   int splits;           // split-K factor (1: none)
   float* part;          // split-K partial tiles [tiles][splits][BM * BN] fp32
   SideDequant side;     // dequant work carried by the launch's last side.wgs workgroups

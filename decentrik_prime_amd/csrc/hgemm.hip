@@ -759,11 +759,26 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs) {
         p.splits > 1 ? p.part + ((int64_t)tile * p.splits + split) * kTile * kTile : nullptr;
     gemm_tile<TRANS, EPI, 256, 256, 2, 2, W4>(p, m0, n0, kt0, nk, part, As, Bs, w4tab);
   } else {
-    int t = b - qbase;
-    if ((tail_wgs & 7) == 0 && (qbase & 7) == 0) t = (t & 7) * (tail_wgs >> 3) + (t >> 3);
-    const int parent = main_tiles + t / 4, quarter = t % 4;
-    const int64_t m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
-    const int64_t n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
+    int64_t m0, n0;
+    const int t = b - qbase;
+    if (p.xcd_gm) {
+      // the quarters' parent tiles form a grid of tiles_m rows by the columns past the full tiles;
+      // XCD x = t % 8 (workgroups are dealt to the XCDs round-robin) takes block (x % gm, x / gm)
+      // of a gm x (8 / gm) split of that grid, so that its L2 holds the A rows and W rows of its
+      // block only (the hplan choice of gm minimises them), and walks the block's quarters
+      // M-fastest
+      const int gm = p.xcd_gm, x = t & 7, r = t >> 3;
+      const int bm = p.tiles_m / gm, bn = (tail_wgs / 4 / p.tiles_m) / (8 / gm);
+      const int qm = r % (2 * bm), qn = r / (2 * bm);
+      m0 = (int64_t)((x % gm) * bm) * kTile + 128 * qm;
+      n0 = (int64_t)(main_tiles / p.tiles_m + (x / gm) * bn) * kTile + 128 * qn;
+    } else {
+      int u = t;
+      if ((tail_wgs & 7) == 0 && (qbase & 7) == 0) u = (u & 7) * (tail_wgs >> 3) + (u >> 3);
+      const int parent = main_tiles + u / 4, quarter = u % 4;
+      m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
+      n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
+    }
     if (m0 >= p.M) return;
     gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk_all, nullptr, As, Bs, w4tab);
   }
@@ -823,10 +838,33 @@ struct HPlan {
   bool ok;
   int64_t tiles_m, tiles_n, main_wgs, tail_wgs;
   int splits;
+  int xcd_gm;   // GemmParams::xcd_gm
 };
 
-HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
-  HPlan h{false, 0, 0, 0, 0, 1};
+// The split of the quarters' parent grid (tiles_m rows by the tail's columns) into one block per
+// XCD, gm blocks along M by 8 / gm along N, that minimises the rows of A plus rows of W one XCD
+// reads (bm + bn tiles); 0 when no split divides the grid (then runs of quarters per XCD).
+int xcd_blocks(int64_t tiles_m, int64_t main_wgs, int64_t tail_wgs, int qbase) {
+  if (tail_wgs <= 0 || tail_wgs % 32 || qbase % 8 || main_wgs % tiles_m) return 0;
+  const int64_t parents = tail_wgs / 4;
+  if (parents % tiles_m) return 0;
+  const int64_t cols = parents / tiles_m;
+  int best = 0;
+  int64_t cost = 0;
+  for (int gm = 1; gm <= 8; gm *= 2) {
+    const int gn = 8 / gm;
+    if (tiles_m % gm || cols % gn) continue;
+    const int64_t c = tiles_m / gm + cols / gn;
+    if (!best || c < cost) {
+      best = gm;
+      cost = c;
+    }
+  }
+  return best;
+}
+
+HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split) {
+  HPlan h{false, 0, 0, 0, 0, 1, 0};
   if (M <= 0 || N % kTile || K % kBK || K < kBK) return h;
   const int cus = cu_count();
   if (cus <= 0) return h;
@@ -867,6 +905,14 @@ HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
   return h;
 }
 
+HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
+  HPlan h = hplan_tiles(M, N, K, epi, no_split);
+  if (h.ok && h.splits == 1)
+    h.xcd_gm = xcd_blocks(h.tiles_m, h.main_wgs, h.tail_wgs,
+                          epi == EPI_SWIGLU_BWD ? 0 : (int)h.main_wgs);
+  return h;
+}
+
 }  // namespace
 
 int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
@@ -902,6 +948,7 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   p.tiles_m = (int)h.tiles_m;
   p.tiles_n = (int)h.tiles_n;
   p.splits = h.splits;
+  p.xcd_gm = h.xcd_gm;
   if (h.splits > 1) {
     // the partials go to the caller's workspace; without room for them, decline
     if (!ws || ws_bytes < h.main_wgs * kTile * kTile * (int64_t)sizeof(float) || !dk_aligned(ws, 256))
