@@ -14,17 +14,18 @@
 
 namespace {
 
-// 8 dwords per lane in 256-thread workgroups (2856 per Qwen2.5-1.5B layer): measured on MI355X
-// against the former one-quad-per-lane kernel with LDS-staged stores (4.8-5.0 TB/s over 28 layer
-// buffers), 4 dwords per lane (4.8-5.0), 16 per lane (4.7-4.8; with 512 threads 5.1-5.2) and
-// 8 per lane with 512 threads (4.7-4.8): 5.1-5.2 TB/s, the same as this access pattern with the
-// conversion replaced by a plain copy of the packed words (5.2), so the conversion is hidden and
-// the read/write mix of the stream is the bound (writes alone reach 6.9 TB/s)
+// 32 dwords per lane (256 weights) in 256-thread workgroups, 714 per Qwen2.5-1.5B layer: measured
+// on MI355X over 28 layer buffers (graph-replayed, gaps included) 5.5-5.6 TB/s, against 4.8-5.0
+// for the former one-quad-per-lane kernel with LDS-staged stores, 5.1-5.2 for 8 or 16 dwords per
+// lane (16 with 512 threads), 4.8-5.1 for 8 or 16 with 1024 threads; cached instead of
+// non-temporal loads of the packed bytes cost 6-7 %.  With the conversion replaced by a plain
+// copy of the packed words, 8 dwords per lane ran at the same 5.2 TB/s: more bytes in flight per
+// wave, not less arithmetic, is what raised the rate (writes alone reach 6.9 TB/s)
 constexpr int kDqThreads = 256;
-constexpr int kDqDwords = 8;                                   // packed dwords per lane
+constexpr int kDqDwords = 32;                                  // packed dwords per lane
 constexpr int kDqOwn = kDqDwords / 8;                          // first-level codes per lane
 constexpr int kDqWgDwords = kDqThreads * kDqDwords;
-static_assert((kDqDwords == 8 || kDqDwords == 16) && kDqThreads >= 256 && kDqThreads % 64 == 0,
+static_assert((kDqDwords == 8 || kDqDwords == 16 || kDqDwords == 32) && kDqThreads >= 256 && kDqThreads % 64 == 0,
               "a wave within one second-level block; one code2 entry per thread");
 
 __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
