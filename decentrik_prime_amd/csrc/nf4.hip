@@ -1,32 +1,31 @@
 // NF4 double-quantised weights on gfx950: the HBM-rate dequant and the blockwise quantiser.
 //
-// Dequant (replaces solution/k_nf4.py:40-57).  Each lane converts kDqDwords packed dwords of 8
-// weights, dword j of wave lane l at wave offset 64 j + l: every load instruction of a wave reads
-// 256 contiguous bytes and every store instruction writes the 64 lanes' 16-byte results, 1 KiB
-// contiguous, straight from registers (no LDS staging, no barrier before the stores).  A wave's
-// 64 kDqDwords dwords lie in one second-level block (2048 dwords), so its scale2/offset2 are
-// wave-uniform (scalar loads).  They span 8 kDqDwords first-level blocks: lane k loads the codes
-// of blocks k, k + 64, ... and forms their absmax once, and each dword takes its block's absmax
-// from the owning lane by a cross-lane read.  Every global load of a lane (tables, codes, packed
-// dwords) is issued before the first conversion.  HBM traffic: 2.516 bytes per weight (0.5
-// packed + 1/64 code + 8/16384 scale/offset in, 2 out).
+// Dequant (replaces solution/k_nf4.py:40-57).  Each wave converts one second-level block (2048
+// packed dwords of 8 weights, 16384 weights) with nf4_dev.h's dq_wave_load / dq_wave_store: every
+// load instruction of the wave reads 256 contiguous bytes and every store instruction writes the
+// 64 lanes' 16-byte results, 1 KiB contiguous, straight from registers (no LDS staging, no
+// barrier before the stores).  A workgroup's four waves fill the two LDS tables (NF4 values and
+// the second-level codes) while their loads are in flight.  HBM traffic: 2.516 bytes per weight
+// (0.5 packed + 1/64 code + 8/16384 scale/offset in, 2 out).
 #include "nf4_dev.h"
+
+using dk::kWaveDwords;
+using dk::WaveLoads;
+using dk::dq_wave_load;
+using dk::dq_wave_store;
 
 namespace {
 
 // 32 dwords per lane (256 weights) in 256-thread workgroups, 714 per Qwen2.5-1.5B layer: measured
 // on MI355X over 28 layer buffers (graph-replayed, gaps included) 5.5-5.6 TB/s, against 4.8-5.0
 // for the former one-quad-per-lane kernel with LDS-staged stores, 5.1-5.2 for 8 or 16 dwords per
-// lane (16 with 512 threads), 4.8-5.1 for 8 or 16 with 1024 threads; cached instead of
-// non-temporal loads of the packed bytes cost 6-7 %.  With the conversion replaced by a plain
-// copy of the packed words, 8 dwords per lane ran at the same 5.2 TB/s: more bytes in flight per
-// wave, not less arithmetic, is what raised the rate (writes alone reach 6.9 TB/s)
+// lane (16 with 512 threads), 4.8-5.1 for 8 or 16 with 1024 threads and 4.9 for 64; cached
+// instead of non-temporal loads of the packed bytes cost 6-7 %.  With the conversion replaced by
+// a plain copy of the packed words, 8 dwords per lane ran at the same 5.2 TB/s: more bytes in
+// flight per wave, not less arithmetic, is what raised the rate (writes alone reach 6.9 TB/s)
 constexpr int kDqThreads = 256;
-constexpr int kDqDwords = 32;                                  // packed dwords per lane
-constexpr int kDqOwn = kDqDwords / 8;                          // first-level codes per lane
-constexpr int kDqWgDwords = kDqThreads * kDqDwords;
-static_assert((kDqDwords == 8 || kDqDwords == 16 || kDqDwords == 32) && kDqThreads >= 256 && kDqThreads % 64 == 0,
-              "a wave within one second-level block; one code2 entry per thread");
+constexpr int kDqWgDwords = kDqThreads * kWaveDwords;
+static_assert(kDqThreads == 256, "one code2 entry per thread");
 
 __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
     const uint32_t* __restrict__ packed, const uint8_t* __restrict__ qabs,
@@ -37,41 +36,17 @@ __global__ __launch_bounds__(kDqThreads) void nf4_dequant_kernel(
   __shared__ float c2[256];
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int64_t d_wave = (int64_t)blockIdx.x * kDqWgDwords + wave * 64 * kDqDwords;
+  const int64_t d_wave = (int64_t)blockIdx.x * kDqWgDwords + wave * 64 * kWaveDwords;
   const int64_t last = n_dwords - 1;
-  // the tables' loads first (the LDS fill waits only for them), then the codes, then the dwords
-  const float c2v = code2[threadIdx.x & 255];
+  // the tables' loads first (the LDS fill waits only for them), then the codes and the dwords
+  const float c2v = code2[threadIdx.x];
   const float lutv = nf4[threadIdx.x & 15];
-  const int64_t blk_last = last / 8;
-  uint8_t q[kDqOwn];
-#pragma unroll
-  for (int o = 0; o < kDqOwn; ++o) {
-    const int64_t blk = d_wave / 8 + 64 * o + lane;
-    q[o] = qabs[blk < blk_last ? blk : blk_last];
-  }
-  const int64_t sb = (d_wave < last ? d_wave : last) / (DK_ELEMS_PER_SB / 8);   // wave-uniform
-  const float s2 = scale2[sb], o2 = offset2[sb];
-  uint32_t w[kDqDwords];
-#pragma unroll
-  for (int j = 0; j < kDqDwords; ++j) {
-    const int64_t d = d_wave + 64 * j + lane;
-    w[j] = __builtin_nontemporal_load(packed + (d < last ? d : last));   // clamped: not stored
-  }
-  if (threadIdx.x < 256) c2[threadIdx.x] = c2v;
+  WaveLoads L;
+  dq_wave_load(packed, qabs, scale2, offset2, d_wave, last, lane, L);
+  c2[threadIdx.x] = c2v;
   if (threadIdx.x < 16) lut[threadIdx.x] = lutv;
   __syncthreads();
-  // absmax of blocks (wave's first block + 64 o + lane); dword j of lane l is in block 8 j + l / 8
-  // of the wave, owned by lane (8 j + l / 8) % 64, entry (8 j) / 64
-  float amax_own[kDqOwn];
-#pragma unroll
-  for (int o = 0; o < kDqOwn; ++o) amax_own[o] = dk_absmax(c2[q[o]], s2, o2);
-#pragma unroll
-  for (int j = 0; j < kDqDwords; ++j) {
-    const float amax = __shfl(amax_own[j / 8], 8 * (j % 8) + (lane >> 3));
-    const int64_t d = d_wave + 64 * j + lane;
-    const u32x4 o = dk_dequant_word(w[j], amax, lut);
-    if (d <= last) out[d] = o;
-  }
+  dq_wave_store<false>(L, c2, lut, out, d_wave, last, lane);
 }
 
 // ---------------------------------------------------------------------------------------------

@@ -40,70 +40,93 @@ struct SideDequant {
   int wgs;
 };
 
-// The part of a SideDequant that workgroup `id` of its `wgs` runs: a contiguous run of
-// second-level blocks (16384 weights, 512 quads of 32), one quad per thread of a 512-thread
-// workgroup.  Blocks go in batches of kSideBatch; the loads of the next batch are issued before
-// the current one is converted, so their latency overlaps the conversion.  Each wave stages its
-// lanes' 64 output bytes in LDS and writes them back lane-contiguous (1 KiB per store
-// instruction); loads and stores are non-temporal, so the stream does not displace the GEMM's
-// operand lines in L2.  `lds` needs side_dequant_lds bytes, 16-byte aligned.
-constexpr int kSideThreads = 512;
-constexpr int kSideBatch = 2;
-constexpr int kSideStageChunks = 64 * 4 + 4;   // per wave: 64 lanes x 4 chunks, 1 pad per 64
-constexpr int side_dequant_lds = 1088 + (kSideThreads / 64) * kSideStageChunks * 16;
+// One wave's share of a dequant: 64 lanes x kWaveDwords packed dwords (8 weights each) from dword
+// d_wave on, dword j of lane l at d_wave + 64 j + l, inside one second-level block (2048 dwords),
+// so scale2/offset2 are wave-uniform.  The wave spans 8 kWaveDwords first-level blocks: lane k
+// loads the codes of blocks k, k + 64, ... and forms their absmax once, and each dword takes its
+// block's absmax from the owning lane by a cross-lane read.  Every load goes out in
+// dq_wave_load, before any conversion; dq_wave_store converts and writes each dword's 8 fp16 as
+// one 16-byte store (the wave's store instruction writes 1 KiB contiguous).  Dwords past `last`
+// are loaded at clamped addresses and not stored.
+constexpr int kWaveDwords = 32;
+constexpr int kWaveOwn = kWaveDwords / 8;   // first-level codes per lane
+static_assert(64 * kWaveDwords <= DK_ELEMS_PER_SB / 8, "a wave within one second-level block");
 
-struct SideLoads {
-  u32x4 w[kSideBatch];
-  uint32_t qa[kSideBatch];
-  float s2[kSideBatch], o2[kSideBatch];
+struct WaveLoads {
+  uint32_t w[kWaveDwords];
+  uint8_t q[kWaveOwn];
+  float s2, o2;
 };
 
-__device__ __forceinline__ void side_load(const SideDequant& s, int64_t b0, int64_t hi, int tid,
-                                          SideLoads& L) {
+__device__ __forceinline__ void dq_wave_load(const uint32_t* __restrict__ packed,
+                                             const uint8_t* __restrict__ qabs,
+                                             const float* __restrict__ scale2,
+                                             const float* __restrict__ offset2, int64_t d_wave,
+                                             int64_t last, int lane, WaveLoads& L) {
+  const int64_t blk_last = last / 8;
 #pragma unroll
-  for (int u = 0; u < kSideBatch; ++u) {
-    const int64_t sb = b0 + u < hi ? b0 + u : hi - 1;   // past the run: loaded, not stored
-    const int64_t quad = sb * kSideThreads + tid;
-    L.w[u] = __builtin_nontemporal_load(s.packed + quad);
-    L.qa[u] = s.qabs[quad >> 1];
-    L.s2[u] = s.scale2[sb];
-    L.o2[u] = s.offset2[sb];
+  for (int o = 0; o < kWaveOwn; ++o) {
+    const int64_t blk = d_wave / 8 + 64 * o + lane;
+    L.q[o] = qabs[blk < blk_last ? blk : blk_last];
+  }
+  const int64_t sb = (d_wave < last ? d_wave : last) / (DK_ELEMS_PER_SB / 8);
+  L.s2 = scale2[sb];
+  L.o2 = offset2[sb];
+#pragma unroll
+  for (int j = 0; j < kWaveDwords; ++j) {
+    const int64_t d = d_wave + 64 * j + lane;
+    L.w[j] = __builtin_nontemporal_load(packed + (d < last ? d : last));
   }
 }
+
+// c2, lut: the 256-entry code table and the 16 NF4 values in LDS.  nt: non-temporal stores.
+template <bool NT>
+__device__ __forceinline__ void dq_wave_store(const WaveLoads& L, const float* c2, const float* lut,
+                                              u32x4* __restrict__ out, int64_t d_wave,
+                                              int64_t last, int lane) {
+  float amax_own[kWaveOwn];
+#pragma unroll
+  for (int o = 0; o < kWaveOwn; ++o) amax_own[o] = dk_absmax(c2[L.q[o]], L.s2, L.o2);
+#pragma unroll
+  for (int j = 0; j < kWaveDwords; ++j) {
+    // dword j of lane l is in block 8 j + l / 8 of the wave: lane (8 j + l / 8) % 64, entry 8 j / 64
+    const float amax = __shfl(amax_own[j / 8], 8 * (j % 8) + (lane >> 3));
+    const int64_t d = d_wave + 64 * j + lane;
+    const u32x4 o = dk_dequant_word(L.w[j], amax, lut);
+    if (d <= last) {
+      if (NT) __builtin_nontemporal_store(o, out + d);
+      else out[d] = o;
+    }
+  }
+}
+
+// The part of a SideDequant that workgroup `id` of its `wgs` runs (512 threads, 8 waves): the
+// second-level blocks sb0 + g, sb0 + g + 8 wgs, ... for its wave g = 8 id + w, one block per wave
+// at a time, the next block's loads issued before the current one is converted.  Stores are
+// non-temporal, so the stream does not displace the GEMM's operand lines in L2.  `lds` needs
+// side_dequant_lds bytes.
+constexpr int kSideThreads = 512;
+constexpr int side_dequant_lds = 64 + 1024;
 
 __device__ __forceinline__ void side_dequant(const SideDequant& s, int id, uint8_t* lds) {
   float* lut = reinterpret_cast<float*>(lds);              // the 16 NF4 values
   float* c2 = reinterpret_cast<float*>(lds + 64);          // the 256 code2 values
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  u32x4* stage = reinterpret_cast<u32x4*>(lds + 1088) + wave * kSideStageChunks;
-  dk_fill_lut(lut, s.nf4, tid);
-  if (tid < 256) c2[tid] = s.code2[tid];
-  const int64_t n = s.sb1 - s.sb0;
-  const int64_t lo = s.sb0 + n * id / s.wgs, hi = s.sb0 + n * (id + 1) / s.wgs;
-  SideLoads cur, nxt;
-  if (lo < hi) side_load(s, lo, hi, tid, cur);
+  const int tid = threadIdx.x, lane = tid & 63;
+  const int g = id * (kSideThreads / 64) + __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t stride = (int64_t)s.wgs * (kSideThreads / 64);
+  const uint32_t* packed = reinterpret_cast<const uint32_t*>(s.packed);
+  const int64_t last = s.sb1 * (DK_ELEMS_PER_SB / 8) - 1;   // the run's last dword
+  const float c2v = s.code2[tid & 255], lutv = s.nf4[tid & 15];
+  WaveLoads cur, nxt;
+  int64_t sb = s.sb0 + g;
+  if (sb < s.sb1) dq_wave_load(packed, s.qabs, s.scale2, s.offset2, sb * 2048, last, lane, cur);
+  if (tid < 256) c2[tid] = c2v;
+  if (tid < 16) lut[tid] = lutv;
   __syncthreads();   // tables
-  for (int64_t b0 = lo; b0 < hi; b0 += kSideBatch) {
-    if (b0 + kSideBatch < hi) side_load(s, b0 + kSideBatch, hi, tid, nxt);
-#pragma unroll
-    for (int u = 0; u < kSideBatch; ++u) {
-      if (b0 + u >= hi) break;
-      const float amax = dk_absmax(c2[cur.qa[u]], cur.s2[u], cur.o2[u]);
-      __builtin_amdgcn_wave_barrier();
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int idx = lane * 4 + j;
-        stage[idx + (idx >> 6)] = dk_dequant_word(cur.w[u][j], amax, lut);
-      }
-      __builtin_amdgcn_wave_barrier();
-      u32x4* dst = s.out + (b0 + u) * 2048 + wave * 256;   // 2048 chunks of 8 weights per block
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int idx = j * 64 + lane;
-        __builtin_nontemporal_store(stage[idx + (idx >> 6)], dst + idx);
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
+  for (; sb < s.sb1; sb += stride) {
+    if (sb + stride < s.sb1)
+      dq_wave_load(packed, s.qabs, s.scale2, s.offset2, (sb + stride) * 2048, last, lane, nxt);
+    dq_wave_store<true>(cur, c2, lut, s.out, sb * 2048, last, lane);
     cur = nxt;
   }
 }
