@@ -1,7 +1,7 @@
 """A whole Qwen2.5 QLoRA training step of the packed batch on this package's kernels.
 
 The linear stack (stack.NF4LinearStack: NF4 weights, LoRA adapters and keep-masks, the dequant
-slots and their carried schedule) with everything around it, in the order of the reference's
+slot and its dequant schedule) with everything around it, in the order of the reference's
 FastQwen2.forward / backward (solution/fast_qwen.py:985-1390):
   forward   x_0 = E[ids] (fp32 residual stream)
             per layer: y = RMSNorm(x_i) (+ the previous MLP output added on the way, x_i kept),
@@ -45,7 +45,7 @@ class QwenQLoRAStep(NF4LinearStack):
     LoRA on q and v, one packed batch of sequences of lengths `lens`."""
 
     def __init__(self, lens, n_layers=28, vocab=VOCAB, seed=0, device="cuda", eps=1e-6,
-                 head_grad_scale=1024.0, head_chunk=k_head.CHUNK, ahead="carried"):
+                 head_grad_scale=1024.0, head_chunk=k_head.CHUNK, ahead="layer"):
         m = int(sum(lens))
         super().__init__(n_layers, m, seed=seed, device=device, ahead=ahead)
         dev, f16, f32 = self.device, torch.float16, torch.float32
