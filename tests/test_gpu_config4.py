@@ -1,17 +1,17 @@
-"""Config 4 at its real size: the bench's 28-layer NF4 linear stack (M = 2048, the carried dequant
-schedule), two steps.
+"""Config 4 at its real size: the bench's 28-layer NF4 linear stack (M = 2048, whole-layer dequant
+launches, the default schedule), two steps.
 
 Every layer's forward outputs, backward dX, saved/overwritten gate|up buffer and LoRA gradients
 are checked bit-identical
-  * to the same stack run with whole-layer dequant launches of their own (``ahead="layer"``): the
-    carried schedule moves the backward's dequant into the GEMM launches and alternates two slots,
-    so a wrong slot, a wrong layer or an ordering error in it changes a result here (every layer
-    has different weights);
+  * to the same stack run with the carried schedule (``ahead="carried"``), which moves the
+    backward's dequant into the GEMM launches and alternates two slots, so a wrong slot, a wrong
+    layer or an ordering error in it changes a result here (every layer has different weights);
   * between the two steps (the slots then hold other layers at the start of each pass).
 Layers 0, 13 and 27 are also checked against the CPU oracle (solution/fast_qwen.py:943-947,
-1037, 1080-1112, 1310-1383 restated in oracle/linear.py and oracle/mlp.py) at rtol 1e-2 /
-atol 2e-2 of each output's scale, on the GPU-dequantised weights (bit-exact with the oracle's
-dequant, which layer 13's whole packed buffer re-checks here).
+1037, 1080-1112, 1310-1383 restated in oracle/linear.py and oracle/mlp.py) on the GPU-dequantised
+weights (bit-exact with the oracle's dequant, which layer 13's whole packed buffer re-checks
+here): forward outputs at rtol 1e-2 / atol 2e-2 on the values, gradients at rtol 1e-2 / atol 2e-2
+of each gradient's scale.
 """
 
 import numpy as np
@@ -88,25 +88,25 @@ def _abs(got, want, what):
 
 @pytest.fixture(scope="module")
 def runs(torch):
-    log(f"config 4: {N_LAYERS}-layer stack, M={M}, carried vs whole-layer schedule, 2 steps")
-    st, carried = _run(torch, "carried")
-    ref_runs = _run(torch, "layer")[1]
-    return st, carried, ref_runs
+    log(f"config 4: {N_LAYERS}-layer stack, M={M}, whole-layer vs carried schedule, 2 steps")
+    st, base = _run(torch, "layer")
+    carried = _run(torch, "carried")[1]
+    return st, base, carried
 
 
 def test_config4_carried_matches_whole_layer_schedule(runs):
-    st, carried, ref_runs = runs
+    st, base, carried = runs
     for step in range(2):
-        assert carried[step].keys() == ref_runs[step].keys()
+        assert carried[step].keys() == base[step].keys()
         for name, t in carried[step].items():
-            _same(t, ref_runs[step][name], f"step {step} {name} (carried vs layer)")
-    for name, t in carried[1].items():
-        _same(t, carried[0][name], f"{name} (step 1 vs step 0)")
+            _same(t, base[step][name], f"step {step} {name} (carried vs layer)")
+    for name, t in base[1].items():
+        _same(t, base[0][name], f"{name} (step 1 vs step 0)")
 
 
 def test_config4_finite(runs, torch):
-    st, carried, _ = runs
-    for name, t in carried[1].items():
+    st, base, _ = runs
+    for name, t in base[1].items():
         assert bool(torch.isfinite(t.float()).all()), f"{name}: non-finite values"
 
 
@@ -115,9 +115,9 @@ def test_config4_layer_vs_oracle(runs, torch, layer):
     """One layer of the bench's stack against the CPU oracle on the same weights and inputs."""
     from decentrik_prime_amd import k_nf4
     from oracle import linear, mlp, nf4
-    st, carried, _ = runs
+    st, base, _ = runs
     log(f"config 4: layer {layer} vs oracle")
-    res = carried[0]
+    res = base[0]
     pk = st.layers[layer]["packed"]
     w_all = torch.empty(pk.numel, dtype=torch.float16, device="cuda")
     k_nf4.dequant_layer(pk, st.code2, st.nf4, w_all)
