@@ -30,7 +30,7 @@
 // leaves a last round at most half full, those last tiles run as four 128 x 128 sub-tiles each
 // (8 waves of 32 x 64), so the final round is short instead of mostly idle; in the SwiGLU
 // backward they are dispatched first, which staggers the rounds' HBM-bound epilogues.  The fp16
-// SwiGLU forward, the one GEMM with several rounds, runs one persistent workgroup per CU that
+// SwiGLU GEMMs, whose tiles take more than one round, run one persistent workgroup per CU that
 // walks the same tiles in the same order, overlapping each tile's first loads with the previous
 // tile's epilogue stores.
 //
@@ -705,11 +705,12 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
 // fp32 partial tile at p.part[tile][split].  Tiles are numbered M-fastest.  The p.sums.wgs
 // workgroups after the tiles (NN LINEAR) run the LoRA column sums the launch carries, the
 // p.side.wgs after those its dequant work; dispatched last, they take the CUs the tiles leave
-// idle.  persist (fp16 SwiGLU forward over several rounds): the grid is one workgroup per CU,
+// idle.  persist (fp16 SwiGLU GEMMs over more than one round): the grid is one workgroup per CU,
 // gridDim.x / 8 per XCD, and each walks its XCD's share of the same tiles in the same order
-// (full tiles, then quarters), so that a tile's first loads go out while the previous tile's
-// epilogue stores drain (measured on MI355X: gate|up forward 111.7-112.0 -> 110.5 us, step
-// -0.05 ms, at M = 2048).
+// (full tiles then quarters, or quarters first in the backward), so that a tile's first loads go
+// out while the previous tile's epilogue stores drain (measured on MI355X at M = 2048: gate|up
+// forward 111.7-112.0 -> 110.5 us, step -0.05 ms; down^T backward 75.0 -> 74.7 us, step
+// -0.03 ms).
 template <bool TRANS, int EPI, bool W4>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2)))
 void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs, int persist) {
@@ -721,39 +722,46 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs, int persist) {
                 "side dequant in the kernel's LDS");
   static_assert(colsum_lds_bytes<16>() <= kStages * kStageHalves * 2 && kSumThreads == kThreads,
                 "carried LoRA column sums in the kernel's LDS");
-  if constexpr (EPI == EPI_SWIGLU_FWD && !W4) {
+  if constexpr ((EPI == EPI_SWIGLU_FWD || EPI == EPI_SWIGLU_BWD) && !W4) {
     if (persist) {
       // workgroup x + 8 r of XCD x takes that XCD's full tiles r, r + per, ... (numbered as
-      // below: XCD x owns the contiguous run [x nf8, (x + 1) nf8)), then its quarters r, r + per,
-      // ... (quarter index 8 qi + x, as below)
+      // below: XCD x owns the contiguous run [x nf8, (x + 1) nf8)) and its quarters r, r + per,
+      // ... (quarter index 8 qi + x, as below), the quarters first in the SwiGLU backward
       const int x = blockIdx.x & 7, r = blockIdx.x >> 3, per = (int)gridDim.x >> 3;
       const int nf8 = main_tiles >> 3, nq8 = tail_wgs >> 3;
       const int nk = (int)(p.K / kBK);
+      bool first = true;
+      auto quarters = [&]() {
+        for (int qi = r; qi < nq8; qi += per) {
+          if (!first) __syncthreads();   // every wave is done with the previous tile's LDS
+          first = false;
+          int64_t m0, n0;
+          if (p.xcd_gm) {
+            const int gm = p.xcd_gm;
+            const int bm = p.tiles_m / gm, bn = (tail_wgs / 4 / p.tiles_m) / (8 / gm);
+            const int qm = qi % (2 * bm), qn = qi / (2 * bm);
+            m0 = (int64_t)((x % gm) * bm) * kTile + 128 * qm;
+            n0 = (int64_t)(main_tiles / p.tiles_m + (x / gm) * bn) * kTile + 128 * qn;
+          } else {
+            const int u = x * nq8 + qi;
+            const int parent = main_tiles + u / 4, quarter = u % 4;
+            m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
+            n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
+          }
+          if (m0 < p.M)
+            gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk, nullptr, As, Bs, w4tab);
+        }
+      };
+      if (EPI == EPI_SWIGLU_BWD) quarters();
       for (int fi = r; fi < nf8; fi += per) {
-        if (fi != r) __syncthreads();   // every wave is done with the previous tile's LDS
+        if (!first) __syncthreads();
+        first = false;
         const int tile = x * nf8 + fi;
         gemm_tile<TRANS, EPI, 256, 256, 2, 2, W4>(p, (int64_t)(tile % p.tiles_m) * kTile,
                                                   (int64_t)(tile / p.tiles_m) * kTile, 0, nk,
                                                   nullptr, As, Bs, w4tab);
       }
-      for (int qi = r; qi < nq8; qi += per) {
-        __syncthreads();
-        int64_t m0, n0;
-        if (p.xcd_gm) {
-          const int gm = p.xcd_gm;
-          const int bm = p.tiles_m / gm, bn = (tail_wgs / 4 / p.tiles_m) / (8 / gm);
-          const int qm = qi % (2 * bm), qn = qi / (2 * bm);
-          m0 = (int64_t)((x % gm) * bm) * kTile + 128 * qm;
-          n0 = (int64_t)(main_tiles / p.tiles_m + (x / gm) * bn) * kTile + 128 * qn;
-        } else {
-          const int u = x * nq8 + qi;
-          const int parent = main_tiles + u / 4, quarter = u % 4;
-          m0 = (int64_t)(parent % p.tiles_m) * kTile + 128 * (quarter & 1);
-          n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
-        }
-        if (m0 < p.M)
-          gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk, nullptr, As, Bs, w4tab);
-      }
+      if (EPI == EPI_SWIGLU_FWD) quarters();
       return;
     }
   }
@@ -1013,11 +1021,12 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   // carried LoRA column sums (NN LINEAR only; the caller sets p.sums.wgs)
   const int sums = TRANS && EPI == EPI_LINEAR ? p.sums.wgs : 0;
   p.sums.wgs = sums;
-  // the fp16 SwiGLU forward over several rounds runs one persistent workgroup per CU when its
-  // tiles divide evenly over the XCDs' CUs
+  // the fp16 SwiGLU GEMMs that take more than one round run one persistent workgroup per CU
+  // when their tiles divide evenly over the XCDs' CUs
   const int cus = cu_count();
-  const int persist = EPI == EPI_SWIGLU_FWD && !W4 && h.splits == 1 && side == 0 &&
-                      cus % 8 == 0 && h.main_wgs > cus && h.main_wgs % 8 == 0 &&
+  const int persist = ((EPI == EPI_SWIGLU_FWD && h.main_wgs > cus) ||
+                       (EPI == EPI_SWIGLU_BWD && h.tail_wgs > 0)) && !W4 && h.splits == 1 &&
+                      side == 0 && cus % 8 == 0 && h.main_wgs % 8 == 0 &&
                       (h.main_wgs / 8) % (cus / 8) == 0 && h.tail_wgs % 8 == 0 &&
                       h.tail_wgs / 8 <= cus / 8;
   hipLaunchKernelGGL((hgemm_kernel<TRANS, EPI, W4>),
