@@ -407,6 +407,15 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
 
 // NST: LDS stages of this tile shape in the kernel's 2 x 64 KB (256 x 256: 2, 128 x 128: 4, so
 // the smaller tiles, whose steps are a quarter as long, still load three steps ahead).
+// 128 x 128 NT tiles of the fp16 weight split the waves by role in the main loop: waves 0-3
+// compute (WAVES_M x 4 / WAVES_M blocks of 64 x 64: four MFMAs per 16-wide sub-step on four
+// operand reads) and never load or wait for loads; waves 4-7 issue every load of the tile and
+// wait for them.  Each computing wave then hands its second 32-row strip to a loading wave, so
+// the eight waves run the epilogue on one 32 x 64 strip each, as in the 8-wave tile.  Measured on
+// MI355X: the loop alone (microbenchmark) 723 against 927 core clocks per 64-wide step (the MFMA
+// work is 512); in the step q|k|v forward 24.4 -> 23.4 us, o forward 20.6 -> 18.8 us.  NN tiles
+// keep the 8-wave form: specialised they ran faster alone but slower in the step (o dX
+// 21.7 -> 22.6 us).  Every output element is summed by the same MFMA sequence either way.
 template <bool TRANS, int EPI, int BM, int BN, int WAVES_M, int NST, bool W4>
 __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64_t n0, int kt0,
                                           int nk, float* part, f16* As, f16* Bs,
@@ -414,11 +423,14 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   constexpr int SA = BM * kBK, SB = BN * kBK;   // halves per stage of A and of W
   static_assert(NST * SA <= kStages * kStageHalves && NST * SB <= kStages * kStageHalves &&
                 (NST & (NST - 1)) == 0 && NST >= 2, "LDS stages");
-  constexpr int WAVES_N = 8 / WAVES_M;
+  constexpr bool SPEC = BM == 128 && BN == 128 && !W4 && !TRANS;   // waves split by role
+  constexpr int NCW = SPEC ? 4 : 8;         // computing waves
+  constexpr int NLW = SPEC ? 4 : 8;         // loading waves
+  constexpr int WAVES_N = NCW / WAVES_M;
   constexpr int WM = BM / WAVES_M, WN = BN / WAVES_N;
   constexpr int TM = WM / 32, TN = WN / 32;
-  constexpr int LA = BM * 8 / kThreads;     // A chunks per lane per stage
-  constexpr int LB = BN * 8 / kThreads;     // W chunks per lane per stage
+  constexpr int LA = BM * 8 / (64 * NLW);   // A chunks per loading lane per stage
+  constexpr int LB = BN * 8 / (64 * NLW);   // W chunks per loading lane per stage
   constexpr int LOADS = W4 ? LA : LA + LB;  // DMA instructions per lane per stage (W4: A only)
   constexpr int NCH = BN / 8;               // NN: 16-byte chunks per W-tile row
   static_assert(TM >= 1 && TN >= 1 && LA >= 1 && LB >= 1, "tile shape");
@@ -427,9 +439,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   const int tid = threadIdx.x, lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int64_t M = p.M, N = p.N, K = p.K;
+  const bool loader = !SPEC || wave >= NCW;            // issues loads and waits for them
+  const int lw = SPEC ? wave - NCW : wave;              // its index among the loading waves
 
-  // ---- DMA sources (first K step kt0; nk steps): instruction j of wave w fills the stage's
-  // chunks [(8 j + w) 64, +64).  Each operand has a wave-uniform base at step kt0 (A: the tile's
+  // ---- DMA sources (first K step kt0; nk steps): instruction j of loading wave w fills the
+  // stage's chunks [(NLW j + w) 64, +64).  Each operand has a wave-uniform base at step kt0 (A: the tile's
   // first row; W: the weight's first row (NT) or the tile's first column (NN)) and a 32-bit byte
   // offset per lane and instruction; the host keeps every offset below 2^32.
   const uint64_t a_base = uniform64((uint64_t)(p.a + m0 * p.lda + (int64_t)kt0 * kBK));
@@ -440,14 +454,14 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   unsigned b_off[LB];
 #pragma unroll
   for (int j = 0; j < LA; ++j) {
-    const int q = (j * 8 + wave) * 64 + lane;
+    const int q = (j * NLW + lw) * 64 + lane;
     const int row = q >> 3, c = (q & 7) ^ swz_k(q >> 3);
     const int64_t r = m0 + row < M ? row : M - 1 - m0;   // rows past M: never stored
     a_off[j] = (unsigned)((r * p.lda + c * 8) * (int64_t)sizeof(f16));
   }
 #pragma unroll
   for (int j = 0; j < LB; ++j) {
-    const int q = (j * 8 + wave) * 64 + lane;
+    const int q = (j * NLW + lw) * 64 + lane;
     if (!TRANS) {
       const int row = q >> 3, c = (q & 7) ^ swz_k(q >> 3);
       int64_t n = n0 + row;
@@ -465,12 +479,12 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   auto issue = [&](int kt, int st, int d) {
     if (d < LA) {
       const unsigned dst = __builtin_amdgcn_readfirstlane(
-          lds_offset(As + st * SA + (d * 8 + wave) * 512));
+          lds_offset(As + st * SA + (d * NLW + lw) * 512));
       dma16s(a_base + (uint64_t)kt * (kBK * sizeof(f16)), a_off[d], dst);
     } else {
       const int j = d - LA;
       const unsigned dst = __builtin_amdgcn_readfirstlane(
-          lds_offset(Bs + st * SB + (j * 8 + wave) * 512));
+          lds_offset(Bs + st * SB + (j * NLW + lw) * 512));
       dma16s(b_base + (uint64_t)kt * b_step, b_off[j], dst);
     }
   };
@@ -626,6 +640,41 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   // step kt + 1 and for every wave's last read of stage kt % NST (one barrier), then refill that
   // stage with step kt + NST, spreading the DMA instructions between the last sub-step's MFMAs,
   // which run beside the first reads of step kt + 1.
+  if constexpr (SPEC) {
+    if (loader) {
+      // the loading waves: the same loads, waits and barriers as below, no MFMAs; the refill
+      // of each stage goes out right after the barrier that frees it
+#pragma unroll
+      for (int q = 0; q < NST; ++q)
+        if (q < nk)
+#pragma unroll
+          for (int d = 0; d < LOADS; ++d) issue(q, q, d);
+      wait_loads((nk < NST ? nk : NST) - 1);
+      __syncthreads();
+      for (int kt = 0; kt < nk; ++kt) {
+        wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
+        __syncthreads();
+        if (kt + NST < nk)
+#pragma unroll
+          for (int d = 0; d < LOADS; ++d) issue(kt + NST, kt & (NST - 1), d);
+      }
+      // the second 32-row strip of computing wave w - NCW, handed over through LDS (below), and
+      // its epilogue: every wave finishes one 32 x 64 strip, as in the 8-wave 128 x 128 tile
+      __syncthreads();
+      const int c = wave - NCW;
+      f32x16 strip[1][TN];
+      const float* hand = reinterpret_cast<const float*>(Bs) + c * (kEpiScratch / 4);
+#pragma unroll
+      for (int j = 0; j < TN; ++j)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) strip[0][j][v] = hand[(j * 16 + v) * 64 + lane];
+      wave_epilogue<TRANS, EPI, 1, TN>(
+          p, strip, m0 + (c / WAVES_N) * WM + 32, n0 + (c % WAVES_N) * WN,
+          reinterpret_cast<uint8_t*>(Bs) + c * kEpiScratch,
+          reinterpret_cast<const uint8_t*>(Bs) + (c ^ 1) * kEpiScratch);
+      return;
+    }
+  }
   W4Piece w4_next;   // W4: the packed piece of step kt + NST (loaded one step before its use)
   if constexpr (W4) {
     // the first NST steps' W tiles converted and written before the loop (their loads waited at
@@ -638,13 +687,15 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       }
     w4_next = w4_load(NST < nk ? NST : nk - 1);   // clamped: its result is then never written
   }
+  if (!SPEC) {
 #pragma unroll
-  for (int q = 0; q < NST; ++q)
-    if (q < nk)
+    for (int q = 0; q < NST; ++q)
+      if (q < nk)
 #pragma unroll
-      for (int d = 0; d < LOADS; ++d) issue(q, q, d);
-  if (W4) wait_vmem<0>();
-  else wait_loads((nk < NST ? nk : NST) - 1);
+        for (int d = 0; d < LOADS; ++d) issue(q, q, d);
+    if (W4) wait_vmem<0>();
+    else wait_loads((nk < NST ? nk : NST) - 1);
+  }
   __syncthreads();
   read_frags(0, 0, 0);
   for (int kt = 0; kt < nk; ++kt) {
@@ -663,10 +714,10 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     }
     // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
     if (W4) wait_vmem<kW4Loads>();
-    else wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
+    else if (!SPEC) wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
     __syncthreads();
     if (kt + 1 < nk) read_frags((kt + 1) & (NST - 1), 0, 0);
-    const bool refill = kt + NST < nk;
+    const bool refill = !SPEC && kt + NST < nk;
     if constexpr (W4) {
       if (refill) w4_write(st);
       w4_next = w4_after;
@@ -689,6 +740,25 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   // every wave is past the last barrier, after which no wave reads a stage and no load is in
   // flight: the stages are free for the per-wave epilogue scratch
 
+  if constexpr (SPEC) {
+    // (128 x 128 tiles have no split K.)  The first 32-row strip is finished here, the second by
+    // loading wave w + NCW: handed over in its epilogue scratch slot (which it reads before it
+    // writes there), lane-major so that the 64 lanes of each store and load are contiguous
+    static_assert(TM == 2, "two 32-row strips per computing wave");
+    float* hand = reinterpret_cast<float*>(Bs) + wave * (kEpiScratch / 4);
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) hand[(j * 16 + v) * 64 + lane] = acc[1][j][v];
+    __syncthreads();
+    f32x16 strip[1][TN];
+#pragma unroll
+    for (int j = 0; j < TN; ++j) strip[0][j] = acc[0][j];
+    wave_epilogue<TRANS, EPI, 1, TN>(p, strip, m0 + wm * WM, n0 + wn * WN,
+                                     reinterpret_cast<uint8_t*>(As) + wave * kEpiScratch,
+                                     reinterpret_cast<const uint8_t*>(As) + (wave ^ 1) * kEpiScratch);
+    return;
+  }
   if (part) {
     // split-K: this wave's fp32 partial blocks; in a block, registers 4 q .. 4 q + 3 of lane l
     // at 256 q + 4 l, so each 16-byte store instruction writes 1 KiB contiguous; the reduce
@@ -768,7 +838,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs, int persist) {
             n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
           }
           if (m0 < p.M)
-            gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk, nullptr, As, Bs, w4tab);
+            gemm_tile<TRANS, EPI, 128, 128, W4 || TRANS ? 4 : 2, 4, W4>(p, m0, n0, 0, nk, nullptr, As, Bs, w4tab);
         }
       };
       if (EPI == EPI_SWIGLU_BWD) quarters();
@@ -851,7 +921,7 @@ void hgemm_kernel(GemmParams p, int main_tiles, int tail_wgs, int persist) {
       n0 = (int64_t)(parent / p.tiles_m) * kTile + 128 * (quarter >> 1);
     }
     if (m0 >= p.M) return;
-    gemm_tile<TRANS, EPI, 128, 128, 4, 4, W4>(p, m0, n0, 0, nk_all, nullptr, As, Bs, w4tab);
+    gemm_tile<TRANS, EPI, 128, 128, W4 || TRANS ? 4 : 2, 4, W4>(p, m0, n0, 0, nk_all, nullptr, As, Bs, w4tab);
   }
 }
 
