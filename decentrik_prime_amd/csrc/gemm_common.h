@@ -67,6 +67,8 @@ constexpr int kHgemmDeclined = -1000;
 // p.w16) and dequantised by each workgroup into LDS, bit-identical to the fp16 form's results.
 template <bool TRANS, int EPI, bool W4 = false>
 int hgemm_launch(const GemmParams& p, void* ws, int64_t ws_bytes, hipStream_t stream);
-int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi);
+// Split-K partials the launch of that shape needs (0: no split; -1: the plan does not take the
+// shape); nt: NT (W stored [N][K]).
+int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi, bool nt);
 
 }  // namespace dk

@@ -1004,7 +1004,7 @@ int xcd_blocks(int64_t tiles_m, int64_t main_wgs, int64_t tail_wgs, int qbase) {
   return best;
 }
 
-HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split) {
+HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split, bool nt) {
   HPlan h{false, 0, 0, 0, 0, 1, 0};
   if (M <= 0 || N % kTile || K % kBK || K < kBK) return h;
   const int cus = cu_count();
@@ -1026,8 +1026,13 @@ HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split) {
   }
   // fewer tiles than CUs: split K so that the splits fill the CUs once.  The fp32 partials cost
   // two passes over splits x tiles x 256 KB, which only long K (4096 or more) repays; LINEAR
-  // only, at least 4 row tiles
-  if (!no_split && epi == EPI_LINEAR && h.tiles_m >= 4 && K >= 4096) {
+  // only, at least 4 row tiles.  NT GEMMs whose 128 x 128 quarters fill half the CUs run as
+  // quarters over the whole K instead: their loop (computing and loading waves apart) does as
+  // much per CU as the full tiles' in the step, without the partials' round trip or the reduce
+  // launch (down forward at M = 2048, K = 8960: 71.8 -> 61.8 us in the step)
+  const int64_t quarters = (M + 127) / 128 * (N / 128);
+  if (!no_split && epi == EPI_LINEAR && h.tiles_m >= 4 && K >= 4096 &&
+      !(nt && quarters * 2 >= cus)) {
     int64_t s = cus / tiles;
     if (s > K / kBK / 8) s = K / kBK / 8;
     if (s >= 2) {
@@ -1038,7 +1043,6 @@ HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split) {
     }
   }
   // otherwise every tile as 128 x 128 quarters, when they fill at least half the CUs
-  const int64_t quarters = (M + 127) / 128 * (N / 128);
   if (quarters * 2 < cus && !no_split) return h;
   h.main_wgs = 0;
   h.tail_wgs = 4 * tiles;
@@ -1046,8 +1050,8 @@ HPlan hplan_tiles(int64_t M, int64_t N, int64_t K, int epi, bool no_split) {
   return h;
 }
 
-HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
-  HPlan h = hplan_tiles(M, N, K, epi, no_split);
+HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split, bool nt) {
+  HPlan h = hplan_tiles(M, N, K, epi, no_split, nt);
   if (h.ok && h.splits == 1)
     h.xcd_gm = xcd_blocks(h.tiles_m, h.main_wgs, h.tail_wgs,
                           epi == EPI_SWIGLU_BWD ? 0 : (int)h.main_wgs);
@@ -1056,9 +1060,10 @@ HPlan hplan(int64_t M, int64_t N, int64_t K, int epi, bool no_split = false) {
 
 }  // namespace
 
-int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
-  const HPlan h = hplan(M, N, K, epi);
-  if (!h.ok || h.splits == 1) return 0;
+int64_t hgemm_workspace(int64_t M, int64_t N, int64_t K, int epi, bool nt) {
+  const HPlan h = hplan(M, N, K, epi, false, nt);
+  if (!h.ok) return -1;
+  if (h.splits == 1) return 0;
   return h.main_wgs * kTile * kTile * (int64_t)sizeof(float);
 }
 
@@ -1089,7 +1094,7 @@ int hgemm_launch(const GemmParams& p0, void* ws, int64_t ws_bytes, hipStream_t s
   if ((kTile * p0.lda + p0.K) * (int64_t)sizeof(f16) >= kOffMax ||
       (!W4 && (TRANS ? (int64_t)kBK * p0.N : p0.N * p0.K) * (int64_t)sizeof(f16) >= kOffMax))
     return kHgemmDeclined;
-  const HPlan h = hplan(p0.M, p0.N, p0.K, EPI, rope);
+  const HPlan h = hplan(p0.M, p0.N, p0.K, EPI, rope, !TRANS);
   if (!h.ok) return kHgemmDeclined;
   GemmParams p = p0;
   p.tiles_m = (int)h.tiles_m;

@@ -622,12 +622,12 @@ int64_t plan_workspace(const Plan& pl) {
 // Workspace of an NF4-reading GEMM: room for whichever path dispatch takes, the 256-tile kernel's
 // split-K partials (reading NF4 itself), or the 128 x 128 kernel's partials with the fp16 weight
 // after them (two-phase shapes).
-int64_t gemm_workspace(int64_t M, int64_t N, int64_t K, int epi) {
+int64_t gemm_workspace(int64_t M, int64_t N, int64_t K, int epi, bool nt) {
   if (M <= 0) return 0;
   const int64_t part = plan_workspace(plan_for(M, N, K, epi));
   const int64_t w16 = two_phase(M, N) ? N * K * (int64_t)sizeof(f16) : 0;
   const int64_t own = w16 ? round256(part) + w16 : part;
-  const int64_t tile = hgemm_workspace(M, N, K, epi);
+  const int64_t tile = hgemm_workspace(M, N, K, epi, nt);
   return own > tile ? own : tile;
 }
 
@@ -675,14 +675,14 @@ int launch_plan(const Plan& pl, GemmParams p, hipStream_t stream) {
 
 template <bool TRANS, int EPI>
 int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, hipStream_t stream) {
-  if (ws && ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI)) return DK_ERR_WORKSPACE;
+  if (ws && ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI, !TRANS)) return DK_ERR_WORKSPACE;
   // the 256-tile kernel with the weight dequantised in LDS (W4) where its plan splits K (few
   // output tiles, long K): there it beats the separate dequant + fp16 GEMM (gate|up dX at
   // M = 2048: 179 against 188 us); elsewhere its per-step conversion costs more than the
   // dequant launch saves (measured on every config-4 shape), and the paths below run
   const int mode = w->kernel;
   if (mode == DK_W4_KERNEL_TILE ||
-      (mode == DK_W4_KERNEL_AUTO && ws && hgemm_workspace(p.M, p.N, p.K, EPI) > 0)) {
+      (mode == DK_W4_KERNEL_AUTO && ws && hgemm_workspace(p.M, p.N, p.K, EPI, !TRANS) > 0)) {
     const int r = hgemm_launch<TRANS, EPI, true>(p, ws, ws_bytes, stream);
     if (r != kHgemmDeclined) return r;
   }
@@ -691,7 +691,7 @@ int dispatch(GemmParams p, const dk_nf4_weight* w, void* ws, int64_t ws_bytes, h
     pl.splits = 1;
     return launch_plan<TRANS, EPI, false>(pl, p, stream);
   }
-  if (ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI)) return DK_ERR_WORKSPACE;
+  if (ws_bytes < gemm_workspace(p.M, p.N, p.K, EPI, !TRANS)) return DK_ERR_WORKSPACE;
   if (!dk_aligned(ws, 256)) return DK_ERR_ALIGN;
   if (pl.splits > 1) p.part = reinterpret_cast<float*>(ws);
   if (!two_phase(p.M, p.N)) return launch_plan<TRANS, EPI, false>(pl, p, stream);
@@ -1155,17 +1155,17 @@ extern "C" int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int o
     case DK_OP_LINEAR_BWD_DX: n = cols; k = rows; break;
     default: return 0;
   }
-  const int64_t big = hgemm_workspace(m, n, k, EPI_LINEAR);
-  return big > 0 ? big : plan_workspace(plan_for(m, n, k, EPI_LINEAR));
+  const int64_t big = hgemm_workspace(m, n, k, EPI_LINEAR, op == DK_OP_LINEAR_FWD);
+  return big >= 0 ? big : plan_workspace(plan_for(m, n, k, EPI_LINEAR));
 }
 
 extern "C" int64_t dk_w4_workspace(int64_t m, const dk_nf4_weight* w, int op) {
   if (m <= 0 || !weight_ok(w)) return 0;
   switch (op) {
-    case DK_OP_LINEAR_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_LINEAR);
-    case DK_OP_LINEAR_BWD_DX: return gemm_workspace(m, w->cols, w->rows, EPI_LINEAR);
-    case DK_OP_GATEUP_SWIGLU_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_SWIGLU_FWD);
-    case DK_OP_DOWN_SWIGLU_BWD: return gemm_workspace(m, w->cols, w->rows, EPI_SWIGLU_BWD);
+    case DK_OP_LINEAR_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_LINEAR, true);
+    case DK_OP_LINEAR_BWD_DX: return gemm_workspace(m, w->cols, w->rows, EPI_LINEAR, false);
+    case DK_OP_GATEUP_SWIGLU_FWD: return gemm_workspace(m, w->rows, w->cols, EPI_SWIGLU_FWD, true);
+    case DK_OP_DOWN_SWIGLU_BWD: return gemm_workspace(m, w->cols, w->rows, EPI_SWIGLU_BWD, false);
     default: return 0;
   }
 }

@@ -309,9 +309,11 @@ def test_w4_without_workspace(torch):
 @pytest.mark.parametrize("m", [2048, 1000])
 def test_split_k(torch, m):
     """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
-    second launch that runs the epilogue): the down forward (NT, K = 8960) and a K = 8960 dX (NN,
-    fp16, fp32 and fp32-accumulate outputs) against the oracle, and two calls bit-identical.
-    M = 1000 has ragged last rows and 10 splits per tile, M = 2048 has 5."""
+    second launch that runs the epilogue) on a K = 8960 dX (NN, fp16, fp32 and fp32-accumulate
+    outputs), and the down forward (NT, K = 8960), which splits K at M = 1000 (its 128 x 128
+    quarters would fill less than half the CUs) and runs as quarters over the whole K at
+    M = 2048: against the oracle, and two calls bit-identical.  M = 1000 has ragged last rows and
+    10 splits per tile, M = 2048 has 5."""
     from decentrik_prime_amd import _lib, w4linear
     from oracle import linear
     lib = _lib.lib()
@@ -319,8 +321,11 @@ def test_split_k(torch, m):
     tiles = (m + 255) // 256 * (D // 256)
     cus = torch.cuda.get_device_properties(0).multi_processor_count
     splits = min(cus // tiles, I // 64 // 8)
-    log(f"split-K, M={m}: {tiles} tiles x {splits} splits on {cus} CUs")
-    assert lib.dk_h16_workspace(m, D, I, _lib.DK_OP_LINEAR_FWD) == tiles * splits * 256 * 256 * 4
+    nt_quarters = (m + 127) // 128 * (D // 128)
+    nt_split = nt_quarters * 2 < cus
+    log(f"split-K, M={m}: {tiles} tiles x {splits} splits on {cus} CUs; NT split: {nt_split}")
+    assert lib.dk_h16_workspace(m, D, I, _lib.DK_OP_LINEAR_FWD) == (
+        tiles * splits * 256 * 256 * 4 if nt_split else 0)
     assert lib.dk_h16_workspace(m, I, D, _lib.DK_OP_LINEAR_BWD_DX) == tiles * splits * 256 * 256 * 4
     qd = nf4_weight(D, I, seed=301)      # down [1536, 8960]: NT, K = 8960
     qg = nf4_weight(I, D, seed=302)      # [8960, 1536]: dX = dy W, K = 8960
