@@ -658,11 +658,13 @@ def _short(name):
 def summarize_trace(db, top=40, ops=()):
     """Per-kernel dispatch statistics of a kernel trace: calls, average and total duration,
     grouped by kernel name and grid (a kernel instance launched at several shapes is split).
-    ops: [(operator, kernel-name substring, grid, (first, end) or None)] for which an 'OPAVG' line
-    is added (what bench.py reads back as the profile's average duration of that operator's
-    kernel): the average over that kernel's dispatches at that grid, or over dispatches
-    [first, end) of them in launch order (bench.py's timed steps: warmup x 28 .. (warmup + steps)
-    x 28 for a kernel launched once per layer)."""
+    ops: [(operator, kernel-name substring, grid, (first, end[, step]) or None)] for which an
+    'OPAVG' line is added (what bench.py reads back as the profile's average duration of that
+    operator's kernel): the average over that kernel's dispatches at that grid, or over
+    dispatches first, first + step, ... below end of them in launch order (bench.py's timed
+    steps: warmup x 28 .. (warmup + steps) x 28 for a kernel launched once per layer; step 2 and
+    an odd first pick the second of two operators that launch the same kernel at the same grid
+    in each layer)."""
     import collections
     import sqlite3
     cur = sqlite3.connect(db).cursor()
@@ -684,7 +686,7 @@ def summarize_trace(db, top=40, ops=()):
         if sel:
             durs = [d for _, v in sel for d in v]
             if span is not None:
-                durs = durs[span[0]:span[1]]
+                durs = durs[span[0]:span[1]:span[2] if len(span) > 2 else 1]
             lines.append(f"OPAVG {op} | {sel[0][0][0]} | {grid} | {sum(durs) / len(durs) / 1e3:.2f} | "
                          f"{len(durs)}")
     return "\n".join(lines)
@@ -702,13 +704,36 @@ def _counter_by_dispatch(db, counter):
     return rows
 
 
+def _grid_sel(spec):
+    """'substring#grid[,grid][first:end]' -> (substring, set of grids or None, (first, end) or
+    None): the dispatch range picks, in launch order, among the matching dispatches (two
+    operators that launch one kernel at one grid, run one after the other)."""
+    span = None
+    if spec.endswith("]"):
+        spec, rng = spec[:-1].rsplit("[", 1)
+        span = tuple(int(v) for v in rng.split(":"))
+    wgs = None
+    if "#" in spec:
+        spec, w = spec.rsplit("#", 1)
+        wgs = {int(v) for v in w.split(",")}
+    return spec, wgs, span
+
+
+def _pick(rows, pattern, wgs, span):
+    """The dispatches (keyed by (dispatch id, kernel, grid, ...)) of `rows` that match, in
+    dispatch order, cut to `span`."""
+    sel = sorted((k, v) for k, v in rows.items()
+                 if pattern in k[1] and (wgs is None or k[2] in wgs))
+    return sel[span[0]:span[1]] if span is not None else sel
+
+
 def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
     """HBM traffic per operator call from a FETCH_SIZE run and a WRITE_SIZE run (KiB per
     dispatch), each scaled by what the same counter reads for the calibration copy of
     `copy_bytes` read + `copy_bytes` written (the __amd_rocclr_copyBuffer dispatches within a
     factor of two of the largest one: nothing else in the run copies a quarter as much).
     groups: [(operator name, kernel-name substring, operator calls in the run, set of grid sizes in
-    workgroups or None for any)]."""
+    workgroups or None for any, (first, end) dispatch range among the matching ones or None)]."""
     out = []
     scaled = {}
     for label, db, counter in (("fetch", fetch_db, "FETCH_SIZE"), ("write", write_db, "WRITE_SIZE")):
@@ -721,9 +746,8 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
         factor = copy_bytes / (kib_avg * 1024.0)
         out.append(f"{counter}: calibration copy {copy_bytes} B -> {kib_avg:.0f} KiB per dispatch "
                    f"(n={len(kib)}), scale factor {factor:.4f}")
-        for op, pattern, calls, wgs_only in groups:
-            sel = {k: v for k, v in rows.items()
-                   if pattern in k[1] and (wgs_only is None or k[2] in wgs_only)}
+        for op, pattern, calls, wgs_only, span in groups:
+            sel = dict(_pick(rows, pattern, wgs_only, span))
             per_kernel = {}
             for k, v in sel.items():
                 per_kernel.setdefault((k[1], k[2]), []).append(v)
@@ -733,7 +757,7 @@ def summarize_pmc(fetch_db, write_db, groups, copy_bytes=512 << 20):
             per_call = sum(sel.values()) * 1024.0 * factor / calls
             scaled[(op, label)] = per_call
             out.append(f"  {op}: {label} {per_call:.4g} B per operator call (scaled, {calls} calls)")
-    for op, _, _, _ in groups:
+    for op, _, _, _, _ in groups:
         f, w = scaled[(op, "fetch")], scaled[(op, "write")]
         out.append(f"TRAFFIC {op} | fetch {f:.0f} | write {w:.0f} | total {f + w:.0f}")
     return "\n".join(out)
@@ -784,13 +808,12 @@ def summarize_counters(db, groups, simds=1024, xcds=8, cus=256):
       memory, LDS DMA included) busy fraction; dma_waves = TA_FLAT_READ_LDS_WAVEFRONTS_sum, the
       LDS-DMA load instructions.
     groups: [(operator name, kernel-name substring, grid in workgroups or None, algorithmic
-    FLOP)]."""
+    FLOP, (first, end) dispatch range among the matching ones or None)]."""
     rows, dur = _counters_by_dispatch(db)
     lines = []
     mean = lambda xs: sum(xs) / len(xs) if xs else float("nan")  # noqa: E731
-    for op, pattern, wgs_only, algo in groups:
-        sel = [(k, v) for k, v in rows.items()
-               if pattern in k[1] and (wgs_only is None or k[2] == wgs_only)]
+    for op, pattern, wgs_only, algo, span in groups:
+        sel = _pick(rows, pattern, None if wgs_only is None else {wgs_only}, span)
         if not sel:
             lines.append(f"{op}: (no dispatch of {pattern})")
             continue
@@ -919,19 +942,21 @@ def main():
     ap.add_argument("--summarize-pmc", nargs=2, metavar=("FETCH_DB", "WRITE_DB"),
                     help="print HBM traffic per operator call from FETCH_SIZE / WRITE_SIZE runs")
     ap.add_argument("--op-avg", action="append", default=[],
-                    help="with --summarize-trace: 'operator=kernel-name substring#grid[first:end]' "
-                         "for an OPAVG line (the dispatch range is optional)")
+                    help="with --summarize-trace: 'operator=kernel-name substring#grid"
+                         "[first:end[:step]]' for an OPAVG line (the dispatch range is optional)")
     ap.add_argument("--summarize-counters", metavar="DB",
                     help="print MFMA busy, clock and MFMA FLOPs per operator from a PMC run")
     ap.add_argument("--group", action="append", default=[],
-                    help="with --summarize-pmc: 'operator=kernel-name substring[#grid[,grid]]@calls' "
-                         "(grid: only dispatches of that many workgroups)")
+                    help="with --summarize-pmc / --summarize-counters: 'operator=kernel-name "
+                         "substring[#grid[,grid]][[first:end]]@calls' (or @GFLOP; grid: only "
+                         "dispatches of that many workgroups; [first:end]: those of the matching "
+                         "dispatches, in launch order)")
     args = ap.parse_args()
     global EAGER
     EAGER = args.eager
     if args.summarize_trace:
         ops = []
-        for o in args.op_avg:   # 'operator=kernel substring#grid[first:end]'
+        for o in args.op_avg:   # 'operator=kernel substring#grid[first:end[:step]]'
             op, rest = o.split("=", 1)
             pattern, grid = rest.rsplit("#", 1)
             span = None
@@ -943,26 +968,21 @@ def main():
         return
     if args.summarize_counters:
         groups = []
-        for g in args.group:   # 'operator=kernel substring[#grid]@GFLOP'
+        for g in args.group:   # 'operator=kernel substring[#grid][[first:end]]@GFLOP'
             op, rest = g.split("=", 1)
             pattern, gflop = rest.rsplit("@", 1)
-            wgs = None
-            if "#" in pattern:
-                pattern, wgs = pattern.rsplit("#", 1)
-                wgs = int(wgs)
-            groups.append((op, pattern, wgs, float(gflop) * 1e9))
+            pattern, wgs, span = _grid_sel(pattern)
+            groups.append((op, pattern, None if wgs is None else min(wgs), float(gflop) * 1e9,
+                           span))
         print(summarize_counters(args.summarize_counters, groups))
         return
     if args.summarize_pmc:
         groups = []
-        for g in args.group:
+        for g in args.group:   # one grid, or several: '#240,3072'; a range: '#192[0:3]'
             op, rest = g.split("=", 1)
             pattern, calls = rest.rsplit("@", 1)
-            wgs = None
-            if "#" in pattern:   # one grid, or several: '#240,3072'
-                pattern, wgs = pattern.rsplit("#", 1)
-                wgs = {int(v) for v in wgs.split(",")}
-            groups.append((op, pattern, int(calls), wgs))
+            pattern, wgs, span = _grid_sel(pattern)
+            groups.append((op, pattern, int(calls), wgs, span))
         print(summarize_pmc(*args.summarize_pmc, groups))
         return
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
