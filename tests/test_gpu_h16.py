@@ -306,14 +306,15 @@ def test_w4_without_workspace(torch):
     _scaled_close(host(dx_o), linear.mm16(dy, qo["deq"]).astype(np.float32), "o dX vs oracle")
 
 
-@pytest.mark.parametrize("m", [2048, 1000])
+@pytest.mark.parametrize("m", [2048, 1900, 1000])
 def test_split_k(torch, m):
     """The 256-tile kernel's split-K (fp32 partials in the workspace, summed in split order by a
     second launch that runs the epilogue) on a K = 8960 dX (NN, fp16, fp32 and fp32-accumulate
     outputs), and the down forward (NT, K = 8960), which splits K at M = 1000 (its 128 x 128
     quarters would fill less than half the CUs) and runs as quarters over the whole K at
-    M = 2048: against the oracle, and two calls bit-identical.  M = 1000 has ragged last rows and
-    10 splits per tile, M = 2048 has 5."""
+    M = 2048 and 1900: against the oracle, and two calls bit-identical.  M = 1000 has ragged last
+    rows and 10 splits per tile, M = 1900 ragged last rows (its last row quarters partial) and 5,
+    M = 2048 has 5."""
     from decentrik_prime_amd import _lib, w4linear
     from oracle import linear
     lib = _lib.lib()
