@@ -116,6 +116,8 @@ SIGNATURES = {
                                       _c_p]),
     "dk_lora_grads_workspace": (_i64, [_i64, _i64, _i64, _i64]),
     "dk_lora_down_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraDownTermC), _int, _c_p]),
+    "dk_lora_down_multi_dequant": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraDownTermC),
+                                          _int, _S, _c_p]),
     "dk_lora_grads_multi_workspace": (_i64, [_i64, _i64, _i64, ctypes.POINTER(_i64), _int]),
     "dk_lora_grads_multi": (_int, [_c_p, _i64, _i64, _i64, ctypes.POINTER(LoraGradsTermC), _int,
                                    _c_p, _i64, _c_p]),

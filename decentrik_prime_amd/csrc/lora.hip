@@ -14,6 +14,7 @@
 // Products of two fp16 values are exact in fp32; only the order of the fp32 sums differs from a
 // cuBLAS or CPU GEMM.
 #include "lora_dev.h"
+#include "nf4_dev.h"
 
 using namespace dk;
 
@@ -57,10 +58,14 @@ struct RowsJobs {
   RowsJob j[kMaxJobs];
 };
 
-template <int R, int MODE, bool MASKED>
-__global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, int64_t rows) {
+// Row block `blk` of the jobs (the body of lora_rows_kernel, also run by the first workgroups of
+// lora_down_dequant_kernel).  NWP: the workgroup's waves; with fewer than the 8 of the K split
+// (MODE 0 only), wave w runs the split's waves w, w + NWP, ... one after the other, so every sum
+// keeps the 8-wave kernel's order.
+template <int R, int MODE, bool MASKED, int NWP = kRowThreads / 64>
+__device__ __forceinline__ void rows_block(const RowsJobs& jobs, int64_t rows, int blk) {
   const int64_t per_job = (rows + kRowTile - 1) / kRowTile;
-  const RowsJob& J = jobs.j[blockIdx.x / per_job];
+  const RowsJob& J = jobs.j[blk / per_job];
   const f16* __restrict__ in = J.in;
   const int64_t ld = J.ld;
   const uint8_t* __restrict__ mask = J.mask;
@@ -77,10 +82,11 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
   constexpr int BI = KC * (R / 8) / kRowThreads;   // MODE 1: 16-byte B pieces per thread per pass
   constexpr int BLD = R + 8;     // halves per staged B row
   static_assert(KU * 32 * NW == KC && BI * kRowThreads == KC * (R / 8), "MODE 1 pass shape");
+  static_assert(NW % NWP == 0 && (MODE == 0 || NWP == NW), "waves");
   __shared__ float red[NW * 16 * R];
   __shared__ __attribute__((aligned(16))) f16 Bs[MODE == 1 ? KC * BLD : 8];
   const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
-  const int64_t row0 = (int64_t)(blockIdx.x % per_job) * kRowTile;
+  const int64_t row0 = (int64_t)(blk % per_job) * kRowTile;
   const int lr = lane & 15, lk = 8 * (lane >> 4);
   const int64_t m = row0 + lr < rows ? row0 + lr : rows - 1;   // clamped: its sums are not stored
   const int trow = 8 * (lane >> 4) + ((lane & 15) >> 2), tcol = 4 * (lane & 3);
@@ -90,7 +96,12 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
 
   if (MODE == 0) {
     const int64_t steps = cols / 32;
-    for (int64_t s0 = w; s0 < steps; s0 += NW * kBatch) {
+    for (int vw = w; vw < NW; vw += NWP) {   // the split's wave vw
+    if (vw != w) {
+#pragma unroll
+      for (int b = 0; b < RB; ++b) acc[b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    }
+    for (int64_t s0 = vw; s0 < steps; s0 += NW * kBatch) {
       f16x8 a[kBatch], bw[kBatch][RB];
       u32x2 mw[kBatch];
       // every load of the batch first (x, keep-mask bytes, A), then the dropout and the MFMAs
@@ -116,6 +127,11 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
         for (int b = 0; b < RB; ++b)
           acc[b] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a[u], bw[u][b], acc[b], 0, 0, 0);
       }
+    }
+#pragma unroll
+    for (int b = 0; b < RB; ++b)
+#pragma unroll
+      for (int v = 0; v < 4; ++v) red[(vw * 16 + 4 * (lane >> 4) + v) * R + 16 * b + lr] = acc[b][v];
     }
   } else {
     // per pass: this wave's dY operands (steps w, w + NW, ...) and this thread's pieces of B are
@@ -166,12 +182,14 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
       }
     }
   }
+  if (MODE == 1) {
 #pragma unroll
-  for (int b = 0; b < RB; ++b)
+    for (int b = 0; b < RB; ++b)
 #pragma unroll
-    for (int v = 0; v < 4; ++v) red[(w * 16 + 4 * (lane >> 4) + v) * R + 16 * b + lr] = acc[b][v];
+      for (int v = 0; v < 4; ++v) red[(w * 16 + 4 * (lane >> 4) + v) * R + 16 * b + lr] = acc[b][v];
+  }
   __syncthreads();
-  for (int i = tid; i < 16 * R; i += kRowThreads) {
+  for (int i = tid; i < 16 * R; i += NWP * 64) {
     const int rr = i / R, r = i % R;
     if (row0 + rr >= rows) continue;
     float sum = 0.0f;
@@ -179,6 +197,41 @@ __global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, i
     for (int ww = 0; ww < NW; ++ww) sum += red[(ww * 16 + rr) * R + r];
     out[(row0 + rr) * R + r] = MODE == 0 ? dk_h(sum) : dk_h(__fmul_rn((float)dk_h(sum), scale));
   }
+}
+
+template <int R, int MODE, bool MASKED>
+__global__ __launch_bounds__(kRowThreads) void lora_rows_kernel(RowsJobs jobs, int64_t rows) {
+  rows_block<R, MODE, MASKED>(jobs, rows, (int)blockIdx.x);
+}
+
+// The LoRA downs (MODE 0 row blocks, workgroups [0, row_wgs)) and a dequant of second-level
+// blocks [dq.sb0, dq.sb1) (the workgroups after them, one block per wave, converted and stored
+// as nf4_dequant_kernel does) in one launch: both memory-bound and independent, so the row
+// blocks' load latency overlaps the dequant's stream instead of adding a launch of its own.
+constexpr int kDqLoraThreads = 256;   // the standalone dequant's workgroup (4 waves)
+template <int R, bool MASKED>
+__global__ __launch_bounds__(kDqLoraThreads) void lora_down_dequant_kernel(RowsJobs jobs,
+                                                                           int64_t rows,
+                                                                           int row_wgs,
+                                                                           SideDequant dq) {
+  if ((int)blockIdx.x < row_wgs) {
+    rows_block<R, 0, MASKED, kDqLoraThreads / 64>(jobs, rows, (int)blockIdx.x);
+    return;
+  }
+  __shared__ float lut[16];
+  __shared__ float c2[256];
+  const int lane = threadIdx.x & 63;
+  const int64_t sb = dq.sb0 + (int64_t)((int)blockIdx.x - row_wgs) * (kDqLoraThreads / 64) +
+                     __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int64_t last = dq.sb1 * (DK_ELEMS_PER_SB / 8) - 1;
+  const uint32_t* packed = reinterpret_cast<const uint32_t*>(dq.packed);
+  const float c2v = dq.code2[threadIdx.x & 255], lutv = dq.nf4[threadIdx.x & 15];
+  WaveLoads L;
+  if (sb < dq.sb1) dq_wave_load(packed, dq.qabs, dq.scale2, dq.offset2, sb * 2048, last, lane, L);
+  if (threadIdx.x < 256) c2[threadIdx.x] = c2v;
+  if (threadIdx.x < 16) lut[threadIdx.x] = lutv;
+  __syncthreads();
+  if (sb < dq.sb1) dq_wave_store<false>(L, c2, lut, dq.out, sb * 2048, last, lane);
 }
 
 template <int R>
@@ -237,6 +290,76 @@ extern "C" int dk_lora_down_multi(const void* x, int64_t m, int64_t k, int64_t r
                                 : rows_launch<0, false>(rank, stream, jobs, 1, m);
     if (e) return e;
   }
+  return 0;
+}
+
+namespace {
+template <int R>
+void down_dequant_launch(bool masked, dim3 grid, dim3 block, hipStream_t stream,
+                         const RowsJobs& jobs, int64_t m, int rw, const SideDequant& dq) {
+  if (masked)
+    hipLaunchKernelGGL((lora_down_dequant_kernel<R, true>), grid, block, 0, stream, jobs, m, rw, dq);
+  else
+    hipLaunchKernelGGL((lora_down_dequant_kernel<R, false>), grid, block, 0, stream, jobs, m, rw, dq);
+}
+}  // namespace
+
+extern "C" int dk_lora_down_multi_dequant(const void* x, int64_t m, int64_t k, int64_t rank,
+                                          const dk_lora_down_term* terms, int n_terms,
+                                          const dk_side_dequant* side, hipStream_t stream) {
+  // the dequant's description, checked as a GEMM's carried dequant is (its wgs is not used)
+  if (!side || side->sb0 < 0 || side->sb1 < side->sb0) return DK_ERR_INVALID;
+  if (side->sb1 > side->sb0 && (!side->packed || !side->qabs || !side->scale2 || !side->offset2 ||
+                                !side->code2 || !side->nf4 || !side->out))
+    return DK_ERR_INVALID;
+  if (side->sb1 > side->sb0 && (!dk_aligned(side->packed, 16) || !dk_aligned(side->out, 16)))
+    return DK_ERR_ALIGN;
+  if (m < 0 || k <= 0 || k % 32 || !rank_ok(rank) || !terms || n_terms < 1 || n_terms > kMaxJobs)
+    return DK_ERR_INVALID;
+  if (!dk_aligned(x, 16)) return DK_ERR_ALIGN;
+  int masked = 0;
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_down_term& u = terms[t];
+    if (m > 0 && (!u.a || !u.z || !(u.x ? u.x : x))) return DK_ERR_INVALID;
+    if (!dk_aligned(u.a, 16) || !dk_aligned(u.x, 16) || (u.mask && !dk_aligned(u.mask, 8)))
+      return DK_ERR_ALIGN;
+    masked += u.mask != nullptr;
+  }
+  const int64_t n_sb = side->sb1 - side->sb0;
+  const int64_t dq_wgs = (n_sb + kDqLoraThreads / 64 - 1) / (kDqLoraThreads / 64);
+  const int64_t row_wgs = n_terms * ((m + kRowTile - 1) / kRowTile);
+  if (m == 0 || n_sb == 0 || (masked != 0 && masked != n_terms) || row_wgs + dq_wgs > 0x7fffffff) {
+    // nothing to share a launch with, or terms that need launches of their own: one call each
+    if (n_sb > 0) {
+      if (int e = dk_nf4_dequant(side->packed + side->sb0 * (DK_ELEMS_PER_SB / 2),
+                                 side->qabs + side->sb0 * (DK_ELEMS_PER_SB / 64),
+                                 side->scale2 + side->sb0, side->offset2 + side->sb0, side->code2,
+                                 side->nf4, reinterpret_cast<f16*>(side->out) +
+                                                side->sb0 * DK_ELEMS_PER_SB,
+                                 n_sb * (DK_ELEMS_PER_SB / 64), stream))
+        return e;
+    }
+    return m > 0 ? dk_lora_down_multi(x, m, k, rank, terms, n_terms, stream) : 0;
+  }
+  RowsJobs jobs = {};
+  for (int t = 0; t < n_terms; ++t) {
+    const dk_lora_down_term& u = terms[t];
+    jobs.j[t] = RowsJob{(const f16*)(u.x ? u.x : x), k, u.mask, u.mask ? u.keep_scale : 1.0f,
+                        (const f16*)u.a, 1.0f, (f16*)u.z, k};
+  }
+  SideDequant dq{reinterpret_cast<const u32x4*>(side->packed), side->qabs, side->scale2,
+                 side->offset2, side->code2, side->nf4, reinterpret_cast<u32x4*>(side->out),
+                 side->sb0, side->sb1, 0};
+  const dim3 grid((unsigned)(row_wgs + dq_wgs)), block(kDqLoraThreads);
+  const int rw = (int)row_wgs;
+  switch (rank) {
+    case 16: down_dequant_launch<16>(masked > 0, grid, block, stream, jobs, m, rw, dq); break;
+    case 32: down_dequant_launch<32>(masked > 0, grid, block, stream, jobs, m, rw, dq); break;
+    case 48: down_dequant_launch<48>(masked > 0, grid, block, stream, jobs, m, rw, dq); break;
+    case 64: down_dequant_launch<64>(masked > 0, grid, block, stream, jobs, m, rw, dq); break;
+    default: return DK_ERR_INVALID;
+  }
+  DK_CHECK_LAUNCH();
   return 0;
 }
 

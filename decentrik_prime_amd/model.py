@@ -145,8 +145,9 @@ class QwenQLoRAStep(NF4LinearStack):
                                xq=self.xq[i], xv=self.xv[i], mq=lo["mq"], mv=lo["mv"],
                                keep_scale=self.keep_scale)
             y = self.y16[i]
-            lora_down_multi(None, [(lo["Aq"], None, 1.0, self.xq[i]),
-                                   (lo["Av"], None, 1.0, self.xv[i])], outs=[z["q"], z["v"]])
+            self._lora_downs(i, lambda dq: lora_down_multi(
+                None, [(lo["Aq"], None, 1.0, self.xq[i]), (lo["Av"], None, 1.0, self.xv[i])],
+                outs=[z["q"], z["v"]], dequant=dq))
             linear_forward_rope(y, Lw["qkv"], lo["bias"], self.qkv_terms(i), self.pos, self.cos,
                                 self.sin, (NQ + NKV) * HD, out=self.qkv_b[i], w16=w16("qkv", i),
                                 side=side("qkv", i + 1))

@@ -89,11 +89,29 @@ class _WholeLayer:
         return out
 
 
+class _WholeLayerWith(_WholeLayer):
+    """_WholeLayer whose launch also runs layer i's LoRA downs: run(dequant) launches them with
+    the layer's dequant (dk_lora_down_multi_dequant)."""
+
+    def __init__(self, stack, i, run):
+        super().__init__(stack, i)
+        self.run = run
+
+    def dequantize(self, out):
+        st = self.stack
+        pk = st.layers[self.i]["packed"]
+        self.run(k_nf4.side_dequant(pk, st.code2, st.nf4, out.view(-1), 0, pk.n_qblocks // 256, -1))
+        return out
+
+
 class NF4LinearStack:
     """Random-init NF4 weights (W ~ N(0, 0.02), quantised on the GPU), rank-16 LoRA on q and v,
     and synthetic activations, all resident on `device`."""
 
     KINDS = ("qkv", "o", "gu", "d")
+    # ahead="layer" on one stream: each forward layer's whole-layer dequant runs in the launch of
+    # that layer's LoRA downs (dk_lora_down_multi_dequant) instead of a launch of its own
+    LORA_WITH_DEQUANT = True
     # ahead="carried": the share of the next layer's dequant (fraction of its second-level blocks)
     # that each GEMM launch carries, in step order; the launches that leave CUs idle (a last round
     # of 128 x 128 tiles, split-K grids short of the CU count, 128 x 128 grids short of a round).
@@ -151,6 +169,7 @@ class NF4LinearStack:
         self.dx_mlp = torch.empty(m, D, dtype=f16, device=dev)
         self.grads = [None] * n_layers
         self.probe = None   # (operator name, [(start event, end event), ...]) or None
+        self._deferred = None   # layer whose whole-layer dequant waits for its LoRA downs
         self._setup_schedule(ahead, dq_stream)
 
     def _setup_schedule(self, ahead, dq_stream):
@@ -250,7 +269,10 @@ class NF4LinearStack:
                 return
             self.dq.release("layer")
             if 0 <= nxt < self.n_layers:
-                self.dq.issue("layer", nxt, _WholeLayer(self, nxt))
+                if self._forward and self.dq.stream is None and self.LORA_WITH_DEQUANT:
+                    self._deferred = nxt   # issued with layer nxt's LoRA downs (_lora_downs)
+                else:
+                    self.dq.issue("layer", nxt, _WholeLayer(self, nxt))
             return
         self.dq.release(kind)
         if 0 <= nxt < self.n_layers:
@@ -266,9 +288,10 @@ class NF4LinearStack:
         self._forward = True
         L, lo, z, x, o = self.layers[i], self.lora[i], self.z[i], self.x, self.out
         op, nm, w16, done, side = self._op, self.op_name, self._w16, self._done, self._side
-        op("lora_down q+v", lora_down_multi, x,
-           [(lo["Aq"], lo["mq"], self.keep_scale), (lo["Av"], lo["mv"], self.keep_scale)],
-           outs=[z["q"], z["v"]])
+        self._lora_downs(i, lambda dq: op(
+            "lora_down q+v", lora_down_multi, x,
+            [(lo["Aq"], lo["mq"], self.keep_scale), (lo["Av"], lo["mv"], self.keep_scale)],
+            outs=[z["q"], z["v"]], dequant=dq))
         op(nm("qkv", "_linear_fwd qkv+lora"), linear_forward_lora, x, L["qkv"], lo["bias"],
            self.qkv_terms(i), out=o["qkv"], w16=w16("qkv", i), side=side("qkv", i + 1))
         done("qkv", i + 1)
@@ -281,6 +304,18 @@ class NF4LinearStack:
         op(nm("d", "_linear_fwd down"), linear_forward, self.act, L["d"], out=o["y"],
            w16=w16("d", i), side=side("d", i + 1))
         done("d", i + 1)
+
+    def _lora_downs(self, i, run):
+        """Layer i's LoRA downs: run(dequant) launches them, in one launch with layer i's
+        whole-layer dequant (a k_nf4.side_dequant description) when _done deferred that dequant
+        to here, else with dequant None.  The downs are the layer's first operator that the
+        dequant can share a launch with: they need the layer's input, and the dequant only has
+        to precede the layer's first GEMM."""
+        if getattr(self, "_deferred", None) == i and self.dq.holds["layer"] != i:
+            self._deferred = None
+            self.dq.issue("layer", i, _WholeLayerWith(self, i, run))
+        else:
+            run(None)
 
     def backward_layer(self, i):
         if i == self.n_layers - 1 or getattr(self, "_forward", True):

@@ -177,12 +177,14 @@ def lora_down(x, lora_A, mask=None, keep_scale=1.0, out=None):
     return out
 
 
-def lora_down_multi(x, terms, outs=None):
+def lora_down_multi(x, terms, outs=None, dequant=None):
     """lora_down of one or two adapters in shared launches (the q and v adapters of the fused QKV
     projection): terms = [(lora_A [r, K], mask or None, keep_scale[, x_term]), ...].  A term's
     input is x, or its own x_term [M, K] (the reference's xq / xv: the fp32 norm output dropped out
     per adapter, solution/k_norm.py:49-53, given with mask None); x may be None when every term has
-    one.  Returns [z, ...], each exactly as lora_down computes it."""
+    one.  dequant: a k_nf4.side_dequant description whose blocks the same launch dequantises
+    (dk_lora_down_multi_dequant; its wgs is not used), or None.  Returns [z, ...], each exactly as
+    lora_down computes it."""
     if not 1 <= len(terms) <= 2:
         raise ValueError("lora_down_multi takes one or two terms")
     ins = [t[3] if len(t) > 3 and t[3] is not None else x for t in terms]
@@ -209,6 +211,12 @@ def lora_down_multi(x, terms, outs=None):
                                     _lib.ptr(own))
         keep.append((a, mask))
         zs.append(z)
+    if dequant is not None:
+        rc = _lib.lib().dk_lora_down_multi_dequant(_lib.ptr(x), m, k, r, arr, len(terms),
+                                                   ctypes.byref(dequant),
+                                                   _lib.stream_handle(ins[0].device))
+        _lib.check(rc, "dk_lora_down_multi_dequant")
+        return zs
     rc = _lib.lib().dk_lora_down_multi(_lib.ptr(x), m, k, r, arr, len(terms),
                                        _lib.stream_handle(ins[0].device))
     _lib.check(rc, "dk_lora_down_multi")

@@ -401,6 +401,19 @@ typedef struct dk_side_dequant {
 } dk_side_dequant;
 #define DK_SIDE_WGS_AUTO (-1)
 
+/* dk_lora_down_multi and a dequant in one launch: the LoRA downs of `terms` over x, and second-
+ * level blocks [side->sb0, side->sb1) of side's layer into side->out as dk_side_dequant describes
+ * (side->wgs is not used: one wave per second-level block).  z and the fp16 weights are
+ * bit-identical to dk_lora_down_multi's and dk_nf4_dequant's; the two must not overlap in memory.
+ * It runs the next layer's dequant ahead of use (k_nf4.dequant_range, solution/k_nf4.py:176-181,
+ * issued by solution/fast_qwen.py:729-731) and that layer's q/v LoRA downs
+ * (solution/fast_qwen.py:943-944, solution/k_norm.py:49-53) together: no counterpart in the
+ * reference as one call.  Terms that mix masked and unmasked inputs, m = 0 or an empty block range
+ * run as the separate calls. */
+int dk_lora_down_multi_dequant(const void* x, int64_t m, int64_t k, int64_t rank,
+                               const dk_lora_down_term* terms, int n_terms,
+                               const dk_side_dequant* side, hipStream_t stream);
+
 int64_t dk_h16_workspace(int64_t m, int64_t rows, int64_t cols, int op);
 int dk_h16_linear_fwd_lora(const void* x, int64_t ldx, int64_t m, const void* w16, int64_t rows,
                            int64_t cols, const void* bias, const dk_lora_term* terms, int n_terms,

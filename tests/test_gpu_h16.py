@@ -387,6 +387,47 @@ def test_lora_multi_matches_single(torch, m):
         _scaled_close(host(got), ref[nm], f"{nm}_q vs oracle")
 
 
+@pytest.mark.parametrize("m", [2048, 200])
+def test_lora_down_with_dequant(torch, m):
+    """dk_lora_down_multi_dequant: the q+v LoRA downs and a whole-layer dequant (or a block range
+    of it) in one launch give z bit-identical to dk_lora_down_multi and fp16 weights
+    bit-identical to dk_nf4_dequant, leaving the rest of the output untouched; masked terms,
+    terms with their own inputs, and a masked beside an unmasked term (run as the separate
+    calls)."""
+    from decentrik_prime_amd import k_nf4, w4linear
+    from decentrik_prime_amd.stack import NF4LinearStack
+    from oracle import linear
+    log(f"LoRA downs + layer dequant in one launch, M={m}")
+    st = NF4LinearStack(1, 256, seed=7, device="cuda")
+    pk, code2, nf4t = st.layers[0]["packed"], st.code2, st.nf4
+    n_sb = pk.n_qblocks // 256
+    whole = torch.empty(pk.numel, dtype=torch.float16, device="cuda")
+    k_nf4.dequant_layer(pk, code2, nf4t, whole)
+    D, KV = 1536, 256
+    x, aq, _, mq, _ = lora_inputs(m, D, D, seed=51)
+    _, av, _, mv, _ = lora_inputs(m, D, KV, seed=52)
+    ks = linear.keep_scale(0.05)
+    tx, taq, tav, tmq, tmv = cuda16(x), cuda16(aq), cuda16(av), cuda(mq), cuda(mv)
+    xq = (torch.randn(m, D, device="cuda") * 0.5).half()
+    xv = (torch.randn(m, D, device="cuda") * 0.5).half()
+    cases = {"masked": (tx, [(taq, tmq, ks), (tav, tmv, ks)]),
+             "own inputs": (None, [(taq, None, 1.0, xq), (tav, None, 1.0, xv)]),
+             "mixed": (tx, [(taq, tmq, ks), (tav, None, 1.0)])}
+    for name, (xin, terms) in cases.items():
+        want = w4linear.lora_down_multi(xin, terms)
+        for sb0, sb1 in ((0, n_sb), (3, n_sb - 5)):
+            out = torch.full((pk.numel,), 7.0, dtype=torch.float16, device="cuda")
+            side = k_nf4.side_dequant(pk, code2, nf4t, out, sb0, sb1, -1)
+            got = w4linear.lora_down_multi(xin, terms, dequant=side)
+            torch.cuda.synchronize()
+            for t, (a, b) in enumerate(zip(got, want)):
+                _same(a, b, f"{name} z[{t}], blocks [{sb0}, {sb1})")
+            lo, hi = sb0 * 16384, sb1 * 16384
+            _same(out[lo:hi], whole[lo:hi], f"{name} dequant, blocks [{sb0}, {sb1})")
+            assert bool((out[:lo] == 7.0).all()) and bool((out[hi:] == 7.0).all()), \
+                f"{name}: blocks outside [{sb0}, {sb1}) written"
+
+
 @pytest.mark.parametrize("rank", [32, 64])
 def test_lora_ranks_and_mixed_masks(torch, rank):
     """Ranks above the reference's 16 (the kernels take 16..64) and a masked term beside an

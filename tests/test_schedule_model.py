@@ -173,7 +173,13 @@ def model(monkeypatch):
     for name in ("linear_forward_lora", "linear_forward", "gateup_swiglu_forward",
                  "down_swiglu_backward", "linear_backward_dx", "linear_backward_dx_lora"):
         monkeypatch.setattr(stack_mod, name, _gemm(g))
-    monkeypatch.setattr(stack_mod, "lora_down_multi", lambda *a, **k: [0, 0])
+    def lora_down_multi(*args, dequant=None, **kwargs):
+        # (the downs touch no slot memory) with a dequant (k_nf4.side_dequant), the launch writes
+        # the dequant's blocks
+        if dequant is not None:
+            g.cur.launch(dequant.act).lora = True
+        return [0, 0]
+    monkeypatch.setattr(stack_mod, "lora_down_multi", lora_down_multi)
     monkeypatch.setattr(stack_mod, "lora_grads_multi", lambda *a, **k: [(0, 0, 0), (0, 0, 0)])
     monkeypatch.setattr(stack_mod, "lora_dz_multi",
                         lambda *a, **k: types.SimpleNamespace(grads=[(0, 0, 0), (0, 0, 0)]))
@@ -229,6 +235,23 @@ def test_dequant_ahead_schedule(model, ahead, where):
     assert per_step[1:] == [2 * n_layers - 2] * (steps - 1)
     if where == "side":
         assert any(len(n.deps) > 1 for n in model.nodes)
+
+
+def test_forward_dequant_rides_on_the_lora_downs(model):
+    """ahead="layer" on one stream: in the forward, every layer's dequant but the resident first
+    one is the launch of that layer's LoRA downs (deferred from the previous layer's last GEMM);
+    the backward's stay launches of their own."""
+    n_layers = 4
+    st = _fake_stack(model, n_layers, "layer", "main")
+    st.step()
+    first = len(model.nodes)
+    st.step()
+    later = model.nodes[first:]
+    writes = [n for n in later if any(a[0] == "write" for a in n.acts)]
+    riding = [n for n in writes if getattr(n, "lora", False)]
+    assert len(riding) == n_layers - 1
+    assert len(writes) == 2 * n_layers - 2
+    assert sorted(n.acts[0][3][0] for n in riding) == list(range(1, n_layers))
 
 
 def test_carried_dequant_rides_on_the_gemm_launches(model):
