@@ -21,8 +21,8 @@
 // to the fp16-weight form.
 //
 // LDS layout: A tiles and NT W tiles are rows of 64 halves (128 bytes) whose eight 16-byte
-// chunks are XOR-swizzled by row (swz_k), so the b128 operand reads of 16 consecutive rows hit
-// distinct banks.  NN W tiles are rows of 256 halves (N contiguous) with chunks swizzled by k (swz_n); the
+// chunks are XOR-swizzled by row (swz_k), so the b128 operand reads hit no bank conflict.  NN W
+// tiles are rows of 256 halves (N contiguous) with chunks swizzled by k (swz_n); the
 // consumers build each K-contiguous operand from two ds_read_b64_tr_b16 (transposing) reads.
 // The DMA writes 64 consecutive 16-byte chunks per instruction, so the swizzle is applied to the
 // global addresses each lane loads.
@@ -102,11 +102,16 @@ __device__ __forceinline__ f16x4 read_tr(const f16* p) {
                                        (__attribute__((address_space(3))) i16x4*)(p)));
 }
 
-// chunk swizzles: 128-byte rows (conflict-free for 8- and 16-lane LDS passes of b128 reads of
-// consecutive rows) and N-contiguous rows of the NN W tile (transposing reads of 4 rows x 32
-// columns hit distinct banks)
-__device__ __forceinline__ int swz_k(int r) { return (r & 7) ^ ((r >> 3) & 1); }
-__device__ __forceinline__ int swz_n(int k) { return 4 * (k & 3); }
+// Chunk swizzles, the 16-byte chunk index of a row XORed with a function of the row: rows of
+// 64 halves (A tiles, NT W tiles; swz_k) and N-contiguous rows of the NN W tile (swz_n).  Chosen by
+// measurement (the SQ_LDS_BANK_CONFLICT counter on MI355X, each candidate in a loop of the
+// GEMM's operand reads): conflict-free for both operand patterns, the 16x16x32 one (lane l: row
+// l % 16, chunk 4 s + l / 16; NN: 16-lane groups reading rows 8 g + 4 h + 0..3) and the 32x32x16
+// one (row l % 32, chunk 2 q + l / 32; NN: rows 8 (l / 32) + 4 h + 0..3).  The earlier
+// (r & 7) ^ (r >> 3 & 1) and 4 (k & 3) were conflict-free for the second only (two-way conflicts
+// for the first).
+__device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 7) ^ ((r & 1) << 2); }
+__device__ __forceinline__ int swz_n(int k) { return (4 * (k & 3)) ^ (2 * ((k >> 3) & 1)); }
 
 // The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
 // element is (mw0, nw0).  Register v of lane l holds, L16 (four 16 x 16 v_mfma_f32_16x16x32_f16
