@@ -6,18 +6,27 @@
 
 namespace {
 
-// forward (solution/k_attn.py:40-83): one workgroup per (block of kBM queries, query head)
-__global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __restrict__ out,
+// forward (solution/k_attn.py:40-83): one workgroup per (block of kBM queries, query head), 8
+// waves: wave w takes queries 32 (w % 4) .. + 31 of the block and the key tiles t with
+// t % 2 == w / 4, so two waves share each SIMD and each walks half of the block's tiles (the
+// causal blocks walk 2 to 8 tiles of 64 keys).  The two halves' softmax states (running maximum,
+// sum, O) are merged through LDS at the end.  Measured on MI355X at 4 x 512 tokens against 4
+// waves each walking every tile (one wave per SIMD): 19.7 -> 18.5 us.
+constexpr int kFThreads = 512;
+constexpr int kFLoads = kTileHalves / 8 / kFThreads;   // DMA instructions per operand per lane: 2
+
+__global__ __launch_bounds__(kFThreads) void attn_fwd_kernel(AttnArgs a, f16* __restrict__ out,
                                                              float* __restrict__ lse) {
   int64_t s0;
   int seqlen, mstart;
   if (!block_of(a, blockIdx.x, &s0, &seqlen, &mstart)) return;
   const int h = blockIdx.y;
-  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6, hl = lane >> 5, c = lane & 31;
-  const int wave = __builtin_amdgcn_readfirstlane(w);
+  const int lane = threadIdx.x & 63, hl = lane >> 5, c = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int qw = wave & 3, kg = wave >> 2;   // query group, key-tile parity
   const int64_t ROW = (int64_t)(a.nq + 2 * a.nkv) * kHD;
   const int kvh = h / (a.nq / a.nkv);
-  const int m = mstart + 32 * w + c;
+  const int m = mstart + 32 * qw + c;
   const bool mval = m < seqlen && s0 + m < a.n_tokens;
   __shared__ __attribute__((aligned(1024))) f16 Ks[kFwdStages * kTileHalves];
   __shared__ __attribute__((aligned(1024))) f16 Vs[kFwdStages * kTileHalves];
@@ -28,29 +37,29 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
   float m_i = -1.0e30f, l_i = 0.0f;
   const int hi = mstart + kBM < seqlen ? mstart + kBM : seqlen;
   const int n_tiles = (hi + kBN - 1) / kBN;
+  const int n_pairs = (n_tiles + 1) / 2;
   const f16* kbase = a.qkv + s0 * ROW + (int64_t)(a.nq + kvh) * kHD;
   const f16* vbase = a.qkv + s0 * ROW + (int64_t)(a.nq + a.nkv + kvh) * kHD;
-  // tile t into stage st: instruction i of wave w fills the stage's chunks (4 i + w) 64 + lane,
+  // tile t into stage t % 4: instruction i of wave w fills the stage's chunks (8 i + w) 64 + lane,
   // row q / 16 (rows past the sequence read its last row: finite, and masked to p = 0)
-  constexpr int kLoads = kTileHalves / 8 / kAThreads;   // per operand per lane: 4
-  auto issue = [&](int t, int st) {
+  auto issue = [&](int t) {
+    const int st = t % kFwdStages;
 #pragma unroll
-    for (int i = 0; i < kLoads; ++i) {
-      const int q = (4 * i + wave) * 64 + lane, r = q >> 4;
+    for (int i = 0; i < kFLoads; ++i) {
+      const int q = (8 * i + wave) * 64 + lane, r = q >> 4;
       const int row = t * kBN + r < seqlen ? t * kBN + r : seqlen - 1;
       const int64_t src = (int64_t)row * ROW + (((q & 15) ^ swz16(r)) << 3);
-      const int dst = st * kTileHalves + (4 * i + wave) * 512;
+      const int dst = st * kTileHalves + (8 * i + wave) * 512;
       dma16(kbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Ks + dst)));
       dma16(vbase + src, __builtin_amdgcn_readfirstlane(lds_addr(Vs + dst)));
     }
   };
-  issue(0, 0);
-  if (n_tiles > 1) issue(1, 1);
-  if (n_tiles > 2) issue(2, 2);
+  // tile pair u = tiles 2 u, 2 u + 1: pair 0 now, pair 1 after the query loads
+  issue(0);
+  if (n_tiles > 1) issue(1);
   // this lane's query row as the B operand (rows past the sequence: zeros).  Loaded at a clamped
   // row unconditionally and selected at once, so the compiler's wait for these loads stands here
-  // (it then also covers the tiles issued above) and not inside the loop, where it would wait for
-  // the tiles in flight every iteration.
+  // (it then also covers pair 0, issued above) and not inside the loop.
   f16x8 qf[kHD / 16];
   {
     const f16* qrow = a.qkv + (s0 + (mval ? m : mstart)) * ROW + h * kHD + 8 * hl;
@@ -63,128 +72,145 @@ __global__ __launch_bounds__(kAThreads) void attn_fwd_kernel(AttnArgs a, f16* __
 #pragma unroll
     for (int s = 0; s < kHD / 16; ++s) qf[s] = mval ? qf[s] : zero8();
   }
-  // S^T = K Q^T of the tile in stage st: keys kb * 32 + (row of the result), queries on the lanes
-  auto scores = [&](f32x16 (&acc)[2], int st) {
-    const f16* Kt = Ks + st * kTileHalves;
-    acc[0] = acc[1] = zero16();
-#pragma unroll
-    for (int s = 0; s < kHD / 16; ++s)
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-        acc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + sw_off(kb * 32 + c, 16 * s + 8 * hl)),
-                       qf[s], acc[kb]);
-  };
-  // software pipeline: iteration t runs the score MFMAs of tile t + 1 beside the softmax of tile
-  // t (its VALU work), then O += V_t P_t.  Tiles t and t + 1 are in LDS at its start.
-  if (n_tiles > 2) wait_vmem<2 * kLoads>();
-  else wait_vmem<0>();
+  wait_vmem<0>();
+  if (n_tiles > 2) issue(2);
+  if (n_tiles > 3) issue(3);
   __syncthreads();
-  f32x16 sc[2];
-  scores(sc, 0);
-  for (int t = 0; t < n_tiles; ++t) {
-    // stage (t + 3) % 4 held tile t - 1, whose last reader (O += V P of iteration t - 1) every wave
-    // finished before the barrier that ended that iteration
-    if (t + 3 < n_tiles) issue(t + 3, (t + 3) % kFwdStages);
-    const f16* Vt = Vs + (t % kFwdStages) * kTileHalves;
-    const int n0 = t * kBN;
-    // tile t + 1's scores (past the last tile: a stale stage, never used)
-    f32x16 sn[2];
-    scores(sn, (t + 1) % kFwdStages);
-    // softmax of tile t in the exp2 domain.  Only tiles that reach the block's first query (the
-    // diagonal, and the sequence end, which lies beyond it) hold masked keys: the test is uniform,
-    // and key n = n0 + off + 4 (l / 32) is kept iff off <= min(m, seqlen - 1) - n0 - 4 (l / 32).
-    if (n0 + kBN > mstart) {
+  for (int u = 0; u < n_pairs; ++u) {
+    const int t = 2 * u + kg;
+    if (t < n_tiles) {
+      const f16* Kt = Ks + (t % kFwdStages) * kTileHalves;
+      const f16* Vt = Vs + (t % kFwdStages) * kTileHalves;
+      const int n0 = t * kBN;
+      // S^T = K Q^T: keys kb * 32 + (row of the result), queries on the lanes
+      f32x16 sc[2];
+      sc[0] = sc[1] = zero16();
+#pragma unroll
+      for (int s = 0; s < kHD / 16; ++s)
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+          sc[kb] = mfma(*reinterpret_cast<const f16x8*>(Kt + sw_off(kb * 32 + c, 16 * s + 8 * hl)),
+                        qf[s], sc[kb]);
+      // keys past this lane's query (or the sequence end) masked: key n = n0 + off + 4 (l / 32)
+      // is kept iff off <= min(m, seqlen - 1) - n0 - 4 (l / 32).  Only tiles that reach the
+      // block's first query hold masked keys (the test is uniform).  A lane can see a tile whose
+      // keys are all masked before any kept key (this wave skips every other tile): its masked
+      // probabilities are set to 0 below rather than computed from the running maximum.
       const int lim = (m < seqlen - 1 ? m : seqlen - 1) - n0 - 4 * hl;
+      const bool diag = n0 + kBN > mstart;
+      if (diag) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            sc[kb][v] = kb * 32 + 8 * (v >> 2) + (v & 3) <= lim ? sc[kb][v] : -1.0e30f;
+      }
+      // the row maximum of the raw scores, scaled once (the scaling is monotonic)
+      float mx = -1.0e30f;
 #pragma unroll
       for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-        for (int v = 0; v < 16; ++v)
-          sc[kb][v] = kb * 32 + 8 * (v >> 2) + (v & 3) <= lim ? sc[kb][v] : -1.0e30f;
-    }
-    // the row maximum of the raw scores, scaled once (the scaling is monotonic)
-    float mx = -1.0e30f;
+        for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kb][v]);
+      mx = fmaxf(mx, __shfl_xor(mx, 32));
+      // m_i is the reference point of l_i and O, not the exact running maximum: it moves (and O
+      // and l are rescaled) only when some lane's maximum exceeds it by more than 2^8, so p =
+      // 2^(s * qk_scale - m_i) stays below 256 and the rescale, a read-modify-write of all of O,
+      // runs on the first tile and rarely after.  The decision is per wave (uniform branch).
+      const float mt = __fmul_rn(mx, a.qk_scale);
+      if (__builtin_amdgcn_ballot_w64(mt > m_i + 8.0f) != 0) {
+        const float m_new = fmaxf(m_i, mt);
+        const float alpha = ex2(__fsub_rn(m_i, m_new));
+        l_i = __fmul_rn(l_i, alpha);
+        m_i = m_new;
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+        for (int hb = 0; hb < kHD / 32; ++hb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, sc[kb][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32));
-    // m_i is the reference point of l_i and O, not the exact running maximum: it moves (and O and
-    // l are rescaled) only when some lane's maximum exceeds it by more than 2^8, so p =
-    // 2^(s * qk_scale - m_i) stays below 256 (exact in fp16 to the same relative precision as
-    // p <= 1) and the rescale, a read-modify-write of all of O, runs on the first tile and rarely
-    // after.  The decision is per wave, so the branch is uniform.
-    const float mt = __fmul_rn(mx, a.qk_scale);
-    if (__builtin_amdgcn_ballot_w64(mt > m_i + 8.0f) != 0) {
-      const float m_new = fmaxf(m_i, mt);
-      const float alpha = ex2(__fsub_rn(m_i, m_new));
-      l_i = __fmul_rn(l_i, alpha);
-      m_i = m_new;
-#pragma unroll
-      for (int hb = 0; hb < kHD / 32; ++hb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) oacc[hb][v] = __fmul_rn(oacc[hb][v], alpha);
-    }
-    float rs = 0.0f;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float p = ex2(__builtin_fmaf(sc[kb][v], a.qk_scale, -m_i));
-        sc[kb][v] = p;
-        rs = __fadd_rn(rs, p);
+          for (int v = 0; v < 16; ++v) oacc[hb][v] = __fmul_rn(oacc[hb][v], alpha);
       }
-    rs = __fadd_rn(rs, __shfl_xor(rs, 32));
-    l_i = __fadd_rn(l_i, rs);
-    // the 16 score MFMAs of tile t + 1 spread among the softmax's VALU work
+      float rs = 0.0f;
 #pragma unroll
-    for (int i = 0; i < 16; ++i) {
-      __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);   // an operand read
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);   // an MFMA
-      __builtin_amdgcn_sched_group_barrier(0x002, 8, 0);   // VALU
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) {
+          const bool kept = !diag || kb * 32 + 8 * (v >> 2) + (v & 3) <= lim;
+          const float p = kept ? ex2(__builtin_fmaf(sc[kb][v], a.qk_scale, -m_i)) : 0.0f;
+          sc[kb][v] = p;
+          rs = __fadd_rn(rs, p);
+        }
+      rs = __fadd_rn(rs, __shfl_xor(rs, 32));
+      l_i = __fadd_rn(l_i, rs);
+      // O^T += V^T P^T over the tile's 64 keys, 16 per step
+#pragma unroll
+      for (int tt = 0; tt < kBN / 16; ++tt) {
+        const int kb = tt >> 1, i0 = 8 * (tt & 1);
+        f16x8 pf;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) pf[j] = (f16)sc[kb][i0 + j];
+#pragma unroll
+        for (int hb = 0; hb < kHD / 32; ++hb)
+          oacc[hb] = mfma(read_col8_sw(Vt, 16 * tt + 4 * hl, hb * 32), pf, oacc[hb]);
+      }
     }
-    // O^T += V^T P^T over the tile's 64 keys, 16 per step
-#pragma unroll
-    for (int tt = 0; tt < kBN / 16; ++tt) {
-      const int kb = tt >> 1, i0 = 8 * (tt & 1);
-      f16x8 pf;
-#pragma unroll
-      for (int j = 0; j < 8; ++j) pf[j] = (f16)sc[kb][i0 + j];
-#pragma unroll
-      for (int hb = 0; hb < kHD / 32; ++hb)
-        oacc[hb] = mfma(read_col8_sw(Vt, 16 * tt + 4 * hl, hb * 32), pf, oacc[hb]);
-    }
-    // tile t + 2 landed (tile t + 3 may still be in flight) and visible to every wave, and every
-    // wave is done with stage t % 4
-    if (t + 3 < n_tiles) wait_vmem<2 * kLoads>();
-    else wait_vmem<0>();
+    // pair u + 1 landed (this wave's loads) and visible to every wave, and every wave is done
+    // with pair u's stages, which then receive pair u + 2
+    wait_vmem<0>();
     __syncthreads();
-    sc[0] = sn[0];
-    sc[1] = sn[1];
+    if (2 * u + 4 < n_tiles) issue(2 * u + 4);
+    if (2 * u + 5 < n_tiles) issue(2 * u + 5);
   }
-  // result register v of block hb: head column hb * 32 + 8 (v / 4) + 4 (l / 32) + v % 4; one
-  // correctly rounded reciprocal per row, then a product per element.  The wave's 32 x 128 block
-  // of O is staged in its part of the K stages (free after the loop's last barrier) and written
-  // back 16 bytes per lane, four whole 256-byte rows per store instruction: stored from the
-  // registers, each instruction would cover 16 bytes of each of 32 rows' cache lines.
-  constexpr int kOStride = kHD + 8;   // halves per staged row
-  static_assert(kAThreads / 64 * 32 * kOStride <= kFwdStages * kTileHalves, "O staging in Ks");
-  f16* ostage = Ks + w * 32 * kOStride;
-  const float inv_l = __fdiv_rn(1.0f, l_i);   // rows past the sequence: not stored
+  // merge: the odd-tile wave of each query group hands its state (O lane-major, 16 KB per wave,
+  // in the K stages; m and l in the V stages' last KB) to the even-tile wave, which combines
+  // O = O0 2^(m0 - m) + O1 2^(m1 - m), l likewise, m = max(m0, m1).  Every stage is free after
+  // the loop's last barrier.
+  float* ohand = reinterpret_cast<float*>(Ks) + qw * (kHD / 32) * 16 * 64;
+  float* mlhand = reinterpret_cast<float*>(Vs) + (kFwdStages * kTileHalves / 2 - 256) + qw * 64;
+  static_assert(4 * (kHD / 32) * 16 * 64 * 4 <= kFwdStages * kTileHalves * 2, "O hand-over in Ks");
+  if (kg == 1) {
 #pragma unroll
-  for (int hb = 0; hb < kHD / 32; ++hb)
+    for (int hb = 0; hb < kHD / 32; ++hb)
 #pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      f16x4 o;
-#pragma unroll
-      for (int e = 0; e < 4; ++e) o[e] = (f16)__fmul_rn(oacc[hb][4 * g + e], inv_l);
-      *reinterpret_cast<f16x4*>(ostage + c * kOStride + hb * 32 + 8 * g + 4 * hl) = o;
+      for (int v = 0; v < 16; ++v) ohand[(hb * 16 + v) * 64 + lane] = oacc[hb][v];
+    if (hl == 0) {
+      mlhand[c] = m_i;
+      mlhand[32 + c] = l_i;
     }
-  if (mval && hl == 0) lse[(int64_t)h * a.n_tokens + s0 + m] = __fadd_rn(m_i, log2f(l_i));
+  }
   __syncthreads();
+  // result register v of block hb: head column hb * 32 + 8 (v / 4) + 4 (l / 32) + v % 4; one
+  // correctly rounded reciprocal per row, then a product per element.  The query group's 32 x 128
+  // block of O is staged in the V stages (clear of the hand-over) and written back 16 bytes per
+  // lane, four whole 256-byte rows per store instruction.
+  constexpr int kOStride = kHD + 8;   // halves per staged row
+  static_assert(4 * 32 * kOStride + 512 <= kFwdStages * kTileHalves, "O staging in Vs");
+  f16* ostage = Vs + qw * 32 * kOStride;
+  if (kg == 0) {
+    const float m1 = mlhand[c], l1 = mlhand[32 + c];
+    const float mm = fmaxf(m_i, m1);
+    const float a0 = ex2(__fsub_rn(m_i, mm)), a1 = ex2(__fsub_rn(m1, mm));
+    const float l = __fadd_rn(__fmul_rn(l_i, a0), __fmul_rn(l1, a1));
+    const float inv_l = __fdiv_rn(1.0f, l);   // rows past the sequence: not stored
 #pragma unroll
-  for (int i = 0; i < 8; ++i) {
-    const int r = 4 * i + (lane >> 4), cc = lane & 15;
-    const int row = mstart + 32 * w + r;
+    for (int hb = 0; hb < kHD / 32; ++hb)
+#pragma unroll
+      for (int g = 0; g < 4; ++g) {
+        f16x4 o;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int v = 4 * g + e;
+          const float ov = __fadd_rn(__fmul_rn(oacc[hb][v], a0),
+                                     __fmul_rn(ohand[(hb * 16 + v) * 64 + lane], a1));
+          o[e] = (f16)__fmul_rn(ov, inv_l);
+        }
+        *reinterpret_cast<f16x4*>(ostage + c * kOStride + hb * 32 + 8 * g + 4 * hl) = o;
+      }
+    if (mval && hl == 0) lse[(int64_t)h * a.n_tokens + s0 + m] = __fadd_rn(mm, log2f(l));
+  }
+  __syncthreads();
+  // the two waves of a query group store 16 of its 32 rows each
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const int r = 16 * kg + 4 * i + (lane >> 4), cc = lane & 15;
+    const int row = mstart + 32 * qw + r;
     const f16x8 v = *reinterpret_cast<const f16x8*>(ostage + r * kOStride + 8 * cc);
     if (row < seqlen && s0 + row < a.n_tokens)
       *reinterpret_cast<f16x8*>(out + (s0 + row) * (int64_t)(a.nq * kHD) + h * kHD + 8 * cc) = v;
@@ -203,7 +229,7 @@ extern "C" int dk_attn_fwd(const void* qkv, const int32_t* cu_seqlens, int32_t n
   if (n_blocks == 0) return 0;
   if (!out || !lse) return DK_ERR_INVALID;
   if (!dk_aligned(out, 16) || !dk_aligned(lse, 4)) return DK_ERR_ALIGN;
-  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kAThreads), 0,
+  hipLaunchKernelGGL(attn_fwd_kernel, dim3((unsigned)n_blocks, (unsigned)nq), dim3(kFThreads), 0,
                      stream, a, (f16*)out, lse);
   DK_CHECK_LAUNCH();
   return 0;
