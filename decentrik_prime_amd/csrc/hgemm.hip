@@ -164,6 +164,22 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   };
   auto staged8 = [&](int row, int col) { return staged8_of(stage, row, col); };
 
+  // SwiGLU backward: the gate/up rows of strip i + 1 are loaded while strip i is finished (two
+  // buffers), so that one strip's HBM round trip stands on the tile's path instead of TM
+  constexpr int BPASSES = 32 / ROWS_PER_PASS;
+  constexpr int BBUF = EPI == EPI_SWIGLU_BWD ? 2 : 1;
+  f16x8 gqb[BBUF][BPASSES], uqb[BBUF][BPASSES];
+  auto load_gu = [&](int i, int b) {
+#pragma unroll
+    for (int q = 0; q < BPASSES; ++q) {
+      const int64_t m = mw0 + 32 * i + srow + q * ROWS_PER_PASS;
+      const f16* gp = p.gu + (m < M ? m : M - 1) * 2 * p.inter + nw0 + 8 * seg;   // rows past M: unused
+      gqb[b][q] = *reinterpret_cast<const f16x8*>(gp);
+      uqb[b][q] = *reinterpret_cast<const f16x8*>(gp + p.inter);
+    }
+  };
+  if constexpr (EPI == EPI_SWIGLU_BWD) load_gu(0, 0);
+
 #pragma unroll
   for (int i = 0; i < TM; ++i) {
     const int64_t mrow0 = mw0 + 32 * i;
@@ -455,6 +471,9 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
       }
       __builtin_amdgcn_wave_barrier();
     } else {  // EPI_SWIGLU_BWD: N == inter; dact = fp16(acc), then the gated-SiLU backward on gu
+      // (strips are disjoint row ranges, so the next strip's loads never read what this one
+      // stores)
+      if (i + 1 < TM) load_gu(i + 1, (i + 1) & 1);
       __builtin_amdgcn_wave_barrier();
 #pragma unroll
       for (int j = 0; j < TN; ++j) {
@@ -464,16 +483,9 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
         stage_block(j, d);
       }
       __builtin_amdgcn_wave_barrier();
-      constexpr int PASSES = 32 / ROWS_PER_PASS;
-      f16x8 gq[PASSES], uq[PASSES];
-      // every pass's gate/up loads first, then the arithmetic and the stores
-#pragma unroll
-      for (int q = 0; q < PASSES; ++q) {
-        const int64_t m = mrow0 + srow + q * ROWS_PER_PASS;
-        const f16* gp = p.gu + (m < M ? m : M - 1) * 2 * p.inter + nw0 + 8 * seg;
-        gq[q] = *reinterpret_cast<const f16x8*>(gp);
-        uq[q] = *reinterpret_cast<const f16x8*>(gp + p.inter);
-      }
+      constexpr int PASSES = BPASSES;
+      const f16x8(&gq)[PASSES] = gqb[i & (BBUF - 1)];
+      const f16x8(&uq)[PASSES] = uqb[i & (BBUF - 1)];
 #pragma unroll
       for (int q = 0; q < PASSES; ++q) {
         const int row = srow + q * ROWS_PER_PASS;
