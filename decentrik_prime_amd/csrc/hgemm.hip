@@ -4,7 +4,7 @@
 //   NN (TRANS = true):  C[m][n] = sum_k A[m][k] * W[k][n]      W = p.w16 stored [K][N]
 //
 // One 512-thread workgroup per CU owns a 256 x 256 tile of C: 8 waves (2 x 4), each a 128 x 64
-// block of v_mfma_f32_16x16x32_f16 results (the 128 x 128 tiles below: v_mfma_f32_32x32x16_f16).
+// block of v_mfma_f32_16x16x32_f16 results.
 // Per output FLOP that is half the operand bytes of a 128 x 128 tile.  With real operand data
 // these GEMMs run at the clock that the power limit allows, so energy per FLOP sets their rate:
 // the 16 x 16 x 32 MFMA takes less of it than the 32 x 32 x 16 one.  K is walked in steps of 64.  Operands go from global memory straight into LDS with
@@ -114,13 +114,12 @@ __device__ __forceinline__ int swz_k(int r) { return ((r >> 1) & 7) ^ ((r & 1) <
 __device__ __forceinline__ int swz_n(int k) { return (4 * (k & 3)) ^ (2 * ((k >> 3) & 1)); }
 
 // The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
-// element is (mw0, nw0).  Register v of lane l holds, L16 (four 16 x 16 v_mfma_f32_16x16x32_f16
-// results), row 16 (v / 8) + 4 (l / 16) + v % 4, column 16 (v / 4 % 2) + l % 16; otherwise (one
-// v_mfma_f32_32x32x16_f16 result) row 8 (v / 4) + 4 (l / 32) + v % 4, column l % 32.  Each 32-row strip i is finished in
+// element is (mw0, nw0).  A block is four 16 x 16 v_mfma_f32_16x16x32_f16 results: register v of
+// lane l holds row 16 (v / 8) + 4 (l / 16) + v % 4, column 16 (v / 4 % 2) + l % 16.  Each 32-row strip i is finished in
 // registers (bias, LoRA terms, fp16 rounding), staged in this wave's LDS scratch `escr`
 // (epi_scratch_bytes(TN) bytes) and written back as 16-byte vectors of 8 consecutive columns, so that the
 // global traffic (and the gate/up reads of the SwiGLU backward) moves in whole 16-byte pieces.
-template <bool TRANS, int EPI, int TM, int TN, bool L16>
+template <bool TRANS, int EPI, int TM, int TN>
 __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
                                               int64_t mw0, int64_t nw0, uint8_t* escr,
                                               const uint8_t* pscr) {
@@ -134,14 +133,10 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   static_assert(32 * SLD * 4 + 3072 == epi_scratch_bytes(TN) && epi_scratch_bytes(TN) <= kEpiScratch,
                 "epilogue scratch");
   const int lane = threadIdx.x & 63;
-  const int lc = lane & 15;          // L16: column in a 16-column block
-  const int lk4 = 4 * (lane >> 4);   // L16: first row in a 16-row block, first rank of an MFMA
-  const int lrow = lane & 31;        // 32 x 32: column; A row of the LoRA MFMA
-  const int lk8 = 8 * (lane >> 5);   // 32 x 32: first rank of the LoRA MFMA
-  auto erow = [&](int v) {
-    return L16 ? 16 * (v >> 3) + lk4 + (v & 3) : 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-  };
-  auto ecol = [&](int v) { return L16 ? 16 * ((v >> 2) & 1) + lc : lrow; };
+  const int lc = lane & 15;          // column in a 16-column block
+  const int lk4 = 4 * (lane >> 4);   // first row in a 16-row block; first rank of a LoRA MFMA
+  auto erow = [&](int v) { return 16 * (v >> 3) + lk4 + (v & 3); };
+  auto ecol = [&](int v) { return 16 * ((v >> 2) & 1) + lc; };
   const int64_t M = p.M, N = p.N;
   float* stage = reinterpret_cast<float*>(escr);
   uint8_t* mscr = escr + 32 * SLD * 4;   // keep-mask bytes (rows of 48 bytes)
@@ -200,14 +195,13 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
       // needs in this strip (the z rows, the B rows or A columns of each block, the keep-mask
       // bytes) is issued, at rows clamped to M (rows past M are never stored), before the first
       // is used: one memory round trip per batch and 16 ranks.  Each 16 x 16 quarter of a block
-      // takes one v_mfma_f32_16x16x16_f16 per 16 ranks (L16), a whole block one
-      // v_mfma_f32_32x32x16_f16 (the result layouts above).  The terms are added to the result in
-      // order, as separate roundings.
+      // takes one v_mfma_f32_16x16x16_f16 per 16 ranks (the result layout above).  The terms are
+      // added to the result in order, as separate roundings.
       constexpr int TB = TM == 1 ? 2 : 1;
       int64_t zm[2];
 #pragma unroll
       for (int h = 0; h < 2; ++h) {
-        const int64_t r = mrow0 + (L16 ? 16 * h + lc : lrow);
+        const int64_t r = mrow0 + 16 * h + lc;
         zm[h] = r < M ? r : M - 1;
       }
       for (int t0 = 0; t0 < p.n_lora; t0 += TB) {
@@ -234,117 +228,59 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
                                                           16 * (lane & 1));
           }
         }
-        if constexpr (L16) {
-          for (int rc = 0; rc < p.rank; rc += 16) {
-            // z rows (16 h + l % 16) and, NT, B rows of the lane's columns (32 j + 16 h + l % 16),
-            // ranks rc + 4 (l / 16) ..; NN, A[rc + l / 4][8 columns of the block]
-            f16x4 zf[TB][2], rr4[TB][TN][2];
-            f16x8 rr8[TB][TN];
-  #pragma unroll
-            for (int b = 0; b < TB; ++b) {
-              if (t0 + b >= p.n_lora) continue;
-              const LoraTerm& L = p.lora[t0 + b];
-  #pragma unroll
-              for (int h = 0; h < 2; ++h)
-                zf[b][h] = *reinterpret_cast<const f16x4*>(L.z + zm[h] * p.rank + rc + lk4);
-  #pragma unroll
-              for (int j = 0; j < TN; ++j) {
-                if (!on[b][j]) continue;
-                if (!TRANS) {
-  #pragma unroll
-                  for (int h = 0; h < 2; ++h)
-                    rr4[b][j][h] = *reinterpret_cast<const f16x4*>(
-                        L.r + (nw0 + 32 * j + 16 * h + lc - L.n_begin) * p.rank + rc + lk4);
-                } else {
-                  rr8[b][j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N +
-                                                             nw0 + 32 * j + 8 * (lane & 3));
-                }
+        for (int rc = 0; rc < p.rank; rc += 16) {
+          // z rows (16 h + l % 16) and, NT, B rows of the lane's columns (32 j + 16 h + l % 16),
+          // ranks rc + 4 (l / 16) ..; NN, A[rc + l / 4][8 columns of the block]
+          f16x4 zf[TB][2], rr4[TB][TN][2];
+          f16x8 rr8[TB][TN];
+#pragma unroll
+          for (int b = 0; b < TB; ++b) {
+            if (t0 + b >= p.n_lora) continue;
+            const LoraTerm& L = p.lora[t0 + b];
+#pragma unroll
+            for (int h = 0; h < 2; ++h)
+              zf[b][h] = *reinterpret_cast<const f16x4*>(L.z + zm[h] * p.rank + rc + lk4);
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+              if (!on[b][j]) continue;
+              if (!TRANS) {
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                  rr4[b][j][h] = *reinterpret_cast<const f16x4*>(
+                      L.r + (nw0 + 32 * j + 16 * h + lc - L.n_begin) * p.rank + rc + lk4);
+              } else {
+                rr8[b][j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N +
+                                                           nw0 + 32 * j + 8 * (lane & 3));
               }
             }
-  #pragma unroll
-            for (int b = 0; b < TB; ++b)
-  #pragma unroll
-              for (int j = 0; j < TN; ++j) {
-                if (!on[b][j]) continue;
-                f16x4 rf[2];
-                if (TRANS) {
-                  // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
-                  // rank-contiguous with transposing reads: lane l gets column 16 h + l % 16, ranks
-                  // 4 (l / 16) .. + 3
-                  __builtin_amdgcn_wave_barrier();
-                  *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr8[b][j];
-                  __builtin_amdgcn_wave_barrier();
-  #pragma unroll
-                  for (int h = 0; h < 2; ++h)
-                    rf[h] = __builtin_bit_cast(
-                        f16x4, read_tr(ascr + (lk4 + (lc >> 2)) * 48 + 16 * h + 4 * (lane & 3)));
-                  __builtin_amdgcn_wave_barrier();
-                } else {
-                  rf[0] = rr4[b][j][0];
-                  rf[1] = rr4[b][j][1];
-                }
-  #pragma unroll
-                for (int q = 0; q < 4; ++q)
-                  lo[b][j][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(zf[b][q >> 1], rf[q & 1],
-                                                                      lo[b][j][q], 0, 0, 0);
-              }
           }
-        } else {
-          f32x16 lo32[TB][TN];
-  #pragma unroll
+#pragma unroll
           for (int b = 0; b < TB; ++b)
-  #pragma unroll
-            for (int j = 0; j < TN; ++j)
-  #pragma unroll
-              for (int v = 0; v < 16; ++v) lo32[b][j][v] = 0.0f;
-          for (int rc = 0; rc < p.rank; rc += 16) {
-            f16x8 zf[TB], rr[TB][TN];
-  #pragma unroll
-            for (int b = 0; b < TB; ++b) {
-              if (t0 + b >= p.n_lora) continue;
-              const LoraTerm& L = p.lora[t0 + b];
-              zf[b] = *reinterpret_cast<const f16x8*>(L.z + zm[0] * p.rank + rc + lk8);
-  #pragma unroll
-              for (int j = 0; j < TN; ++j) {
-                if (!on[b][j]) continue;
-                if (!TRANS)   // B row of this lane's column, ranks rc + lk8 ..
-                  rr[b][j] = *reinterpret_cast<const f16x8*>(
-                      L.r + (nw0 + 32 * j + lrow - L.n_begin) * p.rank + rc + lk8);
-                else          // A[rc + lane / 4][8 columns of the block]
-                  rr[b][j] = *reinterpret_cast<const f16x8*>(L.r + (int64_t)(rc + (lane >> 2)) * N +
-                                                            nw0 + 32 * j + 8 * (lane & 3));
+#pragma unroll
+            for (int j = 0; j < TN; ++j) {
+              if (!on[b][j]) continue;
+              f16x4 rf[2];
+              if (TRANS) {
+                // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
+                // rank-contiguous with transposing reads: lane l gets column 16 h + l % 16, ranks
+                // 4 (l / 16) .. + 3
+                __builtin_amdgcn_wave_barrier();
+                *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr8[b][j];
+                __builtin_amdgcn_wave_barrier();
+#pragma unroll
+                for (int h = 0; h < 2; ++h)
+                  rf[h] = __builtin_bit_cast(
+                      f16x4, read_tr(ascr + (lk4 + (lc >> 2)) * 48 + 16 * h + 4 * (lane & 3)));
+                __builtin_amdgcn_wave_barrier();
+              } else {
+                rf[0] = rr4[b][j][0];
+                rf[1] = rr4[b][j][1];
               }
-            }
-  #pragma unroll
-            for (int b = 0; b < TB; ++b)
-  #pragma unroll
-              for (int j = 0; j < TN; ++j) {
-                if (!on[b][j]) continue;
-                f16x8 rf = rr[b][j];
-                if (TRANS) {
-                  // A[rc .. rc + 16][block columns] staged row-major (rows of 48 halves), read back
-                  // rank-contiguous with transposing reads: lane l gets column l % 32, ranks
-                  // 8 (l / 32) .. + 7
-                  __builtin_amdgcn_wave_barrier();
-                  *reinterpret_cast<f16x8*>(ascr + (lane >> 2) * 48 + 8 * (lane & 3)) = rr[b][j];
-                  __builtin_amdgcn_wave_barrier();
-                  const f16* base = ascr + (lk8 + ((lane & 15) >> 2)) * 48 + 16 * ((lane >> 4) & 1) +
-                                    4 * (lane & 3);
-                  const f16x4 lo4 = read_tr(base), hi4 = read_tr(base + 4 * 48);
-                  rf = f16x8{lo4[0], lo4[1], lo4[2], lo4[3], hi4[0], hi4[1], hi4[2], hi4[3]};
-                  __builtin_amdgcn_wave_barrier();
-                }
-                lo32[b][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(zf[b], rf, lo32[b][j], 0, 0, 0);
-              }
-          }
-  #pragma unroll
-          for (int b = 0; b < TB; ++b)
-  #pragma unroll
-            for (int j = 0; j < TN; ++j)
-  #pragma unroll
+#pragma unroll
               for (int q = 0; q < 4; ++q)
-                lo[b][j][q] = f32x4{lo32[b][j][4 * q], lo32[b][j][4 * q + 1], lo32[b][j][4 * q + 2],
-                                    lo32[b][j][4 * q + 3]};
+                lo[b][j][q] = __builtin_amdgcn_mfma_f32_16x16x16f16(zf[b][q >> 1], rf[q & 1],
+                                                                    lo[b][j][q], 0, 0, 0);
+            }
         }
 #pragma unroll
         for (int b = 0; b < TB; ++b)
@@ -513,7 +449,7 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
 // NST: LDS stages of this tile shape in the kernel's 2 x 64 KB (256 x 256: 2, 128 x 128: 4, so
 // the smaller tiles, whose steps are a quarter as long, still load three steps ahead).
 // 128 x 128 NT tiles of the fp16 weight split the waves by role in the main loop: waves 0-3
-// compute (WAVES_M x 4 / WAVES_M blocks of 64 x 64: four MFMAs per 16-wide sub-step on four
+// compute (WAVES_M x 4 / WAVES_M blocks of 64 x 64: 16 MFMAs per 32-wide sub-step on eight
 // operand reads) and never load or wait for loads; waves 4-7 issue every load of the tile and
 // wait for them.  Each computing wave then hands its second 32-row strip to a loading wave, so
 // the eight waves run the epilogue on one 32 x 64 strip each, as in the 8-wave tile.  Measured on
@@ -529,10 +465,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   static_assert(NST * SA <= kStages * kStageHalves && NST * SB <= kStages * kStageHalves &&
                 (NST & (NST - 1)) == 0 && NST >= 2, "LDS stages");
   constexpr bool SPEC = BM == 128 && BN == 128 && !W4 && !TRANS;   // waves split by role
-  // the 256 x 256 tile on v_mfma_f32_16x16x32_f16, the 128 x 128 tiles on v_mfma_f32_32x32x16_f16
-  // (in the quarters, one computing wave per SIMD or two short sub-steps, the smaller MFMA
-  // measured 5-17 % slower)
-  constexpr bool M16 = BM == 256;
+
   constexpr int NCW = SPEC ? 4 : 8;         // computing waves
   constexpr int NLW = SPEC ? 4 : 8;         // loading waves
   constexpr int WAVES_N = NCW / WAVES_M;
@@ -716,7 +649,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
       for (int j = 0; j < TN; ++j)
 #pragma unroll
         for (int v = 0; v < 16; ++v) strip[0][j][v] = hand[(j * 16 + v) * 64 + lane];
-      wave_epilogue<TRANS, EPI, 1, TN, M16>(
+      wave_epilogue<TRANS, EPI, 1, TN>(
           p, strip, m0 + (c / WAVES_N) * WM + 32, n0 + (c % WAVES_N) * WN,
           reinterpret_cast<uint8_t*>(Bs) + c * kEpiScratch,
           reinterpret_cast<const uint8_t*>(Bs) + (c ^ 1) * kEpiScratch);
@@ -747,240 +680,144 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   __syncthreads();
   const int wm = wave / WAVES_N, wn = wave % WAVES_N;   // this wave's block of the tile
   f32x16 acc[TM][TN];
-  if constexpr (M16) {
-    // ---- MFMA operands: v_mfma_f32_16x16x32_f16 on 16 x 16 blocks (TM16 x TN16 per wave), two
-    // 32-wide sub-steps per 64-wide step.  A operand of lane l: row l % 16 of a 16-row block, k
-    // 8 (l / 16) .. + 7 of the sub-step; W likewise by column.  (Measured on MI355X, a loop of the
-    // GEMM's protocol on random fp16 operands: 1.40 against 1.28-1.29 PFLOP/s with
-    // v_mfma_f32_32x32x16_f16 on 32 x 32 blocks; the clock, which power sets, 1.77 against
-    // 1.51 GHz: the smaller MFMA spends less energy per FLOP.)
-    constexpr int TM16 = 2 * TM, TN16 = 2 * TN;
-    const int r16 = lane & 15;
-    const int hx = swz_k(r16);
-    int fo[2];   // operand offset of each 32-wide sub-step
-  #pragma unroll
-    for (int q = 0; q < 2; ++q) fo[q] = r16 * kBK + ((4 * q + (lane >> 4)) ^ hx) * 8;
-    // NN: the 16-lane group g reads rows 8 g + 4 h .. + 3 of the sub-step (h = 0, 1) transposed
-    const int tr_k = 8 * (lane >> 4) + (r16 >> 2);
-    const int tr_n = 4 * (lane & 3);
-    int nn_off[TN16];
-  #pragma unroll
-    for (int j = 0; j < TN16; ++j) {
-      const int n = wn * WN + 16 * j + tr_n;
-      nn_off[j] = tr_k * BN + (((n >> 3) ^ swz_n(tr_k)) * 8) + (n & 7);
-    }
-
-    f32x4 a16[TM16][TN16];
-  #pragma unroll
-    for (int i = 0; i < TM16; ++i)
-  #pragma unroll
-      for (int j = 0; j < TN16; ++j) a16[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
-    // W fragments double-buffered (the next sub-step's fragment j read after MFMA j); A fragments
-    // single-buffered (128 accumulator registers leave no room for two): the next sub-step's
-    // fragment i is read right after the last MFMA that uses the current one, MFMA
-    // (i + 1) TN16 - 1 (the MFMAs go row by row), a whole sub-step before its first use
-    constexpr int NMFMA = TM16 * TN16;
-    f16x8 fa[TM16], fb[2][TN16];
-    auto read_a = [&](int st, int s, int i) {
-      fa[i] = *reinterpret_cast<const f16x8*>(As + st * SA + (wm * WM + 16 * i) * kBK + fo[s]);
-    };
-    auto a_slot = [](int i) { return (i + 1) * TN16 - 1; };
-    auto read_b = [&](int st, int s, int j, int buf) {
-      if (!TRANS) {
-        fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + st * SB + (wn * WN + 16 * j) * kBK + fo[s]);
-      } else {
-        // ds_read_b64_tr_b16: each 16-lane group reads 4 rows x 16 columns (lane i of the group
-        // addressing row i / 4, columns 4 (i % 4) .. + 3); lane i receives column i's 4 values
-        const f16* q = Bs + st * SB + 32 * s * BN + nn_off[j];
-        const f16x4 lo = read_tr(q), hi = read_tr(q + 4 * BN);
-        fb[buf][j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-      }
-    };
-    // the reads that go out after MFMA k of a sub-step (those of sub-step s of stage st, into
-    // buffer buf)
-    auto reads_after = [&](int k, int st, int s, int buf) {
-  #pragma unroll
-      for (int j = 0; j < TN16; ++j)
-        if (j == k) read_b(st, s, j, buf);
-  #pragma unroll
-      for (int i = 0; i < TM16; ++i)
-        if (a_slot(i) == k) read_a(st, s, i);
-    };
-    static_assert(TN16 <= NMFMA, "W fragment reads beside the MFMAs");
-    // scheduling: MFMA k, then the DS reads placed after it (the other instructions, such as the W4
-    // conversion, free to fill in)
-    auto mfma_group = [&](int k) {
-      __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-      int n = 0;
-  #pragma unroll
-      for (int j = 0; j < TN16; ++j)
-        if (j == k) n += TRANS ? 2 : 1;
-  #pragma unroll
-      for (int i = 0; i < TM16; ++i)
-        if (a_slot(i) == k) n += 1;
-      if (n == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      else if (n == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
-      else if (n == 3) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
-    };
-
-  #pragma unroll
-    for (int i = 0; i < TM16; ++i) read_a(0, 0, i);
-  #pragma unroll
-    for (int j = 0; j < TN16; ++j) read_b(0, 0, j, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int st = kt & (NST - 1);
-      W4Piece w4_after;
-      if constexpr (W4) {
-        // step kt + NST + 1's packed piece (clamped at the end: loaded, never written)
-        w4_after = w4_load(kt + NST + 1 < nk ? kt + NST + 1 : nk - 1);
-      }
-      if (W4) w4_convert(w4_next);   // step kt + NST's W tile, beside the MFMAs
-      // sub-step 0 (W buffer 0), beside the reads of sub-step 1
-  #pragma unroll
-      for (int k = 0; k < NMFMA; ++k) {
-        a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            fa[k / TN16], fb[0][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
-        reads_after(k, st, 1, 1);
-      }
-  #pragma unroll
-      for (int k = 0; k < NMFMA; ++k) mfma_group(k);
-      // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
-      if (W4) wait_vmem<kW4Loads>();
-      else if (!SPEC) wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
-      __syncthreads();
-      const bool more = kt + 1 < nk;
-      const int st1 = (kt + 1) & (NST - 1);
-      const bool refill = !SPEC && kt + NST < nk;
-      if constexpr (W4) {
-        if (refill) w4_write(st);
-        w4_next = w4_after;
-      }
-      // sub-step 1 (W buffer 1), which issues the refill and reads step kt + 1's first operands, at
-      // wave priority 1: the wave past the barrier gets its DMA out ahead of the other wave's
-      // operand reads (measured on MI355X: every GEMM of the step 0.5-6 % faster, the step ~1 %)
-      __builtin_amdgcn_s_setprio(1);
-  #pragma unroll
-      for (int k = 0; k < NMFMA; ++k) {
-        a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-            fa[k / TN16], fb[1][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
-        if (more) reads_after(k, st1, 0, 0);
-  #pragma unroll
-        for (int d = k * LOADS / NMFMA; d < (k + 1) * LOADS / NMFMA; ++d)
-          if (refill) issue(kt + NST, st, d);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    }
-    // the 16 x 16 results as 32 x 32 blocks (register 4 (2 a + b) + r of block (i, j): register r
-    // of 16 x 16 block (2 i + a, 2 j + b)), the layout the epilogue takes
-  #pragma unroll
-    for (int i = 0; i < TM; ++i)
-  #pragma unroll
-      for (int j = 0; j < TN; ++j)
-  #pragma unroll
-        for (int v = 0; v < 16; ++v) acc[i][j][v] = a16[2 * i + (v >> 3)][2 * j + ((v >> 2) & 1)][v & 3];
-  } else {
-    // ---- MFMA operands: v_mfma_f32_32x32x16_f16 on 32 x 32 blocks, four 16-wide sub-steps per
-    // 64-wide step
-    const int lrow = lane & 31;
-    const int hx = swz_k(lane & 15);
-    int fo[4];   // operand offset of each 16-wide sub-step
-  #pragma unroll
-    for (int q = 0; q < 4; ++q) fo[q] = lrow * kBK + ((2 * q + (lane >> 5)) ^ hx) * 8;
-    const int tr_k = 8 * (lane >> 5) + ((lane & 15) >> 2);
-    const int tr_n = 16 * ((lane >> 4) & 1) + 4 * (lane & 3);
-    int nn_off[TN];
-  #pragma unroll
-    for (int j = 0; j < TN; ++j) {
-      const int n = wn * WN + 32 * j + tr_n;
-      nn_off[j] = tr_k * BN + (((n >> 3) ^ swz_n(tr_k)) * 8) + (n & 7);
-    }
-
-  #pragma unroll
-      for (int i = 0; i < TM; ++i)
-  #pragma unroll
-        for (int j = 0; j < TN; ++j)
-  #pragma unroll
-          for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
-    f16x8 fa[2][TM], fb[2][TN];
-
-    auto read_frags = [&](int st, int s, int buf) {   // sub-step s of stage st
-      const f16* as = As + st * SA + wm * WM * kBK + fo[s];
-  #pragma unroll
-      for (int i = 0; i < TM; ++i) fa[buf][i] = *reinterpret_cast<const f16x8*>(as + i * 32 * kBK);
-      if (!TRANS) {
-        const f16* bs = Bs + st * SB + wn * WN * kBK + fo[s];
-  #pragma unroll
-        for (int j = 0; j < TN; ++j) fb[buf][j] = *reinterpret_cast<const f16x8*>(bs + j * 32 * kBK);
-      } else {
-        // ds_read_b64_tr_b16: lane l receives W[16 s + 8 (l / 32) + 4 h + 0..3][column l % 32] of
-        // the 32 columns the lanes of its 16-lane group address; h = 0, 1 give 8 consecutive k
-  #pragma unroll
-        for (int j = 0; j < TN; ++j) {
-          const f16* q = Bs + st * SB + 16 * s * BN + nn_off[j];
-          const f16x4 lo = read_tr(q), hi = read_tr(q + 4 * BN);
-          fb[buf][j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        }
-      }
-    };
-    auto mfmas = [&](int buf) {
-  #pragma unroll
-      for (int i = 0; i < TM; ++i)
-  #pragma unroll
-        for (int j = 0; j < TN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[buf][i], fb[buf][j], acc[i][j], 0, 0, 0);
-    };
-    // one operand read after each of the first MFMAs of a sub-step
-    constexpr int NREAD = TM + (TRANS ? 2 * TN : TN);
-    auto interleave = [&]() {
-  #pragma unroll
-      for (int i = 0; i < TM * TN; ++i) {
-        __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
-        if (i < NREAD) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
-      }
-    };
-
-    read_frags(0, 0, 0);
-    for (int kt = 0; kt < nk; ++kt) {
-      const int st = kt & (NST - 1);
-      W4Piece w4_after;
-      if constexpr (W4) {
-        // step kt + NST + 1's packed piece (clamped at the end: loaded, never written)
-        w4_after = w4_load(kt + NST + 1 < nk ? kt + NST + 1 : nk - 1);
-      }
-  #pragma unroll
-      for (int j = 0; j < 3; ++j) {
-        read_frags(st, j + 1, (j + 1) & 1);
-        if (W4 && j == 0) w4_convert(w4_next);   // step kt + NST's W tile, beside the MFMAs
-        mfmas(j & 1);
-        interleave();
-      }
-      // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
-      if (W4) wait_vmem<kW4Loads>();
-      else if (!SPEC) wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
-      __syncthreads();
-      if (kt + 1 < nk) read_frags((kt + 1) & (NST - 1), 0, 0);
-      const bool refill = !SPEC && kt + NST < nk;
-      if constexpr (W4) {
-        if (refill) w4_write(st);
-        w4_next = w4_after;
-      }
-      // the last sub-step, which issues the refill, at wave priority 1: the wave past the barrier
-      // gets its DMA out ahead of the other wave's operand reads (measured on MI355X: every GEMM of
-      // the step 0.5-6 % faster, the step ~1 %)
-      __builtin_amdgcn_s_setprio(1);
-  #pragma unroll
-      for (int q = 0; q < TM * TN; ++q) {   // sub-step 3 (buffer 1)
-        acc[q / TN][q % TN] = __builtin_amdgcn_mfma_f32_32x32x16_f16(fa[1][q / TN], fb[1][q % TN],
-                                                                   acc[q / TN][q % TN], 0, 0, 0);
-  #pragma unroll
-        for (int d = q * LOADS / (TM * TN); d < (q + 1) * LOADS / (TM * TN); ++d)
-          if (refill) issue(kt + NST, st, d);
-        __builtin_amdgcn_sched_barrier(0);
-      }
-      __builtin_amdgcn_s_setprio(0);
-    }
+  // ---- MFMA operands: v_mfma_f32_16x16x32_f16 on 16 x 16 blocks (TM16 x TN16 per wave), two
+  // 32-wide sub-steps per 64-wide step.  A operand of lane l: row l % 16 of a 16-row block, k
+  // 8 (l / 16) .. + 7 of the sub-step; W likewise by column.  (Measured on MI355X, a loop of the
+  // GEMM's protocol on random fp16 operands: 1.40 against 1.28-1.29 PFLOP/s with
+  // v_mfma_f32_32x32x16_f16 on 32 x 32 blocks; the clock, which power sets, 1.77 against
+  // 1.51 GHz: the smaller MFMA spends less energy per FLOP.  In the step every GEMM's share of
+  // the power budget counts: the 128 x 128 tiles on it too measured slower replayed alone but
+  // 14.05 -> 13.65 ms per step.)
+  constexpr int TM16 = 2 * TM, TN16 = 2 * TN;
+  const int r16 = lane & 15;
+  const int hx = swz_k(r16);
+  int fo[2];   // operand offset of each 32-wide sub-step
+#pragma unroll
+  for (int q = 0; q < 2; ++q) fo[q] = r16 * kBK + ((4 * q + (lane >> 4)) ^ hx) * 8;
+  // NN: the 16-lane group g reads rows 8 g + 4 h .. + 3 of the sub-step (h = 0, 1) transposed
+  const int tr_k = 8 * (lane >> 4) + (r16 >> 2);
+  const int tr_n = 4 * (lane & 3);
+  int nn_off[TN16];
+#pragma unroll
+  for (int j = 0; j < TN16; ++j) {
+    const int n = wn * WN + 16 * j + tr_n;
+    nn_off[j] = tr_k * BN + (((n >> 3) ^ swz_n(tr_k)) * 8) + (n & 7);
   }
+
+  f32x4 a16[TM16][TN16];
+#pragma unroll
+  for (int i = 0; i < TM16; ++i)
+#pragma unroll
+    for (int j = 0; j < TN16; ++j) a16[i][j] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+  // W fragments double-buffered (the next sub-step's fragment j read after MFMA j).  A
+  // fragments: with 32 MFMAs per sub-step (128 accumulator registers, no room for two buffers)
+  // single-buffered, the next sub-step's fragment i read right after the last MFMA that uses
+  // the current one, MFMA (i + 1) TN16 - 1 (the MFMAs go row by row), a whole sub-step before
+  // its first use; with 16 or fewer, double-buffered and read after MFMA TN16 + i
+  constexpr int NMFMA = TM16 * TN16;
+  constexpr bool A2 = NMFMA <= 16;
+  f16x8 fa[A2 ? 2 : 1][TM16], fb[2][TN16];
+  auto read_a = [&](int st, int s, int i, int buf) {
+    fa[A2 ? buf : 0][i] =
+        *reinterpret_cast<const f16x8*>(As + st * SA + (wm * WM + 16 * i) * kBK + fo[s]);
+  };
+  auto a_slot = [](int i) {
+    return A2 ? (TN16 + i < NMFMA ? TN16 + i : NMFMA - 1) : (i + 1) * TN16 - 1;
+  };
+  auto read_b = [&](int st, int s, int j, int buf) {
+    if (!TRANS) {
+      fb[buf][j] = *reinterpret_cast<const f16x8*>(Bs + st * SB + (wn * WN + 16 * j) * kBK + fo[s]);
+    } else {
+      // ds_read_b64_tr_b16: each 16-lane group reads 4 rows x 16 columns (lane i of the group
+      // addressing row i / 4, columns 4 (i % 4) .. + 3); lane i receives column i's 4 values
+      const f16* q = Bs + st * SB + 32 * s * BN + nn_off[j];
+      const f16x4 lo = read_tr(q), hi = read_tr(q + 4 * BN);
+      fb[buf][j] = f16x8{lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+    }
+  };
+  // the reads that go out after MFMA k of a sub-step (those of sub-step s of stage st, into
+  // buffer buf)
+  auto reads_after = [&](int k, int st, int s, int buf) {
+#pragma unroll
+    for (int j = 0; j < TN16; ++j)
+      if (j == k) read_b(st, s, j, buf);
+#pragma unroll
+    for (int i = 0; i < TM16; ++i)
+      if (a_slot(i) == k) read_a(st, s, i, buf);
+  };
+  static_assert(TN16 <= NMFMA, "W fragment reads beside the MFMAs");
+  // scheduling: MFMA k, then the DS reads placed after it (the other instructions, such as the W4
+  // conversion, free to fill in)
+  auto mfma_group = [&](int k) {
+    __builtin_amdgcn_sched_group_barrier(0x008, 1, 0);
+    int n = 0;
+#pragma unroll
+    for (int j = 0; j < TN16; ++j)
+      if (j == k) n += TRANS ? 2 : 1;
+#pragma unroll
+    for (int i = 0; i < TM16; ++i)
+      if (a_slot(i) == k) n += 1;
+    if (n == 1) __builtin_amdgcn_sched_group_barrier(0x100, 1, 0);
+    else if (n == 2) __builtin_amdgcn_sched_group_barrier(0x100, 2, 0);
+    else if (n == 3) __builtin_amdgcn_sched_group_barrier(0x100, 3, 0);
+  };
+
+#pragma unroll
+  for (int i = 0; i < TM16; ++i) read_a(0, 0, i, 0);
+#pragma unroll
+  for (int j = 0; j < TN16; ++j) read_b(0, 0, j, 0);
+  for (int kt = 0; kt < nk; ++kt) {
+    const int st = kt & (NST - 1);
+    W4Piece w4_after;
+    if constexpr (W4) {
+      // step kt + NST + 1's packed piece (clamped at the end: loaded, never written)
+      w4_after = w4_load(kt + NST + 1 < nk ? kt + NST + 1 : nk - 1);
+    }
+    if (W4) w4_convert(w4_next);   // step kt + NST's W tile, beside the MFMAs
+    // sub-step 0 (W buffer 0), beside the reads of sub-step 1
+#pragma unroll
+    for (int k = 0; k < NMFMA; ++k) {
+      a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          fa[0][k / TN16], fb[0][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
+      reads_after(k, st, 1, 1);
+    }
+#pragma unroll
+    for (int k = 0; k < NMFMA; ++k) mfma_group(k);
+    // steps issued after kt + 1 that may still be in flight: min(nk - 1, kt + NST - 1) - (kt + 1)
+    if (W4) wait_vmem<kW4Loads>();
+    else if (!SPEC) wait_loads((nk - 1 < kt + NST - 1 ? nk - 1 : kt + NST - 1) - (kt + 1));
+    __syncthreads();
+    const bool more = kt + 1 < nk;
+    const int st1 = (kt + 1) & (NST - 1);
+    const bool refill = !SPEC && kt + NST < nk;
+    if constexpr (W4) {
+      if (refill) w4_write(st);
+      w4_next = w4_after;
+    }
+    // sub-step 1 (W buffer 1), which issues the refill and reads step kt + 1's first operands, at
+    // wave priority 1: the wave past the barrier gets its DMA out ahead of the other wave's
+    // operand reads (measured on MI355X: every GEMM of the step 0.5-6 % faster, the step ~1 %)
+    __builtin_amdgcn_s_setprio(1);
+#pragma unroll
+    for (int k = 0; k < NMFMA; ++k) {
+      a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          fa[A2 ? 1 : 0][k / TN16], fb[1][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
+      if (more) reads_after(k, st1, 0, 0);
+#pragma unroll
+      for (int d = k * LOADS / NMFMA; d < (k + 1) * LOADS / NMFMA; ++d)
+        if (refill) issue(kt + NST, st, d);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+    __builtin_amdgcn_s_setprio(0);
+  }
+  // the 16 x 16 results as 32 x 32 blocks (register 4 (2 a + b) + r of block (i, j): register r
+  // of 16 x 16 block (2 i + a, 2 j + b)), the layout the epilogue takes
+#pragma unroll
+  for (int i = 0; i < TM; ++i)
+#pragma unroll
+    for (int j = 0; j < TN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = a16[2 * i + (v >> 3)][2 * j + ((v >> 2) & 1)][v & 3];
   // every wave is past the last barrier, after which no wave reads a stage and no load is in
   // flight: the stages are free for the per-wave epilogue scratch
 
@@ -998,7 +835,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     f32x16 strip[1][TN];
 #pragma unroll
     for (int j = 0; j < TN; ++j) strip[0][j] = acc[0][j];
-    wave_epilogue<TRANS, EPI, 1, TN, M16>(p, strip, m0 + wm * WM, n0 + wn * WN,
+    wave_epilogue<TRANS, EPI, 1, TN>(p, strip, m0 + wm * WM, n0 + wn * WN,
                                      reinterpret_cast<uint8_t*>(As) + wave * kEpiScratch,
                                      reinterpret_cast<const uint8_t*>(As) + (wave ^ 1) * kEpiScratch);
     return;
@@ -1024,7 +861,7 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   const int pw = wave ^ 1;
   const uint8_t* pscr = reinterpret_cast<const uint8_t*>(pw < 4 ? As : Bs) + (pw & 3) * kEpiScratch;
   static_assert(WAVES_N % 2 == 0, "partner waves share rows");
-  wave_epilogue<TRANS, EPI, TM, TN, M16>(p, acc, m0 + wm * WM, n0 + wn * WN, escr, pscr);
+  wave_epilogue<TRANS, EPI, TM, TN>(p, acc, m0 + wm * WM, n0 + wn * WN, escr, pscr);
 }
 
 // main_tiles workgroups run 256 x 256 tiles and tail_wgs run the tiles past main_tiles as
@@ -1203,8 +1040,7 @@ __global__ __launch_bounds__(64) void hgemm_reduce_kernel(GemmParams p) {
         for (int v = 0; v < 16; ++v)
           acc[0][0][v] = sp + u == 0 ? v_all[u][v >> 2][v & 3] : acc[0][0][v] + v_all[u][v >> 2][v & 3];
   }
-  // split K runs on 256 x 256 tiles only, whose results are in the 16 x 16 layout
-  wave_epilogue<TRANS, EPI, 1, 1, true>(p, acc, m0, n0, escr, escr);   // never rotary: no split-K
+  wave_epilogue<TRANS, EPI, 1, 1>(p, acc, m0, n0, escr, escr);   // never rotary: no split-K
 }
 
 int cu_count() {
