@@ -58,8 +58,8 @@ constexpr int kStageHalves = kTile * kBK;    // one operand of one stage: 32 KB
 constexpr int kEpiScratch = 16384;           // bytes of LDS per wave for the epilogue
 
 // Epilogue scratch of a wave with TN 32-column blocks per strip: the staged strip (32 rows of
-// 32 TN + 8 floats) plus the keep-mask and LoRA A slices (1536 bytes each).
-constexpr int epi_scratch_bytes(int tn) { return 32 * (32 * tn + 8) * 4 + 3072; }
+// 32 TN + 4 floats) plus the keep-mask and LoRA A slices (1536 bytes each).
+constexpr int epi_scratch_bytes(int tn) { return 32 * (32 * tn + 4) * 4 + 3072; }
 
 __device__ __forceinline__ unsigned lds_offset(const void* p) {
   return (unsigned)(size_t)(__attribute__((address_space(3))) const void*)p;
@@ -124,10 +124,11 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
                                               int64_t mw0, int64_t nw0, uint8_t* escr,
                                               const uint8_t* pscr) {
   constexpr int COLS = 32 * TN;          // columns of a strip
-  constexpr int SLD = COLS + 8;          // floats per staged row: the two half-waves' rows
-                                         // (4 apart) land 32 banks apart; on odd rows the
-                                         // 16-byte chunks swap in pairs (column bit 2), so the
-                                         // read-back's neighbouring rows hit distinct banks
+  // floats per staged row: the four row groups a staging store covers (rows 4 apart) land 16
+  // banks apart, so the stores are free of bank conflicts (measured with SQ_LDS_BANK_CONFLICT on
+  // MI355X: rows of COLS + 8 floats with the 16-byte chunks of odd rows swapped in pairs, the
+  // previous layout, cost these stores two-way conflicts; the read-backs cost the same either way)
+  constexpr int SLD = COLS + 4;
   constexpr int SEGS = COLS / 8;         // 8-column segments per row
   constexpr int ROWS_PER_PASS = 64 / SEGS;
   static_assert(32 * SLD * 4 + 3072 == epi_scratch_bytes(TN) && epi_scratch_bytes(TN) <= kEpiScratch,
@@ -147,14 +148,12 @@ __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)
   auto stage_block = [&](int j, const f32x16& r) {
 #pragma unroll
     for (int v = 0; v < 16; ++v) {
-      const int row = erow(v);
-      stage[row * SLD + ((32 * j + ecol(v)) ^ ((row & 1) << 2))] = r[v];
+      stage[erow(v) * SLD + 32 * j + ecol(v)] = r[v];
     }
   };
   auto staged8_of = [&](const float* st, int row, int col) {
-    const int sw = (row & 1) << 2;
-    const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * SLD + (col ^ sw));
-    const f32x4 b = *reinterpret_cast<const f32x4*>(st + row * SLD + ((col + 4) ^ sw));
+    const f32x4 a = *reinterpret_cast<const f32x4*>(st + row * SLD + col);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(st + row * SLD + col + 4);
     return f32x8_t{a[0], a[1], a[2], a[3], b[0], b[1], b[2], b[3]};
   };
   auto staged8 = [&](int row, int col) { return staged8_of(stage, row, col); };
