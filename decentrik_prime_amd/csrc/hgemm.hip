@@ -714,6 +714,11 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   // the current one, MFMA (i + 1) TN16 - 1 (the MFMAs go row by row), a whole sub-step before
   // its first use; with 16 or fewer, double-buffered and read after MFMA TN16 + i
   constexpr int NMFMA = TM16 * TN16;
+  // MFMA k of a sub-step: A fragment k / TN16 and, row by row in a serpentine, W fragment kj(k),
+  // so that two MFMAs in a row share an operand at each row change too (every accumulator still
+  // takes its sub-steps in order: the sums are unchanged).  Measured on MI355X, bit-identical: the
+  // large GEMMs 0.7-0.9 % faster in the step
+  auto kj = [](int k) { return (k / TN16) & 1 ? TN16 - 1 - k % TN16 : k % TN16; };
   constexpr bool A2 = NMFMA <= 16;
   f16x8 fa[A2 ? 2 : 1][TM16], fb[2][TN16];
   auto read_a = [&](int st, int s, int i, int buf) {
@@ -776,8 +781,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     // sub-step 0 (W buffer 0), beside the reads of sub-step 1
 #pragma unroll
     for (int k = 0; k < NMFMA; ++k) {
-      a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          fa[0][k / TN16], fb[0][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
+      a16[k / TN16][kj(k)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          fa[0][k / TN16], fb[0][kj(k)], a16[k / TN16][kj(k)], 0, 0, 0);
       reads_after(k, st, 1, 1);
     }
 #pragma unroll
@@ -799,8 +804,8 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
     __builtin_amdgcn_s_setprio(1);
 #pragma unroll
     for (int k = 0; k < NMFMA; ++k) {
-      a16[k / TN16][k % TN16] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
-          fa[A2 ? 1 : 0][k / TN16], fb[1][k % TN16], a16[k / TN16][k % TN16], 0, 0, 0);
+      a16[k / TN16][kj(k)] = __builtin_amdgcn_mfma_f32_16x16x32_f16(
+          fa[A2 ? 1 : 0][k / TN16], fb[1][kj(k)], a16[k / TN16][kj(k)], 0, 0, 0);
       if (more) reads_after(k, st1, 0, 0);
 #pragma unroll
       for (int d = k * LOADS / NMFMA; d < (k + 1) * LOADS / NMFMA; ++d)
