@@ -4,15 +4,15 @@
 //   NN (TRANS = true):  C[m][n] = sum_k A[m][k] * W[k][n]      W = p.w16 stored [K][N]
 //
 // One 512-thread workgroup per CU owns a 256 x 256 tile of C: 8 waves (2 x 4), each a 128 x 64
-// block of v_mfma_f32_16x16x32_f16 results.
-// Per output FLOP that is half the operand bytes of a 128 x 128 tile.  With real operand data
-// these GEMMs run at the clock that the power limit allows, so energy per FLOP sets their rate:
-// the 16 x 16 x 32 MFMA takes less of it than the 32 x 32 x 16 one.  K is walked in steps of 64.  Operands go from global memory straight into LDS with
-// global_load_lds_dwordx4 (LDS DMA: no registers, no LDS write instructions) into two stages
-// (2 x 64 KB): the loads of step k + 2 go out during the last MFMAs of step k, into the stage
-// step k has just finished reading.  Each wave waits only for its own loads (vmcnt), and one
-// barrier per step both publishes the next step's tiles and frees the stage just read.  The MFMA
-// operands of the next 16-wide sub-step are read while the MFMAs of the current one run; the
+// block of v_mfma_f32_16x16x32_f16 results.  Per output FLOP that is half the operand bytes of a
+// 128 x 128 tile.  With real operand data these GEMMs run at the clock that the power limit
+// allows, so energy per FLOP sets their rate: the 16 x 16 x 32 MFMA takes less of it than the
+// 32 x 32 x 16 one.  K is walked in steps of 64.  Operands go from global memory straight into
+// LDS with global_load_lds_dwordx4 (LDS DMA: no registers, no LDS write instructions) into two
+// stages (2 x 64 KB): the loads of step k + 2 go out during the last MFMAs of step k, into the
+// stage step k has just finished reading.  Each wave waits only for its own loads (vmcnt), and
+// one barrier per step both publishes the next step's tiles and frees the stage just read.  The
+// MFMA operands of the next 32-wide sub-step are read while the MFMAs of the current one run; the
 // last sub-step, which issues the refill, runs at wave priority 1 so that its loads go out ahead
 // of the other wave's operand reads.  (Measured on MI355X: 64-wide steps in two stages run about
 // 8% faster than 32-wide steps in a four-stage ring; the barriers, not the load distance, are
@@ -115,10 +115,11 @@ __device__ __forceinline__ int swz_n(int k) { return (4 * (k & 3)) ^ (2 * ((k >>
 
 // The fused epilogue of one wave's TM x TN blocks of 32 x 32 results, whose top-left output
 // element is (mw0, nw0).  A block is four 16 x 16 v_mfma_f32_16x16x32_f16 results: register v of
-// lane l holds row 16 (v / 8) + 4 (l / 16) + v % 4, column 16 (v / 4 % 2) + l % 16.  Each 32-row strip i is finished in
-// registers (bias, LoRA terms, fp16 rounding), staged in this wave's LDS scratch `escr`
-// (epi_scratch_bytes(TN) bytes) and written back as 16-byte vectors of 8 consecutive columns, so that the
-// global traffic (and the gate/up reads of the SwiGLU backward) moves in whole 16-byte pieces.
+// lane l holds row 16 (v / 8) + 4 (l / 16) + v % 4, column 16 (v / 4 % 2) + l % 16.  Each 32-row
+// strip i is finished in registers (bias, LoRA terms, fp16 rounding), staged in this wave's LDS
+// scratch `escr` (epi_scratch_bytes(TN) bytes) and written back as 16-byte vectors of 8
+// consecutive columns, so that the global traffic (and the gate/up reads of the SwiGLU backward)
+// moves in whole 16-byte pieces.
 template <bool TRANS, int EPI, int TM, int TN>
 __device__ __forceinline__ void wave_epilogue(const GemmParams& p, f32x16 (&acc)[TM][TN],
                                               int64_t mw0, int64_t nw0, uint8_t* escr,
@@ -484,9 +485,9 @@ __device__ __forceinline__ void gemm_tile(const GemmParams& p, int64_t m0, int64
   const int lw = SPEC ? wave - NCW : wave;              // its index among the loading waves
 
   // ---- DMA sources (first K step kt0; nk steps): instruction j of loading wave w fills the
-  // stage's chunks [(NLW j + w) 64, +64).  Each operand has a wave-uniform base at step kt0 (A: the tile's
-  // first row; W: the weight's first row (NT) or the tile's first column (NN)) and a 32-bit byte
-  // offset per lane and instruction; the host keeps every offset below 2^32.
+  // stage's chunks [(NLW j + w) 64, +64).  Each operand has a wave-uniform base at step kt0 (A:
+  // the tile's first row; W: the weight's first row (NT) or the tile's first column (NN)) and a
+  // 32-bit byte offset per lane and instruction; the host keeps every offset below 2^32.
   const uint64_t a_base = uniform64((uint64_t)(p.a + m0 * p.lda + (int64_t)kt0 * kBK));
   const uint64_t b_base = uniform64(
       (uint64_t)(TRANS ? p.w16 + (int64_t)kt0 * kBK * N + n0 : p.w16 + (int64_t)kt0 * kBK));
