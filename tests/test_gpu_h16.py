@@ -57,7 +57,7 @@ def torch():
     return t
 
 
-@pytest.mark.parametrize("m", [2048, 200])
+@pytest.mark.parametrize("m", [2048, 200, 17])
 def test_h16_fused_qkv(torch, m):
     """Fused QKV forward (two column-range LoRA terms, bias) and the dX GEMM with both masked LoRA
     terms, on the fp16 weight."""
@@ -127,8 +127,9 @@ def test_h16_o_projection(torch):
 
 
 # M = 2300: 9 row tiles, so the down^T SwiGLU backward has 315 tiles (256 full + 59 leftover as
-# 236 quarter workgroups, dispatched first: a count that is not a multiple of the 8 XCDs)
-@pytest.mark.parametrize("m", [2048, 2300, 300])
+# 236 quarter workgroups, dispatched first: a count that is not a multiple of the 8 XCDs); M = 1:
+# one token, every tile's rows but the first clamped
+@pytest.mark.parametrize("m", [2048, 2300, 300, 1])
 def test_h16_mlp(torch, m):
     """gate|up SwiGLU forward, down forward, down^T + SwiGLU backward and gate|up^T on fp16
     weights."""
